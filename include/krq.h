@@ -1,0 +1,151 @@
+/*
+ * krq.h - C ABI of libkrq.so, the gfx950 (MI355X) decode-matmul path for Qwen3-4B shapes.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, element counts and a hipStream_t passed as void*;
+ *   - allocates nothing and never synchronises the host, so it can be captured into a hipGraph;
+ *   - returns KRQ_OK (0) on success, KRQ_EINVAL for a bad shape or argument (raised as
+ *     ValueError / AssertionError by the Python layer, mirroring the reference), or KRQ_EHIP for a
+ *     HIP launch error (raised as RuntimeError). krq_last_error() gives the message of the
+ *     calling thread's last failure.
+ *
+ * Data formats:
+ *   bf16      - IEEE bfloat16 bit patterns (uint16), row-major.
+ *   e4m3      - OCP FP8 E4M3 "fn" bytes (max 448, no infinities, NaN = 0x7F/0xFF), i.e. the
+ *               values of torch.float8_e4m3fn.
+ *   tiled     - the FP8 weight copy read by the GEMV kernels. A [N, K] matrix is cut into
+ *               16-row x 64-byte tiles, stored tile-row-major ([N/16][K/64]); inside a tile,
+ *               lane l (0..63) owns the 16 contiguous bytes of row (l % 16), columns
+ *               64*t + 16*(l / 16) .. +16. One 64-lane 128-bit load reads one whole tile (1 KiB,
+ *               contiguous). Needs N % 16 == 0 and K % 64 == 0. krq_unpack_fp8 inverts it.
+ *   partials  - split-K output: fp32 [split, M, N]; the consumer sums slices 0..split-1 in that
+ *               order and rounds once to bf16 (reference engine/kernels/ops.py:29-39).
+ */
+#ifndef KRQ_H
+#define KRQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KRQ_OK 0
+#define KRQ_EINVAL (-1)
+#define KRQ_EHIP (-2)
+
+/* GEMV output modes */
+#define KRQ_OUT_BF16 0     /* bf16 [M, N]; split must be 1 */
+#define KRQ_OUT_PARTIAL 1  /* fp32 [split, M, N] */
+#define KRQ_OUT_SWIGLU 2   /* w = [gate; up] with 2*I rows; bf16 [M, I] = bf16(bf16(silu(g)) * u) */
+
+/* weight layouts for the FP8 GEMV */
+#define KRQ_W_ROWMAJOR 0
+#define KRQ_W_TILED 1
+
+/* lm-head weight kinds */
+#define KRQ_LM_BF16 0
+#define KRQ_LM_FP8 1
+
+/*
+ * Per-output-channel weight quantizer. Replaces the weight-packing step of engine loading
+ * (reference engine/engine.py:496-501) with the per-row form the reference's experiments call as
+ * fp8.quantize (experiments/modal_fp8.py:59-60; row formula experiments/modal_fq.py:62-63, clamp
+ * convention experiments/i8.py:11-17):
+ *   amax[n]  = max_k |w[n,k]|;  scale[n] = max(amax[n], 1e-12) * fp32(1/448)
+ *   w8[n,k]  = e4m3_rne(clamp(float(w[n,k]) / scale[n], -448, 448))     (IEEE division)
+ * w_bf16 rows are ldw elements apart. w8 (row-major [N,K], may be NULL) and w8_tiled (may be
+ * NULL) receive the same bytes in the two layouts; at least one must be given.
+ */
+int krq_quant_fp8_rows(const void* w_bf16, int64_t N, int64_t K, int64_t ldw,
+                       void* w8, void* w8_tiled, float* scale, void* stream);
+
+/*
+ * Per-tensor weight quantizer: quantize_weight (reference engine/kernels/fp8.py:17-23).
+ *   scale0 = max(max|w|, 1e-12) * fp32(1/448);  w8 = e4m3_rne(clamp(float(w) / scale0, +-448))
+ * row_amax_ws: caller workspace of N floats (overwritten).
+ */
+int krq_quant_fp8_tensor(const void* w_bf16, int64_t N, int64_t K, int64_t ldw,
+                         float* row_amax_ws, void* w8, void* w8_tiled, float* scale0,
+                         void* stream);
+
+/*
+ * Activation scale: ActScale (reference engine/kernels/fp8.py:26-35).
+ *   amax = max(max|x|, 1e-6) * headroom;  inv = fp32(1/amax) * 448;  scale = amax * fp32(1/448)
+ * per_row = 0: one scale for the whole [M,K] tensor (amax, inv, scale hold 1 float each);
+ *              ws must hold at least krq_act_scale_ws_floats(M, K) floats.
+ * per_row = 1: one scale per row (amax, inv, scale hold M floats each); ws may be NULL.
+ */
+int krq_act_scale(const void* x_bf16, int64_t M, int64_t K, int per_row, float headroom,
+                  float* amax, float* inv, float* scale, float* ws, void* stream);
+int64_t krq_act_scale_ws_floats(int64_t M, int64_t K);
+
+/*
+ * FP8 cast: _cast_kernel / _cast_torch (reference engine/kernels/fp8.py:38-56).
+ *   x8[m,k] = e4m3_rne(clamp(float(x[m,k]) * inv[per_row ? m : 0], -448, 448))
+ */
+int krq_cast_fp8(const void* x_bf16, int64_t M, int64_t K, const float* inv, int per_row,
+                 void* x8, void* stream);
+
+/*
+ * Per-token dynamic quantization in one launch: fp8.quant_rows as called by the reference's
+ * experiments/modal_fp8.py:84-85 (x8, xs for torch._scaled_mm scale_a); ActScale per row plus
+ * the cast above. xs[m] = scale of row m (amax[m]/448 as above).
+ */
+int krq_quant_rows(const void* x_bf16, int64_t M, int64_t K, void* x8, float* xs, void* stream);
+
+/*
+ * FP8 skinny GEMM/GEMV, M <= 32: replaces linear_fp8 -> torch._scaled_mm (reference
+ * engine/kernels/fp8.py:97-106) at decode sizes, and supplies gemv_fp8 / gemv_swiglu_fp8 as
+ * called by experiments/modal_fp8.py:67-69 under the output contract of gemv / gemv_swiglu
+ * (engine/kernels/gemv.py:83-88, :125-130, :137-167).
+ *   acc[m,n] = sum_k x8[m,k] * w8[n,k]   (fp32 accumulate)
+ *   y[m,n]   = acc[m,n] * x_scale[m or 0] * w_scale[n or 0]
+ * x8: e4m3 [M,K] row-major. w8: e4m3 [N,K] (or [2I,K] for SWIGLU) in layout w_layout.
+ * mode KRQ_OUT_BF16 -> bf16 [M,N] (split 1); KRQ_OUT_PARTIAL -> fp32 [split,M,N] of the K-slices
+ * [s*K/split, (s+1)*K/split); KRQ_OUT_SWIGLU -> bf16 [M,I] (split 1).
+ * Needs N % 16 == 0, K % split == 0 and (K/split) % 64 == 0.
+ * algo: 0 = automatic, 1 = matrix-core (MFMA) kernel, 2 = vector-ALU kernel (M == 1 only).
+ */
+int krq_gemv_fp8(const void* x8, const float* x_scale, int x_per_row,
+                 const void* w8, int w_layout, const float* w_scale, int w_per_row,
+                 int64_t M, int64_t N, int64_t K, int split, int mode, int algo,
+                 void* out, void* stream);
+
+/*
+ * BF16 skinny GEMM/GEMV, M <= 32, row-major weights: gemv / gemv_m1 / gemv_swiglu /
+ * gemv_m1_swiglu / gemv_rows (reference engine/kernels/gemv.py:43-348).
+ *   acc = x[M,K] . w[N,K]^T in fp32; modes as krq_gemv_fp8.
+ * Needs N % 16 == 0, K % split == 0 and (K/split) % 32 == 0.
+ */
+int krq_gemv_bf16(const void* x, const void* w, int64_t M, int64_t N, int64_t K, int split,
+                  int mode, void* out, void* stream);
+
+/*
+ * LM head + greedy argmax, one launch: logits = bf16(h . E^T) and idx[m] = lowest index of the
+ * maximum bf16 logit of row m. Reference: engine/engine.py:1021-1022 (gemv(h, lm_head, 1) then
+ * torch.argmax) and the fused form engine/kernels/mega.py:396-441.
+ * w_kind KRQ_LM_BF16: h bf16 [M,K], w bf16 [V,K] row-major, w_scale/h_scale unused.
+ * w_kind KRQ_LM_FP8:  h e4m3 [M,K] with h_scale[M] (per token), w e4m3 [V,K] in w_layout with
+ *                     w_scale[V]; logits as krq_gemv_fp8 KRQ_OUT_BF16.
+ * logits: optional bf16 [M,V] output (NULL to skip). ws: caller workspace of at least
+ * krq_lmhead_ws_bytes(M, V) bytes; its leading counter word must be zero before the first call
+ * and is left zero by every call.
+ */
+int krq_lmhead_argmax(const void* h, const float* h_scale, const void* w, int w_kind, int w_layout,
+                      const float* w_scale, int64_t M, int64_t V, int64_t K, void* logits,
+                      void* ws, int64_t ws_bytes, int64_t* idx_out, void* stream);
+int64_t krq_lmhead_ws_bytes(int64_t M, int64_t V);
+
+/* Tiled <-> row-major FP8 weight copies (byte permutations; see "tiled" above). */
+int krq_pack_fp8(const void* w8_rowmajor, int64_t N, int64_t K, void* w8_tiled, void* stream);
+int krq_unpack_fp8(const void* w8_tiled, int64_t N, int64_t K, void* w8_rowmajor, void* stream);
+
+const char* krq_version(void);
+const char* krq_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KRQ_H */

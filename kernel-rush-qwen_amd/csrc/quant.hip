@@ -1,0 +1,291 @@
+// Quantization kernels of the decode-matmul path (gfx950):
+//   weight quantizers (per output channel, per tensor), activation scales (per tensor, per
+//   token), the scaled FP8 cast, and the tiled <-> row-major FP8 weight permutations.
+// Every quantized byte goes through krq::clamp_to_e4m3, the software OCP E4M3 RNE encoder, so
+// the bytes equal torch's float8_e4m3fn cast of the same fp32 values.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "krq_common.h"
+
+using namespace krq;
+
+// ---------------------------------------------------------------------------------------------
+// error plumbing
+// ---------------------------------------------------------------------------------------------
+static thread_local char g_err[512] = "";
+
+void krq_set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+int krq_check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    krq_set_error("%s: %s", what, hipGetErrorString(e));
+    return KRQ_EHIP;
+  }
+  return KRQ_OK;
+}
+
+extern "C" const char* krq_last_error(void) { return g_err; }
+extern "C" const char* krq_version(void) { return "krq 0.1.0 gfx950"; }
+
+#define KRQ_REQUIRE(cond, ...)        \
+  do {                                \
+    if (!(cond)) {                    \
+      krq_set_error(__VA_ARGS__);     \
+      return KRQ_EINVAL;              \
+    }                                 \
+  } while (0)
+
+namespace {
+
+constexpr int kQT = 256;  // threads of the row-wise kernels
+
+// ---------------------------------------------------------------------------------------------
+// Weight rows. One block per row n.
+//   MODE 0 (per channel): amax -> scale[n] -> cast with IEEE division by scale[n]
+//   MODE 1 (per tensor, pass 1): row_amax[n] = amax
+//   MODE 2 (per tensor, pass 3): cast with IEEE division by scale[0]
+// Reference: engine/kernels/fp8.py:17-23 (per tensor), experiments/i8.py:11-17 and
+// experiments/modal_fq.py:62-63 (per row).
+// ---------------------------------------------------------------------------------------------
+template <int MODE>
+__global__ __launch_bounds__(kQT) void k_weight_rows(const uint16_t* __restrict__ w, int64_t K,
+                                                     int64_t ldw, uint8_t* __restrict__ w8,
+                                                     uint8_t* __restrict__ w8t,
+                                                     float* __restrict__ scale,
+                                                     float* __restrict__ row_amax) {
+  const int64_t n = blockIdx.x;
+  const uint16_t* row = w + n * ldw;
+  float s;
+  if (MODE == 2) {
+    s = scale[0];
+  } else {
+    float m = 0.0f;
+    for (int64_t k = threadIdx.x; k < K; k += kQT) m = fmaxf(m, fabsf(bf16_to_f32(row[k])));
+    m = block_max<kQT>(m);
+    if (MODE == 1) {
+      if (threadIdx.x == 0) row_amax[n] = m;
+      return;
+    }
+    s = scale_from_amax(fmaxf(m, 1e-12f));
+    if (threadIdx.x == 0) scale[n] = s;
+  }
+  for (int64_t k = threadIdx.x; k < K; k += kQT) {
+    const uint8_t q = clamp_to_e4m3(bf16_to_f32(row[k]) / s);
+    if (w8) w8[n * K + k] = q;
+    if (w8t) w8t[tiled_offset(n, k, K)] = q;
+  }
+}
+
+// per-tensor pass 2: one block folds the N row maxima into scale0
+__global__ __launch_bounds__(1024) void k_fold_scale(const float* __restrict__ row_amax, int64_t N,
+                                                     float* __restrict__ scale0) {
+  float m = 0.0f;
+  for (int64_t i = threadIdx.x; i < N; i += 1024) m = fmaxf(m, row_amax[i]);
+  m = block_max<1024>(m);
+  if (threadIdx.x == 0) scale0[0] = scale_from_amax(fmaxf(m, 1e-12f));
+}
+
+// ---------------------------------------------------------------------------------------------
+// Activation scales (ActScale, engine/kernels/fp8.py:26-35):
+//   amax = max(max|x|, 1e-6) * headroom; inv = fp32(1/amax) * 448; scale = amax * fp32(1/448)
+// ---------------------------------------------------------------------------------------------
+KRQ_DEV void act_finish(float m, float headroom, float* amax, float* inv, float* scale, int64_t i) {
+  const float a = fmaxf(m, 1e-6f) * headroom;
+  amax[i] = a;
+  inv[i] = inv_from_amax(a);
+  scale[i] = scale_from_amax(a);
+}
+
+// per tensor pass 1: block-strided partial maxima into ws[blockIdx.x]
+__global__ __launch_bounds__(kQT) void k_absmax_partial(const uint16_t* __restrict__ x, int64_t n,
+                                                        float* __restrict__ ws) {
+  float m = 0.0f;
+  for (int64_t i = blockIdx.x * (int64_t)kQT + threadIdx.x; i < n; i += (int64_t)gridDim.x * kQT)
+    m = fmaxf(m, fabsf(bf16_to_f32(x[i])));
+  m = block_max<kQT>(m);
+  if (threadIdx.x == 0) ws[blockIdx.x] = m;
+}
+
+// per tensor pass 2
+__global__ __launch_bounds__(1024) void k_act_fold(const float* __restrict__ ws, int g,
+                                                   float headroom, float* amax, float* inv,
+                                                   float* scale) {
+  float m = 0.0f;
+  for (int i = threadIdx.x; i < g; i += 1024) m = fmaxf(m, ws[i]);
+  m = block_max<1024>(m);
+  if (threadIdx.x == 0) act_finish(m, headroom, amax, inv, scale, 0);
+}
+
+// per row: one block per row m; with x8 != nullptr the row is also cast (quant_rows)
+__global__ __launch_bounds__(kQT) void k_act_rows(const uint16_t* __restrict__ x, int64_t K,
+                                                  float headroom, float* amax, float* inv,
+                                                  float* scale, uint8_t* __restrict__ x8) {
+  const int64_t r = blockIdx.x;
+  const uint16_t* row = x + r * K;
+  float m = 0.0f;
+  for (int64_t k = threadIdx.x; k < K; k += kQT) m = fmaxf(m, fabsf(bf16_to_f32(row[k])));
+  m = block_max<kQT>(m);
+  const float a = fmaxf(m, 1e-6f) * headroom;
+  const float iv = inv_from_amax(a);
+  if (threadIdx.x == 0) {
+    if (amax) amax[r] = a;
+    if (inv) inv[r] = iv;
+    scale[r] = scale_from_amax(a);
+  }
+  if (x8)
+    for (int64_t k = threadIdx.x; k < K; k += kQT) x8[r * K + k] = clamp_to_e4m3(bf16_to_f32(row[k]) * iv);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Cast (engine/kernels/fp8.py:38-56): x8 = e4m3(clamp(float(x) * inv, +-448))
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(kQT) void k_cast(const uint16_t* __restrict__ x, int64_t M, int64_t K,
+                                              const float* __restrict__ inv, int per_row,
+                                              uint8_t* __restrict__ x8) {
+  const int64_t n = M * K;
+  for (int64_t i = blockIdx.x * (int64_t)kQT + threadIdx.x; i < n; i += (int64_t)gridDim.x * kQT) {
+    const float iv = inv[per_row ? i / K : 0];
+    x8[i] = clamp_to_e4m3(bf16_to_f32(x[i]) * iv);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Tiled <-> row-major: one thread moves one lane's 16 bytes of one tile.
+// ---------------------------------------------------------------------------------------------
+template <bool PACK>
+__global__ __launch_bounds__(kQT) void k_permute(const uint8_t* __restrict__ src, int64_t N, int64_t K,
+                                                 uint8_t* __restrict__ dst) {
+  const int64_t total = (N >> 4) * (K >> 6) * 64;
+  for (int64_t i = blockIdx.x * (int64_t)kQT + threadIdx.x; i < total; i += (int64_t)gridDim.x * kQT) {
+    const int64_t tile = i >> 6;
+    const int lane = static_cast<int>(i & 63);
+    const int64_t kt = K >> 6;
+    const int64_t n = (tile / kt) * 16 + (lane & 15);
+    const int64_t k = (tile % kt) * 64 + (lane >> 4) * 16;
+    const uint4* a = reinterpret_cast<const uint4*>(src + (PACK ? n * K + k : i * 16));
+    uint4* b = reinterpret_cast<uint4*>(dst + (PACK ? i * 16 : n * K + k));
+    *b = *a;
+  }
+}
+
+int grid_for(int64_t work, int per_block, int cap) {
+  int64_t g = (work + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return static_cast<int>(g);
+}
+
+}  // namespace
+
+// =============================================================================================
+// C ABI
+// =============================================================================================
+extern "C" int krq_quant_fp8_rows(const void* w_bf16, int64_t N, int64_t K, int64_t ldw, void* w8,
+                                  void* w8_tiled, float* scale, void* stream) {
+  KRQ_REQUIRE(w_bf16 && scale && (w8 || w8_tiled), "quant_fp8_rows: null pointer");
+  KRQ_REQUIRE(N > 0 && K > 0 && ldw >= K, "quant_fp8_rows: bad shape N=%lld K=%lld ldw=%lld",
+              (long long)N, (long long)K, (long long)ldw);
+  KRQ_REQUIRE(N <= 0x7fffffff, "quant_fp8_rows: N=%lld too large", (long long)N);
+  KRQ_REQUIRE(!w8_tiled || (N % 16 == 0 && K % 64 == 0),
+              "quant_fp8_rows: tiled layout needs N %% 16 == 0 and K %% 64 == 0 (N=%lld K=%lld)",
+              (long long)N, (long long)K);
+  hipLaunchKernelGGL(k_weight_rows<0>, dim3(static_cast<unsigned>(N)), dim3(kQT), 0,
+                     (hipStream_t)stream, (const uint16_t*)w_bf16, K, ldw, (uint8_t*)w8,
+                     (uint8_t*)w8_tiled, scale, nullptr);
+  return krq_check_launch("quant_fp8_rows");
+}
+
+extern "C" int krq_quant_fp8_tensor(const void* w_bf16, int64_t N, int64_t K, int64_t ldw,
+                                    float* row_amax_ws, void* w8, void* w8_tiled, float* scale0,
+                                    void* stream) {
+  KRQ_REQUIRE(w_bf16 && row_amax_ws && scale0 && (w8 || w8_tiled), "quant_fp8_tensor: null pointer");
+  KRQ_REQUIRE(N > 0 && K > 0 && ldw >= K, "quant_fp8_tensor: bad shape N=%lld K=%lld ldw=%lld",
+              (long long)N, (long long)K, (long long)ldw);
+  KRQ_REQUIRE(N <= 0x7fffffff, "quant_fp8_tensor: N=%lld too large", (long long)N);
+  KRQ_REQUIRE(!w8_tiled || (N % 16 == 0 && K % 64 == 0),
+              "quant_fp8_tensor: tiled layout needs N %% 16 == 0 and K %% 64 == 0 (N=%lld K=%lld)",
+              (long long)N, (long long)K);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_weight_rows<1>, dim3(static_cast<unsigned>(N)), dim3(kQT), 0, s,
+                     (const uint16_t*)w_bf16, K, ldw, nullptr, nullptr, nullptr, row_amax_ws);
+  hipLaunchKernelGGL(k_fold_scale, dim3(1), dim3(1024), 0, s, row_amax_ws, N, scale0);
+  hipLaunchKernelGGL(k_weight_rows<2>, dim3(static_cast<unsigned>(N)), dim3(kQT), 0, s,
+                     (const uint16_t*)w_bf16, K, ldw, (uint8_t*)w8, (uint8_t*)w8_tiled, scale0,
+                     nullptr);
+  return krq_check_launch("quant_fp8_tensor");
+}
+
+static constexpr int kActPartials = 1024;
+
+extern "C" int64_t krq_act_scale_ws_floats(int64_t M, int64_t K) {
+  return grid_for(M * K, kQT * 16, kActPartials);
+}
+
+extern "C" int krq_act_scale(const void* x_bf16, int64_t M, int64_t K, int per_row, float headroom,
+                             float* amax, float* inv, float* scale, float* ws, void* stream) {
+  KRQ_REQUIRE(x_bf16 && amax && inv && scale, "act_scale: null pointer");
+  KRQ_REQUIRE(M > 0 && K > 0, "act_scale: bad shape M=%lld K=%lld", (long long)M, (long long)K);
+  hipStream_t s = (hipStream_t)stream;
+  if (per_row) {
+    KRQ_REQUIRE(M <= 0x7fffffff, "act_scale: M=%lld too large", (long long)M);
+    hipLaunchKernelGGL(k_act_rows, dim3(static_cast<unsigned>(M)), dim3(kQT), 0, s,
+                       (const uint16_t*)x_bf16, K, headroom, amax, inv, scale, nullptr);
+  } else {
+    KRQ_REQUIRE(ws != nullptr, "act_scale: per-tensor scale needs a workspace");
+    const int g = grid_for(M * K, kQT * 16, kActPartials);
+    hipLaunchKernelGGL(k_absmax_partial, dim3(g), dim3(kQT), 0, s, (const uint16_t*)x_bf16, M * K, ws);
+    hipLaunchKernelGGL(k_act_fold, dim3(1), dim3(1024), 0, s, ws, g, headroom, amax, inv, scale);
+  }
+  return krq_check_launch("act_scale");
+}
+
+extern "C" int krq_cast_fp8(const void* x_bf16, int64_t M, int64_t K, const float* inv, int per_row,
+                            void* x8, void* stream) {
+  KRQ_REQUIRE(x_bf16 && inv && x8, "cast_fp8: null pointer");
+  KRQ_REQUIRE(M > 0 && K > 0, "cast_fp8: bad shape M=%lld K=%lld", (long long)M, (long long)K);
+  const int g = grid_for(M * K, kQT * 4, 8192);
+  hipLaunchKernelGGL(k_cast, dim3(g), dim3(kQT), 0, (hipStream_t)stream, (const uint16_t*)x_bf16, M,
+                     K, inv, per_row, (uint8_t*)x8);
+  return krq_check_launch("cast_fp8");
+}
+
+extern "C" int krq_quant_rows(const void* x_bf16, int64_t M, int64_t K, void* x8, float* xs,
+                              void* stream) {
+  KRQ_REQUIRE(x_bf16 && x8 && xs, "quant_rows: null pointer");
+  KRQ_REQUIRE(M > 0 && K > 0 && M <= 0x7fffffff, "quant_rows: bad shape M=%lld K=%lld",
+              (long long)M, (long long)K);
+  hipLaunchKernelGGL(k_act_rows, dim3(static_cast<unsigned>(M)), dim3(kQT), 0, (hipStream_t)stream,
+                     (const uint16_t*)x_bf16, K, 1.0f, nullptr, nullptr, xs, (uint8_t*)x8);
+  return krq_check_launch("quant_rows");
+}
+
+extern "C" int krq_pack_fp8(const void* w8_rowmajor, int64_t N, int64_t K, void* w8_tiled,
+                            void* stream) {
+  KRQ_REQUIRE(w8_rowmajor && w8_tiled, "pack_fp8: null pointer");
+  KRQ_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 64 == 0,
+              "pack_fp8: needs N %% 16 == 0 and K %% 64 == 0 (N=%lld K=%lld)", (long long)N,
+              (long long)K);
+  const int g = grid_for((N / 16) * (K / 64) * 64, kQT, 65536);
+  hipLaunchKernelGGL(k_permute<true>, dim3(g), dim3(kQT), 0, (hipStream_t)stream,
+                     (const uint8_t*)w8_rowmajor, N, K, (uint8_t*)w8_tiled);
+  return krq_check_launch("pack_fp8");
+}
+
+extern "C" int krq_unpack_fp8(const void* w8_tiled, int64_t N, int64_t K, void* w8_rowmajor,
+                              void* stream) {
+  KRQ_REQUIRE(w8_rowmajor && w8_tiled, "unpack_fp8: null pointer");
+  KRQ_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 64 == 0,
+              "unpack_fp8: needs N %% 16 == 0 and K %% 64 == 0 (N=%lld K=%lld)", (long long)N,
+              (long long)K);
+  const int g = grid_for((N / 16) * (K / 64) * 64, kQT, 65536);
+  hipLaunchKernelGGL(k_permute<false>, dim3(g), dim3(kQT), 0, (hipStream_t)stream,
+                     (const uint8_t*)w8_tiled, N, K, (uint8_t*)w8_rowmajor);
+  return krq_check_launch("unpack_fp8");
+}

@@ -1,0 +1,275 @@
+"""FP8 (OCP e4m3) decode matmuls on MI355X: quantizers, activation scales, the scaled cast, and
+the dequant-fused skinny GEMM/GEMV that replaces torch._scaled_mm at decode sizes.
+
+Drop-in for the reference's engine/kernels/fp8.py (signatures of quantize_weight, ActScale,
+SharedScale, linear_fp8, pick_cast, FP8_MAX, HEADROOM kept as at fp8.py:13-106), plus the
+per-channel / per-token family its experiments call (experiments/modal_fp8.py:59-85): quantize,
+quant_rows, gemv_fp8, gemv_swiglu_fp8.
+
+Numerics (every quantized byte is the OCP e4m3 round-to-nearest-even of the clamped value, as
+torch's float8_e4m3fn cast gives):
+  quantize_weight  scale = max(max|w|, 1e-12) / 448;  w8 = e4m3(clamp(w / scale, +-448))
+  quantize         the same per output row (scale [N])
+  ActScale         amax = max(max|x|, 1e-6) * headroom; inv = 448 / amax; scale = amax / 448
+  quant_rows       ActScale per row, then x8 = e4m3(clamp(x * inv[m], +-448)); xs = scale [M, 1]
+  gemv_fp8 et al.  y = (sum_k x8 w8) * x_scale * w_scale with fp32 accumulation
+Quantized weights carry, beside the reference's row-major [N, K] bytes, a copy in the GEMV
+kernels' tiled layout (FP8Weight.tiled).
+"""
+
+import os
+
+import torch
+
+from . import _lib as L
+
+FP8_MAX = 448.0
+HEADROOM = float(os.environ.get("ENGINE_FP8_HEADROOM", "4"))
+DECODE_MAX_ROWS = 32  # rows handled by one launch of the skinny kernels
+
+
+class FP8Weight(tuple):
+    """(w8, scale) as the reference returns it - w8 the row-major float8_e4m3fn [N, K] matrix,
+    scale fp32 0-d (per tensor) or [N] (per output channel) - with the same bytes in the tiled
+    layout of include/krq.h as .tiled (uint8 [N*K], or None when N % 16 or K % 64)."""
+
+    def __new__(cls, w8, scale, tiled=None):
+        self = super().__new__(cls, (w8, scale))
+        self.tiled = tiled
+        return self
+
+
+def _check_weight(w):
+    L.require_device(w)
+    if w.dim() != 2 or w.dtype != torch.bfloat16:
+        raise ValueError(f"expected a bf16 [N, K] weight, got {w.dtype} {tuple(w.shape)}")
+    return w if w.stride(1) == 1 else w.contiguous()
+
+
+def _weight_out(w, tiled):
+    N, K = w.shape
+    w8 = torch.empty((N, K), device=w.device, dtype=torch.float8_e4m3fn)
+    t = None
+    if tiled and N % 16 == 0 and K % 64 == 0:
+        t = torch.empty((N * K,), device=w.device, dtype=torch.uint8)
+    return w8, t
+
+
+@torch.no_grad()
+def quantize_weight(w, tiled=True):
+    """w [N, K] bf16 -> (w8 [N, K] float8_e4m3fn, scale fp32 scalar), w ~= w8 * scale.
+    Reference: engine/kernels/fp8.py:17-23."""
+    w = _check_weight(w)
+    N, K = w.shape
+    w8, t = _weight_out(w, tiled)
+    scale = torch.empty((), device=w.device, dtype=torch.float32)
+    ws = torch.empty((N,), device=w.device, dtype=torch.float32)
+    L.call("krq_quant_fp8_tensor", L.ptr(w), N, K, w.stride(0), L.ptr(ws), L.ptr(w8), L.ptr(t),
+           L.ptr(scale), L.stream(w))
+    return FP8Weight(w8, scale, t)
+
+
+@torch.no_grad()
+def quantize(w, tiled=True):
+    """w [N, K] bf16 -> (w8 [N, K] float8_e4m3fn, scale fp32 [N]), w ~= w8 * scale[:, None].
+    Per-output-channel form called by the reference's experiments/modal_fp8.py:59-60."""
+    w = _check_weight(w)
+    N, K = w.shape
+    w8, t = _weight_out(w, tiled)
+    scale = torch.empty((N,), device=w.device, dtype=torch.float32)
+    L.call("krq_quant_fp8_rows", L.ptr(w), N, K, w.stride(0), L.ptr(w8), L.ptr(t), L.ptr(scale),
+           L.stream(w))
+    return FP8Weight(w8, scale, t)
+
+
+def _rows(x):
+    L.require_device(x)
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"expected bf16 activations, got {x.dtype}")
+    x2 = x.reshape(-1, x.shape[-1]) if x.dim() != 2 else x
+    return x2.contiguous()
+
+
+class ActScale:
+    """Activation scale for one call: x8 = clamp(x * inv), x ~= x8 * scale.
+    Computed on device from this tensor's own range (no sync, graph-safe).
+    Reference: engine/kernels/fp8.py:26-35."""
+
+    def __init__(self, x, headroom=1.0):
+        x2 = _rows(x)
+        M, K = x2.shape
+        dev = x2.device
+        self.amax = torch.empty((), device=dev, dtype=torch.float32)
+        self.inv = torch.empty((1,), device=dev, dtype=torch.float32)
+        self.scale = torch.empty((), device=dev, dtype=torch.float32)
+        ws = torch.empty((max(1, L.lib().krq_act_scale_ws_floats(M, K)),), device=dev,
+                         dtype=torch.float32)
+        L.call("krq_act_scale", L.ptr(x2), M, K, 0, float(headroom), L.ptr(self.amax),
+               L.ptr(self.inv), L.ptr(self.scale), L.ptr(ws), L.stream(x2))
+
+
+class SharedScale:
+    """Scale slots living in caller-owned device tensors (read by decode graphs).
+    Reference: engine/kernels/fp8.py:90-94."""
+
+    def __init__(self, inv, scale):
+        self.inv, self.scale = inv, scale
+
+
+def quant_rows(x):
+    """Per-token dynamic FP8: x [M, K] bf16 -> (x8 [M, K] float8_e4m3fn, xs fp32 [M, 1]) with
+    x ~= x8 * xs, the operands of torch._scaled_mm(x8, w8.t(), scale_a=xs, ...) in the
+    reference's experiments/modal_fp8.py:84-85."""
+    x2 = _rows(x)
+    M, K = x2.shape
+    x8 = torch.empty((M, K), device=x2.device, dtype=torch.float8_e4m3fn)
+    xs = torch.empty((M, 1), device=x2.device, dtype=torch.float32)
+    L.call("krq_quant_rows", L.ptr(x2), M, K, L.ptr(x8), L.ptr(xs), L.stream(x2))
+    return x8, xs
+
+
+def _cast_hip(x, a):
+    x2 = _rows(x)
+    M, K = x2.shape
+    L.require_device(a.inv)
+    y = torch.empty(x.shape, device=x.device, dtype=torch.float8_e4m3fn)
+    L.call("krq_cast_fp8", L.ptr(x2), M, K, L.ptr(a.inv), 0, L.ptr(y), L.stream(x2))
+    return y
+
+
+def _cast_torch(x, a):
+    return (x.float() * a.inv).clamp_(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+
+
+_cast = _cast_hip
+
+
+def pick_cast(log):
+    """Validate the HIP cast against torch's cast on this GPU (bit-exact) and report both
+    timings. Keeps the HIP cast when every byte matches; otherwise falls back to the torch cast
+    and says so, as the reference does on a failed check (engine/kernels/fp8.py:62-87)."""
+    global _cast
+    _cast = _cast_hip
+    try:
+        x = torch.randn((4096, 2560), device="cuda", dtype=torch.bfloat16) * 3
+        a = ActScale(x)
+        ref = _cast_torch(x, a).view(torch.uint8)
+        got = _cast_hip(x, a).view(torch.uint8)
+        bad = int((ref != got).sum().item())
+        ts = {}
+        for name, fn in (("torch", _cast_torch), ("hip", _cast_hip)):
+            fn(x, a)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(5):
+                fn(x, a)
+            e1.record()
+            e1.synchronize()
+            ts[name] = e0.elapsed_time(e1) / 5
+        if bad:
+            _cast = _cast_torch
+        log(f"fp8 cast: {ts} mismatched bytes={bad} -> {_cast.__name__}")
+    except Exception as e:  # pragma: no cover - mirrors the reference's guarded check
+        log(f"fp8 hip cast check failed: {e!r}")
+
+
+# ---------------------------------------------------------------------------------------------
+# skinny GEMM / GEMV
+# ---------------------------------------------------------------------------------------------
+def _weight_operand(q):
+    w8, ws = q[0], q[1]
+    tiled = getattr(q, "tiled", None)
+    L.require_device(w8, ws)
+    if ws.dtype != torch.float32:
+        raise ValueError("weight scale must be fp32")
+    if tiled is not None:
+        return tiled, L.W_TILED, ws, w8.shape
+    if w8.dtype != torch.float8_e4m3fn or w8.dim() != 2 or not w8.is_contiguous():
+        raise ValueError("expected a contiguous float8_e4m3fn [N, K] weight")
+    return w8, L.W_ROWMAJOR, ws, w8.shape
+
+
+def gemv_fp8_launch(x8, xs, q, split=1, mode=L.OUT_BF16, algo=L.ALGO_AUTO, out=None):
+    """One launch of the FP8 GEMV kernel on already-quantized activations.
+    x8 float8_e4m3fn [M, K] (M <= 32); xs fp32 with 1 (per tensor) or M (per token) values;
+    q = quantize(W) or quantize_weight(W). Returns out (allocated when None): bf16 [M, N],
+    fp32 partials [split, M, N], or bf16 [M, N/2] for mode OUT_SWIGLU."""
+    w, layout, ws, (N, K) = _weight_operand(q)
+    L.require_device(x8, xs)
+    M = x8.shape[0]
+    if x8.dtype != torch.float8_e4m3fn or x8.dim() != 2 or x8.shape[1] != K or not x8.is_contiguous():
+        raise ValueError(f"x8 must be a contiguous float8_e4m3fn [M, {K}] tensor")
+    if xs.dtype != torch.float32 or xs.numel() not in (1, M):
+        raise ValueError("xs must be fp32 with 1 or M values")
+    xpr = 1 if (xs.numel() == M and M > 1) else 0
+    wpr = 1 if ws.numel() > 1 else 0
+    if out is None:
+        if mode == L.OUT_PARTIAL:
+            out = torch.empty((split, M, N), device=x8.device, dtype=torch.float32)
+        else:
+            out = torch.empty((M, N // 2 if mode == L.OUT_SWIGLU else N), device=x8.device,
+                              dtype=torch.bfloat16)
+    L.call("krq_gemv_fp8", L.ptr(x8), L.ptr(xs), xpr, L.ptr(w), layout, L.ptr(ws), wpr, M, N, K,
+           split, mode, algo, L.ptr(out), L.stream(x8))
+    return out
+
+
+def _activation_fp8(x, a, xs):
+    """(x8, x_scale) for the GEMV: x8 given (fp8 dtype) with xs; a static or per-call ActScale a;
+    or per-token dynamic scales."""
+    if x.dtype == torch.float8_e4m3fn:
+        if xs is None:
+            raise ValueError("float8 activations need their scale xs")
+        return x.contiguous(), xs.reshape(-1).contiguous()
+    if a is not None:
+        return _cast(x, a), a.scale.reshape(1)
+    x8, s = quant_rows(x)
+    return x8, s.reshape(-1)
+
+
+def _chunked(x8, xs, fn):
+    M = x8.shape[0]
+    if M <= DECODE_MAX_ROWS:
+        return fn(x8, xs)
+    outs = []
+    for m0 in range(0, M, DECODE_MAX_ROWS):
+        m1 = min(M, m0 + DECODE_MAX_ROWS)
+        outs.append(fn(x8[m0:m1], xs[m0:m1] if xs.numel() == M else xs))
+    return torch.cat(outs, dim=-2)
+
+
+def gemv_fp8(x, q, split=1, a=None, xs=None, algo=L.ALGO_AUTO):
+    """FP8 counterpart of kernels.gemv.gemv: x [M, K] bf16 (or float8_e4m3fn with xs), q from
+    quantize / quantize_weight. split == 1: bf16 [M, N]; split > 1: fp32 partials [split, M, N]
+    whose in-order sum is the product. Activations are scaled per token unless an ActScale /
+    SharedScale `a` is given. Called as fp8.gemv_fp8(x, q, split) by the reference's
+    experiments/modal_fp8.py:69."""
+    M, K = x.shape
+    assert K % split == 0
+    x8, s = _activation_fp8(x, a, xs)
+    mode = L.OUT_BF16 if split == 1 else L.OUT_PARTIAL
+    return _chunked(x8, s, lambda xc, sc: gemv_fp8_launch(xc, sc, q, split, mode, algo))
+
+
+def gemv_swiglu_fp8(x, q, a=None, xs=None, algo=L.ALGO_AUTO):
+    """FP8 counterpart of kernels.gemv.gemv_swiglu: q quantizes w_gu [2I, K] = [gate; up];
+    returns bf16(bf16(silu(bf16 g)) * bf16 u) [M, I]. Called as fp8.gemv_swiglu_fp8(x, q) by the
+    reference's experiments/modal_fp8.py:67."""
+    x8, s = _activation_fp8(x, a, xs)
+    return _chunked(x8, s, lambda xc, sc: gemv_fp8_launch(xc, sc, q, 1, L.OUT_SWIGLU, algo))
+
+
+def linear_fp8(x, q, a=None, amax_out=None):
+    """bf16 [M, N] ~= x @ W^T with q = quantize_weight(W); a = given scale, or
+    None to scale by this tensor's own range (running max kept in amax_out).
+    Reference: engine/kernels/fp8.py:97-106. Decode sizes (M <= 32) run the HIP GEMV; larger M
+    (prefill) keep the reference's library GEMM, torch._scaled_mm (hipBLASLt on ROCm)."""
+    w8, ws = q[0], q[1]
+    if a is None:
+        a = ActScale(x)
+        if amax_out is not None:
+            amax_out.copy_(torch.maximum(amax_out, a.amax.reshape(1)))
+    x8 = _cast(x, a)
+    if x.shape[0] <= DECODE_MAX_ROWS:
+        return gemv_fp8_launch(x8, a.scale.reshape(1), q, 1, L.OUT_BF16)
+    return torch._scaled_mm(x8, w8.t(), scale_a=a.scale, scale_b=ws, out_dtype=torch.bfloat16)

@@ -1,0 +1,84 @@
+"""Host-side checks of the drop-in boundary that need no GPU: the C-ABI library loads and exports
+every symbol include/krq.h declares, argument validation maps to the reference's exception
+types, and nothing silently runs on the CPU."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from kernels import _lib as L
+from kernels import fp8, gemv as G
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "krq.h")).read()
+    return set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(krq_\w+)\s*\(", text, re.M))
+
+
+def test_library_exports_every_header_symbol():
+    lib = L.lib()
+    declared = header_symbols()
+    assert declared == set(L.EXPORTS), declared ^ set(L.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name)
+    assert lib.krq_version().decode().startswith("krq")
+
+
+def test_workspace_sizes_are_host_only():
+    lib = L.lib()
+    assert lib.krq_lmhead_ws_bytes(16, 151936) >= 256 + 16 * 8 * (151936 // 64)
+    assert lib.krq_act_scale_ws_floats(16, 2560) >= 1
+
+
+def _null():
+    return ctypes.c_void_p(0)
+
+
+def test_invalid_arguments_fail_before_any_launch():
+    lib = L.lib()
+    p = ctypes.c_void_p(4096)  # never dereferenced: validation rejects the call first
+    # M out of range
+    rc = lib.krq_gemv_fp8(p, p, 0, p, 1, p, 1, 0, 64, 256, 1, 0, 0, p, _null())
+    assert rc == L.KRQ_EINVAL and b"M=0" in lib.krq_last_error()
+    # K/split not a multiple of 64
+    rc = lib.krq_gemv_fp8(p, p, 0, p, 1, p, 1, 1, 64, 200, 1, 0, 0, p, _null())
+    assert rc == L.KRQ_EINVAL and b"K_SPLIT" in lib.krq_last_error()
+    # split > 1 without the partials output
+    rc = lib.krq_gemv_bf16(p, p, 1, 64, 256, 2, 0, p, _null())
+    assert rc == L.KRQ_EINVAL
+    # null pointers
+    rc = lib.krq_quant_fp8_rows(None, 16, 64, 64, p, None, p, _null())
+    assert rc == L.KRQ_EINVAL
+    # workspace too small
+    rc = lib.krq_lmhead_argmax(p, None, p, 0, 0, None, 1, 1024, 256, None, p, 8, p, _null())
+    assert rc == L.KRQ_EINVAL and b"workspace" in lib.krq_last_error()
+    with pytest.raises(ValueError):
+        L.call("krq_pack_fp8", p, 17, 64, p, _null())
+
+
+def test_no_cpu_path():
+    w = torch.zeros(16, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        fp8.quantize(w)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        G.gemv(torch.zeros(1, 64, dtype=torch.bfloat16), w)
+
+
+def test_reference_helpers():
+    assert G._bm(1) == 16 and G._bm(16) == 16 and G._bm(17) == 32 and G._bm(32) == 32
+    with pytest.raises(ValueError):
+        G._prune(G._CONFIGS, {"K_SPLIT": 48, "N": 64})
+    assert G._prune(G._CONFIGS, {"K": 64, "N": 32})
+    with pytest.raises(ValueError):
+        G.gemv_tma(torch.zeros(1, 64), torch.zeros(64, 64))
+    with pytest.raises(AssertionError):
+        G.gemv_m1(torch.zeros(2, 64, dtype=torch.bfloat16), torch.zeros(16, 64, dtype=torch.bfloat16))
+    assert fp8.FP8_MAX == 448.0
+    q = fp8.FP8Weight(torch.zeros(1), torch.ones(()), None)
+    w8, s = q
+    assert isinstance(q, tuple) and q.tiled is None and s.item() == 1.0

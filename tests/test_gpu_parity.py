@@ -1,0 +1,399 @@
+"""Parity of the HIP path (through the C ABI, via the kernels package) with the CPU oracle.
+
+Integer/byte work (quantizers, casts, packing, argmax indices) must be bit-exact. GEMM outputs
+must satisfy max|y - ref| <= 1e-2 * max|ref| (the normalisation of the reference's own check,
+engine/engine.py:876) against the exact oracle of the same FP8 semantics; the measured error is
+printed. Seeds follow the measurement plan: W ~ N(0, 0.02), x ~ N(0, 1), bf16.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from kernels import _lib as L
+from kernels import fp8, lmhead
+from kernels.gemv import gemv, gemv_m1, gemv_m1_swiglu, gemv_rows, gemv_swiglu
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+QKV, O_PROJ, GATE_UP, DOWN = (6144, 2560), (2560, 4096), (19456, 2560), (2560, 9728)
+
+
+def u16(t):
+    return t.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def u8(t):
+    return t.cpu().contiguous().view(torch.uint8).numpy()
+
+
+def weight(N, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+
+
+def act(M, K, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(M, K, generator=g) * scale).to(torch.bfloat16)
+
+
+def rel_err(y, ref):
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.abs(y - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+# ---------------------------------------------------------------------------------------------
+# casts and scale arithmetic
+# ---------------------------------------------------------------------------------------------
+def test_torch_device_scale_arithmetic(dev):
+    """Pins the oracle's device form of the reference's scale expressions on this GPU:
+    tensor / 448.0 multiplies by fp32(1/448); 448.0 / tensor is reciprocal() * 448."""
+    a = torch.rand(1 << 20, generator=torch.Generator().manual_seed(3)) * 8 + 1e-3
+    d = a.to(dev)
+    got_div = (d / fp8.FP8_MAX).cpu().numpy()
+    got_rdiv = (fp8.FP8_MAX / d).cpu().numpy()
+    an = a.numpy()
+    assert np.array_equal(got_div, O.div448(an, "device"))
+    assert np.array_equal(got_rdiv, O.inv_from_amax(an))
+
+
+@pytest.mark.parametrize("inv", [1.0, 3.0, 0.0123, 448.0 / 3.1])
+def test_cast_all_bf16_patterns(dev, inv):
+    bits = np.arange(65536, dtype=np.uint16)
+    x = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).reshape(256, 256)
+    a = fp8.SharedScale(torch.tensor([inv], dtype=torch.float32, device=dev), None)
+    got = u8(fp8._cast_hip(x.to(dev), a))
+    ref_torch = u8((x.float() * torch.tensor([inv], dtype=torch.float32)).clamp(-448, 448).to(torch.float8_e4m3fn))
+    assert np.array_equal(got, O.cast(bits.reshape(256, 256), np.float32(inv)))
+    assert np.array_equal(got, ref_torch)
+    dev_ref = u8(fp8._cast_torch(x.to(dev), a))
+    assert np.array_equal(got, dev_ref)
+
+
+def test_act_scale_and_cast(dev):
+    x = act(16, 2560, 5, 3.0)
+    a = fp8.ActScale(x.to(dev))
+    amax, inv, scale = O.act_scale(u16(x))
+    assert a.amax.shape == () and a.inv.shape == (1,) and a.scale.shape == ()
+    assert a.amax.item() == amax and a.inv.item() == inv and a.scale.item() == scale
+    # the reference expression evaluated by torch on this device
+    xd = x.to(dev)
+    mn, mx = torch.aminmax(xd)
+    am = torch.maximum(-mn, mx).float().clamp_min(1e-6) * 1.0
+    assert torch.equal(am, a.amax) and torch.equal((fp8.FP8_MAX / am).reshape(1), a.inv)
+    assert torch.equal((am / fp8.FP8_MAX).reshape(()), a.scale)
+    assert np.array_equal(u8(fp8._cast_hip(xd, a)), O.cast(u16(x), inv))
+    # headroom and an all-zero tensor (clamp_min(1e-6))
+    a4 = fp8.ActScale(xd, headroom=4.0)
+    assert a4.amax.item() == O.act_scale(u16(x), 4.0)[0]
+    z = fp8.ActScale(torch.zeros(2, 64, dtype=torch.bfloat16, device=dev))
+    assert z.amax.item() == np.float32(1e-6)
+
+
+@pytest.mark.parametrize("M,K", [(1, 2560), (16, 9728), (32, 4096), (3, 64)])
+def test_quant_rows(dev, M, K):
+    x = act(M, K, 7 + M)
+    x[0, 0] = 0.0
+    x8, xs = fp8.quant_rows(x.to(dev))
+    r8, rs = O.quant_rows(u16(x))
+    assert xs.shape == (M, 1)
+    assert np.array_equal(u8(x8), r8)
+    assert np.array_equal(xs.cpu().numpy().reshape(-1), rs)
+
+
+# ---------------------------------------------------------------------------------------------
+# weight quantizers and packing
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("N,K", [(64, 256), QKV, (48, 200)])
+def test_quantize_per_channel(dev, N, K):
+    w = weight(N, K, 11)
+    w[1] = 0.0            # zero row: scale = 1e-12 / 448
+    w[2, :7] = -1e-30     # bf16 denormal-ish negatives -> signed zero codes
+    q = fp8.quantize(w.to(dev))
+    r8, rs = O.quantize(u16(w))
+    assert np.array_equal(u8(q[0]), r8)
+    assert np.array_equal(q[1].cpu().numpy(), rs)
+    if N % 16 == 0 and K % 64 == 0:
+        assert np.array_equal(q.tiled.cpu().numpy(), O.tile(r8))
+    else:
+        assert q.tiled is None
+    # the per-row expression (experiments/modal_fq.py:62-63 with the i8.py clamp) in torch on device
+    wf = w.to(dev).float()
+    s = wf.abs().amax(1).clamp_min(1e-12) / fp8.FP8_MAX
+    ref = (wf / s[:, None]).clamp(-448, 448).to(torch.float8_e4m3fn)
+    assert torch.equal(s, q[1])
+    assert torch.equal(ref.view(torch.uint8), q[0].view(torch.uint8))
+
+
+@pytest.mark.parametrize("N,K", [(64, 256), QKV])
+def test_quantize_weight_per_tensor(dev, N, K):
+    w = weight(N, K, 13)
+    q = fp8.quantize_weight(w.to(dev))
+    r8, rs = O.quantize_weight(u16(w))
+    assert q[1].shape == ()
+    assert q[1].item() == rs
+    assert np.array_equal(u8(q[0]), r8)
+    # engine/kernels/fp8.py:20-23 evaluated by torch on this device
+    wf = w.to(dev).float()
+    scale = (wf.abs().max().clamp_min(1e-12) / fp8.FP8_MAX).reshape(())
+    ref = (wf / scale).clamp_(-448, 448).to(torch.float8_e4m3fn)
+    assert torch.equal(scale, q[1])
+    assert torch.equal(ref.view(torch.uint8), q[0].view(torch.uint8))
+
+
+def test_pack_unpack_roundtrip(dev):
+    N, K = 256, 1280
+    w8 = torch.randint(0, 256, (N, K), dtype=torch.uint8, generator=torch.Generator().manual_seed(1))
+    wd = w8.to(dev)
+    t = torch.empty(N * K, dtype=torch.uint8, device=dev)
+    back = torch.empty_like(wd)
+    s = L.stream(wd)
+    L.call("krq_pack_fp8", L.ptr(wd), N, K, L.ptr(t), s)
+    L.call("krq_unpack_fp8", L.ptr(t), N, K, L.ptr(back), s)
+    assert np.array_equal(t.cpu().numpy(), O.tile(w8.numpy()))
+    assert torch.equal(back, wd)
+
+
+# ---------------------------------------------------------------------------------------------
+# FP8 GEMV / skinny GEMM
+# ---------------------------------------------------------------------------------------------
+def _fp8_case(N, K, M, seed):
+    w = weight(N, K, 1000 + seed)
+    x = act(M, K, 2000 + seed)
+    return w, x
+
+
+SHAPES = {"qkv": QKV, "o": O_PROJ, "down": DOWN, "small": (64, 384)}
+SEEDS = {"qkv": 0, "o": 1, "down": 3, "small": 5}
+
+
+@pytest.mark.parametrize("name", list(SHAPES))
+@pytest.mark.parametrize("M", [1, 2, 16, 32])
+def test_gemv_fp8(dev, name, M):
+    N, K = SHAPES[name]
+    w, x = _fp8_case(N, K, M, SEEDS[name])
+    q = fp8.quantize(w.to(dev))
+    r8, rs = O.quantize(u16(w))
+    x8r, xsr = O.quant_rows(u16(x))
+    _, yref = O.fp8_matmul(x8r, xsr, r8, rs)
+    xd = x.to(dev)
+    for split in (1, 2, 4):
+        if (K // split) % 64:
+            continue
+        y = fp8.gemv_fp8(xd, q, split)
+        if split > 1:
+            assert y.shape == (split, M, N) and y.dtype == torch.float32
+            y = _sum_partials(y)
+        else:
+            assert y.shape == (M, N) and y.dtype == torch.bfloat16
+            y = y.float().cpu().numpy()
+        e = rel_err(y, yref)
+        print(f"{name} M={M} split={split}: max-rel {e:.2e}")
+        assert e <= TOL
+
+
+def _sum_partials(p):
+    """The consumer's rule (engine/kernels/ops.py:35-38): fp32 sum in split order, then bf16."""
+    acc = p[0].float().clone()
+    for s in range(1, p.shape[0]):
+        acc += p[s]
+    return acc.to(torch.bfloat16).float().cpu().numpy()
+
+
+@pytest.mark.parametrize("layout", ["tiled", "rowmajor"])
+@pytest.mark.parametrize("algo", [L.ALGO_MFMA, L.ALGO_VALU])
+def test_gemv_fp8_layouts_and_algos(dev, layout, algo):
+    N, K = QKV
+    w, x = _fp8_case(N, K, 1, 42)
+    q = fp8.quantize(w.to(dev))
+    if layout == "rowmajor":
+        q = fp8.FP8Weight(q[0], q[1], None)
+    x8, xs = fp8.quant_rows(x.to(dev))
+    outs = []
+    for split, mode in ((1, L.OUT_BF16), (2, L.OUT_PARTIAL), (5, L.OUT_PARTIAL)):
+        y = fp8.gemv_fp8_launch(x8, xs, q, split, mode, algo)
+        outs.append(y.float().cpu().numpy() if split == 1 else _sum_partials(y))
+    r8, rs = O.quantize(u16(w))
+    _, yref = O.fp8_matmul(u8(x8), xs.cpu().numpy(), r8, rs)
+    for y in outs:
+        assert rel_err(y, yref) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 16, 32])
+def test_gemv_swiglu_fp8(dev, M):
+    N, K = GATE_UP
+    I = N // 2
+    w, x = _fp8_case(N, K, M, 2)
+    q = fp8.quantize(w.to(dev))
+    y = fp8.gemv_swiglu_fp8(x.to(dev), q)
+    assert y.shape == (M, I) and y.dtype == torch.bfloat16
+    r8, rs = O.quantize(u16(w))
+    x8r, xsr = O.quant_rows(u16(x))
+    _, full = O.fp8_matmul(x8r, xsr, r8, rs)
+    ref = O.bf16_to_f32(O.swiglu(full[:, :I].astype(np.float32), full[:, I:].astype(np.float32)))
+    e = rel_err(y.float().cpu().numpy(), ref)
+    print(f"gate_up swiglu M={M}: max-rel {e:.2e}")
+    assert e <= TOL
+    if M == 1:
+        yv = fp8.gemv_swiglu_fp8(x.to(dev), q, algo=L.ALGO_VALU)
+        assert rel_err(yv.float().cpu().numpy(), ref) <= TOL
+
+
+def test_gemv_fp8_per_tensor_static_scale(dev):
+    """The shipped decode form: per-tensor weights and a static SharedScale
+    (engine/engine.py:977-981 through linear_fp8)."""
+    N, K = DOWN
+    w, x = _fp8_case(N, K, 16, 3)
+    q = fp8.quantize_weight(w.to(dev))
+    inv = torch.tensor([448.0 / 5.0], device=dev)
+    sc = torch.tensor(5.0 / 448.0, device=dev)
+    y = fp8.linear_fp8(x.to(dev), q, fp8.SharedScale(inv, sc))
+    r8, rs = O.quantize_weight(u16(w))
+    x8r = O.cast(u16(x), np.float32(448.0 / 5.0))
+    _, yref = O.fp8_matmul(x8r, np.float32(5.0 / 448.0), r8, rs)
+    assert rel_err(y.float().cpu().numpy(), yref) <= TOL
+    # dynamic per-call scale, running amax kept
+    amax_out = torch.zeros(1, device=dev)
+    y2 = fp8.linear_fp8(x.to(dev), q, amax_out=amax_out)
+    am, inv2, s2 = O.act_scale(u16(x))
+    assert amax_out.item() == am
+    _, yref2 = O.fp8_matmul(O.cast(u16(x), inv2), s2, r8, rs)
+    assert rel_err(y2.float().cpu().numpy(), yref2) <= TOL
+
+
+def test_gemv_fp8_rejects_bad_shapes(dev):
+    w = weight(64, 200, 1).to(dev)
+    q = fp8.quantize(w)
+    with pytest.raises(ValueError):
+        fp8.gemv_fp8(act(1, 200, 1).to(dev), q)   # K % 64 != 0
+    q2 = fp8.quantize(weight(64, 256, 1).to(dev))
+    with pytest.raises(AssertionError):
+        fp8.gemv_fp8(act(1, 256, 1).to(dev), q2, split=3)
+
+
+# ---------------------------------------------------------------------------------------------
+# BF16 GEMV family
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("M", [1, 4, 16, 32])
+def test_gemv_bf16(dev, M):
+    N, K = QKV
+    w, x = weight(N, K, 21), act(M, K, 22)
+    ref = O.bf16_matmul(u16(x), u16(w))
+    wd, xd = w.to(dev), x.to(dev)
+    y = gemv(xd, wd)
+    assert rel_err(y.float().cpu().numpy(), ref) <= TOL
+    p = gemv(xd, wd, 4)
+    assert p.shape == (4, M, N)
+    assert rel_err(_sum_partials(p), ref) <= TOL
+    assert rel_err(gemv_rows(xd, wd, 256).float().cpu().numpy(), ref) <= TOL
+    if M == 1:
+        assert rel_err(gemv_m1(xd, wd, 2).sum(0).float().cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_gemv_swiglu_bf16(dev, M):
+    N, K = 2 * 1024, 2560
+    I = N // 2
+    w, x = weight(N, K, 31), act(M, K, 32)
+    full = O.bf16_matmul(u16(x), u16(w))
+    ref = O.bf16_to_f32(O.swiglu(full[:, :I].astype(np.float32), full[:, I:].astype(np.float32)))
+    y = gemv_swiglu(x.to(dev), w.to(dev))
+    assert rel_err(y.float().cpu().numpy(), ref) <= TOL
+    if M == 1:
+        assert rel_err(gemv_m1_swiglu(x.to(dev), w.to(dev)).float().cpu().numpy(), ref) <= TOL
+
+
+# ---------------------------------------------------------------------------------------------
+# LM head + argmax
+# ---------------------------------------------------------------------------------------------
+def _margins(ref64):
+    """fp64 gap between the best and second-best logit of each row."""
+    part = np.partition(ref64, -2, axis=-1)
+    return part[:, -1] - part[:, -2]
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_lmhead_bf16_argmax(dev, M):
+    V, K = 151936, 2560
+    E, h = weight(V, K, 7), act(M, K, 100 + M)
+    ref64 = O.bf16_matmul(u16(h), u16(E))
+    ref_bf = O.round_bf16(ref64.astype(np.float32))
+    ref_idx = O.argmax_lowest(ref_bf)
+    idx, logits = lmhead.lm_head_argmax(h.to(dev), E.to(dev), return_logits=True)
+    idx = idx.cpu().numpy()
+    lg = logits.float().cpu().numpy()
+    assert np.array_equal(idx, O.argmax_lowest(lg)), "kernel idx disagrees with its own logits"
+    assert rel_err(lg, ref64) <= TOL
+    print(f"lm_head bf16 M={M}: idx {idx[:4]} fp64 top-2 margins {_margins(ref64)[:4]}")
+    assert np.array_equal(idx, ref_idx)
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_lmhead_fp8_argmax(dev, M):
+    V, K = 151936, 2560
+    E, h = weight(V, K, 7), act(M, K, 100 + M)
+    q = fp8.quantize(E.to(dev))
+    h8, hs = fp8.quant_rows(h.to(dev))
+    idx, logits = lmhead.lm_head_argmax(h.to(dev), q, return_logits=True)
+    idx = idx.cpu().numpy()
+    lg = logits.float().cpu().numpy()
+    assert np.array_equal(idx, O.argmax_lowest(lg))
+    # exact FP8 oracle on the kernel's own (separately verified) operand bytes
+    _, ref = O.fp8_matmul(u8(h8), hs.cpu().numpy(), u8(q[0]), q[1].cpu().numpy())
+    ref_idx = O.argmax_lowest(O.round_bf16(ref.astype(np.float32)))
+    assert rel_err(lg, ref) <= TOL
+    assert np.array_equal(idx, ref_idx)
+
+
+def test_lmhead_ties_lowest_index(dev):
+    V, K = 4096, 256
+    E = torch.zeros(V, K, dtype=torch.bfloat16)
+    for j in (3000, 17, 2049, 4095):      # four identical best rows
+        E[j, :] = 0.5
+    h = torch.ones(2, K, dtype=torch.bfloat16)
+    idx = lmhead.lm_head_argmax(h.to(dev), E.to(dev)).cpu().numpy()
+    assert idx.tolist() == [17, 17]
+
+
+# ---------------------------------------------------------------------------------------------
+# graph replay and determinism
+# ---------------------------------------------------------------------------------------------
+def test_graph_replay_matches_eager(dev):
+    N, K = QKV
+    w, x = _fp8_case(N, K, 16, 9)
+    q = fp8.quantize(w.to(dev))
+    xd = x.to(dev)
+    E = weight(8192, 2560, 8).to(dev)
+    h = act(16, 2560, 9).to(dev)
+    eager_y = fp8.gemv_fp8(xd, q, 2).clone()
+    eager_i = lmhead.lm_head_argmax(h, E).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fp8.gemv_fp8(xd, q, 2)
+        lmhead.lm_head_argmax(h, E)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gy = fp8.gemv_fp8(xd, q, 2)
+        gi = lmhead.lm_head_argmax(h, E)
+    for _ in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gy, eager_y)
+        assert torch.equal(gi, eager_i)
+        lmhead.lm_head_argmax(h, E)   # eager work between replays
+        torch.cuda.synchronize()
+
+
+def test_deterministic(dev):
+    N, K = DOWN
+    w, x = _fp8_case(N, K, 32, 4)
+    q = fp8.quantize(w.to(dev))
+    xd = x.to(dev)
+    a = fp8.gemv_fp8(xd, q, 4)
+    b = fp8.gemv_fp8(xd, q, 4)
+    assert torch.equal(a, b)
