@@ -1,0 +1,282 @@
+"""Benchmark of the FP8 decode-matmul path on one MI355X.
+
+Default workload ("C2"): one Qwen3-4B decoder layer's projections at
+M = 1 - QKV [6144x2560], O [2560x4096], gate_up [19456x2560] (SwiGLU epilogue), down
+[2560x9728] - with per-channel FP8 e4m3 weights and per-token dynamic FP8 activation scales.
+One step = the four projections of one layer, each = per-token quantization kernel + GEMV
+kernel, with the reference engine's output contract (engine/engine.py:69, :1005): QKV split 2,
+O split 4, down split 4 (fp32 split-K partials), gate_up bf16 SwiGLU. Successive steps use the
+next of 36 layers of distinct weights (3.6 GB) so the 256 MB MALL cannot serve repeats, as the
+reference's tuner cycles layers (engine/engine.py:845-847, :887-891). The K timed steps are one
+hipGraph replay.
+
+value = algorithmic bytes of the K steps / their time, in GB/s. Bytes per projection call:
+N*K (w8) + 4N (w scale) + 2MK (bf16 x) + 4M (x scale) + output (2MN bf16, 4SMN partials,
+2MI SwiGLU).
+
+Also printed (stderr): per-kernel table from graph-replayed back-to-back launches (hipEvents),
+and the roofline of the dominant kernel (the gate_up GEMV). --config c3 runs M = 16,
+--config c3m32 M = 32, --config c4 the lm_head + argmax, --config c5 the full decode step.
+"""
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "kernel-rush-qwen_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK = 8.0e12
+H, I, NQKV, NQD, V = 2560, 9728, 6144, 4096, 151936
+LAYERS = 36
+METRIC = "FP8 skinny-GEMM HBM GB/s (% of 8 TB/s peak) at Qwen3-4B shapes, M=1 and M=16"
+# (name, N rows of W, K, split, mode)
+PROJ = [("qkv", NQKV, H, 2, "partial"), ("o", H, NQD, 4, "partial"),
+        ("gate_up", 2 * I, H, 1, "swiglu"), ("down", H, I, 4, "partial")]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def out_bytes(M, N, split, mode):
+    if mode == "partial":
+        return 4 * split * M * N
+    if mode == "swiglu":
+        return 2 * M * (N // 2)
+    return 2 * M * N
+
+
+def proj_bytes(M, N, K, split, mode):
+    return N * K + 4 * N + 2 * M * K + 4 * M + out_bytes(M, N, split, mode)
+
+
+def make_layers(torch, fp8, dev, n_layers):
+    """Seeded random-init weights W ~ N(0, 0.02) generated on the device (seed 1000+10l+p),
+    quantized per output channel by the HIP quantizer."""
+    layers = []
+    g = torch.Generator(device=dev)
+    for li in range(n_layers):
+        L = {}
+        for p, (name, N, K, _, _) in enumerate(PROJ):
+            g.manual_seed(1000 + 10 * li + p)
+            w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            L[name] = fp8.quantize(w)
+            del w
+        layers.append(L)
+    return layers
+
+
+def make_inputs(torch, dev, M):
+    """x ~ N(0, 1) bf16 per projection (seed 2000+p); the down input is SwiGLU of N(0, 1) pairs,
+    bf16(bf16(silu(g)) * u) as engine/kernels/ops.py:171-172 rounds it."""
+    xs = {}
+    for p, (name, N, K, _, _) in enumerate(PROJ):
+        g = torch.Generator().manual_seed(2000 + p)
+        if name == "down":
+            gg = torch.randn(M, K, generator=g).to(torch.bfloat16).float()
+            uu = torch.randn(M, K, generator=g).to(torch.bfloat16).float()
+            s = (gg / (1.0 + torch.exp(-gg))).to(torch.bfloat16).float()
+            xs[name] = (s * uu).to(torch.bfloat16).to(dev)
+        else:
+            xs[name] = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    return xs
+
+
+def run_proj(fp8, L_, name, x, split, mode):
+    q = L_[name]
+    if mode == "swiglu":
+        return fp8.gemv_swiglu_fp8(x, q)
+    return fp8.gemv_fp8(x, q, split)
+
+
+def graph_time(torch, fn, reps, iters=5):
+    """Capture fn(i) for i in range(reps) into one graph; return (min, median) us per call over
+    `iters` replays timed with hipEvents on the capture stream."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(0)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(reps):
+            fn(i)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(iters):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e3 / reps)
+    ts.sort()
+    del g
+    return ts[0], ts[len(ts) // 2]
+
+
+def kernel_table(torch, fp8, L, layers, xs, M, reps):
+    """GEMV kernel alone (pre-quantized activations), back-to-back launches cycling layers."""
+    rows = []
+    for name, N, K, split, mode in PROJ:
+        x8, sc = fp8.quant_rows(xs[name])
+        sc = sc.reshape(-1)
+        m = {"partial": L.OUT_PARTIAL, "swiglu": L.OUT_SWIGLU, "bf16": L.OUT_BF16}[mode]
+        outs = [fp8.gemv_fp8_launch(x8, sc, layers[0][name], split, m)]
+        fn = lambda i, name=name, x8=x8, sc=sc, split=split, m=m, o=outs[0]: fp8.gemv_fp8_launch(
+            x8, sc, layers[i % len(layers)][name], split, m, out=o)
+        tmin, tmed = graph_time(torch, fn, reps)
+        b = N * K + 4 * N + M * K + 4 * M + out_bytes(M, N, split, mode)
+        rows.append(dict(name=name, N=N, K=K, M=M, split=split, mode=mode, us_min=tmin, us_med=tmed,
+                         bytes=b, gbs=b / tmin / 1e3, frac=b / (tmin * 1e-6) / HBM_PEAK))
+    # the per-token quantization kernel of the largest input
+    x = xs["down"]
+    tq, tqm = graph_time(torch, lambda i: fp8.quant_rows(x), reps)
+    rows.append(dict(name="quant_rows", N=0, K=I, M=M, split=1, mode="-", us_min=tq, us_med=tqm,
+                     bytes=3 * M * I + 4 * M, gbs=(3 * M * I + 4 * M) / tq / 1e3,
+                     frac=(3 * M * I + 4 * M) / (tq * 1e-6) / HBM_PEAK))
+    return rows
+
+
+def cpu_baseline(torch, M, budget_s):
+    """The reference's CPU path ("torch dequant+matmul", dequant inside the timed region) on
+    this host, over the four projections of one layer; bounded to about budget_s seconds."""
+    from oracle import oracle as O
+    torch.set_num_threads(os.cpu_count() or 1)
+    total_b, total_t, reps_done = 0, 0.0, 0
+    g = torch.Generator().manual_seed(0)
+    cases = []
+    for name, N, K, split, mode in PROJ:
+        w8 = (torch.randn(N, K, generator=g) * 200).clamp(-448, 448).to(torch.float8_e4m3fn)
+        ws = torch.rand(N, generator=g) * 1e-4
+        x8 = (torch.randn(M, K, generator=g) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
+        xs = torch.rand(M, 1, generator=g) * 1e-2
+        cases.append((name, N, K, split, mode, w8, ws, x8, xs))
+    for c in cases:
+        O.torch_dequant_matmul(c[7], c[8], c[5], c[6])   # warm-up
+    t_start = time.perf_counter()
+    while True:
+        for name, N, K, split, mode, w8, ws, x8, xs in cases:
+            t0 = time.perf_counter()
+            O.torch_dequant_matmul(x8, xs, w8, ws)
+            total_t += time.perf_counter() - t0
+            total_b += proj_bytes(M, N, K, 1, "bf16")
+        reps_done += 1
+        if time.perf_counter() - t_start > budget_s or reps_done >= 50:
+            break
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": total_b / total_t / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{reps_done} passes over the 4 projections of one layer at M={M} "
+                      f"(torch CPU dequant+matmul, bf16 out), {total_t:.1f} s of CPU time; "
+                      f"host {model or platform.processor()}, os.cpu_count()={os.cpu_count()}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=360)
+    ap.add_argument("--warmup", type=int, default=36)
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c3m32"])
+    ap.add_argument("--reps", type=int, default=72, help="launches per graph in the kernel table")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the path is single-GPU; see the "
+              "sharding notes in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from kernels import _lib as L
+    from kernels import fp8
+
+    M = {"c2": 1, "c3": 16, "c3m32": 32}[args.config]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t0 = time.time()
+    layers = make_layers(torch, fp8, dev, LAYERS)
+    xs = make_inputs(torch, dev, M)
+    torch.cuda.synchronize()
+    log(f"[bench] {LAYERS} layers quantized on device in {time.time() - t0:.1f} s; M={M}")
+
+    def step(i):
+        Lw = layers[i % LAYERS]
+        for name, N, K, split, mode in PROJ:
+            run_proj(fp8, Lw, name, xs[name], split, mode)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # the K timed steps: one graph of K steps, one replay
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step(0)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(args.steps):
+            step(i)
+    g.replay()                      # untimed replay: first-touch of the graph's resources
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    g.replay()
+    e1.record()
+    e1.synchronize()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    step_bytes = sum(proj_bytes(M, N, K, split, mode) for _, N, K, split, mode in PROJ)
+    value = step_bytes * args.steps / (ms * 1e-3) / 1e9
+    del g
+
+    rows = kernel_table(torch, fp8, L, layers, xs, M, args.reps)
+    log(f"[bench] per-kernel (graph of {args.reps} back-to-back launches, cycling {LAYERS} layers):")
+    log(f"  {'kernel':<10} {'N':>6} {'K':>5} {'M':>3} {'S':>2} {'us(min)':>8} {'us(med)':>8} "
+        f"{'bytes':>11} {'GB/s':>7} {'%peak':>6}")
+    for r in rows:
+        log(f"  {r['name']:<10} {r['N']:>6} {r['K']:>5} {r['M']:>3} {r['split']:>2} {r['us_min']:>8.2f} "
+            f"{r['us_med']:>8.2f} {r['bytes']:>11} {r['gbs']:>7.0f} {100 * r['frac']:>5.1f}%")
+    dom = max(rows[:4], key=lambda r: r["bytes"])
+    roofline = {"bound": "hbm", "achieved": round(dom["gbs"], 1), "peak": 8000.0, "unit": "GB/s",
+                "frac": round(dom["frac"], 4), "traffic": None,
+                "kernel": f"gemv_fp8 {dom['name']} [{dom['N']}x{dom['K']}] M={M}",
+                "bytes_per_launch": dom["bytes"], "us_per_launch": round(dom["us_min"], 3)}
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(torch, M, args.cpu_seconds)
+
+    print(json.dumps({
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8_e4m3",
+        "data": "synthetic (seeded N(0,0.02) weights generated on device, N(0,1) activations)",
+        "config": {"workload": f"{args.config.upper()}: one Qwen3-4B decoder layer's QKV/O/gate_up/down "
+                               f"FP8 projections at M={M}, per-token dynamic scales, per-channel weights, "
+                               f"cycling {LAYERS} layers",
+                   "M": M, "bytes_per_step": step_bytes, "pct_of_hbm_peak": round(100 * value / 8000.0, 2)},
+        "roofline": roofline, "cpu_baseline": cpu}), flush=True)
+
+
+if __name__ == "__main__":
+    main()
