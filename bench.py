@@ -125,25 +125,48 @@ def graph_time(torch, fn, reps, iters=5):
 
 
 def kernel_table(torch, fp8, L, layers, xs, M, reps):
-    """GEMV kernel alone (pre-quantized activations), back-to-back launches cycling layers."""
+    """Each kernel of the step alone, back-to-back launches cycling layers (hipEvents around a
+    graph replay). At M = 1 the GEMV quantizes its activations itself (one kernel per
+    projection); at larger M the per-token quantization kernel runs first and the GEMV reads
+    e4m3 activations."""
     rows = []
+    fused = M == 1
     for name, N, K, split, mode in PROJ:
-        x8, sc = fp8.quant_rows(xs[name])
-        sc = sc.reshape(-1)
         m = {"partial": L.OUT_PARTIAL, "swiglu": L.OUT_SWIGLU, "bf16": L.OUT_BF16}[mode]
-        outs = [fp8.gemv_fp8_launch(x8, sc, layers[0][name], split, m)]
-        fn = lambda i, name=name, x8=x8, sc=sc, split=split, m=m, o=outs[0]: fp8.gemv_fp8_launch(
-            x8, sc, layers[i % len(layers)][name], split, m, out=o)
+        x = xs[name]
+        if fused:
+            o = fp8.gemv_fp8_bf16_launch(x, layers[0][name], split, m)
+            fn = lambda i, name=name, x=x, split=split, m=m, o=o: fp8.gemv_fp8_bf16_launch(
+                x, layers[i % len(layers)][name], split, m, out=o)
+            xbytes = 2 * M * K
+        else:
+            x8, sc = fp8.quant_rows(x)
+            sc = sc.reshape(-1)
+            o = fp8.gemv_fp8_launch(x8, sc, layers[0][name], split, m)
+            fn = lambda i, name=name, x8=x8, sc=sc, split=split, m=m, o=o: fp8.gemv_fp8_launch(
+                x8, sc, layers[i % len(layers)][name], split, m, out=o)
+            xbytes = M * K
         tmin, tmed = graph_time(torch, fn, reps)
-        b = N * K + 4 * N + M * K + 4 * M + out_bytes(M, N, split, mode)
+        b = N * K + 4 * N + xbytes + 4 * M + out_bytes(M, N, split, mode)
         rows.append(dict(name=name, N=N, K=K, M=M, split=split, mode=mode, us_min=tmin, us_med=tmed,
                          bytes=b, gbs=b / tmin / 1e3, frac=b / (tmin * 1e-6) / HBM_PEAK))
-    # the per-token quantization kernel of the largest input
-    x = xs["down"]
-    tq, tqm = graph_time(torch, lambda i: fp8.quant_rows(x), reps)
-    rows.append(dict(name="quant_rows", N=0, K=I, M=M, split=1, mode="-", us_min=tq, us_med=tqm,
-                     bytes=3 * M * I + 4 * M, gbs=(3 * M * I + 4 * M) / tq / 1e3,
-                     frac=(3 * M * I + 4 * M) / (tq * 1e-6) / HBM_PEAK))
+    if fused:   # the vector-ALU kernel on the same operands, for the M = 1 design comparison
+        for name, N, K, split, mode in PROJ:
+            m = {"partial": L.OUT_PARTIAL, "swiglu": L.OUT_SWIGLU, "bf16": L.OUT_BF16}[mode]
+            x = xs[name]
+            o = fp8.gemv_fp8_bf16_launch(x, layers[0][name], split, m, None, L.ALGO_VALU)
+            fn = lambda i, name=name, x=x, split=split, m=m, o=o: fp8.gemv_fp8_bf16_launch(
+                x, layers[i % len(layers)][name], split, m, None, L.ALGO_VALU, out=o)
+            tmin, tmed = graph_time(torch, fn, reps)
+            b = N * K + 4 * N + 2 * M * K + 4 * M + out_bytes(M, N, split, mode)
+            rows.append(dict(name=name + "/valu", N=N, K=K, M=M, split=split, mode=mode, us_min=tmin,
+                             us_med=tmed, bytes=b, gbs=b / tmin / 1e3, frac=b / (tmin * 1e-6) / HBM_PEAK))
+    if not fused:
+        x = xs["down"]
+        tq, tqm = graph_time(torch, lambda i: fp8.quant_rows(x), reps)
+        qb = 3 * M * I + 4 * M
+        rows.append(dict(name="quant_rows", N=0, K=I, M=M, split=1, mode="-", us_min=tq, us_med=tqm,
+                         bytes=qb, gbs=qb / tq / 1e3, frac=qb / (tq * 1e-6) / HBM_PEAK))
     return rows
 
 
@@ -171,7 +194,7 @@ def cpu_baseline(torch, M, budget_s):
             total_t += time.perf_counter() - t0
             total_b += proj_bytes(M, N, K, 1, "bf16")
         reps_done += 1
-        if time.perf_counter() - t_start > budget_s or reps_done >= 50:
+        if time.perf_counter() - t_start > budget_s or reps_done >= 2000:
             break
     model = ""
     try:
@@ -188,44 +211,35 @@ def cpu_baseline(torch, M, budget_s):
                       f"host {model or platform.processor()}, os.cpu_count()={os.cpu_count()}"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=360)
-    ap.add_argument("--warmup", type=int, default=36)
-    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c3m32"])
-    ap.add_argument("--reps", type=int, default=72, help="launches per graph in the kernel table")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--no-cpu", action="store_true")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one GPU only (the path is single-GPU; see the "
-              "sharding notes in DESIGN.md); run with --gpus 1", file=sys.stderr)
-        sys.exit(2)
+def lm_bytes(M, kind):
+    if kind == "bf16":
+        return 2 * V * H + 2 * M * H + 8 * M
+    return V * H + 4 * V + 2 * M * H + 4 * M + 8 * M
 
-    import torch
-    from kernels import _lib as L
-    from kernels import fp8
 
-    M = {"c2": 1, "c3": 16, "c3m32": 32}[args.config]
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    t0 = time.time()
-    layers = make_layers(torch, fp8, dev, LAYERS)
-    xs = make_inputs(torch, dev, M)
-    torch.cuda.synchronize()
-    log(f"[bench] {LAYERS} layers quantized on device in {time.time() - t0:.1f} s; M={M}")
+def dominant_key(M, mode, fused, layout):
+    """The template name rocprofv3 reports for the GEMV kernel of these arguments
+    (k_gemv_fp8<MT, MODE, LAYOUT, XK, ALGO, U>), to look up its measured HBM traffic."""
+    mt = 1 if M <= 16 else 2
+    u = 4 if M <= 4 else 2
+    return f"k_gemv_fp8<{mt}, {mode}, {layout}, {1 if fused else 0}, 1, {u}>"
 
-    def step(i):
-        Lw = layers[i % LAYERS]
-        for name, N, K, split, mode in PROJ:
-            run_proj(fp8, Lw, name, xs[name], split, mode)
 
-    for i in range(args.warmup):
+def measured_traffic(cfg, key):
+    path = os.path.join(ROOT, "profiles", f"traffic_{cfg}.json")
+    try:
+        k = json.load(open(path))["kernels"][key]
+        return int(round(k["read_bytes_median"] + k["write_bytes_median"]))
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def timed_graph(torch, step, steps, warmup):
+    """W untimed eager steps, then K steps captured into one graph and replayed once untimed and
+    once timed between synchronizations. Returns ms for the K steps."""
+    for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
-
-    # the K timed steps: one graph of K steps, one replay
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -233,9 +247,9 @@ def main():
     torch.cuda.current_stream().wait_stream(s)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        for i in range(args.steps):
+        for i in range(steps):
             step(i)
-    g.replay()                      # untimed replay: first-touch of the graph's resources
+    g.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -244,37 +258,139 @@ def main():
     e1.record()
     e1.synchronize()
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1)
-    step_bytes = sum(proj_bytes(M, N, K, split, mode) for _, N, K, split, mode in PROJ)
-    value = step_bytes * args.steps / (ms * 1e-3) / 1e9
     del g
+    return e0.elapsed_time(e1)
 
-    rows = kernel_table(torch, fp8, L, layers, xs, M, args.reps)
-    log(f"[bench] per-kernel (graph of {args.reps} back-to-back launches, cycling {LAYERS} layers):")
-    log(f"  {'kernel':<10} {'N':>6} {'K':>5} {'M':>3} {'S':>2} {'us(min)':>8} {'us(med)':>8} "
+
+def print_rows(rows, reps):
+    log(f"[bench] per-kernel (graph of {reps} back-to-back launches, cycling {LAYERS} layers):")
+    log(f"  {'kernel':<12} {'N':>6} {'K':>5} {'M':>3} {'S':>2} {'us(min)':>8} {'us(med)':>8} "
         f"{'bytes':>11} {'GB/s':>7} {'%peak':>6}")
     for r in rows:
-        log(f"  {r['name']:<10} {r['N']:>6} {r['K']:>5} {r['M']:>3} {r['split']:>2} {r['us_min']:>8.2f} "
+        log(f"  {r['name']:<12} {r['N']:>6} {r['K']:>5} {r['M']:>3} {r['split']:>2} {r['us_min']:>8.2f} "
             f"{r['us_med']:>8.2f} {r['bytes']:>11} {r['gbs']:>7.0f} {100 * r['frac']:>5.1f}%")
-    dom = max(rows[:4], key=lambda r: r["bytes"])
-    roofline = {"bound": "hbm", "achieved": round(dom["gbs"], 1), "peak": 8000.0, "unit": "GB/s",
-                "frac": round(dom["frac"], 4), "traffic": None,
-                "kernel": f"gemv_fp8 {dom['name']} [{dom['N']}x{dom['K']}] M={M}",
-                "bytes_per_launch": dom["bytes"], "us_per_launch": round(dom["us_min"], 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c3m32", "c4", "c5"])
+    ap.add_argument("--m", type=int, default=None, help="rows for --config c4 / c5 (default 1)")
+    ap.add_argument("--lm", default="bf16", choices=["bf16", "fp8"], help="lm head weights (c4)")
+    ap.add_argument("--layout", default="tiled", choices=["tiled", "rowmajor"],
+                    help="FP8 weight layout read by the GEMV")
+    ap.add_argument("--reps", type=int, default=72, help="launches per graph in the kernel table")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run one 256 MiB device copy (known bytes) to scale HBM counters")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the path is single-GPU; see the "
+              "sharding notes in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from kernels import _lib as L
+    from kernels import fp8, lmhead
+
+    cfg = args.config
+    M = {"c2": 1, "c3": 16, "c3m32": 32}.get(cfg, args.m or 1)
+    steps = args.steps or {"c4": 20, "c5": 5}.get(cfg, 360)
+    warmup = args.warmup if args.warmup is not None else {"c4": 2, "c5": 1}.get(cfg, 36)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t0 = time.time()
+    layers, xs, E, q8 = None, None, None, None
+    if cfg != "c4":
+        layers = make_layers(torch, fp8, dev, LAYERS)
+        if args.layout == "rowmajor":
+            layers = [{k: fp8.FP8Weight(q[0], q[1], None) for k, q in Lw.items()} for Lw in layers]
+        xs = make_inputs(torch, dev, M)
+    if cfg in ("c4", "c5"):
+        g = torch.Generator(device=dev).manual_seed(7)
+        E = (torch.randn(V, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        if cfg == "c4" and args.lm == "fp8":
+            q8 = fp8.quantize(E)
+            if args.layout == "rowmajor":
+                q8 = fp8.FP8Weight(q8[0], q8[1], None)
+            E = None
+        hg = torch.Generator().manual_seed(100 + M)
+        h = torch.randn(M, H, generator=hg).to(torch.bfloat16).to(dev)
+    torch.cuda.synchronize()
+    log(f"[bench] {cfg}: weights ready in {time.time() - t0:.1f} s; M={M}")
+
+    layer_bytes = sum(proj_bytes(M, N, K, split, mode) for _, N, K, split, mode in PROJ)
+
+    def layer_step(i):
+        Lw = layers[i % LAYERS]
+        for name, N, K, split, mode in PROJ:
+            run_proj(fp8, Lw, name, xs[name], split, mode)
+
+    if cfg in ("c2", "c3", "c3m32"):
+        step, step_bytes = layer_step, layer_bytes
+        work = (f"{cfg.upper()}: one Qwen3-4B decoder layer's QKV/O/gate_up/down FP8 projections "
+                f"at M={M}, per-token dynamic scales, per-channel weights, cycling {LAYERS} layers")
+    elif cfg == "c4":
+        w_lm = E if E is not None else q8
+        step = lambda i: lmhead.lm_head_argmax(h, w_lm)
+        step_bytes = lm_bytes(M, args.lm)
+        work = (f"C4: tied lm_head [{V}x{H}] {args.lm.upper()} GEMV fused with greedy argmax at M={M}")
+    else:
+        def step(i):
+            for li in range(LAYERS):
+                layer_step(li)
+            lmhead.lm_head_argmax(h, E)
+        step_bytes = LAYERS * layer_bytes + lm_bytes(M, "bf16")
+        work = (f"C5: full decode-step weight stream at M={M}: {LAYERS} layers x FP8 QKV/O/gate_up/down "
+                f"+ BF16 lm_head with argmax, one hipGraph")
+
+    ms = timed_graph(torch, step, steps, warmup)
+    value = step_bytes * steps / (ms * 1e-3) / 1e9
+
+    if args.calibrate_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log("[bench] calibration copy: 268435456 bytes read, 268435456 bytes written")
+        del src, dst
+
+    if cfg in ("c2", "c3", "c3m32"):
+        rows = kernel_table(torch, fp8, L, layers, xs, M, args.reps)
+        print_rows(rows, args.reps)
+        dom = max(rows[:4], key=lambda r: r["bytes"])
+        key = dominant_key(M, L.OUT_SWIGLU, M == 1, L.W_TILED if args.layout == "tiled" else L.W_ROWMAJOR)
+        kern = f"gemv_fp8 {dom['name']} [{dom['N']}x{dom['K']}] M={M} ({key})"
+        dom_bytes, dom_us = dom["bytes"], dom["us_min"]
+    else:
+        w_lm = E if E is not None else q8
+        tmin, tmed = graph_time(torch, lambda i: lmhead.lm_head_argmax(h, w_lm), 8 if cfg == "c4" else 4)
+        kind = "bf16" if E is not None else "fp8"
+        dom_bytes, dom_us = lm_bytes(M, kind), tmin
+        key = None
+        kern = f"lmhead_argmax {kind} [{V}x{H}] M={M}"
+        log(f"[bench] lm_head {kind} M={M}: {tmin:.2f} us (median {tmed:.2f}), "
+            f"{dom_bytes / tmin / 1e3:.0f} GB/s, {100 * dom_bytes / (tmin * 1e-6) / HBM_PEAK:.1f}% of 8 TB/s")
+    roofline = {"bound": "hbm", "achieved": round(dom_bytes / dom_us / 1e3, 1), "peak": 8000.0,
+                "unit": "GB/s", "frac": round(dom_bytes / (dom_us * 1e-6) / HBM_PEAK, 4),
+                "traffic": measured_traffic(cfg, key) if key else None,
+                "kernel": kern, "bytes_per_launch": dom_bytes, "us_per_launch": round(dom_us, 3)}
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and cfg in ("c2", "c3", "c3m32"):
         cpu = cpu_baseline(torch, M, args.cpu_seconds)
 
     print(json.dumps({
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 5),
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms / steps, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8_e4m3",
         "data": "synthetic (seeded N(0,0.02) weights generated on device, N(0,1) activations)",
-        "config": {"workload": f"{args.config.upper()}: one Qwen3-4B decoder layer's QKV/O/gate_up/down "
-                               f"FP8 projections at M={M}, per-token dynamic scales, per-channel weights, "
-                               f"cycling {LAYERS} layers",
-                   "M": M, "bytes_per_step": step_bytes, "pct_of_hbm_peak": round(100 * value / 8000.0, 2)},
+        "config": {"workload": work, "M": M, "bytes_per_step": step_bytes, "layout": args.layout,
+                   "pct_of_hbm_peak": round(100 * value / 8000.0, 2)},
         "roofline": roofline, "cpu_baseline": cpu}), flush=True)
 
 

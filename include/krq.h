@@ -43,6 +43,11 @@ extern "C" {
 #define KRQ_W_ROWMAJOR 0
 #define KRQ_W_TILED 1
 
+/* activation kinds of the FP8 GEMV */
+#define KRQ_X_FP8 0          /* x is e4m3 [M,K]; x_scale holds its scale (per row or tensor) */
+#define KRQ_X_BF16_DYN 1     /* x is bf16 [1,K]; the per-token scale is computed in the kernel */
+#define KRQ_X_BF16_STATIC 2  /* x is bf16 [M,K]; quantized with x_inv, scaled by x_scale */
+
 /* lm-head weight kinds */
 #define KRQ_LM_BF16 0
 #define KRQ_LM_FP8 1
@@ -99,15 +104,20 @@ int krq_quant_rows(const void* x_bf16, int64_t M, int64_t K, void* x8, float* xs
  * engine/kernels/fp8.py:97-106) at decode sizes, and supplies gemv_fp8 / gemv_swiglu_fp8 as
  * called by experiments/modal_fp8.py:67-69 under the output contract of gemv / gemv_swiglu
  * (engine/kernels/gemv.py:83-88, :125-130, :137-167).
+ *   x8[m,k]  = x (x_kind KRQ_X_FP8), or e4m3(clamp(x[m,k] * inv, +-448)) computed in the kernel:
+ *              inv = x_inv[m or 0] (KRQ_X_BF16_STATIC), or the per-token ActScale inverse of row
+ *              0 (KRQ_X_BF16_DYN, M == 1; amax over all of K)
  *   acc[m,n] = sum_k x8[m,k] * w8[n,k]   (fp32 accumulate)
- *   y[m,n]   = acc[m,n] * x_scale[m or 0] * w_scale[n or 0]
- * x8: e4m3 [M,K] row-major. w8: e4m3 [N,K] (or [2I,K] for SWIGLU) in layout w_layout.
+ *   y[m,n]   = acc[m,n] * xs[m] * w_scale[n or 0], xs = x_scale[m or 0] or the in-kernel scale
+ * w8: e4m3 [N,K] (or [2I,K] for SWIGLU) in layout w_layout.
  * mode KRQ_OUT_BF16 -> bf16 [M,N] (split 1); KRQ_OUT_PARTIAL -> fp32 [split,M,N] of the K-slices
  * [s*K/split, (s+1)*K/split); KRQ_OUT_SWIGLU -> bf16 [M,I] (split 1).
- * Needs N % 16 == 0, K % split == 0 and (K/split) % 64 == 0.
+ * Needs N % 16 == 0, K % split == 0 and (K/split) % 64 == 0; the in-kernel kinds need the
+ * activation slice (K for DYN, M*K/split for STATIC) to fit 4096 elements per 64-thread wave
+ * of at most 8 waves.
  * algo: 0 = automatic, 1 = matrix-core (MFMA) kernel, 2 = vector-ALU kernel (M == 1 only).
  */
-int krq_gemv_fp8(const void* x8, const float* x_scale, int x_per_row,
+int krq_gemv_fp8(const void* x, int x_kind, const float* x_scale, const float* x_inv, int x_per_row,
                  const void* w8, int w_layout, const float* w_scale, int w_per_row,
                  int64_t M, int64_t N, int64_t K, int split, int mode, int algo,
                  void* out, void* stream);
@@ -122,15 +132,16 @@ int krq_gemv_bf16(const void* x, const void* w, int64_t M, int64_t N, int64_t K,
                   int mode, void* out, void* stream);
 
 /*
- * LM head + greedy argmax, one launch: logits = bf16(h . E^T) and idx[m] = lowest index of the
- * maximum bf16 logit of row m. Reference: engine/engine.py:1021-1022 (gemv(h, lm_head, 1) then
- * torch.argmax) and the fused form engine/kernels/mega.py:396-441.
- * w_kind KRQ_LM_BF16: h bf16 [M,K], w bf16 [V,K] row-major, w_scale/h_scale unused.
- * w_kind KRQ_LM_FP8:  h e4m3 [M,K] with h_scale[M] (per token), w e4m3 [V,K] in w_layout with
- *                     w_scale[V]; logits as krq_gemv_fp8 KRQ_OUT_BF16.
- * logits: optional bf16 [M,V] output (NULL to skip). ws: caller workspace of at least
- * krq_lmhead_ws_bytes(M, V) bytes; its leading counter word must be zero before the first call
- * and is left zero by every call.
+ * LM head + greedy argmax: logits = bf16(h . E^T) and idx[m] = lowest index of the maximum bf16
+ * logit of row m. Reference: engine/engine.py:1021-1022 (gemv(h, lm_head, 1) then torch.argmax)
+ * and the fused form engine/kernels/mega.py:396-441. Two launches (GEMV with an argmax epilogue,
+ * then a per-row fold).
+ * w_kind KRQ_LM_BF16: h bf16 [M,K], w bf16 [V,K] row-major; h_scale / w_scale unused.
+ * w_kind KRQ_LM_FP8:  w e4m3 [V,K] in w_layout with per-row w_scale[V]; h e4m3 [M,K] with
+ *                     per-token h_scale[M], or (h_scale NULL, M == 1) h bf16 [1,K] scaled per
+ *                     token inside the kernel; logits as krq_gemv_fp8 KRQ_OUT_BF16.
+ * logits: optional bf16 [M,V] output (NULL to skip). ws: scratch of at least
+ * krq_lmhead_ws_bytes(M, V) bytes (overwritten; calls that overlap must not share it).
  */
 int krq_lmhead_argmax(const void* h, const float* h_scale, const void* w, int w_kind, int w_layout,
                       const float* w_scale, int64_t M, int64_t V, int64_t K, void* logits,

@@ -1,0 +1,160 @@
+// BF16 skinny GEMM / GEMV (M <= 32), row-major weights: y = x . w^T in fp32.
+// A step is 64 bf16 of K per weight row (two 32-element tiles, one v_mfma_f32_16x16x32_bf16 each);
+// M == 1 runs on the vector ALUs with cross-lane sums. Conventions: gemv_common.h.
+#include "gemv_common.h"
+
+using namespace krq;
+
+namespace {
+
+template <int MT, int MODE, int ALGO, int U>
+__global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x,
+                                                  const uint8_t* __restrict__ w, int M, int64_t NO,
+                                                  int64_t K, int kts, void* __restrict__ out,
+                                                  void* __restrict__ aux) {
+  extern __shared__ float red[];
+  __shared__ float ones[32];
+  constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : 1;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t rb = blockIdx.x, rbu = rb + (NO >> 4);
+  const int sidx = blockIdx.y;
+  const int nsteps = (kts + 1) >> 1;
+  const int64_t tbase = (int64_t)sidx * kts;
+  const int64_t rowb = 2 * K;
+  const int jcount = wave < nsteps ? (nsteps - wave + nw - 1) / nw : 0;
+  if (threadIdx.x < 32) ones[threadIdx.x] = 1.0f;
+
+  v4f acc[MT], accu[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+    accu[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+  }
+  float s0 = 0.f, s1 = 0.f, q0 = 0.f, q1 = 0.f;
+  for (int c0 = 0; c0 < jcount; c0 += U) {
+    uint4 wl[U], wh[U], ul[U], uh[U], xl[U][MT], xh[U][MT];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = wave + min(c0 + u, jcount - 1) * nw;
+      const int64_t t0 = tbase + 2 * j;
+      const int64_t t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
+      wl[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rb, t0, rowb, lane));
+      wh[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rb, t1, rowb, lane));
+      if (P == 2) {
+        ul[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rbu, t0, rowb, lane));
+        uh[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rbu, t1, rowb, lane));
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = ALGO == 2 ? 0 : mt * 16 + r;
+        uint4 a = zero4(), b = zero4();
+        if (m < M) {
+          const uint8_t* xr = x + (int64_t)m * rowb + g * 16;
+          a = ld16(xr + t0 * 64);
+          b = ld16(xr + t1 * 64);
+        }
+        xl[u][mt] = a;
+        xh[u][mt] = b;
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int cc = c0 + u;
+      const int j = wave + min(cc, jcount - 1) * nw;
+      const bool ok = cc < jcount, hi = ok && (2 * j + 1 < kts);
+      const uint4 bl = sel4(ok, wl[u]), bh = sel4(hi, wh[u]);
+      if (ALGO == 2) {
+        s0 = dot8_bf16(bl, xl[u][0], s0);
+        s1 = dot8_bf16(bh, xh[u][0], s1);
+        if (P == 2) {
+          q0 = dot8_bf16(sel4(ok, ul[u]), xl[u][0], q0);
+          q1 = dot8_bf16(sel4(hi, uh[u]), xh[u][0], q1);
+        }
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xl[u][mt]), as_v8bf(bl), acc[mt], 0, 0, 0);
+          acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xh[u][mt]), as_v8bf(bh), acc[mt], 0, 0, 0);
+        }
+        if (P == 2) {
+          const uint4 cl = sel4(ok, ul[u]), ch = sel4(hi, uh[u]);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xl[u][mt]), as_v8bf(cl), accu[mt], 0, 0, 0);
+            accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xh[u][mt]), as_v8bf(ch), accu[mt], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+  if (ALGO == 2) {
+    float a = s0 + s1, au = q0 + q1;
+    a += __shfl_xor(a, 16, kWave);
+    a += __shfl_xor(a, 32, kWave);
+    au += __shfl_xor(au, 16, kWave);
+    au += __shfl_xor(au, 32, kWave);
+    acc[0] = v4f{g == 0 ? a : 0.f, 0.f, 0.f, 0.f};
+    accu[0] = v4f{g == 0 ? au : 0.f, 0.f, 0.f, 0.f};
+  }
+  stash<MT, P>(red, wave, lane, acc, accu);
+  __syncthreads();
+  epilogue<MT, MODE>(red, nw, M, NO, rb, sidx, ones, ColScales{1.0f, 1.0f}, out, aux);
+}
+
+template <int MODE>
+void launch(int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* x,
+            const uint8_t* w, int m, int64_t NO, int64_t K, int kts, void* out, void* aux) {
+  const dim3 block(nw * 64);
+  if (M == 1)
+    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, 2, 4>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+  else if (M <= 4)
+    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, 1, 4>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+  else if (M <= 16)
+    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, 1, 2>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+  else
+    hipLaunchKernelGGL((k_gemv_bf16<2, MODE, 1, 2>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+}
+
+}  // namespace
+
+int krq::gemv_bf16_run(const void* x, const void* w, int64_t M, int64_t N, int64_t K, int split,
+                       int mode, void* out, void* aux, void* stream) {
+  KRQ_REQUIRE(x && w && (out || mode == kOutArgmax) && (aux || mode != kOutArgmax),
+              "gemv_bf16: null pointer");
+  KRQ_REQUIRE(aligned16(x) && aligned16(w), "gemv_bf16: x and w must be 16-byte aligned");
+  KRQ_REQUIRE(M >= 1 && M <= 32, "gemv_bf16: M=%lld outside 1..32", (long long)M);
+  KRQ_REQUIRE(N > 0 && K > 0 && split >= 1, "gemv_bf16: bad shape N=%lld K=%lld split=%d",
+              (long long)N, (long long)K, split);
+  KRQ_REQUIRE(K % split == 0 && (K / split) % 32 == 0,
+              "gemv_bf16: no tiling divides K_SPLIT (K=%lld split=%d; K/split must be a multiple of 32)",
+              (long long)K, split);
+  KRQ_REQUIRE(mode >= KRQ_OUT_BF16 && mode <= kOutArgmax, "gemv_bf16: bad mode %d", mode);
+  KRQ_REQUIRE(mode == KRQ_OUT_PARTIAL || split == 1, "gemv_bf16: split %d needs the partials output", split);
+  const int64_t NO = mode == KRQ_OUT_SWIGLU ? N / 2 : N;
+  KRQ_REQUIRE(NO % 16 == 0 && (mode != KRQ_OUT_SWIGLU || N % 2 == 0),
+              "gemv_bf16: no tiling divides N=%lld (output columns must be a multiple of 16)", (long long)N);
+  KRQ_REQUIRE(NO / 16 <= 0x7fffffff && split <= 65535, "gemv_bf16: grid too large");
+  const int kts = static_cast<int>(K / split / 32);
+  const int P = mode == KRQ_OUT_SWIGLU ? 2 : 1;
+  const int MT = M <= 16 ? 1 : 2;
+  const int nw = plan_waves((kts + 1) / 2, P, static_cast<int>(M));
+  const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float);
+  const dim3 grid(static_cast<unsigned>(NO / 16), static_cast<unsigned>(split));
+  const uint8_t* xb = (const uint8_t*)x;
+  const uint8_t* wb = (const uint8_t*)w;
+  const int m = static_cast<int>(M);
+  hipStream_t s = (hipStream_t)stream;
+  if (mode == KRQ_OUT_BF16) launch<KRQ_OUT_BF16>(m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
+  else if (mode == KRQ_OUT_PARTIAL) launch<KRQ_OUT_PARTIAL>(m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
+  else if (mode == KRQ_OUT_SWIGLU) launch<KRQ_OUT_SWIGLU>(m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
+  else launch<kOutArgmax>(m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
+  return krq_check_launch("gemv_bf16");
+}
+
+extern "C" int krq_gemv_bf16(const void* x, const void* w, int64_t M, int64_t N, int64_t K, int split,
+                             int mode, void* out, void* stream) {
+  KRQ_REQUIRE(mode >= KRQ_OUT_BF16 && mode <= KRQ_OUT_SWIGLU, "gemv_bf16: bad mode %d", mode);
+  return gemv_bf16_run(x, w, M, N, K, split, mode, out, nullptr, stream);
+}

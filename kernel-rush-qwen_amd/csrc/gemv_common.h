@@ -1,0 +1,265 @@
+// Device helpers shared by the skinny GEMM / GEMV kernels (gfx950, wave64).
+//
+// Work unit. A "row block" is 16 output columns (16 weight rows). A "step" is 128 bytes of each of
+// those 16 weight rows: two 16 x 64-byte tiles. In a step lane l (r = l % 16, g = l / 16) reads 16
+// bytes of weight row r from each tile, at byte 16*g of the tile, and the same bytes (same k) of
+// activation row r. The FP8 matrix-core instruction v_mfma_f32_16x16x128_f8f6f4 takes exactly
+// this: 32 bytes of A row r and of B column r per lane, with the k order of a lane's bytes the
+// same for A and B, so the product is sum_k x[m,k] w[n,k] for any assignment of byte offsets to
+// lanes that A and B share. The BF16 kernels use v_mfma_f32_16x16x32_bf16 twice per step.
+// Accumulator layout of both instructions: lane l, element i holds C[4*(l/16) + i][l % 16],
+// i.e. output row m = 4*g + i (+16 for the second M tile) and column n = 16*rb + r.
+//
+// Steps of one (row block, K split) are dealt to the waves of a block round-robin (wave w takes
+// steps w, w + nw, ...), so at any moment a block's waves read adjacent tiles; each wave issues
+// the loads of U steps before its first matrix instruction. Weight loads are non-temporal
+// (streamed once, kept out of the caches' reuse set).
+#pragma once
+
+#include "krq_common.h"
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+#define KRQ_REQUIRE(cond, ...)        \
+  do {                                \
+    if (!(cond)) {                    \
+      krq_set_error(__VA_ARGS__);     \
+      return KRQ_EINVAL;              \
+    }                                 \
+  } while (0)
+
+namespace krq {
+
+constexpr int kU = 4;  // steps per load batch
+
+// Internal output mode (not part of the C ABI's modes): the lm-head epilogue. Logits are rounded
+// to bf16 (optionally stored to `out`) and each block writes, per output row m, the largest
+// logit of its 16 columns and the lowest column index holding it to `aux` ([row block][M] Best).
+constexpr int kOutArgmax = 3;
+
+struct Best {
+  float v;
+  int i;
+};
+
+// larger value wins; among equal values the lower index (torch.argmax keeps the first maximum)
+KRQ_DEV bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+KRQ_DEV Best shfl_best(Best b, int o) {
+  Best r;
+  r.v = __shfl_xor(b.v, o, kWave);
+  r.i = __shfl_xor(b.i, o, kWave);
+  return r;
+}
+
+KRQ_DEV uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+KRQ_DEV uint4 ld16nt(const uint8_t* p) {
+  const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+KRQ_DEV v8i pack_v8i(uint4 a, uint4 b) {
+  v8i v;
+  v[0] = (int)a.x; v[1] = (int)a.y; v[2] = (int)a.z; v[3] = (int)a.w;
+  v[4] = (int)b.x; v[5] = (int)b.y; v[6] = (int)b.z; v[7] = (int)b.w;
+  return v;
+}
+
+KRQ_DEV v8bf as_v8bf(uint4 a) { return __builtin_bit_cast(v8bf, a); }
+
+KRQ_DEV uint4 sel4(bool keep, uint4 a) {
+  uint4 z;
+  z.x = keep ? a.x : 0u; z.y = keep ? a.y : 0u; z.z = keep ? a.z : 0u; z.w = keep ? a.w : 0u;
+  return z;
+}
+
+KRQ_DEV uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
+
+// Byte address of the 16 bytes lane `lane` reads from weight tile t of row block rb.
+// row_bytes = bytes per weight row (K for FP8, 2K for BF16); tiles are 64 bytes wide.
+template <int LAYOUT>
+KRQ_DEV const uint8_t* w_addr(const uint8_t* w, int64_t rb, int64_t t, int64_t row_bytes, int lane) {
+  if (LAYOUT == KRQ_W_TILED) return w + ((rb * (row_bytes >> 6) + t) * 64 + lane) * 16;
+  return w + (rb * 16 + (lane & 15)) * row_bytes + t * 64 + (lane >> 4) * 16;
+}
+
+// Hardware fp32 -> OCP e4m3 pair conversion after the reference's clamp to +-448. Bit-identical to
+// f32_to_e4m3 (round to nearest even) on the clamped range; NaN stays NaN.
+KRQ_DEV float clamp448(float v) { return v != v ? v : fminf(fmaxf(v, -kFp8Max), kFp8Max); }
+
+// NaN inputs: the hardware writes an unsigned NaN code; torch's cast keeps the sign (S.1111.111).
+KRQ_DEV uint32_t nan_sign(uint32_t p, float v, int shift) {
+  const uint32_t u = as_u32(v);
+  const bool nan = (u & 0x7fffffffu) > 0x7f800000u;
+  const uint32_t code = ((u >> 24) & 0x80u) | 0x7fu;
+  return nan ? (p & ~(0xffu << shift)) | (code << shift) : p;
+}
+
+KRQ_DEV uint32_t cvt4_e4m3(float a, float b, float c, float d) {
+  int p = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(a), clamp448(b), 0, false);
+  p = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(c), clamp448(d), p, true);
+  uint32_t q = static_cast<uint32_t>(p);
+  q = nan_sign(q, a, 0);
+  q = nan_sign(q, b, 8);
+  q = nan_sign(q, c, 16);
+  return nan_sign(q, d, 24);
+}
+
+// 8 bf16 (one 16-byte chunk) times s -> 8 e4m3 bytes
+KRQ_DEV uint2 quant8(uint4 v, float s) {
+  uint2 r;
+  r.x = cvt4_e4m3(as_f32(v.x << 16) * s, as_f32(v.x & 0xffff0000u) * s, as_f32(v.y << 16) * s,
+                  as_f32(v.y & 0xffff0000u) * s);
+  r.y = cvt4_e4m3(as_f32(v.z << 16) * s, as_f32(v.z & 0xffff0000u) * s, as_f32(v.w << 16) * s,
+                  as_f32(v.w & 0xffff0000u) * s);
+  return r;
+}
+
+KRQ_DEV float absmax8(uint4 v, float m) {
+  const uint32_t a[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    m = fmaxf(m, fabsf(as_f32(a[q] << 16)));
+    m = fmaxf(m, fabsf(as_f32(a[q] & 0xffff0000u)));
+  }
+  return m;
+}
+
+// vector-ALU dot products (M == 1 kernels)
+KRQ_DEV float dot4_fp8(uint32_t a, uint32_t b, float acc) {
+  const auto a0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)a, false);
+  const auto a1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)a, true);
+  const auto b0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)b, false);
+  const auto b1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)b, true);
+  acc = fmaf(a0[0], b0[0], acc);
+  acc = fmaf(a0[1], b0[1], acc);
+  acc = fmaf(a1[0], b1[0], acc);
+  return fmaf(a1[1], b1[1], acc);
+}
+
+KRQ_DEV float dot16_fp8(uint4 a, uint4 b, float acc) {
+  acc = dot4_fp8(a.x, b.x, acc);
+  acc = dot4_fp8(a.y, b.y, acc);
+  acc = dot4_fp8(a.z, b.z, acc);
+  return dot4_fp8(a.w, b.w, acc);
+}
+
+KRQ_DEV float dot8_bf16(uint4 a, uint4 b, float acc) {
+  const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    acc = fmaf(as_f32(av[q] << 16), as_f32(bv[q] << 16), acc);
+    acc = fmaf(as_f32(av[q] & 0xffff0000u), as_f32(bv[q] & 0xffff0000u), acc);
+  }
+  return acc;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Epilogue of every GEMV kernel. red holds nw (waves) x P (1, or 2 for gate/up) x MT x 256
+// accumulator values in the MFMA lane layout; xs[m] is row m's activation scale (1 if unscaled).
+// Sums the waves in wave order (deterministic), applies scales, rounds, and writes bf16 [M, NO],
+// fp32 partials [split, M, NO], or SwiGLU bf16 [M, NO].
+// ---------------------------------------------------------------------------------------------
+// Weight scales of the columns this thread writes in the epilogue (thread t writes columns
+// 16*rb + t % 16), loaded at kernel start so their latency hides under the weight stream.
+struct ColScales {
+  float g, u;
+};
+
+template <int MODE>
+KRQ_DEV ColScales load_col_scales(const float* __restrict__ wsc, int w_per_row, int64_t NO, int64_t rb) {
+  ColScales c{1.0f, 1.0f};
+  if (wsc) {
+    const int64_t n = rb * 16 + (threadIdx.x & 15);
+    c.g = wsc[w_per_row ? n : 0];
+    if (MODE == KRQ_OUT_SWIGLU) c.u = wsc[w_per_row ? NO + n : 0];
+  }
+  return c;
+}
+
+template <int MT, int MODE>
+KRQ_DEV void epilogue(const float* red, int nw, int M, int64_t NO, int64_t rb, int split_idx,
+                      const float* xs, ColScales cs, void* __restrict__ out, void* __restrict__ aux) {
+  constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : 1;
+  constexpr int NV = MT * 256;
+  for (int v = threadIdx.x; v < NV; v += blockDim.x) {
+    const int mt = v >> 8, i = (v >> 6) & 3, ln = v & 63;
+    const int m = mt * 16 + 4 * (ln >> 4) + i;
+    const bool valid = m < M;
+    const int64_t n = rb * 16 + (ln & 15);
+    float a = 0.0f, au = 0.0f;
+    for (int w = 0; w < nw; ++w) {
+      a += red[(w * P + 0) * NV + v];
+      if (P == 2) au += red[(w * P + 1) * NV + v];
+    }
+    const float x = valid ? xs[m] : 0.0f;
+    if (MODE == kOutArgmax) {
+      // the 16 lanes sharing (mt, i, g) hold the 16 columns of one output row: fold them
+      Best b{-INFINITY, 0x7fffffff};
+      if (valid) {
+        const uint16_t yb = f32_to_bf16(a * x * cs.g);
+        if (out) reinterpret_cast<uint16_t*>(out)[(int64_t)m * NO + n] = yb;
+        b = Best{bf16_to_f32(yb), static_cast<int>(n)};
+      }
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const Best c = shfl_best(b, o);
+        if (better(c.v, c.i, b.v, b.i)) b = c;
+      }
+      if (valid && (ln & 15) == 0) reinterpret_cast<Best*>(aux)[rb * M + m] = b;
+      continue;
+    }
+    if (!valid) continue;
+    if (MODE == KRQ_OUT_SWIGLU) {
+      const float gg = round_bf16(a * x * cs.g);
+      const float uu = round_bf16(au * x * cs.u);
+      const float sl = round_bf16(gg / (1.0f + expf(-gg)));
+      reinterpret_cast<uint16_t*>(out)[(int64_t)m * NO + n] = f32_to_bf16(sl * uu);
+    } else {
+      const float y = a * x * cs.g;
+      if (MODE == KRQ_OUT_BF16)
+        reinterpret_cast<uint16_t*>(out)[(int64_t)m * NO + n] = f32_to_bf16(y);
+      else
+        reinterpret_cast<float*>(out)[((int64_t)split_idx * M + m) * NO + n] = y;
+    }
+  }
+}
+
+template <int MT, int P>
+KRQ_DEV void stash(float* red, int wave, int lane, const v4f* acc, const v4f* accu) {
+  constexpr int NV = MT * 256;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      red[(wave * P + 0) * NV + mt * 256 + i * 64 + lane] = acc[mt][i];
+      if (P == 2) red[(wave * P + 1) * NV + mt * 256 + i * 64 + lane] = accu[mt][i];
+    }
+}
+
+// block of launch planning shared by the GEMV entry points
+struct Plan {
+  int nw;  // waves per block
+};
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Waves per block: few enough that each wave has a batch or more of steps, enough that small
+// per-block step counts still spread over the block. Overridable (for launch-shape sweeps) by the
+// environment variable KRQ_GEMV_WAVES.
+int plan_waves(int nsteps, int P, int M);
+
+// Validated launches shared by the C ABI entry points (gemv_fp8.hip, gemv_bf16.hip); mode may
+// also be kOutArgmax (then split == 1, aux = [N/16][M] Best, out = optional bf16 logits).
+int gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const float* x_inv, int x_per_row,
+                 const void* w8, int w_layout, const float* w_scale, int w_per_row, int64_t M,
+                 int64_t N, int64_t K, int split, int mode, int algo, void* out, void* aux,
+                 void* stream);
+int gemv_bf16_run(const void* x, const void* w, int64_t M, int64_t N, int64_t K, int split, int mode,
+                  void* out, void* aux, void* stream);
+
+}  // namespace krq

@@ -1,12 +1,13 @@
 // Quantization kernels of the decode-matmul path (gfx950):
 //   weight quantizers (per output channel, per tensor), activation scales (per tensor, per
 //   token), the scaled FP8 cast, and the tiled <-> row-major FP8 weight permutations.
-// Every quantized byte goes through krq::clamp_to_e4m3, the software OCP E4M3 RNE encoder, so
-// the bytes equal torch's float8_e4m3fn cast of the same fp32 values.
+// Quantized bytes come from the software OCP E4M3 RNE encoder (krq::clamp_to_e4m3) on the scalar
+// paths and from the hardware convert after the same clamp (krq::cvt4_e4m3, bit-identical) on the
+// vectorized paths; both equal torch's float8_e4m3fn cast of the same fp32 values.
 #include <stdarg.h>
 #include <stdio.h>
 
-#include "krq_common.h"
+#include "gemv_common.h"
 
 using namespace krq;
 
@@ -33,14 +34,6 @@ int krq_check_launch(const char* what) {
 
 extern "C" const char* krq_last_error(void) { return g_err; }
 extern "C" const char* krq_version(void) { return "krq 0.1.0 gfx950"; }
-
-#define KRQ_REQUIRE(cond, ...)        \
-  do {                                \
-    if (!(cond)) {                    \
-      krq_set_error(__VA_ARGS__);     \
-      return KRQ_EINVAL;              \
-    }                                 \
-  } while (0)
 
 namespace {
 
@@ -175,6 +168,107 @@ __global__ __launch_bounds__(kQT) void k_permute(const uint8_t* __restrict__ src
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Vectorized forms (K % 8 == 0, 16-byte aligned rows, K <= kVecMaxK): each thread keeps its
+// 16-byte chunks of the row in registers between the amax pass and the cast.
+// ---------------------------------------------------------------------------------------------
+constexpr int kVecChunks = 8;
+constexpr int64_t kVecMaxK = (int64_t)kVecChunks * 8 * kQT;
+
+KRQ_DEV uint2 quant8_div(uint4 v, float s) {
+  uint2 r;
+  r.x = cvt4_e4m3(as_f32(v.x << 16) / s, as_f32(v.x & 0xffff0000u) / s, as_f32(v.y << 16) / s,
+                  as_f32(v.y & 0xffff0000u) / s);
+  r.y = cvt4_e4m3(as_f32(v.z << 16) / s, as_f32(v.z & 0xffff0000u) / s, as_f32(v.w << 16) / s,
+                  as_f32(v.w & 0xffff0000u) / s);
+  return r;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kQT) void k_weight_rows_vec(const uint16_t* __restrict__ w, int64_t K,
+                                                         int64_t ldw, uint8_t* __restrict__ w8,
+                                                         uint8_t* __restrict__ w8t,
+                                                         float* __restrict__ scale,
+                                                         float* __restrict__ row_amax) {
+  const int64_t n = blockIdx.x;
+  const uint8_t* row = reinterpret_cast<const uint8_t*>(w + n * ldw);
+  uint4 v[kVecChunks];
+  float m = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kVecChunks; ++c) {
+    const int64_t e = 8 * (int64_t)(threadIdx.x + c * kQT);
+    v[c] = e < K ? ld16nt(row + 2 * e) : zero4();
+    m = absmax8(v[c], m);
+  }
+  float s;
+  if (MODE == 2) {
+    s = scale[0];
+  } else {
+    m = block_max<kQT>(m);
+    if (MODE == 1) {
+      if (threadIdx.x == 0) row_amax[n] = m;
+      return;
+    }
+    s = scale_from_amax(fmaxf(m, 1e-12f));
+    if (threadIdx.x == 0) scale[n] = s;
+  }
+#pragma unroll
+  for (int c = 0; c < kVecChunks; ++c) {
+    const int64_t e = 8 * (int64_t)(threadIdx.x + c * kQT);
+    if (e < K) {
+      const uint2 q = quant8_div(v[c], s);
+      if (w8) *reinterpret_cast<uint2*>(w8 + n * K + e) = q;
+      if (w8t) *reinterpret_cast<uint2*>(w8t + tiled_offset(n, e, K)) = q;
+    }
+  }
+}
+
+// per-row activation scale, and with x8 the per-token cast (quant_rows)
+__global__ __launch_bounds__(kQT) void k_act_rows_vec(const uint16_t* __restrict__ x, int64_t K,
+                                                      float headroom, float* amax, float* inv,
+                                                      float* scale, uint8_t* __restrict__ x8) {
+  const int64_t r = blockIdx.x;
+  const uint8_t* row = reinterpret_cast<const uint8_t*>(x + r * K);
+  uint4 v[kVecChunks];
+  float m = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kVecChunks; ++c) {
+    const int64_t e = 8 * (int64_t)(threadIdx.x + c * kQT);
+    v[c] = e < K ? ld16(row + 2 * e) : zero4();
+    m = absmax8(v[c], m);
+  }
+  m = block_max<kQT>(m);
+  const float a = fmaxf(m, 1e-6f) * headroom;
+  const float iv = inv_from_amax(a);
+  if (threadIdx.x == 0) {
+    if (amax) amax[r] = a;
+    if (inv) inv[r] = iv;
+    scale[r] = scale_from_amax(a);
+  }
+  if (x8) {
+#pragma unroll
+    for (int c = 0; c < kVecChunks; ++c) {
+      const int64_t e = 8 * (int64_t)(threadIdx.x + c * kQT);
+      if (e < K) *reinterpret_cast<uint2*>(x8 + r * K + e) = quant8(v[c], iv);
+    }
+  }
+}
+
+// cast, one 16-byte chunk (8 values) per thread
+__global__ __launch_bounds__(kQT) void k_cast_vec(const uint16_t* __restrict__ x, int64_t M, int64_t K,
+                                                  const float* __restrict__ inv, int per_row,
+                                                  uint8_t* __restrict__ x8) {
+  const int64_t nch = M * K / 8;
+  for (int64_t i = blockIdx.x * (int64_t)kQT + threadIdx.x; i < nch; i += (int64_t)gridDim.x * kQT) {
+    const float iv = inv[per_row ? (8 * i) / K : 0];
+    *reinterpret_cast<uint2*>(x8 + 8 * i) = quant8(ld16(reinterpret_cast<const uint8_t*>(x) + 16 * i), iv);
+  }
+}
+
+bool vec_ok(const void* p, int64_t K, int64_t ld) {
+  return K % 8 == 0 && ld % 8 == 0 && K <= kVecMaxK && aligned16(p);
+}
+
 int grid_for(int64_t work, int per_block, int cap) {
   int64_t g = (work + per_block - 1) / per_block;
   if (g < 1) g = 1;
@@ -196,8 +290,9 @@ extern "C" int krq_quant_fp8_rows(const void* w_bf16, int64_t N, int64_t K, int6
   KRQ_REQUIRE(!w8_tiled || (N % 16 == 0 && K % 64 == 0),
               "quant_fp8_rows: tiled layout needs N %% 16 == 0 and K %% 64 == 0 (N=%lld K=%lld)",
               (long long)N, (long long)K);
-  hipLaunchKernelGGL(k_weight_rows<0>, dim3(static_cast<unsigned>(N)), dim3(kQT), 0,
-                     (hipStream_t)stream, (const uint16_t*)w_bf16, K, ldw, (uint8_t*)w8,
+  const bool vec = vec_ok(w_bf16, K, ldw) && (!w8 || aligned16(w8));
+  hipLaunchKernelGGL(vec ? k_weight_rows_vec<0> : k_weight_rows<0>, dim3(static_cast<unsigned>(N)),
+                     dim3(kQT), 0, (hipStream_t)stream, (const uint16_t*)w_bf16, K, ldw, (uint8_t*)w8,
                      (uint8_t*)w8_tiled, scale, nullptr);
   return krq_check_launch("quant_fp8_rows");
 }
@@ -213,12 +308,14 @@ extern "C" int krq_quant_fp8_tensor(const void* w_bf16, int64_t N, int64_t K, in
               "quant_fp8_tensor: tiled layout needs N %% 16 == 0 and K %% 64 == 0 (N=%lld K=%lld)",
               (long long)N, (long long)K);
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(k_weight_rows<1>, dim3(static_cast<unsigned>(N)), dim3(kQT), 0, s,
-                     (const uint16_t*)w_bf16, K, ldw, nullptr, nullptr, nullptr, row_amax_ws);
+  const bool vec = vec_ok(w_bf16, K, ldw) && (!w8 || aligned16(w8));
+  hipLaunchKernelGGL(vec ? k_weight_rows_vec<1> : k_weight_rows<1>, dim3(static_cast<unsigned>(N)),
+                     dim3(kQT), 0, s, (const uint16_t*)w_bf16, K, ldw, nullptr, nullptr, nullptr,
+                     row_amax_ws);
   hipLaunchKernelGGL(k_fold_scale, dim3(1), dim3(1024), 0, s, row_amax_ws, N, scale0);
-  hipLaunchKernelGGL(k_weight_rows<2>, dim3(static_cast<unsigned>(N)), dim3(kQT), 0, s,
-                     (const uint16_t*)w_bf16, K, ldw, (uint8_t*)w8, (uint8_t*)w8_tiled, scale0,
-                     nullptr);
+  hipLaunchKernelGGL(vec ? k_weight_rows_vec<2> : k_weight_rows<2>, dim3(static_cast<unsigned>(N)),
+                     dim3(kQT), 0, s, (const uint16_t*)w_bf16, K, ldw, (uint8_t*)w8,
+                     (uint8_t*)w8_tiled, scale0, nullptr);
   return krq_check_launch("quant_fp8_tensor");
 }
 
@@ -235,8 +332,8 @@ extern "C" int krq_act_scale(const void* x_bf16, int64_t M, int64_t K, int per_r
   hipStream_t s = (hipStream_t)stream;
   if (per_row) {
     KRQ_REQUIRE(M <= 0x7fffffff, "act_scale: M=%lld too large", (long long)M);
-    hipLaunchKernelGGL(k_act_rows, dim3(static_cast<unsigned>(M)), dim3(kQT), 0, s,
-                       (const uint16_t*)x_bf16, K, headroom, amax, inv, scale, nullptr);
+    hipLaunchKernelGGL(vec_ok(x_bf16, K, K) ? k_act_rows_vec : k_act_rows, dim3(static_cast<unsigned>(M)),
+                       dim3(kQT), 0, s, (const uint16_t*)x_bf16, K, headroom, amax, inv, scale, nullptr);
   } else {
     KRQ_REQUIRE(ws != nullptr, "act_scale: per-tensor scale needs a workspace");
     const int g = grid_for(M * K, kQT * 16, kActPartials);
@@ -250,9 +347,15 @@ extern "C" int krq_cast_fp8(const void* x_bf16, int64_t M, int64_t K, const floa
                             void* x8, void* stream) {
   KRQ_REQUIRE(x_bf16 && inv && x8, "cast_fp8: null pointer");
   KRQ_REQUIRE(M > 0 && K > 0, "cast_fp8: bad shape M=%lld K=%lld", (long long)M, (long long)K);
-  const int g = grid_for(M * K, kQT * 4, 8192);
-  hipLaunchKernelGGL(k_cast, dim3(g), dim3(kQT), 0, (hipStream_t)stream, (const uint16_t*)x_bf16, M,
-                     K, inv, per_row, (uint8_t*)x8);
+  if (vec_ok(x_bf16, K, K) && aligned16(x8)) {
+    const int g = grid_for(M * K / 8, kQT, 8192);
+    hipLaunchKernelGGL(k_cast_vec, dim3(g), dim3(kQT), 0, (hipStream_t)stream, (const uint16_t*)x_bf16,
+                       M, K, inv, per_row, (uint8_t*)x8);
+  } else {
+    const int g = grid_for(M * K, kQT * 4, 8192);
+    hipLaunchKernelGGL(k_cast, dim3(g), dim3(kQT), 0, (hipStream_t)stream, (const uint16_t*)x_bf16, M,
+                       K, inv, per_row, (uint8_t*)x8);
+  }
   return krq_check_launch("cast_fp8");
 }
 
@@ -261,7 +364,8 @@ extern "C" int krq_quant_rows(const void* x_bf16, int64_t M, int64_t K, void* x8
   KRQ_REQUIRE(x_bf16 && x8 && xs, "quant_rows: null pointer");
   KRQ_REQUIRE(M > 0 && K > 0 && M <= 0x7fffffff, "quant_rows: bad shape M=%lld K=%lld",
               (long long)M, (long long)K);
-  hipLaunchKernelGGL(k_act_rows, dim3(static_cast<unsigned>(M)), dim3(kQT), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(vec_ok(x_bf16, K, K) && aligned16(x8) ? k_act_rows_vec : k_act_rows,
+                     dim3(static_cast<unsigned>(M)), dim3(kQT), 0, (hipStream_t)stream,
                      (const uint16_t*)x_bf16, K, 1.0f, nullptr, nullptr, xs, (uint8_t*)x8);
   return krq_check_launch("quant_rows");
 }

@@ -189,34 +189,62 @@ def _weight_operand(q):
     return w8, L.W_ROWMAJOR, ws, w8.shape
 
 
+FUSED_MAX_ELEMS = 8 * 64 * 64  # activation slice the GEMV can quantize in its prologue
+
+
+def _gemv(xin, x_kind, x_scale, x_inv, M, q, split, mode, algo, out):
+    w, layout, ws, (N, K) = _weight_operand(q)
+    L.require_device(xin, x_scale, x_inv)
+    xpr = 1 if (x_scale is not None and x_scale.numel() == M and M > 1) else 0
+    wpr = 1 if ws.numel() > 1 else 0
+    if out is None:
+        if mode == L.OUT_PARTIAL:
+            out = torch.empty((split, M, N), device=xin.device, dtype=torch.float32)
+        else:
+            out = torch.empty((M, N // 2 if mode == L.OUT_SWIGLU else N), device=xin.device,
+                              dtype=torch.bfloat16)
+    L.call("krq_gemv_fp8", L.ptr(xin), x_kind, L.ptr(x_scale), L.ptr(x_inv), xpr, L.ptr(w), layout,
+           L.ptr(ws), wpr, M, N, K, split, mode, algo, L.ptr(out), L.stream(xin))
+    return out
+
+
 def gemv_fp8_launch(x8, xs, q, split=1, mode=L.OUT_BF16, algo=L.ALGO_AUTO, out=None):
     """One launch of the FP8 GEMV kernel on already-quantized activations.
     x8 float8_e4m3fn [M, K] (M <= 32); xs fp32 with 1 (per tensor) or M (per token) values;
     q = quantize(W) or quantize_weight(W). Returns out (allocated when None): bf16 [M, N],
     fp32 partials [split, M, N], or bf16 [M, N/2] for mode OUT_SWIGLU."""
-    w, layout, ws, (N, K) = _weight_operand(q)
-    L.require_device(x8, xs)
+    K = q[0].shape[1]
     M = x8.shape[0]
     if x8.dtype != torch.float8_e4m3fn or x8.dim() != 2 or x8.shape[1] != K or not x8.is_contiguous():
         raise ValueError(f"x8 must be a contiguous float8_e4m3fn [M, {K}] tensor")
     if xs.dtype != torch.float32 or xs.numel() not in (1, M):
         raise ValueError("xs must be fp32 with 1 or M values")
-    xpr = 1 if (xs.numel() == M and M > 1) else 0
-    wpr = 1 if ws.numel() > 1 else 0
-    if out is None:
-        if mode == L.OUT_PARTIAL:
-            out = torch.empty((split, M, N), device=x8.device, dtype=torch.float32)
-        else:
-            out = torch.empty((M, N // 2 if mode == L.OUT_SWIGLU else N), device=x8.device,
-                              dtype=torch.bfloat16)
-    L.call("krq_gemv_fp8", L.ptr(x8), L.ptr(xs), xpr, L.ptr(w), layout, L.ptr(ws), wpr, M, N, K,
-           split, mode, algo, L.ptr(out), L.stream(x8))
-    return out
+    return _gemv(x8, L.X_FP8, xs.reshape(-1), None, M, q, split, mode, algo, out)
+
+
+def gemv_fp8_bf16_launch(x, q, split=1, mode=L.OUT_BF16, a=None, algo=L.ALGO_AUTO, out=None):
+    """One launch of the FP8 GEMV kernel on bf16 activations quantized inside the kernel:
+    per token (M == 1, a is None) or with the inverse scale of an ActScale / SharedScale a."""
+    x = _rows(x)
+    M = x.shape[0]
+    if a is None:
+        return _gemv(x, L.X_BF16_DYN, None, None, M, q, split, mode, algo, out)
+    return _gemv(x, L.X_BF16_STATIC, a.scale.reshape(1), a.inv.reshape(1), M, q, split, mode, algo, out)
+
+
+def _fits_fused(x, split, a):
+    M, K = x.shape
+    if x.dtype != torch.bfloat16 or M > DECODE_MAX_ROWS or K % 64:
+        return False
+    if a is None:
+        return M == 1 and K <= FUSED_MAX_ELEMS
+    return M * (K // split) <= FUSED_MAX_ELEMS
 
 
 def _activation_fp8(x, a, xs):
-    """(x8, x_scale) for the GEMV: x8 given (fp8 dtype) with xs; a static or per-call ActScale a;
-    or per-token dynamic scales."""
+    """(x8, x_scale) for the GEMV when it does not quantize in its prologue: x8 given (fp8
+    dtype) with xs; a static or per-call ActScale a (cast kernel); or per-token scales
+    (quant_rows kernel)."""
     if x.dtype == torch.float8_e4m3fn:
         if xs is None:
             raise ValueError("float8 activations need their scale xs")
@@ -246,8 +274,10 @@ def gemv_fp8(x, q, split=1, a=None, xs=None, algo=L.ALGO_AUTO):
     experiments/modal_fp8.py:69."""
     M, K = x.shape
     assert K % split == 0
-    x8, s = _activation_fp8(x, a, xs)
     mode = L.OUT_BF16 if split == 1 else L.OUT_PARTIAL
+    if xs is None and _fits_fused(x, split, a):
+        return gemv_fp8_bf16_launch(x, q, split, mode, a, algo)
+    x8, s = _activation_fp8(x, a, xs)
     return _chunked(x8, s, lambda xc, sc: gemv_fp8_launch(xc, sc, q, split, mode, algo))
 
 
@@ -255,6 +285,8 @@ def gemv_swiglu_fp8(x, q, a=None, xs=None, algo=L.ALGO_AUTO):
     """FP8 counterpart of kernels.gemv.gemv_swiglu: q quantizes w_gu [2I, K] = [gate; up];
     returns bf16(bf16(silu(bf16 g)) * bf16 u) [M, I]. Called as fp8.gemv_swiglu_fp8(x, q) by the
     reference's experiments/modal_fp8.py:67."""
+    if xs is None and _fits_fused(x, 1, a):
+        return gemv_fp8_bf16_launch(x, q, 1, L.OUT_SWIGLU, a, algo)
     x8, s = _activation_fp8(x, a, xs)
     return _chunked(x8, s, lambda xc, sc: gemv_fp8_launch(xc, sc, q, 1, L.OUT_SWIGLU, algo))
 
@@ -269,6 +301,8 @@ def linear_fp8(x, q, a=None, amax_out=None):
         a = ActScale(x)
         if amax_out is not None:
             amax_out.copy_(torch.maximum(amax_out, a.amax.reshape(1)))
+    if _fits_fused(x, 1, a):
+        return gemv_fp8_bf16_launch(x, q, 1, L.OUT_BF16, a)
     x8 = _cast(x, a)
     if x.shape[0] <= DECODE_MAX_ROWS:
         return gemv_fp8_launch(x8, a.scale.reshape(1), q, 1, L.OUT_BF16)

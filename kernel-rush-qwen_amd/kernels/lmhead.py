@@ -1,29 +1,16 @@
-"""LM head GEMV fused with greedy argmax, one launch.
+"""LM head GEMV fused with greedy argmax (a GEMV launch with an argmax epilogue plus a fold).
 
 Reference semantics: logits = gemv(h, lm_head, 1) (bf16) then torch.argmax(logits, -1)
 (engine/engine.py:1021-1022), i.e. the lowest index among the largest bf16-rounded logits; the
 reference's fused form keeps the same rule (engine/kernels/mega.py:412-436). The FP8 variant
-scales activations per token (fp8.quant_rows) and uses per-channel weights (fp8.quantize).
+scales activations per token (inside the GEMV at M == 1, else fp8.quant_rows) and uses
+per-channel weights (fp8.quantize).
 """
 
 import torch
 
 from . import _lib as L
 from . import fp8 as _fp8
-
-# Workspace per (device, M, V): block results plus an arrival counter that the kernel leaves at
-# zero. Calls that overlap on one device with the same (M, V) would share it, so issue them on
-# one stream.
-_WS = {}
-
-
-def _workspace(device, M, V):
-    key = (device.index, M, V)
-    ws = _WS.get(key)
-    if ws is None:
-        n = int(L.lib().krq_lmhead_ws_bytes(M, V))
-        ws = _WS[key] = torch.zeros((n,), device=device, dtype=torch.uint8)
-    return ws
 
 
 def lm_head_argmax(h, w, return_logits=False):
@@ -38,8 +25,11 @@ def lm_head_argmax(h, w, return_logits=False):
         V = w8.shape[0]
         if ws.numel() != V:
             raise ValueError("the FP8 lm head needs per-channel scales (fp8.quantize)")
-        h8, hs = _fp8.quant_rows(h)
-        hin, hsc, wk = h8, hs.reshape(-1), L.LM_FP8
+        if M == 1:   # per-token scale computed inside the GEMV
+            hin, hsc, wk = _fp8._rows(h), None, L.LM_FP8
+        else:
+            h8, hs = _fp8.quant_rows(h)
+            hin, hsc, wk = h8, hs.reshape(-1), L.LM_FP8
         wt, layout = (tiled, L.W_TILED) if tiled is not None else (w8, L.W_ROWMAJOR)
         wsc = ws
     else:
@@ -52,7 +42,7 @@ def lm_head_argmax(h, w, return_logits=False):
         raise ValueError(f"lm_head_argmax: M={M} > 32")
     idx = torch.empty((M,), device=h.device, dtype=torch.int64)
     logits = torch.empty((M, V), device=h.device, dtype=torch.bfloat16) if return_logits else None
-    ws_buf = _workspace(h.device, M, V)
+    ws_buf = torch.empty((int(L.lib().krq_lmhead_ws_bytes(M, V)),), device=h.device, dtype=torch.uint8)
     L.call("krq_lmhead_argmax", L.ptr(hin), L.ptr(hsc), L.ptr(wt), wk, layout, L.ptr(wsc), M, V, K,
            L.ptr(logits), L.ptr(ws_buf), ws_buf.numel(), L.ptr(idx), L.stream(h))
     return (idx, logits) if return_logits else idx

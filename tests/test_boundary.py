@@ -43,11 +43,16 @@ def test_invalid_arguments_fail_before_any_launch():
     lib = L.lib()
     p = ctypes.c_void_p(4096)  # never dereferenced: validation rejects the call first
     # M out of range
-    rc = lib.krq_gemv_fp8(p, p, 0, p, 1, p, 1, 0, 64, 256, 1, 0, 0, p, _null())
+    rc = lib.krq_gemv_fp8(p, 0, p, None, 0, p, 1, p, 1, 0, 64, 256, 1, 0, 0, p, _null())
     assert rc == L.KRQ_EINVAL and b"M=0" in lib.krq_last_error()
     # K/split not a multiple of 64
-    rc = lib.krq_gemv_fp8(p, p, 0, p, 1, p, 1, 1, 64, 200, 1, 0, 0, p, _null())
+    rc = lib.krq_gemv_fp8(p, 0, p, None, 0, p, 1, p, 1, 1, 64, 200, 1, 0, 0, p, _null())
     assert rc == L.KRQ_EINVAL and b"K_SPLIT" in lib.krq_last_error()
+    # in-kernel per-token scaling takes one row; static scaling needs x_inv
+    rc = lib.krq_gemv_fp8(p, 1, None, None, 0, p, 1, p, 1, 2, 64, 256, 1, 0, 0, p, _null())
+    assert rc == L.KRQ_EINVAL and b"M == 1" in lib.krq_last_error()
+    rc = lib.krq_gemv_fp8(p, 2, p, None, 0, p, 1, p, 1, 2, 64, 256, 1, 0, 0, p, _null())
+    assert rc == L.KRQ_EINVAL and b"x_inv" in lib.krq_last_error()
     # split > 1 without the partials output
     rc = lib.krq_gemv_bf16(p, p, 1, 64, 256, 2, 0, p, _null())
     assert rc == L.KRQ_EINVAL

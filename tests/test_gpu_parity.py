@@ -397,3 +397,56 @@ def test_deterministic(dev):
     a = fp8.gemv_fp8(xd, q, 4)
     b = fp8.gemv_fp8(xd, q, 4)
     assert torch.equal(a, b)
+
+
+# ---------------------------------------------------------------------------------------------
+# in-kernel activation quantization: identical to quantizing first
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("name", ["qkv", "o", "down"])
+@pytest.mark.parametrize("algo", [L.ALGO_MFMA, L.ALGO_VALU])
+def test_fused_dynamic_quant_matches_two_kernel_path(dev, name, algo):
+    N, K = SHAPES[name]
+    w, x = _fp8_case(N, K, 1, SEEDS[name])
+    q = fp8.quantize(w.to(dev))
+    xd = x.to(dev)
+    x8, xs = fp8.quant_rows(xd)
+    r8, rs = O.quantize(u16(w))
+    _, yref = O.fp8_matmul(u8(x8), xs.cpu().numpy(), r8, rs)
+    for split in (1, 2, 4):
+        mode = L.OUT_BF16 if split == 1 else L.OUT_PARTIAL
+        fused = fp8.gemv_fp8_bf16_launch(xd, q, split, mode, None, algo)
+        two = fp8.gemv_fp8_launch(x8, xs, q, split, mode, algo)
+        # same operands; the launch shape (and so the fp32 summation order) may differ
+        f = fused.float().cpu().numpy() if split == 1 else _sum_partials(fused)
+        t = two.float().cpu().numpy() if split == 1 else _sum_partials(two)
+        assert rel_err(f, t) <= 1e-2 and rel_err(f, yref) <= TOL, (name, split)
+    sw = fp8.gemv_fp8_bf16_launch(xd, fp8.quantize(weight(2 * 1024, K, 5).to(dev)), 1, L.OUT_SWIGLU, None, algo)
+    assert sw.shape == (1, 1024)
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_fused_static_quant_matches_cast_path(dev, M):
+    N, K = O_PROJ
+    w, x = _fp8_case(N, K, M, 17)
+    q = fp8.quantize_weight(w.to(dev))
+    xd = x.to(dev)
+    a = fp8.SharedScale(torch.tensor([448.0 / 4.5], device=dev), torch.tensor(4.5 / 448.0, device=dev))
+    x8 = fp8._cast_hip(xd, a)
+    for split in (4, 8):
+        fused = fp8.gemv_fp8_bf16_launch(xd, q, split, L.OUT_PARTIAL, a)
+        two = fp8.gemv_fp8_launch(x8, a.scale.reshape(1), q, split, L.OUT_PARTIAL)
+        assert torch.equal(fused, two), split
+    r8, rs = O.quantize_weight(u16(w))
+    _, yref = O.fp8_matmul(O.cast(u16(x), np.float32(448.0 / 4.5)), np.float32(4.5 / 448.0), r8, rs)
+    assert rel_err(_sum_partials(fused), yref) <= TOL
+
+
+def test_fused_quant_rejects_oversized_slices(dev):
+    w = weight(64, 9728, 1).to(dev)
+    q = fp8.quantize(w)
+    a = fp8.SharedScale(torch.ones(1, device=dev), torch.ones((), device=dev))
+    with pytest.raises(ValueError, match="too large"):
+        fp8.gemv_fp8_bf16_launch(act(16, 9728, 1).to(dev), q, 1, L.OUT_BF16, a)
+    # the public entry point routes such shapes through the cast kernel instead
+    y = fp8.gemv_fp8(act(16, 9728, 1).to(dev), q, 1, a=a)
+    assert y.shape == (16, 64)
