@@ -3,10 +3,11 @@
 Default workload ("C2"): one Qwen3-4B decoder layer's projections at
 M = 1 - QKV [6144x2560], O [2560x4096], gate_up [19456x2560] (SwiGLU epilogue), down
 [2560x9728] - with per-channel FP8 e4m3 weights and per-token dynamic FP8 activation scales.
-One step = the four projections of one layer, each = per-token quantization kernel + GEMV
-kernel, with the reference engine's output contract (engine/engine.py:69, :1005): QKV split 2,
-O split 4, down split 4 (fp32 split-K partials), gate_up bf16 SwiGLU. Successive steps use the
-next of 36 layers of distinct weights (3.6 GB) so the 256 MB MALL cannot serve repeats, as the
+One step = the four projections of one layer with the reference engine's output contract
+(engine/engine.py:69, :1005): QKV split 2, O split 4, down split 4 (fp32 split-K partials),
+gate_up bf16 SwiGLU. At M = 1 each projection is one GEMV launch that quantizes its activations
+itself; at larger M the per-token quantization kernel runs first. Successive steps use the next
+of 36 layers of distinct weights (3.6 GB) so the 256 MB MALL cannot serve repeats, as the
 reference's tuner cycles layers (engine/engine.py:845-847, :887-891). The K timed steps are one
 hipGraph replay.
 
@@ -15,8 +16,9 @@ N*K (w8) + 4N (w scale) + 2MK (bf16 x) + 4M (x scale) + output (2MN bf16, 4SMN p
 2MI SwiGLU).
 
 Also printed (stderr): per-kernel table from graph-replayed back-to-back launches (hipEvents),
-and the roofline of the dominant kernel (the gate_up GEMV). --config c3 runs M = 16,
---config c3m32 M = 32, --config c4 the lm_head + argmax, --config c5 the full decode step.
+and the roofline of the dominant kernel (the gate_up GEMV; its HBM traffic from the committed
+rocprofv3 counter summary). --config c3 runs M = 16, --config c3m32 M = 32, --config c4 the
+lm_head + argmax (--lm bf16|fp8, --m 1|16), --config c5 the full decode step (36 layers + lm_head).
 """
 
 import argparse
