@@ -32,61 +32,68 @@ __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x
     accu[mt] = v4f{0.f, 0.f, 0.f, 0.f};
   }
   float s0 = 0.f, s1 = 0.f, q0 = 0.f, q1 = 0.f;
-  for (int c0 = 0; c0 < jcount; c0 += U) {
-    uint4 wl[U], wh[U], ul[U], uh[U], xl[U][MT], xh[U][MT];
+  // a ring of U step slots: consume slot u (step cc), then refill it with step cc + U
+  uint4 wl[U], wh[U], ul[U], uh[U], xl[U][MT], xh[U][MT];
+  auto load_slot = [&](int u, int cc) {
+    const int j = wave + min(cc, jcount - 1) * nw;
+    const int64_t t0 = tbase + 2 * j;
+    const int64_t t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
+    wl[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rb, t0, rowb, lane));
+    wh[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rb, t1, rowb, lane));
+    if (P == 2) {
+      ul[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rbu, t0, rowb, lane));
+      uh[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rbu, t1, rowb, lane));
+    }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int j = wave + min(c0 + u, jcount - 1) * nw;
-      const int64_t t0 = tbase + 2 * j;
-      const int64_t t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
-      wl[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rb, t0, rowb, lane));
-      wh[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rb, t1, rowb, lane));
-      if (P == 2) {
-        ul[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rbu, t0, rowb, lane));
-        uh[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rbu, t1, rowb, lane));
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = ALGO == 2 ? 0 : mt * 16 + r;
+      uint4 lo = zero4(), hi = zero4();
+      if (m < M) {
+        const uint8_t* xr = x + (int64_t)m * rowb + g * 16;
+        lo = ld16(xr + t0 * 64);
+        hi = ld16(xr + t1 * 64);
       }
+      xl[u][mt] = lo;
+      xh[u][mt] = hi;
+    }
+  };
+  auto consume_slot = [&](int u, int cc) {
+    const int j = wave + min(cc, jcount - 1) * nw;
+    const bool ok = cc < jcount, hi = ok && (2 * j + 1 < kts);
+    const uint4 bl = sel4(ok, wl[u]), bh = sel4(hi, wh[u]);
+    if (ALGO == 2) {
+      s0 = dot8_bf16(bl, xl[u][0], s0);
+      s1 = dot8_bf16(bh, xh[u][0], s1);
+      if (P == 2) {
+        q0 = dot8_bf16(sel4(ok, ul[u]), xl[u][0], q0);
+        q1 = dot8_bf16(sel4(hi, uh[u]), xh[u][0], q1);
+      }
+    } else {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const int m = ALGO == 2 ? 0 : mt * 16 + r;
-        uint4 a = zero4(), b = zero4();
-        if (m < M) {
-          const uint8_t* xr = x + (int64_t)m * rowb + g * 16;
-          a = ld16(xr + t0 * 64);
-          b = ld16(xr + t1 * 64);
-        }
-        xl[u][mt] = a;
-        xh[u][mt] = b;
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xl[u][mt]), as_v8bf(bl), acc[mt], 0, 0, 0);
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xh[u][mt]), as_v8bf(bh), acc[mt], 0, 0, 0);
       }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int cc = c0 + u;
-      const int j = wave + min(cc, jcount - 1) * nw;
-      const bool ok = cc < jcount, hi = ok && (2 * j + 1 < kts);
-      const uint4 bl = sel4(ok, wl[u]), bh = sel4(hi, wh[u]);
-      if (ALGO == 2) {
-        s0 = dot8_bf16(bl, xl[u][0], s0);
-        s1 = dot8_bf16(bh, xh[u][0], s1);
-        if (P == 2) {
-          q0 = dot8_bf16(sel4(ok, ul[u]), xl[u][0], q0);
-          q1 = dot8_bf16(sel4(hi, uh[u]), xh[u][0], q1);
-        }
-      } else {
+      if (P == 2) {
+        const uint4 cl = sel4(ok, ul[u]), ch = sel4(hi, uh[u]);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xl[u][mt]), as_v8bf(bl), acc[mt], 0, 0, 0);
-          acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xh[u][mt]), as_v8bf(bh), acc[mt], 0, 0, 0);
-        }
-        if (P == 2) {
-          const uint4 cl = sel4(ok, ul[u]), ch = sel4(hi, uh[u]);
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xl[u][mt]), as_v8bf(cl), accu[mt], 0, 0, 0);
-            accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xh[u][mt]), as_v8bf(ch), accu[mt], 0, 0, 0);
-          }
+          accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xl[u][mt]), as_v8bf(cl), accu[mt], 0, 0, 0);
+          accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xh[u][mt]), as_v8bf(ch), accu[mt], 0, 0, 0);
         }
       }
+    }
+  };
+  if (jcount > 0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) load_slot(u, u);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  for (int base = 0; base < jcount; base += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      consume_slot(u, base + u);
+      if (base + u + U < jcount) load_slot(u, base + u + U);
     }
   }
   if (ALGO == 2) {

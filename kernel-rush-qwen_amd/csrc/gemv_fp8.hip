@@ -24,8 +24,10 @@ int plan_waves(int nsteps, int P, int M) {
     return s ? atoi(s) : 0;
   }();
   if (env >= 1 && env <= 8) return env;
-  if (P == 1 && M <= 4 && nsteps <= 12) return 4;
-  return nsteps >= 2 ? 2 : 1;
+  if (nsteps < 2) return 1;
+  // measured on MI355X at the Qwen3-4B shapes: two waves for one-row (U = 4) blocks and for the
+  // two-matrix SwiGLU block, four for the multi-row single-matrix block
+  return (M > 4 && P == 1 && nsteps >= 4) ? 4 : 2;
 }
 }  // namespace krq
 
@@ -73,42 +75,45 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(
     }
   }
 
-  // ---- weight (and, for e4m3 activations, A operand) batch loads ----
+  // scale of this thread's activation row, read now so its latency hides under the weight stream
+  const float xs_reg = (XK != KRQ_X_BF16_DYN && threadIdx.x < (unsigned)M) ? xsc[x_per_row ? threadIdx.x : 0] : 1.0f;
+
+  // ---- weight (and, for e4m3 activations, A operand) loads: a ring of U step slots ----
   uint4 wl[U], wh[U], ul[U], uh[U], xl[U][MT], xh[U][MT];
-  auto load_batch = [&](int c0) {
+  auto load_slot = [&](int u, int cc) {
+    const int j = wave + min(cc, jcount - 1) * nw;
+    const int64_t t0 = tbase + 2 * j;
+    const int64_t t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
+    wl[u] = ld16nt(w_addr<LAYOUT>(w8, rb, t0, K, lane));
+    wh[u] = ld16nt(w_addr<LAYOUT>(w8, rb, t1, K, lane));
+    if (P == 2) {
+      ul[u] = ld16nt(w_addr<LAYOUT>(w8, rbu, t0, K, lane));
+      uh[u] = ld16nt(w_addr<LAYOUT>(w8, rbu, t1, K, lane));
+    }
+    if (!FUSED) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int j = wave + min(c0 + u, jcount - 1) * nw;
-      const int64_t t0 = tbase + 2 * j;
-      const int64_t t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
-      wl[u] = ld16nt(w_addr<LAYOUT>(w8, rb, t0, K, lane));
-      wh[u] = ld16nt(w_addr<LAYOUT>(w8, rb, t1, K, lane));
-      if (P == 2) {
-        ul[u] = ld16nt(w_addr<LAYOUT>(w8, rbu, t0, K, lane));
-        uh[u] = ld16nt(w_addr<LAYOUT>(w8, rbu, t1, K, lane));
-      }
-      if (!FUSED) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int m = ALGO == 2 ? 0 : mt * 16 + r;
-          uint4 a = zero4(), b = zero4();
-          if (m < M) {
-            const uint8_t* xr = x + (int64_t)m * K + g * 16;
-            a = ld16(xr + t0 * 64);
-            b = ld16(xr + t1 * 64);
-          }
-          xl[u][mt] = a;
-          xh[u][mt] = b;
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = ALGO == 2 ? 0 : mt * 16 + r;
+        uint4 lo = zero4(), hi = zero4();
+        if (m < M) {
+          const uint8_t* xr = x + (int64_t)m * K + g * 16;
+          lo = ld16(xr + t0 * 64);
+          hi = ld16(xr + t1 * 64);
         }
+        xl[u][mt] = lo;
+        xh[u][mt] = hi;
       }
     }
   };
-  if (jcount > 0) load_batch(0);
+  if (jcount > 0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) load_slot(u, u);
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- fused activation prologue, part 2: scale, quantize the slice into LDS ----
   if (XK == KRQ_X_FP8) {
-    if (threadIdx.x < (unsigned)M) xs_l[threadIdx.x] = xsc[x_per_row ? threadIdx.x : 0];
+    if (threadIdx.x < (unsigned)M) xs_l[threadIdx.x] = xs_reg;
   } else if (XK == KRQ_X_BF16_DYN) {
     float am = 0.0f;
 #pragma unroll
@@ -135,11 +140,11 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(
         *reinterpret_cast<uint2*>(xq + (int64_t)m * ks + 8 * (idx - m * cpr)) =
             quant8(xv[c], xinv[x_per_row ? m : 0]);
     }
-    if (threadIdx.x < (unsigned)M) xs_l[threadIdx.x] = xsc[x_per_row ? threadIdx.x : 0];
+    if (threadIdx.x < (unsigned)M) xs_l[threadIdx.x] = xs_reg;
   }
   if (FUSED) __syncthreads();
 
-  // ---- main loop ----
+  // ---- main loop: consume slot u (step cc), then refill it with step cc + U ----
   v4f acc[MT], accu[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -147,54 +152,53 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(
     accu[mt] = v4f{0.f, 0.f, 0.f, 0.f};
   }
   float s0 = 0.f, s1 = 0.f, q0 = 0.f, q1 = 0.f;  // vector-ALU partial sums
-  for (int c0 = 0; c0 < jcount; c0 += U) {
-    if (c0 > 0) {
-      load_batch(c0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+  auto consume_slot = [&](int u, int cc) {
+    const int j = wave + min(cc, jcount - 1) * nw;
+    const bool ok = cc < jcount, hi = ok && (2 * j + 1 < kts);
+    if (FUSED) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int cc = c0 + u;
-      const int j = wave + min(cc, jcount - 1) * nw;
-      const bool ok = cc < jcount, hi = ok && (2 * j + 1 < kts);
-      if (FUSED) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int m = ALGO == 2 ? 0 : mt * 16 + r;
-          uint4 a = zero4(), b = zero4();
-          if (m < M) {
-            const uint8_t* xr = xq + (int64_t)m * ks + g * 16;
-            a = *reinterpret_cast<const uint4*>(xr + (2 * j) * 64);
-            if (2 * j + 1 < kts) b = *reinterpret_cast<const uint4*>(xr + (2 * j + 1) * 64);
-          }
-          xl[u][mt] = a;
-          xh[u][mt] = b;
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = ALGO == 2 ? 0 : mt * 16 + r;
+        uint4 lo = zero4(), hh = zero4();
+        if (m < M) {
+          const uint8_t* xr = xq + (int64_t)m * ks + g * 16;
+          lo = *reinterpret_cast<const uint4*>(xr + (2 * j) * 64);
+          if (2 * j + 1 < kts) hh = *reinterpret_cast<const uint4*>(xr + (2 * j + 1) * 64);
         }
+        xl[u][mt] = lo;
+        xh[u][mt] = hh;
       }
-      const uint4 bl = sel4(ok, wl[u]), bh = sel4(hi, wh[u]);
-      if (ALGO == 2) {
-        s0 = dot16_fp8(bl, xl[u][0], s0);
-        s1 = dot16_fp8(bh, xh[u][0], s1);
-        if (P == 2) {
-          q0 = dot16_fp8(sel4(ok, ul[u]), xl[u][0], q0);
-          q1 = dot16_fp8(sel4(hi, uh[u]), xh[u][0], q1);
-        }
-      } else {
-        const v8i B = pack_v8i(bl, bh);
+    }
+    const uint4 bl = sel4(ok, wl[u]), bh = sel4(hi, wh[u]);
+    if (ALGO == 2) {
+      s0 = dot16_fp8(bl, xl[u][0], s0);
+      s1 = dot16_fp8(bh, xh[u][0], s1);
+      if (P == 2) {
+        q0 = dot16_fp8(sel4(ok, ul[u]), xl[u][0], q0);
+        q1 = dot16_fp8(sel4(hi, uh[u]), xh[u][0], q1);
+      }
+    } else {
+      const v8i B = pack_v8i(bl, bh);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const v8i A = pack_v8i(xl[u][mt], xh[u][mt]);
+        acc[mt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc[mt], 0, 0, 0, 0, 0, 0);
+      }
+      if (P == 2) {
+        const v8i Bu = pack_v8i(sel4(ok, ul[u]), sel4(hi, uh[u]));
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const v8i A = pack_v8i(xl[u][mt], xh[u][mt]);
-          acc[mt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc[mt], 0, 0, 0, 0, 0, 0);
-        }
-        if (P == 2) {
-          const v8i Bu = pack_v8i(sel4(ok, ul[u]), sel4(hi, uh[u]));
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const v8i A = pack_v8i(xl[u][mt], xh[u][mt]);
-            accu[mt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, Bu, accu[mt], 0, 0, 0, 0, 0, 0);
-          }
+          accu[mt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, Bu, accu[mt], 0, 0, 0, 0, 0, 0);
         }
       }
+    }
+  };
+  for (int base = 0; base < jcount; base += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      consume_slot(u, base + u);
+      if (base + u + U < jcount) load_slot(u, base + u + U);
     }
   }
   if (ALGO == 2) {
