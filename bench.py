@@ -297,6 +297,7 @@ def main():
     import torch
     from kernels import _lib as L
     from kernels import fp8, lmhead
+    from kernels import gemv as G
 
     cfg = args.config
     M = {"c2": 1, "c3": 16, "c3m32": 32}.get(cfg, args.m or 1)
@@ -314,6 +315,8 @@ def main():
     if cfg in ("c4", "c5"):
         g = torch.Generator(device=dev).manual_seed(7)
         E = (torch.randn(V, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        if args.layout == "tiled":
+            G.pack(E)
         if cfg == "c4" and args.lm == "fp8":
             q8 = fp8.quantize(E)
             if args.layout == "rowmajor":

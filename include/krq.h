@@ -123,20 +123,23 @@ int krq_gemv_fp8(const void* x, int x_kind, const float* x_scale, const float* x
                  void* out, void* stream);
 
 /*
- * BF16 skinny GEMM/GEMV, M <= 32, row-major weights: gemv / gemv_m1 / gemv_swiglu /
- * gemv_m1_swiglu / gemv_rows (reference engine/kernels/gemv.py:43-348).
+ * BF16 skinny GEMM/GEMV, M <= 32: gemv / gemv_m1 / gemv_swiglu / gemv_m1_swiglu / gemv_rows
+ * (reference engine/kernels/gemv.py:43-348).
  *   acc = x[M,K] . w[N,K]^T in fp32; modes as krq_gemv_fp8.
+ * w_layout KRQ_W_ROWMAJOR: bf16 [N,K]; KRQ_W_TILED: the tiled layout above applied to the [N, 2K]
+ * byte matrix (made by krq_pack_fp8(w, N, 2K, w_tiled)).
  * Needs N % 16 == 0, K % split == 0 and (K/split) % 32 == 0.
  */
-int krq_gemv_bf16(const void* x, const void* w, int64_t M, int64_t N, int64_t K, int split,
-                  int mode, void* out, void* stream);
+int krq_gemv_bf16(const void* x, const void* w, int w_layout, int64_t M, int64_t N, int64_t K,
+                  int split, int mode, void* out, void* stream);
 
 /*
  * LM head + greedy argmax: logits = bf16(h . E^T) and idx[m] = lowest index of the maximum bf16
  * logit of row m. Reference: engine/engine.py:1021-1022 (gemv(h, lm_head, 1) then torch.argmax)
  * and the fused form engine/kernels/mega.py:396-441. Two launches (GEMV with an argmax epilogue,
  * then a per-row fold).
- * w_kind KRQ_LM_BF16: h bf16 [M,K], w bf16 [V,K] row-major; h_scale / w_scale unused.
+ * w_kind KRQ_LM_BF16: h bf16 [M,K], w bf16 [V,K] in w_layout (row-major, or tiled as for
+ *                     krq_gemv_bf16); h_scale / w_scale unused.
  * w_kind KRQ_LM_FP8:  w e4m3 [V,K] in w_layout with per-row w_scale[V]; h e4m3 [M,K] with
  *                     per-token h_scale[M], or (h_scale NULL, M == 1) h bf16 [1,K] scaled per
  *                     token inside the kernel; logits as krq_gemv_fp8 KRQ_OUT_BF16.
@@ -148,7 +151,8 @@ int krq_lmhead_argmax(const void* h, const float* h_scale, const void* w, int w_
                       void* ws, int64_t ws_bytes, int64_t* idx_out, void* stream);
 int64_t krq_lmhead_ws_bytes(int64_t M, int64_t V);
 
-/* Tiled <-> row-major FP8 weight copies (byte permutations; see "tiled" above). */
+/* Tiled <-> row-major weight copies (byte permutations; see "tiled" above). For a bf16 [N, K]
+ * matrix pass its [N, 2K] byte view (K -> 2K). */
 int krq_pack_fp8(const void* w8_rowmajor, int64_t N, int64_t K, void* w8_tiled, void* stream);
 int krq_unpack_fp8(const void* w8_tiled, int64_t N, int64_t K, void* w8_rowmajor, void* stream);
 

@@ -1,4 +1,5 @@
-// BF16 skinny GEMM / GEMV (M <= 32), row-major weights: y = x . w^T in fp32.
+// BF16 skinny GEMM / GEMV (M <= 32): y = x . w^T in fp32. Weights row-major, or tiled: the FP8
+// tile permutation of include/krq.h applied to the [N, 2K] byte matrix (16 rows x 32 bf16).
 // A step is 64 bf16 of K per weight row (two 32-element tiles, one v_mfma_f32_16x16x32_bf16 each);
 // M == 1 runs on the vector ALUs with cross-lane sums. Conventions: gemv_common.h.
 #include "gemv_common.h"
@@ -7,7 +8,7 @@ using namespace krq;
 
 namespace {
 
-template <int MT, int MODE, int ALGO, int U>
+template <int MT, int MODE, int LAYOUT, int ALGO, int U>
 __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x,
                                                   const uint8_t* __restrict__ w, int M, int64_t NO,
                                                   int64_t K, int kts, void* __restrict__ out,
@@ -38,11 +39,11 @@ __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x
     const int j = wave + min(cc, jcount - 1) * nw;
     const int64_t t0 = tbase + 2 * j;
     const int64_t t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
-    wl[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rb, t0, rowb, lane));
-    wh[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rb, t1, rowb, lane));
+    wl[u] = ld16nt(w_addr<LAYOUT>(w, rb, t0, rowb, lane));
+    wh[u] = ld16nt(w_addr<LAYOUT>(w, rb, t1, rowb, lane));
     if (P == 2) {
-      ul[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rbu, t0, rowb, lane));
-      uh[u] = ld16nt(w_addr<KRQ_W_ROWMAJOR>(w, rbu, t1, rowb, lane));
+      ul[u] = ld16nt(w_addr<LAYOUT>(w, rbu, t0, rowb, lane));
+      uh[u] = ld16nt(w_addr<LAYOUT>(w, rbu, t1, rowb, lane));
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -110,24 +111,33 @@ __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x
   epilogue<MT, MODE>(red, nw, M, NO, rb, sidx, ones, ColScales{1.0f, 1.0f}, out, aux);
 }
 
-template <int MODE>
+template <int MODE, int LAYOUT>
 void launch(int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* x,
             const uint8_t* w, int m, int64_t NO, int64_t K, int kts, void* out, void* aux) {
   const dim3 block(nw * 64);
   if (M == 1)
-    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, 2, 4>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, LAYOUT, 2, 4>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
   else if (M <= 4)
-    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, 1, 4>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, LAYOUT, 1, 4>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
   else if (M <= 16)
-    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, 1, 2>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, LAYOUT, 1, 2>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
   else
-    hipLaunchKernelGGL((k_gemv_bf16<2, MODE, 1, 2>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+    hipLaunchKernelGGL((k_gemv_bf16<2, MODE, LAYOUT, 1, 2>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+}
+
+template <int MODE>
+void launch_layout(int layout, int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* x,
+                   const uint8_t* w, int m, int64_t NO, int64_t K, int kts, void* out, void* aux) {
+  if (layout == KRQ_W_TILED)
+    launch<MODE, KRQ_W_TILED>(M, grid, nw, smem, s, x, w, m, NO, K, kts, out, aux);
+  else
+    launch<MODE, KRQ_W_ROWMAJOR>(M, grid, nw, smem, s, x, w, m, NO, K, kts, out, aux);
 }
 
 }  // namespace
 
-int krq::gemv_bf16_run(const void* x, const void* w, int64_t M, int64_t N, int64_t K, int split,
-                       int mode, void* out, void* aux, void* stream) {
+int krq::gemv_bf16_run(const void* x, const void* w, int w_layout, int64_t M, int64_t N, int64_t K,
+                       int split, int mode, void* out, void* aux, void* stream) {
   KRQ_REQUIRE(x && w && (out || mode == kOutArgmax) && (aux || mode != kOutArgmax),
               "gemv_bf16: null pointer");
   KRQ_REQUIRE(aligned16(x) && aligned16(w), "gemv_bf16: x and w must be 16-byte aligned");
@@ -138,6 +148,7 @@ int krq::gemv_bf16_run(const void* x, const void* w, int64_t M, int64_t N, int64
               "gemv_bf16: no tiling divides K_SPLIT (K=%lld split=%d; K/split must be a multiple of 32)",
               (long long)K, split);
   KRQ_REQUIRE(mode >= KRQ_OUT_BF16 && mode <= kOutArgmax, "gemv_bf16: bad mode %d", mode);
+  KRQ_REQUIRE(w_layout == KRQ_W_ROWMAJOR || w_layout == KRQ_W_TILED, "gemv_bf16: bad layout %d", w_layout);
   KRQ_REQUIRE(mode == KRQ_OUT_PARTIAL || split == 1, "gemv_bf16: split %d needs the partials output", split);
   const int64_t NO = mode == KRQ_OUT_SWIGLU ? N / 2 : N;
   KRQ_REQUIRE(NO % 16 == 0 && (mode != KRQ_OUT_SWIGLU || N % 2 == 0),
@@ -153,15 +164,15 @@ int krq::gemv_bf16_run(const void* x, const void* w, int64_t M, int64_t N, int64
   const uint8_t* wb = (const uint8_t*)w;
   const int m = static_cast<int>(M);
   hipStream_t s = (hipStream_t)stream;
-  if (mode == KRQ_OUT_BF16) launch<KRQ_OUT_BF16>(m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
-  else if (mode == KRQ_OUT_PARTIAL) launch<KRQ_OUT_PARTIAL>(m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
-  else if (mode == KRQ_OUT_SWIGLU) launch<KRQ_OUT_SWIGLU>(m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
-  else launch<kOutArgmax>(m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
+  if (mode == KRQ_OUT_BF16) launch_layout<KRQ_OUT_BF16>(w_layout, m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
+  else if (mode == KRQ_OUT_PARTIAL) launch_layout<KRQ_OUT_PARTIAL>(w_layout, m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
+  else if (mode == KRQ_OUT_SWIGLU) launch_layout<KRQ_OUT_SWIGLU>(w_layout, m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
+  else launch_layout<kOutArgmax>(w_layout, m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
   return krq_check_launch("gemv_bf16");
 }
 
-extern "C" int krq_gemv_bf16(const void* x, const void* w, int64_t M, int64_t N, int64_t K, int split,
-                             int mode, void* out, void* stream) {
+extern "C" int krq_gemv_bf16(const void* x, const void* w, int w_layout, int64_t M, int64_t N, int64_t K,
+                             int split, int mode, void* out, void* stream) {
   KRQ_REQUIRE(mode >= KRQ_OUT_BF16 && mode <= KRQ_OUT_SWIGLU, "gemv_bf16: bad mode %d", mode);
-  return gemv_bf16_run(x, w, M, N, K, split, mode, out, nullptr, stream);
+  return gemv_bf16_run(x, w, w_layout, M, N, K, split, mode, out, nullptr, stream);
 }

@@ -259,7 +259,7 @@ int gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const float* x
                  const void* w8, int w_layout, const float* w_scale, int w_per_row, int64_t M,
                  int64_t N, int64_t K, int split, int mode, int algo, void* out, void* aux,
                  void* stream);
-int gemv_bf16_run(const void* x, const void* w, int64_t M, int64_t N, int64_t K, int split, int mode,
-                  void* out, void* aux, void* stream);
+int gemv_bf16_run(const void* x, const void* w, int w_layout, int64_t M, int64_t N, int64_t K,
+                  int split, int mode, void* out, void* aux, void* stream);
 
 }  // namespace krq

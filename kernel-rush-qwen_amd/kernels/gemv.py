@@ -34,16 +34,39 @@ def _prune(configs, named_args, **kwargs):
     return ok
 
 
+def pack(w):
+    """Attach to the bf16 weight w [N, K] (N % 16 == 0, K % 32 == 0) a copy in the tiled layout
+    the kernels stream fastest (w.krq_tiled); later gemv*/lm-head calls on w read it. Returns w.
+    The reference has no counterpart: it is the load-time packing step for bf16 weights (the
+    tied lm_head), like the tiled copy fp8.quantize makes for FP8 weights."""
+    L.require_device(w)
+    if w.dtype != torch.bfloat16 or w.dim() != 2 or not w.is_contiguous():
+        raise ValueError("pack expects a contiguous bf16 [N, K] tensor")
+    N, K = w.shape
+    t = torch.empty((N * K * 2,), device=w.device, dtype=torch.uint8)
+    L.call("krq_pack_fp8", L.ptr(w), N, 2 * K, L.ptr(t), L.stream(w))
+    w.krq_tiled = t
+    return w
+
+
+def _weight(w):
+    """(pointer tensor, layout) of the bf16 weight the kernels read."""
+    t = getattr(w, "krq_tiled", None)
+    if t is not None:
+        return t, L.W_TILED
+    return (w if w.is_contiguous() else w.contiguous()), L.W_ROWMAJOR
+
+
 def _launch(x, w, split, mode):
     L.require_device(x, w)
     if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
         raise ValueError("gemv expects bf16 x and w")
     x = x.contiguous()
-    w = w if w.is_contiguous() else w.contiguous()
     M, K = x.shape
     N = w.shape[0]
     if w.shape[1] != K:
         raise ValueError(f"x [{M}, {K}] and w {tuple(w.shape)} do not match")
+    w, layout = _weight(w)
 
     def one(xc):
         m = xc.shape[0]
@@ -52,7 +75,7 @@ def _launch(x, w, split, mode):
         else:
             out = torch.empty((m, N // 2 if mode == L.OUT_SWIGLU else N), device=x.device,
                               dtype=torch.bfloat16)
-        L.call("krq_gemv_bf16", L.ptr(xc), L.ptr(w), m, N, K, split, mode, L.ptr(out), L.stream(x))
+        L.call("krq_gemv_bf16", L.ptr(xc), L.ptr(w), layout, m, N, K, split, mode, L.ptr(out), L.stream(x))
         return out
 
     if M <= MAX_ROWS:

@@ -11,6 +11,7 @@ import torch
 
 from . import _lib as L
 from . import fp8 as _fp8
+from . import gemv as _gemv
 
 
 def lm_head_argmax(h, w, return_logits=False):
@@ -36,7 +37,8 @@ def lm_head_argmax(h, w, return_logits=False):
         if h.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
             raise ValueError("the bf16 lm head expects bf16 h and w")
         V = w.shape[0]
-        hin, hsc, wk, wt, layout, wsc = h.contiguous(), None, L.LM_BF16, w.contiguous(), L.W_ROWMAJOR, None
+        wt, layout = _gemv._weight(w)
+        hin, hsc, wk, wsc = h.contiguous(), None, L.LM_BF16, None
     L.require_device(wt)
     if M > 32:
         raise ValueError(f"lm_head_argmax: M={M} > 32")

@@ -54,7 +54,7 @@ def test_invalid_arguments_fail_before_any_launch():
     rc = lib.krq_gemv_fp8(p, 2, p, None, 0, p, 1, p, 1, 2, 64, 256, 1, 0, 0, p, _null())
     assert rc == L.KRQ_EINVAL and b"x_inv" in lib.krq_last_error()
     # split > 1 without the partials output
-    rc = lib.krq_gemv_bf16(p, p, 1, 64, 256, 2, 0, p, _null())
+    rc = lib.krq_gemv_bf16(p, p, 0, 1, 64, 256, 2, 0, p, _null())
     assert rc == L.KRQ_EINVAL
     # null pointers
     rc = lib.krq_quant_fp8_rows(None, 16, 64, 64, p, None, p, _null())

@@ -450,3 +450,28 @@ def test_fused_quant_rejects_oversized_slices(dev):
     # the public entry point routes such shapes through the cast kernel instead
     y = fp8.gemv_fp8(act(16, 9728, 1).to(dev), q, 1, a=a)
     assert y.shape == (16, 64)
+
+
+def test_bf16_tiled_layout_matches_rowmajor(dev):
+    from kernels import gemv as G
+    N, K = 2048, 2560
+    w, x1, x16 = weight(N, K, 41), act(1, K, 42), act(16, K, 43)
+    wr = w.to(dev)
+    ref1, ref16 = G.gemv(x1.to(dev), wr).clone(), G.gemv(x16.to(dev), wr, 4).clone()
+    wt = G.pack(w.to(dev))
+    assert np.array_equal(wt.krq_tiled.cpu().numpy(), O.tile(u16(w).view(np.uint8).reshape(N, 2 * K)))
+    assert torch.equal(G.gemv(x1.to(dev), wt), ref1)
+    assert torch.equal(G.gemv(x16.to(dev), wt, 4), ref16)
+    assert torch.equal(G.gemv_swiglu(x16.to(dev), wt), G.gemv_swiglu(x16.to(dev), wr))
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_lmhead_bf16_tiled(dev, M):
+    from kernels import gemv as G
+    V, K = 151936, 2560
+    E, h = weight(V, K, 7), act(M, K, 100 + M)
+    Ed = E.to(dev)
+    idx_r, lg_r = lmhead.lm_head_argmax(h.to(dev), Ed, return_logits=True)
+    G.pack(Ed)
+    idx_t, lg_t = lmhead.lm_head_argmax(h.to(dev), Ed, return_logits=True)
+    assert torch.equal(idx_t, idx_r) and torch.equal(lg_t, lg_r)
