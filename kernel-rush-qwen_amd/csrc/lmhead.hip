@@ -14,16 +14,24 @@ using namespace krq;
 
 namespace {
 
-constexpr int kFoldThreads = 256;
+constexpr int kFoldThreads = 1024;
 
 __global__ __launch_bounds__(kFoldThreads) void k_argmax_fold(const Best* __restrict__ cand, int64_t nrb,
                                                               int M, int64_t* __restrict__ idx_out) {
   __shared__ Best wb[kFoldThreads / 64];
   const int m = blockIdx.x;
   Best b{-INFINITY, 0x7fffffff};
-  for (int64_t rb = threadIdx.x; rb < nrb; rb += kFoldThreads) {
-    const Best c = cand[rb * M + m];
-    if (better(c.v, c.i, b.v, b.i)) b = c;
+  // four independent loads in flight per thread per round
+  for (int64_t rb0 = threadIdx.x; rb0 < nrb; rb0 += 4 * kFoldThreads) {
+    Best c[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t rb = rb0 + (int64_t)q * kFoldThreads;
+      c[q] = rb < nrb ? cand[rb * M + m] : Best{-INFINITY, 0x7fffffff};
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (better(c[q].v, c[q].i, b.v, b.i)) b = c[q];
   }
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
