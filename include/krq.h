@@ -151,6 +151,29 @@ int krq_lmhead_argmax(const void* h, const float* h_scale, const void* w, int w_
                       void* ws, int64_t ws_bytes, int64_t* idx_out, void* stream);
 int64_t krq_lmhead_ws_bytes(int64_t M, int64_t V);
 
+/*
+ * Fused decode MLP, one launch: replaces PersistentMLP (reference engine/kernels/mlp.py:22-118,
+ * called at engine/engine.py:911-915 and :1015) for FP8 weights, M <= 32.
+ *   act[m,i]   = SwiGLU as krq_gemv_fp8 KRQ_OUT_SWIGLU of x with w_gu (e4m3 [2I,H] = [gate; up])
+ *   out[s,m,h] = fp32 partial of act . w_down^T over i in [s*I/split, (s+1)*I/split), with act
+ *                quantized per token (amax of the whole act row, the arithmetic of quant_rows)
+ *                and w_down e4m3 [H,I]; the consumer sums the partials in order s = 0..split-1.
+ * x: e4m3 [M,H] with x_scale[M] (KRQ_X_FP8), or bf16 [1,H] scaled per token in the kernel
+ * (KRQ_X_BF16_DYN, M == 1). Both weights in w_layout with per-row (or per-tensor) scales.
+ * act: bf16 [M,I] workspace (also an output: the SwiGLU activations).
+ * ctl: krq_mlp_ctl_words() uint32 words, zero before the first call; the kernel leaves them zero
+ *      again, except the last word, which it sets to 1 if a block waited too long for phase 1
+ *      (then the output is not valid). Calls sharing ctl must not overlap.
+ * programs: number of blocks (0 = one per CU); clamped to what the device holds at once.
+ * Needs H % 64 == 0, I % 16 == 0, (I/split) % 64 == 0 and M*I/split within the kernel's staging
+ * limit (raise split for large M).
+ */
+int krq_mlp_fp8(const void* x, int x_kind, const float* x_scale, const void* w_gu, int w_layout,
+                const float* gu_scale, int gu_per_row, const void* w_down, const float* down_scale,
+                int down_per_row, int64_t M, int64_t H, int64_t I, int split, void* act,
+                uint32_t* ctl, int programs, void* out, void* stream);
+int64_t krq_mlp_ctl_words(void);
+
 /* Tiled <-> row-major weight copies (byte permutations; see "tiled" above). For a bf16 [N, K]
  * matrix pass its [N, 2K] byte view (K -> 2K). */
 int krq_pack_fp8(const void* w8_rowmajor, int64_t N, int64_t K, void* w8_tiled, void* stream);

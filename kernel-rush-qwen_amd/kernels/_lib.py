@@ -36,6 +36,9 @@ EXPORTS = {
     "krq_lmhead_argmax": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp, _i64, _i64, _i64, _vp, _vp, _i64,
                                  _vp, _vp]),
     "krq_lmhead_ws_bytes": (_i64, [_i64, _i64]),
+    "krq_mlp_fp8": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64,
+                           _i32, _vp, _vp, _i32, _vp, _vp]),
+    "krq_mlp_ctl_words": (_i64, []),
     "krq_pack_fp8": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "krq_unpack_fp8": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "krq_version": (ctypes.c_char_p, []),

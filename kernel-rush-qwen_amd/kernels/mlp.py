@@ -1,0 +1,72 @@
+"""Persistent fused decode MLP: act = SwiGLU(h @ [gate; up]^T), then the fp32 split-K partials of
+the down projection, in one launch of the HIP kernel k_mlp_fp8 (libkrq.so, krq_mlp_fp8).
+
+Drop-in for the reference's engine/kernels/mlp.py: PersistentMLP(M, H, I, device, programs,
+split=4, bn=16, bn2=16, chunk=512) and __call__(h, w_gu, w_down) -> fp32 [split, M, H], summed
+in split order by the consumer (engine/engine.py:911-915, :1015; ops.py:29-39). Weights are the
+FP8Weight tuples of fp8.quantize (per-channel e4m3) and activations are scaled per token, as
+linear_fp8 / quant_rows do: at M == 1 the kernel scales h itself, at larger M fp8.quant_rows runs
+first; the SwiGLU activations are re-quantized per token inside the kernel once all of them exist.
+
+`programs` is the number of blocks, as in the reference; the library clamps it to the blocks the
+device holds at once (so spin-waits cannot deadlock), and `programs=None` takes one per CU. The
+control words are zeroed here once and left zeroed by every launch.
+"""
+
+import torch
+
+from . import _lib as L
+from . import fp8 as _fp8
+
+
+class PersistentMLP:
+    """Workspace for one M. Call with (h [M, H] bf16, w_gu [2I, H], w_down [H, I]) as FP8Weight."""
+
+    def __init__(self, M, H, I, device, programs=None, split=4, bn=16, bn2=16, chunk=512):
+        # the reference's shape contract (engine/kernels/mlp.py:100-103)
+        assert I % chunk == 0 and chunk % bn == 0 and I % split == 0
+        assert (I // split) % 64 == 0 and H % bn2 == 0
+        if bn != 16 or bn2 != 16:
+            raise ValueError("the HIP kernel's row blocks are 16 columns (bn = bn2 = 16)")
+        if not 1 <= M <= 32:
+            raise ValueError(f"PersistentMLP: M={M} outside 1..32")
+        self.M, self.H, self.I, self.G = M, H, I, programs
+        self.split, self.bn, self.bn2, self.chunk = split, bn, bn2, chunk
+        self.ctl = torch.zeros((int(L.lib().krq_mlp_ctl_words()),), device=device, dtype=torch.int32)
+        self.act = None   # bf16 [M, I] SwiGLU activations of the last call
+
+    def __call__(self, h, w_gu, w_down):
+        if not (isinstance(w_gu, tuple) and isinstance(w_down, tuple)):
+            raise ValueError("PersistentMLP: the HIP kernel takes FP8 weights (fp8.quantize)")
+        H, I, S = self.H, self.I, self.split
+        gu, lay_gu, gs, gshape = _fp8._weight_operand(w_gu)
+        dn, lay_dn, ds, dshape = _fp8._weight_operand(w_down)
+        if tuple(gshape) != (2 * I, H) or tuple(dshape) != (H, I):
+            raise ValueError(f"PersistentMLP: weights {tuple(gshape)} / {tuple(dshape)} do not match "
+                             f"H={H}, I={I}")
+        if lay_gu != lay_dn:
+            raise ValueError("PersistentMLP: gate/up and down weights must share a layout")
+        g_pr = 1 if gs.numel() == 2 * I else 0
+        d_pr = 1 if ds.numel() == H else 0
+        if gs.numel() not in (1, 2 * I) or ds.numel() not in (1, H):
+            raise ValueError("PersistentMLP: weight scales must be per tensor or per row")
+        h2 = _fp8._rows(h)
+        M = h2.shape[0]
+        if M != self.M:
+            raise ValueError(f"PersistentMLP built for M={self.M}, called with M={M}")
+        if M == 1:
+            xin, kind, xs = h2, L.X_BF16_DYN, None
+        else:
+            xin, xs = _fp8.quant_rows(h2)
+            kind, xs = L.X_FP8, xs.reshape(-1)
+        act = torch.empty((M, I), device=h.device, dtype=torch.bfloat16)
+        out = torch.empty((S, M, H), device=h.device, dtype=torch.float32)
+        L.call("krq_mlp_fp8", L.ptr(xin), kind, L.ptr(xs), L.ptr(gu), lay_gu, L.ptr(gs), g_pr,
+               L.ptr(dn), L.ptr(ds), d_pr, M, H, I, S, L.ptr(act), L.ptr(self.ctl),
+               int(self.G or 0), L.ptr(out), L.stream(h))
+        self.act = act
+        return out
+
+    def failed(self):
+        """True if a launch flagged a phase-1 wait that timed out (synchronizes the device)."""
+        return bool(self.ctl[-1].item())

@@ -23,6 +23,8 @@ How each function is pinned (tests/test_oracle.py; tests/golden/):
                   codes; against torch._scaled_mm (CPU) within fp32-accumulation tolerance.
   bf16_matmul     against torch float64 matmul.
   swiglu          against torch.nn.functional.silu in fp32 (at most 1 bf16 ulp, rare).
+  mlp_fp8         composition of the pinned functions above; its split partials are checked to
+                  sum to the unsplit product, and act to equal swiglu of the gate/up product.
   argmax_lowest   against torch.argmax with planted ties.
   tile / untile   against an element-by-element loop over the layout definition.
 """
@@ -204,6 +206,25 @@ def argmax_lowest(logits):
     """torch.argmax over the last axis: the first (lowest) index of the maximum
     (engine/engine.py:1022; tie rule of engine/kernels/mega.py:412-419)."""
     return np.argmax(np.asarray(logits), axis=-1)
+
+
+def mlp_fp8(h_u16, wgu8, gs, wd8, ds, split):
+    """Fused decode MLP, engine/kernels/mlp.py:30-85 (phase 1 SwiGLU of the gate/up GEMV, phase 2
+    the down GEMV as fp32 split-K partials), with the FP8 quantization of linear_fp8 / quant_rows
+    applied to both GEMVs: per-token h, per-token act (amax over the whole act row).
+    wgu8 [2I, H] and wd8 [H, I] e4m3 codes with per-row (or per-tensor) scales gs, ds.
+    Returns (act u16 [M, I], partials float64 [split, M, H]); the partials sum to the unsplit
+    product of the same quantized act."""
+    I = wgu8.shape[0] // 2
+    x8, xs = quant_rows(h_u16)
+    gs = np.broadcast_to(np.asarray(gs, dtype=np.float32).reshape(-1), (2 * I,))
+    _, full = fp8_matmul(x8, xs, wgu8, gs)
+    act = swiglu(full[:, :I].astype(np.float32), full[:, I:].astype(np.float32))
+    a8, as_ = quant_rows(act)
+    ks = I // split
+    parts = [fp8_matmul(a8[:, s * ks:(s + 1) * ks], as_, wd8[:, s * ks:(s + 1) * ks], ds)[1]
+             for s in range(split)]
+    return act, np.stack(parts)
 
 
 # ---------------------------------------------------------------------------------------------

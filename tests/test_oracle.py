@@ -232,6 +232,49 @@ def test_swiglu_epilogue_vs_torch_silu():
     assert np.all(np.abs(got - ref)[diff] <= np.abs(ref[diff]) * 2 ** -6)
 
 
+def test_mlp_fp8_composition():
+    """mlp_fp8 against an independent torch evaluation of the same steps (torch casts, F.silu,
+    float64 products of dequantized values), and the split invariant: partials sum to the
+    unsplit product of the quantized act."""
+    g = torch.Generator().manual_seed(12)
+    M, H, I, S = 3, 256, 512, 4
+    h = torch.randn(M, H, generator=g).to(torch.bfloat16)
+    wgu = (torch.randn(2 * I, H, generator=g) * 0.02).to(torch.bfloat16)
+    wd = (torch.randn(H, I, generator=g) * 0.02).to(torch.bfloat16)
+    gu8, gs = O.quantize(bf16_bits(wgu), scalar_div="cpu")
+    d8, ds = O.quantize(bf16_bits(wd), scalar_div="cpu")
+    act, parts = O.mlp_fp8(bf16_bits(h), gu8, gs, d8, ds, S)
+    assert act.shape == (M, I) and parts.shape == (S, M, H)
+
+    def tq(x):   # per-token quantization in torch: (dequantized values, scale)
+        amax = x.float().abs().amax(-1, keepdim=True).clamp_min(1e-6)
+        x8 = (x.float() * (448.0 / amax)).clamp(-448, 448).to(torch.float8_e4m3fn)
+        return x8.double(), (amax / 448.0).double()
+
+    def deq(w8, s):
+        return torch.from_numpy(w8).view(torch.float8_e4m3fn).double() * torch.from_numpy(s).double()[:, None]
+
+    hx, hs = tq(h)
+    full = (hx @ deq(gu8, gs).T) * hs
+    gg = full[:, :I].float().to(torch.bfloat16).float()
+    uu = full[:, I:].float().to(torch.bfloat16).float()
+    act_t = (F.silu(gg).to(torch.bfloat16).float() * uu).to(torch.bfloat16)
+    got = O.bf16_to_f32(act)
+    ref = act_t.float().numpy()
+    assert np.mean(got != ref) < 1e-2
+    assert np.abs(got - ref).max() <= 2 ** -6 * np.abs(ref).max()
+    ax, asc = tq(act_t)
+    ref_out = ((ax @ deq(d8, ds).T) * asc).numpy()
+    assert np.abs(parts.sum(0) - ref_out).max() <= 2e-2 * np.abs(ref_out).max()
+    a8, as_ = O.quant_rows(act)
+    _, unsplit = O.fp8_matmul(a8, as_, d8, ds)
+    assert np.allclose(parts.sum(0), unsplit, rtol=1e-12, atol=1e-12 * np.abs(unsplit).max())
+    # gate and up swapped is a different function
+    swapped = np.concatenate([gu8[I:], gu8[:I]])
+    act_sw, _ = O.mlp_fp8(bf16_bits(h), swapped, np.concatenate([gs[I:], gs[:I]]), d8, ds, S)
+    assert not np.allclose(O.bf16_to_f32(act_sw), got, rtol=1e-2)
+
+
 def test_argmax_lowest_index():
     v = np.float32([[1, 5, 5, 2], [7, 7, 7, 7], [-np.inf, -1, -1, -3]])
     assert O.argmax_lowest(v).tolist() == [1, 0, 1]
