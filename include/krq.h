@@ -113,8 +113,8 @@ int krq_quant_rows(const void* x_bf16, int64_t M, int64_t K, void* x8, float* xs
  * mode KRQ_OUT_BF16 -> bf16 [M,N] (split 1); KRQ_OUT_PARTIAL -> fp32 [split,M,N] of the K-slices
  * [s*K/split, (s+1)*K/split); KRQ_OUT_SWIGLU -> bf16 [M,I] (split 1).
  * Needs N % 16 == 0, K % split == 0 and (K/split) % 64 == 0; the in-kernel kinds need the
- * activation slice (K for DYN, M*K/split for STATIC) to fit 4096 elements per 64-thread wave
- * of at most 8 waves.
+ * activation slice to fit a block of at most 8 64-thread waves: K <= 16384 for DYN (2048
+ * elements per wave), M*K/split <= 32768 for STATIC (4096 per wave).
  * algo: 0 = automatic, 1 = matrix-core (MFMA) kernel, 2 = vector-ALU kernel (M == 1 only).
  */
 int krq_gemv_fp8(const void* x, int x_kind, const float* x_scale, const float* x_inv, int x_per_row,

@@ -35,8 +35,12 @@ __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x
   float s0 = 0.f, s1 = 0.f, q0 = 0.f, q1 = 0.f;
   // a ring of U step slots: consume slot u (step cc), then refill it with step cc + U
   uint4 wl[U], wh[U], ul[U], uh[U], xl[U][MT], xh[U][MT];
+  // Every slot load is issued unconditionally (a branch around a load makes the compiler drain all
+  // outstanding loads at the join): a slot past this wave's last step reloads that step (already
+  // in flight or cached) and is masked where consumed; rows m >= M read row M - 1, whose products
+  // land in accumulator rows the epilogue never writes.
   auto load_slot = [&](int u, int cc) {
-    const int j = wave + min(cc, jcount - 1) * nw;
+    const int j = jcount > 0 ? wave + min(cc, jcount - 1) * nw : 0;
     const int64_t t0 = tbase + 2 * j;
     const int64_t t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
     wl[u] = ld16nt(w_addr<LAYOUT>(w, rb, t0, rowb, lane));
@@ -47,19 +51,14 @@ __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int m = ALGO == 2 ? 0 : mt * 16 + r;
-      uint4 lo = zero4(), hi = zero4();
-      if (m < M) {
-        const uint8_t* xr = x + (int64_t)m * rowb + g * 16;
-        lo = ld16(xr + t0 * 64);
-        hi = ld16(xr + t1 * 64);
-      }
-      xl[u][mt] = lo;
-      xh[u][mt] = hi;
+      const int m = ALGO == 2 ? 0 : min(mt * 16 + r, M - 1);
+      const uint8_t* xr = x + (int64_t)m * rowb + g * 16;
+      xl[u][mt] = ld16(xr + t0 * 64);
+      xh[u][mt] = ld16(xr + t1 * 64);
     }
   };
   auto consume_slot = [&](int u, int cc) {
-    const int j = wave + min(cc, jcount - 1) * nw;
+    const int j = jcount > 0 ? wave + min(cc, jcount - 1) * nw : 0;
     const bool ok = cc < jcount, hi = ok && (2 * j + 1 < kts);
     const uint4 bl = sel4(ok, wl[u]), bh = sel4(hi, wh[u]);
     if (ALGO == 2) {
@@ -85,18 +84,21 @@ __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x
       }
     }
   };
-  if (jcount > 0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) load_slot(u, u);
-  }
+  for (int u = 0; u < U; ++u) load_slot(u, u);
   __builtin_amdgcn_sched_barrier(0);
-  for (int base = 0; base < jcount; base += U) {
+  // the last batch is peeled off (consume only), so no load sits behind a branch and the first
+  // batch's loads stay ahead of everything else
+  int base = 0;
+  for (; base + U < jcount; base += U) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       consume_slot(u, base + u);
-      if (base + u + U < jcount) load_slot(u, base + u + U);
+      load_slot(u, base + u + U);
     }
   }
+#pragma unroll
+  for (int u = 0; u < U; ++u) consume_slot(u, base + u);
   if (ALGO == 2) {
     float a = s0 + s1, au = q0 + q1;
     a += __shfl_xor(a, 16, kWave);

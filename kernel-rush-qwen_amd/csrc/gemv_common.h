@@ -79,6 +79,13 @@ KRQ_DEV uint4 sel4(bool keep, uint4 a) {
 
 KRQ_DEV uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
 
+// The same address, held in vector registers the compiler cannot prove uniform.
+KRQ_DEV const uint8_t* vgpr_ptr(const uint8_t* p) {
+  uint64_t v = reinterpret_cast<uint64_t>(p);
+  asm volatile("" : "+v"(v));
+  return reinterpret_cast<const uint8_t*>(v);
+}
+
 // Byte address of the 16 bytes lane `lane` reads from weight tile t of row block rb.
 // row_bytes = bytes per weight row (K for FP8, 2K for BF16); tiles are 64 bytes wide.
 template <int LAYOUT>
@@ -165,7 +172,8 @@ KRQ_DEV float dot8_bf16(uint4 a, uint4 b, float acc) {
 // fp32 partials [split, M, NO], or SwiGLU bf16 [M, NO].
 // ---------------------------------------------------------------------------------------------
 // Weight scales of the columns this thread writes in the epilogue (thread t writes columns
-// 16*rb + t % 16), loaded at kernel start so their latency hides under the weight stream.
+// 16*rb + t % 16), loaded at kernel start so their latency hides under the weight stream
+// (wsc must not be null).
 struct ColScales {
   float g, u;
 };
@@ -173,11 +181,9 @@ struct ColScales {
 template <int MODE>
 KRQ_DEV ColScales load_col_scales(const float* __restrict__ wsc, int w_per_row, int64_t NO, int64_t rb) {
   ColScales c{1.0f, 1.0f};
-  if (wsc) {
-    const int64_t n = rb * 16 + (threadIdx.x & 15);
-    c.g = wsc[w_per_row ? n : 0];
-    if (MODE == KRQ_OUT_SWIGLU) c.u = wsc[w_per_row ? NO + n : 0];
-  }
+  const int64_t n = rb * 16 + (threadIdx.x & 15);
+  c.g = wsc[w_per_row ? n : 0];
+  if (MODE == KRQ_OUT_SWIGLU) c.u = wsc[w_per_row ? NO + n : 0];
   return c;
 }
 

@@ -33,7 +33,11 @@ int plan_waves(int nsteps, int P, int M) {
 
 namespace {
 
-constexpr int kXChunks = 8;     // 16-byte activation chunks per thread in the fused prologue
+// 16-byte activation chunks per thread in the fused prologues: every chunk load is issued (see
+// the kernel), so the one-row prologue, which reads the whole row for its amax, keeps the count
+// small and takes more waves for long rows instead
+constexpr int kXChunks = 8;
+constexpr int kXChunksDyn = 4;
 constexpr int kMaxThreads = 512;
 
 template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U>
@@ -59,29 +63,38 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(
   const ColScales cs = load_col_scales<MODE>(wsc, w_per_row, NO, rb);
 
   // ---- fused activation prologue, part 1: activation loads ahead of the weight stream ----
+  // Every load of the prologue and of the step ring is issued unconditionally, at a clamped (valid)
+  // address where it is not needed: a branch around a load makes the compiler's wait counts
+  // conservative (a full drain, vmcnt(0)) at the join, which serializes the weight stream.
   uint4 xv[kXChunks];
   if (XK == KRQ_X_BF16_DYN) {
 #pragma unroll
-    for (int c = 0; c < kXChunks; ++c) {
+    for (int c = 0; c < kXChunksDyn; ++c) {
       const int64_t e = 8 * (int64_t)(threadIdx.x + c * blockDim.x);
-      xv[c] = e < K ? ld16(x + 2 * e) : zero4();
+      xv[c] = ld16(x + 2 * min(e, K - 8));  // chunks past K repeat the last one (same amax)
     }
   } else if (XK == KRQ_X_BF16_STATIC) {
     const int cpr = ks >> 3;  // chunks per row of the slice
 #pragma unroll
     for (int c = 0; c < kXChunks; ++c) {
       const int idx = threadIdx.x + c * blockDim.x, m = idx / cpr;
-      xv[c] = m < M ? ld16(x + 2 * ((int64_t)m * K + k0 + 8 * (idx - m * cpr))) : zero4();
+      xv[c] = ld16(x + 2 * ((int64_t)min(m, M - 1) * K + k0 + 8 * (idx - m * cpr)));
     }
   }
 
   // scale of this thread's activation row, read now so its latency hides under the weight stream
-  const float xs_reg = (XK != KRQ_X_BF16_DYN && threadIdx.x < (unsigned)M) ? xsc[x_per_row ? threadIdx.x : 0] : 1.0f;
+  // (every thread loads and stores it, threads t and t + 32 the same value, so the load is not
+  // sunk into a branch after the weight loads)
+  const int xrow = min((int)(threadIdx.x & 31), M - 1);
+  const float xs_reg = XK != KRQ_X_BF16_DYN ? xsc[x_per_row ? xrow : 0] : 1.0f;
 
   // ---- weight (and, for e4m3 activations, A operand) loads: a ring of U step slots ----
   uint4 wl[U], wh[U], ul[U], uh[U], xl[U][MT], xh[U][MT];
+  // A slot past this wave's last step reloads that step (an address already in flight or cached,
+  // so no extra HBM traffic) and is masked where consumed. Rows m >= M read row M - 1: their
+  // products land in accumulator rows the epilogue never writes.
   auto load_slot = [&](int u, int cc) {
-    const int j = wave + min(cc, jcount - 1) * nw;
+    const int j = jcount > 0 ? wave + min(cc, jcount - 1) * nw : 0;
     const int64_t t0 = tbase + 2 * j;
     const int64_t t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
     wl[u] = ld16nt(w_addr<LAYOUT>(w8, rb, t0, K, lane));
@@ -93,31 +106,24 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(
     if (!FUSED) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const int m = ALGO == 2 ? 0 : mt * 16 + r;
-        uint4 lo = zero4(), hi = zero4();
-        if (m < M) {
-          const uint8_t* xr = x + (int64_t)m * K + g * 16;
-          lo = ld16(xr + t0 * 64);
-          hi = ld16(xr + t1 * 64);
-        }
-        xl[u][mt] = lo;
-        xh[u][mt] = hi;
+        const int m = ALGO == 2 ? 0 : min(mt * 16 + r, M - 1);
+        const uint8_t* xr = x + (int64_t)m * K + g * 16;
+        xl[u][mt] = ld16(xr + t0 * 64);
+        xh[u][mt] = ld16(xr + t1 * 64);
       }
     }
   };
-  if (jcount > 0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) load_slot(u, u);
-  }
+  for (int u = 0; u < U; ++u) load_slot(u, u);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- fused activation prologue, part 2: scale, quantize the slice into LDS ----
   if (XK == KRQ_X_FP8) {
-    if (threadIdx.x < (unsigned)M) xs_l[threadIdx.x] = xs_reg;
+    xs_l[threadIdx.x & 31] = xs_reg;
   } else if (XK == KRQ_X_BF16_DYN) {
     float am = 0.0f;
 #pragma unroll
-    for (int c = 0; c < kXChunks; ++c) am = absmax8(xv[c], am);
+    for (int c = 0; c < kXChunksDyn; ++c) am = absmax8(xv[c], am);
     am = wave_max(am);
     if (lane == 0) amax_w[wave] = am;
     __syncthreads();
@@ -127,7 +133,7 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(
     const float inv = inv_from_amax(a);
     if (threadIdx.x == 0) xs_l[0] = scale_from_amax(a);
 #pragma unroll
-    for (int c = 0; c < kXChunks; ++c) {
+    for (int c = 0; c < kXChunksDyn; ++c) {
       const int64_t e = 8 * (int64_t)(threadIdx.x + c * blockDim.x);
       if (e >= k0 && e < k0 + ks) *reinterpret_cast<uint2*>(xq + (e - k0)) = quant8(xv[c], inv);
     }
@@ -140,7 +146,7 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(
         *reinterpret_cast<uint2*>(xq + (int64_t)m * ks + 8 * (idx - m * cpr)) =
             quant8(xv[c], xinv[x_per_row ? m : 0]);
     }
-    if (threadIdx.x < (unsigned)M) xs_l[threadIdx.x] = xs_reg;
+    xs_l[threadIdx.x & 31] = xs_reg;
   }
   if (FUSED) __syncthreads();
 
@@ -153,20 +159,16 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(
   }
   float s0 = 0.f, s1 = 0.f, q0 = 0.f, q1 = 0.f;  // vector-ALU partial sums
   auto consume_slot = [&](int u, int cc) {
-    const int j = wave + min(cc, jcount - 1) * nw;
+    const int j = jcount > 0 ? wave + min(cc, jcount - 1) * nw : 0;
     const bool ok = cc < jcount, hi = ok && (2 * j + 1 < kts);
     if (FUSED) {
+      // the quantized slice ends at ks: the high tile of an odd last step is zero (not stale LDS)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const int m = ALGO == 2 ? 0 : mt * 16 + r;
-        uint4 lo = zero4(), hh = zero4();
-        if (m < M) {
-          const uint8_t* xr = xq + (int64_t)m * ks + g * 16;
-          lo = *reinterpret_cast<const uint4*>(xr + (2 * j) * 64);
-          if (2 * j + 1 < kts) hh = *reinterpret_cast<const uint4*>(xr + (2 * j + 1) * 64);
-        }
-        xl[u][mt] = lo;
-        xh[u][mt] = hh;
+        const int m = ALGO == 2 ? 0 : min(mt * 16 + r, M - 1);
+        const uint8_t* xr = xq + (int64_t)m * ks + g * 16;
+        xl[u][mt] = *reinterpret_cast<const uint4*>(xr + (2 * j) * 64);
+        xh[u][mt] = sel4(2 * j + 1 < kts, *reinterpret_cast<const uint4*>(xr + min(2 * j + 1, kts - 1) * 64));
       }
     }
     const uint4 bl = sel4(ok, wl[u]), bh = sel4(hi, wh[u]);
@@ -194,13 +196,18 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(
       }
     }
   };
-  for (int base = 0; base < jcount; base += U) {
+  // the last batch is peeled off (consume only), so no load sits behind a branch and the first
+  // batch's loads stay ahead of everything else
+  int base = 0;
+  for (; base + U < jcount; base += U) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       consume_slot(u, base + u);
-      if (base + u + U < jcount) load_slot(u, base + u + U);
+      load_slot(u, base + u + U);
     }
   }
+#pragma unroll
+  for (int u = 0; u < U; ++u) consume_slot(u, base + u);
   if (ALGO == 2) {
     // the four lanes of row r (g = 0..3) hold partial sums of disjoint k: add them; lanes 0..15
     // then carry columns 16*rb + lane in MFMA slot (mt 0, i 0), i.e. output row m = 0
@@ -288,8 +295,9 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   int64_t xchunks = 0;
   if (x_kind == KRQ_X_BF16_DYN) xchunks = (K + 7) / 8;
   if (x_kind == KRQ_X_BF16_STATIC) xchunks = M * (ks / 8);
-  while ((int64_t)nw * 64 * kXChunks < xchunks && nw < kMaxThreads / 64) ++nw;
-  KRQ_REQUIRE((int64_t)nw * 64 * kXChunks >= xchunks,
+  const int xc = x_kind == KRQ_X_BF16_DYN ? kXChunksDyn : kXChunks;
+  while ((int64_t)nw * 64 * xc < xchunks && nw < kMaxThreads / 64) ++nw;
+  KRQ_REQUIRE((int64_t)nw * 64 * xc >= xchunks,
               "gemv_fp8: activation slice of %lld elements too large for in-kernel quantization",
               (long long)(xchunks * 8));
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) +

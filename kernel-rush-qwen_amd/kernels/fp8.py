@@ -189,7 +189,8 @@ def _weight_operand(q):
     return w8, L.W_ROWMAJOR, ws, w8.shape
 
 
-FUSED_MAX_ELEMS = 8 * 64 * 64  # activation slice the GEMV can quantize in its prologue
+FUSED_MAX_ELEMS = 8 * 64 * 64  # activation slice the GEMV can quantize in its prologue (static scale)
+FUSED_MAX_ELEMS_DYN = 8 * 64 * 32  # row the GEMV can scale per token itself (M == 1)
 
 
 def _gemv(xin, x_kind, x_scale, x_inv, M, q, split, mode, algo, out):
@@ -237,7 +238,7 @@ def _fits_fused(x, split, a):
     if x.dtype != torch.bfloat16 or M > DECODE_MAX_ROWS or K % 64:
         return False
     if a is None:
-        return M == 1 and K <= FUSED_MAX_ELEMS
+        return M == 1 and K <= FUSED_MAX_ELEMS_DYN
     return M * (K // split) <= FUSED_MAX_ELEMS
 
 
