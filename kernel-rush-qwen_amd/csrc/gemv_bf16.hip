@@ -159,7 +159,7 @@ int krq::gemv_bf16_run(const void* x, const void* w, int w_layout, int64_t M, in
   const int kts = static_cast<int>(K / split / 32);
   const int P = mode == KRQ_OUT_SWIGLU ? 2 : 1;
   const int MT = M <= 16 ? 1 : 2;
-  const int nw = plan_waves((kts + 1) / 2, P, static_cast<int>(M));
+  const int nw = plan_waves((kts + 1) / 2, P, M <= 4 ? 4 : 2);  // U of the variant launch() picks
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float);
   const dim3 grid(static_cast<unsigned>(NO / 16), static_cast<unsigned>(split));
   const uint8_t* xb = (const uint8_t*)x;

@@ -18,16 +18,18 @@
 using namespace krq;
 
 namespace krq {
-int plan_waves(int nsteps, int P, int M) {
+int plan_waves(int nsteps, int P, int U) {
   static const int env = [] {
     const char* s = getenv("KRQ_GEMV_WAVES");
     return s ? atoi(s) : 0;
   }();
   if (env >= 1 && env <= 8) return env;
   if (nsteps < 2) return 1;
-  // measured on MI355X at the Qwen3-4B shapes: two waves for one-row (U = 4) blocks and for the
-  // two-matrix SwiGLU block, four for the multi-row single-matrix block
-  return (M > 4 && P == 1 && nsteps >= 4) ? 4 : 2;
+  // measured on MI355X at the Qwen3-4B shapes: a single-matrix block takes just enough waves for
+  // all of its steps to be in flight at once (one memory round trip), up to 4; past that, and for
+  // the two-matrix SwiGLU block, two waves
+  const int w = (nsteps + U - 1) / U;
+  return (P == 1 && w <= 4) ? w : 2;
 }
 }  // namespace krq
 
@@ -290,7 +292,9 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   const int ks = kts * 64;
   const int P = mode == KRQ_OUT_SWIGLU ? 2 : 1;
   const int MT = (algo == 2 || M <= 16) ? 1 : 2;
-  int nw = plan_waves((kts + 1) / 2, P, static_cast<int>(M));
+  // step slots per wave of the variant launch() picks
+  const int U = (algo == 2 || M <= 4) ? 4 : 2;
+  int nw = plan_waves((kts + 1) / 2, P, U);
   // fused prologues hold at most kXChunks 16-byte chunks per thread
   int64_t xchunks = 0;
   if (x_kind == KRQ_X_BF16_DYN) xchunks = (K + 7) / 8;
