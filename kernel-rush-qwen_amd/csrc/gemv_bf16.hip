@@ -4,21 +4,25 @@
 // M == 1 runs on the vector ALUs with cross-lane sums. Conventions: gemv_common.h.
 #include "gemv_common.h"
 
+#include <stdlib.h>
+
 using namespace krq;
 
 namespace {
 
-template <int MT, int MODE, int LAYOUT, int ALGO, int U>
+// PB = 2: two adjacent row blocks per block sharing the activation loads (as in gemv_fp8.hip).
+template <int MT, int MODE, int LAYOUT, int ALGO, int U, int PB>
 __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x,
                                                   const uint8_t* __restrict__ w, int M, int64_t NO,
                                                   int64_t K, int kts, void* __restrict__ out,
                                                   void* __restrict__ aux) {
   extern __shared__ float red[];
   __shared__ float ones[32];
-  constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : 1;
+  static_assert(PB == 1 || (MODE != KRQ_OUT_SWIGLU && ALGO != 2), "paired row blocks: MFMA, no SwiGLU");
+  constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : PB;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int64_t rb = blockIdx.x, rbu = rb + (NO >> 4);
+  const int64_t rb = (int64_t)blockIdx.x * PB, rbu = MODE == KRQ_OUT_SWIGLU ? rb + (NO >> 4) : rb + 1;
   const int sidx = blockIdx.y;
   const int nsteps = (kts + 1) >> 1;
   const int64_t tbase = (int64_t)sidx * kts;
@@ -110,30 +114,36 @@ __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x
   }
   stash<MT, P>(red, wave, lane, acc, accu);
   __syncthreads();
-  epilogue<MT, MODE>(red, nw, M, NO, rb, sidx, ones, ColScales{1.0f, 1.0f}, out, aux);
+  epilogue<MT, MODE, P>(red, 0, nw, M, NO, rb, sidx, ones, ColScales{1.0f, 1.0f}, out, aux);
+  if (PB == 2) epilogue<MT, MODE, P>(red, 1, nw, M, NO, rbu, sidx, ones, ColScales{1.0f, 1.0f}, out, aux);
 }
 
 template <int MODE, int LAYOUT>
-void launch(int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* x,
+void launch(int M, int pb, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* x,
             const uint8_t* w, int m, int64_t NO, int64_t K, int kts, void* out, void* aux) {
   const dim3 block(nw * 64);
+  constexpr int PB2 = MODE == KRQ_OUT_SWIGLU ? 1 : 2;
   if (M == 1)
-    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, LAYOUT, 2, 4>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, LAYOUT, 2, 4, 1>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
   else if (M <= 4)
-    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, LAYOUT, 1, 4>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, LAYOUT, 1, 4, 1>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+  else if (M <= 16 && pb == 2)
+    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, LAYOUT, 1, 2, PB2>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
   else if (M <= 16)
-    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, LAYOUT, 1, 2>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, LAYOUT, 1, 2, 1>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+  else if (pb == 2)
+    hipLaunchKernelGGL((k_gemv_bf16<2, MODE, LAYOUT, 1, 2, PB2>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
   else
-    hipLaunchKernelGGL((k_gemv_bf16<2, MODE, LAYOUT, 1, 2>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+    hipLaunchKernelGGL((k_gemv_bf16<2, MODE, LAYOUT, 1, 2, 1>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
 }
 
 template <int MODE>
-void launch_layout(int layout, int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* x,
+void launch_layout(int layout, int M, int pb, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* x,
                    const uint8_t* w, int m, int64_t NO, int64_t K, int kts, void* out, void* aux) {
   if (layout == KRQ_W_TILED)
-    launch<MODE, KRQ_W_TILED>(M, grid, nw, smem, s, x, w, m, NO, K, kts, out, aux);
+    launch<MODE, KRQ_W_TILED>(M, pb, grid, nw, smem, s, x, w, m, NO, K, kts, out, aux);
   else
-    launch<MODE, KRQ_W_ROWMAJOR>(M, grid, nw, smem, s, x, w, m, NO, K, kts, out, aux);
+    launch<MODE, KRQ_W_ROWMAJOR>(M, pb, grid, nw, smem, s, x, w, m, NO, K, kts, out, aux);
 }
 
 }  // namespace
@@ -157,19 +167,26 @@ int krq::gemv_bf16_run(const void* x, const void* w, int w_layout, int64_t M, in
               "gemv_bf16: no tiling divides N=%lld (output columns must be a multiple of 16)", (long long)N);
   KRQ_REQUIRE(NO / 16 <= 0x7fffffff && split <= 65535, "gemv_bf16: grid too large");
   const int kts = static_cast<int>(K / split / 32);
-  const int P = mode == KRQ_OUT_SWIGLU ? 2 : 1;
+  static const bool pair_ok = [] {
+    const char* e = getenv("KRQ_GEMV_PAIR");
+    return !(e && atoi(e) == 0);
+  }();
+  // paired only where halving the blocks still leaves thousands (the lm_head), as in gemv_fp8.hip
+  const int pb = (pair_ok && mode != KRQ_OUT_SWIGLU && M > 4 && (NO / 16) % 2 == 0 &&
+                  (NO / 16) * split >= 4096) ? 2 : 1;
+  const int P = mode == KRQ_OUT_SWIGLU ? 2 : pb;
   const int MT = M <= 16 ? 1 : 2;
   const int nw = plan_waves((kts + 1) / 2, P, M <= 4 ? 4 : 2);  // U of the variant launch() picks
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float);
-  const dim3 grid(static_cast<unsigned>(NO / 16), static_cast<unsigned>(split));
+  const dim3 grid(static_cast<unsigned>(NO / 16 / pb), static_cast<unsigned>(split));
   const uint8_t* xb = (const uint8_t*)x;
   const uint8_t* wb = (const uint8_t*)w;
   const int m = static_cast<int>(M);
   hipStream_t s = (hipStream_t)stream;
-  if (mode == KRQ_OUT_BF16) launch_layout<KRQ_OUT_BF16>(w_layout, m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
-  else if (mode == KRQ_OUT_PARTIAL) launch_layout<KRQ_OUT_PARTIAL>(w_layout, m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
-  else if (mode == KRQ_OUT_SWIGLU) launch_layout<KRQ_OUT_SWIGLU>(w_layout, m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
-  else launch_layout<kOutArgmax>(w_layout, m, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
+  if (mode == KRQ_OUT_BF16) launch_layout<KRQ_OUT_BF16>(w_layout, m, pb, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
+  else if (mode == KRQ_OUT_PARTIAL) launch_layout<KRQ_OUT_PARTIAL>(w_layout, m, pb, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
+  else if (mode == KRQ_OUT_SWIGLU) launch_layout<KRQ_OUT_SWIGLU>(w_layout, m, pb, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
+  else launch_layout<kOutArgmax>(w_layout, m, pb, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
   return krq_check_launch("gemv_bf16");
 }
 

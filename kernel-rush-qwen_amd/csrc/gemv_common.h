@@ -178,19 +178,22 @@ struct ColScales {
   float g, u;
 };
 
-template <int MODE>
+// g: row block rb; u: its second matrix, the up half (SwiGLU) or row block rb + 1 (paired blocks)
+template <int MODE, int PB>
 KRQ_DEV ColScales load_col_scales(const float* __restrict__ wsc, int w_per_row, int64_t NO, int64_t rb) {
   ColScales c{1.0f, 1.0f};
   const int64_t n = rb * 16 + (threadIdx.x & 15);
   c.g = wsc[w_per_row ? n : 0];
   if (MODE == KRQ_OUT_SWIGLU) c.u = wsc[w_per_row ? NO + n : 0];
+  else if (PB == 2) c.u = wsc[w_per_row ? n + 16 : 0];
   return c;
 }
 
-template <int MT, int MODE>
-KRQ_DEV void epilogue(const float* red, int nw, int M, int64_t NO, int64_t rb, int split_idx,
+// P accumulator sets per wave in red; this call reads set p0 (and p0 + 1 for SwiGLU) and writes
+// row block rb.
+template <int MT, int MODE, int P>
+KRQ_DEV void epilogue(const float* red, int p0, int nw, int M, int64_t NO, int64_t rb, int split_idx,
                       const float* xs, ColScales cs, void* __restrict__ out, void* __restrict__ aux) {
-  constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : 1;
   constexpr int NV = MT * 256;
   for (int v = threadIdx.x; v < NV; v += blockDim.x) {
     const int mt = v >> 8, i = (v >> 6) & 3, ln = v & 63;
@@ -199,8 +202,8 @@ KRQ_DEV void epilogue(const float* red, int nw, int M, int64_t NO, int64_t rb, i
     const int64_t n = rb * 16 + (ln & 15);
     float a = 0.0f, au = 0.0f;
     for (int w = 0; w < nw; ++w) {
-      a += red[(w * P + 0) * NV + v];
-      if (P == 2) au += red[(w * P + 1) * NV + v];
+      a += red[(w * P + p0) * NV + v];
+      if (MODE == KRQ_OUT_SWIGLU) au += red[(w * P + p0 + 1) * NV + v];
     }
     const float x = valid ? xs[m] : 0.0f;
     if (MODE == kOutArgmax) {

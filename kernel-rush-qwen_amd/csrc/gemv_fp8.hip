@@ -42,7 +42,10 @@ constexpr int kXChunks = 8;
 constexpr int kXChunksDyn = 4;
 constexpr int kMaxThreads = 512;
 
-template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U>
+// PB = 2 (MFMA kernels, modes other than SwiGLU): the block owns two adjacent row blocks, so each
+// activation load feeds two matrix-core products (at M > 1 the activation slices are as large as
+// the weight steps, and every row block re-reads them).
+template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, int PB>
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(
     const uint8_t* __restrict__ x, const float* __restrict__ xsc, const float* __restrict__ xinv,
     int x_per_row, const uint8_t* __restrict__ w8, const float* __restrict__ wsc, int w_per_row,
@@ -50,11 +53,12 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(
   extern __shared__ float red[];  // nw*P*MT*256 partial sums, then the e4m3 activation slice
   __shared__ float xs_l[32];
   __shared__ float amax_w[kMaxThreads / 64];
-  constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : 1;
+  static_assert(PB == 1 || (MODE != KRQ_OUT_SWIGLU && ALGO != 2), "paired row blocks: MFMA, no SwiGLU");
+  constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : PB;  // weight row blocks streamed per step
   constexpr bool FUSED = XK != KRQ_X_FP8;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int64_t rb = blockIdx.x, rbu = rb + (NO >> 4);
+  const int64_t rb = (int64_t)blockIdx.x * PB, rbu = MODE == KRQ_OUT_SWIGLU ? rb + (NO >> 4) : rb + 1;
   const int sidx = blockIdx.y;
   const int nsteps = (kts + 1) >> 1;
   const int64_t tbase = (int64_t)sidx * kts;
@@ -62,7 +66,7 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(
   const int ks = kts * 64;        // K elements of this split
   uint8_t* xq = reinterpret_cast<uint8_t*>(red + nw * P * MT * 256);
   const int jcount = wave < nsteps ? (nsteps - wave + nw - 1) / nw : 0;
-  const ColScales cs = load_col_scales<MODE>(wsc, w_per_row, NO, rb);
+  const ColScales cs = load_col_scales<MODE, PB>(wsc, w_per_row, NO, rb);
 
   // ---- fused activation prologue, part 1: activation loads ahead of the weight stream ----
   // Every load of the prologue and of the step ring is issued unconditionally, at a clamped (valid)
@@ -223,39 +227,45 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(
   }
   stash<MT, P>(red, wave, lane, acc, accu);
   __syncthreads();
-  epilogue<MT, MODE>(red, nw, M, NO, rb, sidx, xs_l, cs, out, aux);
+  epilogue<MT, MODE, P>(red, 0, nw, M, NO, rb, sidx, xs_l, cs, out, aux);
+  if (PB == 2) epilogue<MT, MODE, P>(red, 1, nw, M, NO, rbu, sidx, xs_l, ColScales{cs.u, 1.0f}, out, aux);
 }
 
 #define KRQ_GEMV_ARGS xb, x_scale, x_inv, x_per_row, wb, w_scale, w_per_row, m, NO, K, kts, out, aux
 
 template <int MODE, int LAYOUT, int XK>
-int launch(int algo, int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb,
+int launch(int algo, int pb, int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb,
            const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
            const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out,
            void* aux) {
   const dim3 block(nw * 64);
+  constexpr int PB2 = MODE == KRQ_OUT_SWIGLU ? 1 : 2;  // no paired variant of the SwiGLU kernel
   if (algo == 2)
-    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 2, 4>), grid, block, smem, s, KRQ_GEMV_ARGS);
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 2, 4, 1>), grid, block, smem, s, KRQ_GEMV_ARGS);
   else if (M <= 4)
-    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, 4>), grid, block, smem, s, KRQ_GEMV_ARGS);
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, 4, 1>), grid, block, smem, s, KRQ_GEMV_ARGS);
+  else if (M <= 16 && pb == 2)
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, 2, PB2>), grid, block, smem, s, KRQ_GEMV_ARGS);
   else if (M <= 16)
-    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, 2>), grid, block, smem, s, KRQ_GEMV_ARGS);
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, 2, 1>), grid, block, smem, s, KRQ_GEMV_ARGS);
+  else if (pb == 2)
+    hipLaunchKernelGGL((k_gemv_fp8<2, MODE, LAYOUT, XK, 1, 2, PB2>), grid, block, smem, s, KRQ_GEMV_ARGS);
   else
-    hipLaunchKernelGGL((k_gemv_fp8<2, MODE, LAYOUT, XK, 1, 2>), grid, block, smem, s, KRQ_GEMV_ARGS);
+    hipLaunchKernelGGL((k_gemv_fp8<2, MODE, LAYOUT, XK, 1, 2, 1>), grid, block, smem, s, KRQ_GEMV_ARGS);
   return 0;
 }
 
 template <int MODE, int LAYOUT>
-void launch_xk(int xk, int algo, int M, dim3 grid, int nw, size_t smem, hipStream_t s,
+void launch_xk(int xk, int algo, int pb, int M, dim3 grid, int nw, size_t smem, hipStream_t s,
                const uint8_t* xb, const float* x_scale, const float* x_inv, int x_per_row,
                const uint8_t* wb, const float* w_scale, int w_per_row, int m, int64_t NO,
                int64_t K, int kts, void* out, void* aux) {
   if (xk == KRQ_X_FP8)
-    launch<MODE, LAYOUT, KRQ_X_FP8>(algo, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
+    launch<MODE, LAYOUT, KRQ_X_FP8>(algo, pb, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
   else if (xk == KRQ_X_BF16_DYN)
-    launch<MODE, LAYOUT, KRQ_X_BF16_DYN>(algo, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
+    launch<MODE, LAYOUT, KRQ_X_BF16_DYN>(algo, pb, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
   else
-    launch<MODE, LAYOUT, KRQ_X_BF16_STATIC>(algo, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
+    launch<MODE, LAYOUT, KRQ_X_BF16_STATIC>(algo, pb, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
 }
 
 }  // namespace
@@ -290,7 +300,16 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   if (algo == 0) algo = 1;
   const int kts = static_cast<int>(K / split / 64);
   const int ks = kts * 64;
-  const int P = mode == KRQ_OUT_SWIGLU ? 2 : 1;
+  // paired row blocks for the multi-row matrix-core kernels (KRQ_GEMV_PAIR=0 turns them off)
+  static const bool pair_ok = [] {
+    const char* e = getenv("KRQ_GEMV_PAIR");
+    return !(e && atoi(e) == 0);
+  }();
+  // Measured: pairing halves the blocks, which costs the Qwen3-4B projections (640-768 blocks)
+  // more than the saved activation reads gain; the lm_head (9,496 blocks) gains 10-15%.
+  const int pb = (pair_ok && mode != KRQ_OUT_SWIGLU && algo != 2 && M > 4 && (NO / 16) % 2 == 0 &&
+                  (NO / 16) * split >= 4096) ? 2 : 1;
+  const int P = mode == KRQ_OUT_SWIGLU ? 2 : pb;
   const int MT = (algo == 2 || M <= 16) ? 1 : 2;
   // step slots per wave of the variant launch() picks
   const int U = (algo == 2 || M <= 4) ? 4 : 2;
@@ -306,13 +325,13 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
               (long long)(xchunks * 8));
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) +
                       (x_kind == KRQ_X_FP8 ? 0 : (size_t)M * ks);
-  const dim3 grid(static_cast<unsigned>(NO / 16), static_cast<unsigned>(split));
+  const dim3 grid(static_cast<unsigned>(NO / 16 / pb), static_cast<unsigned>(split));
   const uint8_t* xb = (const uint8_t*)x;
   const uint8_t* wb = (const uint8_t*)w8;
   const int m = static_cast<int>(M);
   hipStream_t s = (hipStream_t)stream;
-#define KRQ_FP8_CASE(MODE, LAYOUT)                                                               \
-  launch_xk<MODE, LAYOUT>(x_kind, algo, m, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, \
+#define KRQ_FP8_CASE(MODE, LAYOUT)                                                                   \
+  launch_xk<MODE, LAYOUT>(x_kind, algo, pb, m, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, \
                           w_scale, w_per_row, m, NO, K, kts, out, aux)
   if (w_layout == KRQ_W_TILED) {
     if (mode == KRQ_OUT_BF16) KRQ_FP8_CASE(KRQ_OUT_BF16, KRQ_W_TILED);
