@@ -195,6 +195,26 @@ def test_gemv_fp8(dev, name, M):
         assert e <= TOL
 
 
+@pytest.mark.parametrize("M", [16, 32])
+def test_gemv_paired_row_blocks(dev, M):
+    """Grids of >= 4096 row blocks x splits run the paired-row-block kernels (two 16-column
+    blocks per workgroup sharing the activation loads): FP8 and BF16, bf16 and partial outputs,
+    both layouts."""
+    N, K = 65536, 256
+    w, x = _fp8_case(N, K, M, 61)
+    wd, xd = w.to(dev), x.to(dev)
+    q = fp8.quantize(wd)
+    r8, rs = O.quantize(u16(w))
+    x8r, xsr = O.quant_rows(u16(x))
+    _, yref = O.fp8_matmul(x8r, xsr, r8, rs)
+    for qq in (q, fp8.FP8Weight(q[0], q[1], None)):
+        assert rel_err(fp8.gemv_fp8(xd, qq, 1).float().cpu().numpy(), yref) <= TOL
+        assert rel_err(_sum_partials(fp8.gemv_fp8(xd, qq, 2)), yref) <= TOL
+    bref = O.bf16_matmul(u16(x), u16(w))
+    assert rel_err(gemv(xd, wd, 1).float().cpu().numpy(), bref) <= TOL
+    assert rel_err(_sum_partials(gemv(xd, wd, 2)), bref) <= TOL
+
+
 def _sum_partials(p):
     """The consumer's rule (engine/kernels/ops.py:35-38): fp32 sum in split order, then bf16."""
     acc = p[0].float().clone()
