@@ -174,6 +174,34 @@ int krq_mlp_fp8(const void* x, int x_kind, const float* x_scale, const void* w_g
                 uint32_t* ctl, int programs, void* out, void* stream);
 int64_t krq_mlp_ctl_words(void);
 
+/*
+ * BF16 GEMV with the RMSNorm prologue and the residual epilogue folded in: gemv_fused /
+ * gemv_swiglu_fused (reference engine/kernels/fused_gemv.py:48-221, called at
+ * engine/engine.py:953-961).
+ *   ln != NULL (RMSNorm): x rows are normalized on the fly, h = bf16(bf16(x * rstd) * ln) with
+ *                 rstd[m] = rsqrt(sum(ss_in[m][0..K/16)) / K + eps); ss_in is [M][K/16] fp32.
+ *   mode KRQ_OUT_BF16 / KRQ_OUT_PARTIAL / KRQ_OUT_SWIGLU: as krq_gemv_bf16, into out.
+ *   mode KRQ_OUT_RESIDUAL: y = bf16(sum of the split partials in split order);
+ *                 res_out = bf16(res_in + y) (bf16 [M][N]); ss_out[m][t] = sum over the 16
+ *                 columns of tile t of res_out^2 (fp32 [M][N/16]); nothing is written to out
+ *                 except, for split > 1, the fp32 [split][M][N] partials (scratch), and cnt
+ *                 ([N/16] uint32, zero before the first call) is left zero again.
+ * The per-tile sums of squares replace the reference's per-row atomic accumulator (same-address
+ * atomics serialize on MI355X); every producer overwrites all N/16 tiles, so nothing needs zeroing.
+ * krq_gemv_fused_fits() tells whether the block's K slice (and ss_in) fits the in-kernel staging;
+ * otherwise normalize the rows with krq_rmsnorm_rows and call krq_gemv_bf16. Calls sharing cnt must
+ * not overlap.
+ */
+#define KRQ_OUT_RESIDUAL 4
+int krq_gemv_bf16_fused(const void* x, const void* w, int w_layout, int64_t M, int64_t N, int64_t K,
+                        int split, int mode, const void* ln, const float* ss_in, float eps,
+                        const void* res_in, void* res_out, float* ss_out, uint32_t* cnt, void* out,
+                        void* stream);
+int64_t krq_gemv_fused_fits(int64_t M, int64_t K, int split, int mode, int norm);
+/* h = bf16(bf16(x * rstd) * ln) for whole bf16 rows x [M][K], rstd as above. */
+int krq_rmsnorm_rows(const void* x, const float* ss_in, const void* ln, float eps, int64_t M, int64_t K,
+                     void* h, void* stream);
+
 /* Tiled <-> row-major weight copies (byte permutations; see "tiled" above). For a bf16 [N, K]
  * matrix pass its [N, 2K] byte view (K -> 2K). */
 int krq_pack_fp8(const void* w8_rowmajor, int64_t N, int64_t K, void* w8_tiled, void* stream);

@@ -2,18 +2,20 @@
 
     python kernel-rush-qwen_amd/build_lib.py
 
-Objects go to kernel-rush-qwen_amd/_build/, the library to kernel-rush-qwen_amd/kernels/libkrq.so.
+One hipcc -c per source (run in parallel), then one hipcc -shared link. Objects go to
+kernel-rush-qwen_amd/_build/, the library to kernel-rush-qwen_amd/kernels/libkrq.so.
 """
 
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "kernels", "libkrq.so")
-SOURCES = ["quant.hip", "gemv_fp8.hip", "gemv_bf16.hip", "lmhead.hip", "mlp.hip"]
+SOURCES = ["quant.hip", "gemv_fp8.hip", "gemv_bf16.hip", "lmhead.hip", "mlp.hip", "fused_gemv.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in the generated code.
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17",
@@ -28,14 +30,17 @@ def _run(cmd):
 
 def build(verbose=False):
     os.makedirs(BUILD, exist_ok=True)
-    objs = []
-    for src in SOURCES:
-        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+    objs = [os.path.join(BUILD, src.replace(".hip", ".o")) for src in SOURCES]
+
+    def compile_one(src, obj):
         cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         _run(cmd)
-        objs.append(obj)
+
+    workers = max(1, min(len(SOURCES), os.cpu_count() or 1))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        list(pool.map(compile_one, SOURCES, objs))  # re-raises the first failure
     tmp = OUT + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, OUT)

@@ -250,6 +250,32 @@ KRQ_DEV void stash(float* red, int wave, int lane, const v4f* acc, const v4f* ac
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Cross-block data within one launch (fused MLP, residual epilogue). Agent-scope relaxed atomics:
+// their stores write through to memory and their loads read memory, on every XCD, so no cache
+// writeback or invalidate is needed. A producer calls stores_done() before it signals.
+// ---------------------------------------------------------------------------------------------
+KRQ_DEV uint32_t cload(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+KRQ_DEV uint64_t cload64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+KRQ_DEV void cstore(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+KRQ_DEV void cstore64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+KRQ_DEV uint32_t cadd(uint32_t* p, uint32_t v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+KRQ_DEV void cmax(uint32_t* p, uint32_t v) {
+  __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// waits until every store and atomic this thread issued has completed
+KRQ_DEV void stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // block of launch planning shared by the GEMV entry points
 struct Plan {
   int nw;  // waves per block

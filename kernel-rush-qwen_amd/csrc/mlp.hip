@@ -39,27 +39,6 @@ enum : int { kDone = 0, kExitG = 1, kAmax = 2, kTop = kGroups * kGroupWords, kEx
 constexpr uint32_t kSpinLimit = 1u << 20;  // polls of the phase-1 counter (~1 s) before flagging an error
 constexpr int kXC = 4;                     // 16-byte x chunks per thread in the M == 1 prologue
 
-KRQ_DEV uint32_t cload(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-KRQ_DEV uint64_t cload64(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-KRQ_DEV void cstore(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-KRQ_DEV void cstore64(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-KRQ_DEV uint32_t cadd(uint32_t* p, uint32_t v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-KRQ_DEV void cmax(uint32_t* p, uint32_t v) {
-  __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// waits until every store and atomic this thread issued has completed
-KRQ_DEV void stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
 template <int MT, int XK, int LAYOUT, int NW, int U1, int U2>
 __global__ __launch_bounds__(NW * 64, 2) void k_mlp_fp8(
     const uint8_t* __restrict__ x, const float* __restrict__ xsc, const uint8_t* __restrict__ wgu,

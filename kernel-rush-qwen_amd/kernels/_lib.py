@@ -14,7 +14,7 @@ import torch
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkrq.so")
 
 KRQ_OK, KRQ_EINVAL, KRQ_EHIP = 0, -1, -2
-OUT_BF16, OUT_PARTIAL, OUT_SWIGLU = 0, 1, 2
+OUT_BF16, OUT_PARTIAL, OUT_SWIGLU, OUT_RESIDUAL = 0, 1, 2, 4
 W_ROWMAJOR, W_TILED = 0, 1
 LM_BF16, LM_FP8 = 0, 1
 ALGO_AUTO, ALGO_MFMA, ALGO_VALU = 0, 1, 2
@@ -39,6 +39,10 @@ EXPORTS = {
     "krq_mlp_fp8": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64,
                            _i32, _vp, _vp, _i32, _vp, _vp]),
     "krq_mlp_ctl_words": (_i64, []),
+    "krq_gemv_bf16_fused": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _f32, _vp,
+                                   _vp, _vp, _vp, _vp, _vp]),
+    "krq_gemv_fused_fits": (_i64, [_i64, _i64, _i32, _i32, _i32]),
+    "krq_rmsnorm_rows": (_i32, [_vp, _vp, _vp, _f32, _i64, _i64, _vp, _vp]),
     "krq_pack_fp8": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "krq_unpack_fp8": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "krq_version": (ctypes.c_char_p, []),

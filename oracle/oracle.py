@@ -25,6 +25,9 @@ How each function is pinned (tests/test_oracle.py; tests/golden/):
   swiglu          against torch.nn.functional.silu in fp32 (at most 1 bf16 ulp, rare).
   mlp_fp8         composition of the pinned functions above; its split partials are checked to
                   sum to the unsplit product, and act to equal swiglu of the gate/up product.
+  rmsnorm_rows    torch evaluating Qwen3RMSNorm's expression (fp32 rsqrt of the mean square,
+  tile_sumsq,     bf16 casts) on the CPU; residual_add and tile_sumsq against torch's bf16 add
+  residual_add    and a float64 sum of squares.
   argmax_lowest   against torch.argmax with planted ties.
   tile / untile   against an element-by-element loop over the layout definition.
 """
@@ -225,6 +228,31 @@ def mlp_fp8(h_u16, wgu8, gs, wd8, ds, split):
     parts = [fp8_matmul(a8[:, s * ks:(s + 1) * ks], as_, wd8[:, s * ks:(s + 1) * ks], ds)[1]
              for s in range(split)]
     return act, np.stack(parts)
+
+
+def tile_sumsq(x_u16):
+    """Per-16-column sums of squares of bf16 rows, [M, N/16] float64: the fused residual
+    epilogue's partials (the reference accumulates their sum per row, fused_gemv.py:104-105)."""
+    xf = bf16_to_f32(x_u16).astype(np.float64)
+    M, N = xf.shape
+    return (xf * xf).reshape(M, N // 16, 16).sum(-1)
+
+
+def rmsnorm_rows(x_u16, ss, ln_u16, eps):
+    """RMSNorm with the reference's cast points (fused_gemv.py:39-45 = Qwen3RMSNorm):
+    rstd = rsqrt(ss / K + eps) in fp32, h = bf16(bf16(x * rstd) * w_ln). ss [M]: sums of squares."""
+    K = x_u16.shape[1]
+    ms = (np.asarray(ss, dtype=np.float32) / np.float32(K) + np.float32(eps)).astype(np.float32)
+    rstd = (_ONE / np.sqrt(ms)).astype(np.float32)
+    xr = round_bf16((bf16_to_f32(x_u16) * rstd[:, None]).astype(np.float32))
+    return f32_to_bf16((xr * bf16_to_f32(ln_u16)[None, :]).astype(np.float32))
+
+
+def residual_add(y, res_u16):
+    """Residual epilogue (fused_gemv.py:97-105): y (the GEMV's fp32 sum) rounds to bf16, is added
+    to the residual in fp32 and rounded: x_new = bf16(res + bf16(y)). Returns x_new (uint16)."""
+    yb = round_bf16(np.asarray(y, dtype=np.float32))
+    return f32_to_bf16((bf16_to_f32(res_u16) + yb).astype(np.float32))
 
 
 # ---------------------------------------------------------------------------------------------

@@ -64,6 +64,34 @@ def test_invalid_arguments_fail_before_any_launch():
     assert rc == L.KRQ_EINVAL and b"workspace" in lib.krq_last_error()
     with pytest.raises(ValueError):
         L.call("krq_pack_fp8", p, 17, 64, p, _null())
+    # fused MLP: one-row in-kernel scaling only; staging limit
+    rc = lib.krq_mlp_fp8(p, 1, None, p, 1, p, 1, p, p, 1, 2, 2560, 9728, 4, p, p, 0, p, _null())
+    assert rc == L.KRQ_EINVAL and b"M == 1" in lib.krq_last_error()
+    rc = lib.krq_mlp_fp8(p, 0, p, p, 1, p, 1, p, p, 1, 32, 2560, 9728, 1, p, p, 0, p, _null())
+    assert rc == L.KRQ_EINVAL and b"raise split" in lib.krq_last_error()
+    # fused BF16 GEMV: residual epilogue needs its buffers; slices that do not fit are refused
+    rc = lib.krq_gemv_bf16_fused(p, p, 0, 1, 2560, 4096, 4, L.OUT_RESIDUAL, None, None, 1e-6,
+                                 None, None, None, None, p, _null())
+    assert rc == L.KRQ_EINVAL and b"res_in" in lib.krq_last_error()
+    rc = lib.krq_gemv_bf16_fused(p, p, 0, 16, 19456, 2560, 1, L.OUT_SWIGLU, p, p, 1e-6,
+                                 None, None, None, None, p, _null())
+    assert rc == L.KRQ_EINVAL and b"krq_rmsnorm_rows" in lib.krq_last_error()
+    assert lib.krq_gemv_fused_fits(1, 2560, 2, L.OUT_PARTIAL, 1) == 1
+    assert lib.krq_gemv_fused_fits(16, 2560, 1, L.OUT_SWIGLU, 1) == 0
+
+
+def test_fused_buffers_and_mlp_contracts():
+    from kernels.fused_gemv import FusedLayerBuffers
+    from kernels.mlp import PersistentMLP
+    b = FusedLayerBuffers(4, 2560, 151936, "cpu")
+    assert b.res.shape == (2, 4, 2560) and b.res.dtype == torch.bfloat16
+    assert b.ss.shape == (2, 4, 160) and b.cnt.shape == (151936 // 8,)
+    pm = PersistentMLP(1, 2560, 9728, "cpu")
+    assert pm.ctl.numel() == L.lib().krq_mlp_ctl_words() and int(pm.ctl.abs().sum()) == 0
+    with pytest.raises(AssertionError):
+        PersistentMLP(1, 2560, 9728 + 16, "cpu")          # the reference's chunk contract
+    with pytest.raises(ValueError):
+        pm(torch.zeros(1, 2560, dtype=torch.bfloat16), torch.zeros(1), torch.zeros(1))
 
 
 def test_no_cpu_path():

@@ -1,0 +1,166 @@
+"""Fused BF16 decode GEMVs (kernels.fused_gemv over krq_gemv_bf16_fused / krq_rmsnorm_rows) against
+the CPU oracle: the RMSNorm prologue, the residual epilogue with split-K last-arriver reduction,
+the per-tile sums of squares, and an engine-shaped layer fragment (engine/engine.py:953-961).
+GEMV outputs: max|y - ref| <= 1e-2 * max|ref|; residual rows and ss within the same bar."""
+
+import numpy as np
+import pytest
+import torch
+
+from kernels import gemv as G
+from kernels.fused_gemv import FusedLayerBuffers, gemv_fused, gemv_swiglu_fused
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+H, I, NQKV, V = 2560, 9728, 6144, 151936
+EPS = 1e-6
+
+
+def u16(t):
+    return t.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def rel_err(y, ref):
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.abs(y - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def bf(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+def sum_partials(p):
+    acc = p[0].float().clone()
+    for s in range(1, p.shape[0]):
+        acc += p[s]
+    return acc.to(torch.bfloat16).float().cpu().numpy()
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_plain_outputs_match_gemv(dev, M):
+    w, x = bf((NQKV, H), 1, 0.02), bf((M, H), 2)
+    ref = O.bf16_matmul(u16(x), u16(w))
+    xd, wd = x.to(dev), w.to(dev)
+    assert rel_err(gemv_fused(xd, wd, 1).float().cpu().numpy(), ref) <= TOL
+    assert rel_err(sum_partials(gemv_fused(xd, wd, 2)), ref) <= TOL
+
+
+@pytest.mark.parametrize("M,K,N,split,swiglu", [(1, H, NQKV, 2, False), (16, H, NQKV, 2, False),
+                                                (1, H, 2 * I, 1, True), (16, H, 2 * I, 1, True),
+                                                (4, H, V, 1, False)])
+def test_rmsnorm_prologue(dev, M, K, N, split, swiglu):
+    """norm=(ln, ss): includes shapes whose normalized slice fits the in-kernel staging and ones that
+    take the separate row-normalization launch (M=16 with the full K=2560 slice)."""
+    x = bf((M, K), 10 + M)
+    w = bf((N, K), 11, 0.02)
+    ln = (1 + 0.1 * torch.randn(K, generator=torch.Generator().manual_seed(12))).to(torch.bfloat16)
+    ss_t = O.tile_sumsq(u16(x)).astype(np.float32)           # as a residual epilogue leaves it
+    h = O.rmsnorm_rows(u16(x), ss_t.astype(np.float64).sum(1), u16(ln), EPS)
+    full = O.bf16_matmul(h, u16(w))
+    xd, wd, lnd = x.to(dev), w.to(dev), ln.to(dev)
+    ssd = torch.from_numpy(ss_t).to(dev)
+    if swiglu:
+        got = gemv_swiglu_fused(xd, wd, norm=(lnd, ssd), eps=EPS).float().cpu().numpy()
+        ref = O.bf16_to_f32(O.swiglu(full[:, :N // 2].astype(np.float32), full[:, N // 2:].astype(np.float32)))
+    else:
+        y = gemv_fused(xd, wd, split, norm=(lnd, ssd), eps=EPS)
+        got = sum_partials(y) if split > 1 else y.float().cpu().numpy()
+        ref = full
+    e = rel_err(got, ref)
+    print(f"norm M={M} N={N} split={split}: max-rel {e:.2e}")
+    assert e <= TOL
+
+
+@pytest.mark.parametrize("M,split", [(1, 4), (16, 4), (1, 1), (32, 2)])
+def test_residual_epilogue(dev, M, split):
+    """ep=(res_in, res_out, ss_out, cnt): res_out = bf16(res_in + bf16(y)), ss_out per 16-column
+    tile; the split counters are back at zero afterwards (twice in a row)."""
+    K = 4096
+    a, w, res = bf((M, K), 20), bf((H, K), 21, 0.02), bf((M, H), 22)
+    y = O.bf16_matmul(u16(a), u16(w))
+    ref_res = O.residual_add(y, u16(res))
+    ref_ss = O.tile_sumsq(ref_res)
+    bufs = FusedLayerBuffers(M, H, V, dev)
+    res_in = res.to(dev)
+    for _ in range(2):
+        out = gemv_fused(a.to(dev), w.to(dev), split, ep=(res_in, bufs.res[1], bufs.ss[1], bufs.cnt))
+        assert out is None
+        torch.cuda.synchronize()
+        got = bufs.res[1].float().cpu().numpy()
+        mism = float(np.mean(got != O.bf16_to_f32(ref_res)))
+        assert rel_err(got, O.bf16_to_f32(ref_res)) <= TOL and mism < 0.02
+        assert rel_err(bufs.ss[1].cpu().numpy(), ref_ss) <= TOL
+        assert int(bufs.cnt.abs().sum()) == 0
+
+
+def test_layer_fragment_like_the_engine(dev):
+    """o (ep) -> gate_up (norm, SwiGLU) -> down (ep) -> next layer's qkv (norm), as
+    engine/engine.py:955-959 chains them, against the unfused oracle sequence."""
+    M = 1
+    cur, a = bf((M, H), 30), bf((M, 4096), 31)
+    wo, wgu, wd, wqkv = bf((H, 4096), 32, 0.02), bf((2 * I, H), 33, 0.02), bf((H, I), 34, 0.02), bf((NQKV, H), 35, 0.02)
+    ln2 = (1 + 0.1 * torch.randn(H, generator=torch.Generator().manual_seed(36))).to(torch.bfloat16)
+    ln1 = (1 + 0.1 * torch.randn(H, generator=torch.Generator().manual_seed(37))).to(torch.bfloat16)
+    # oracle
+    res_b = O.residual_add(O.bf16_matmul(u16(a), u16(wo)), u16(cur))
+    h2 = O.rmsnorm_rows(res_b, O.tile_sumsq(res_b).sum(1), u16(ln2), EPS)
+    full = O.bf16_matmul(h2, u16(wgu))
+    act = O.swiglu(full[:, :I].astype(np.float32), full[:, I:].astype(np.float32))
+    res_a = O.residual_add(O.bf16_matmul(act, u16(wd)), res_b)
+    h1 = O.rmsnorm_rows(res_a, O.tile_sumsq(res_a).sum(1), u16(ln1), EPS)
+    qkv_ref = O.bf16_matmul(h1, u16(wqkv))
+    # fused
+    bufs = FusedLayerBuffers(M, H, V, dev)
+    res_a_d, res_b_d = bufs.res[0], bufs.res[1]
+    ss_a, ss_b = bufs.ss[0], bufs.ss[1]
+    d = lambda t: t.to(dev)
+    gemv_fused(d(a), d(wo), 4, ep=(d(cur), res_b_d, ss_b, bufs.cnt))
+    act_d = gemv_swiglu_fused(res_b_d, d(wgu), norm=(d(ln2), ss_b), zero_ss=ss_a, eps=EPS)
+    gemv_fused(act_d, d(wd), 4, ep=(res_b_d, res_a_d, ss_a, bufs.cnt))
+    qkv = gemv_fused(res_a_d, d(wqkv), 2, norm=(d(ln1), ss_a), zero_ss=ss_b, eps=EPS)
+    assert rel_err(res_b_d.float().cpu().numpy(), O.bf16_to_f32(res_b)) <= TOL
+    assert rel_err(act_d.float().cpu().numpy(), O.bf16_to_f32(act)) <= TOL
+    assert rel_err(res_a_d.float().cpu().numpy(), O.bf16_to_f32(res_a)) <= TOL
+    e = rel_err(sum_partials(qkv), qkv_ref)
+    print(f"layer fragment: qkv max-rel {e:.2e}")
+    assert e <= TOL
+
+
+def test_fused_graph_replays(dev):
+    """The residual epilogue's counters reset themselves: replays match eager, with eager calls
+    in between."""
+    M = 4
+    a, w, res = bf((M, 4096), 40), bf((H, 4096), 41, 0.02), bf((M, H), 42)
+    ad, wd, rd = a.to(dev), w.to(dev), res.to(dev)
+    bufs = FusedLayerBuffers(M, H, V, dev)
+    gemv_fused(ad, wd, 4, ep=(rd, bufs.res[1], bufs.ss[1], bufs.cnt))
+    eager_res, eager_ss = bufs.res[1].clone(), bufs.ss[1].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        gemv_fused(ad, wd, 4, ep=(rd, bufs.res[1], bufs.ss[1], bufs.cnt))
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gemv_fused(ad, wd, 4, ep=(rd, bufs.res[1], bufs.ss[1], bufs.cnt))
+    for _ in range(3):
+        bufs.res[1].zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(bufs.res[1], eager_res) and torch.equal(bufs.ss[1], eager_ss)
+        gemv_fused(ad, wd, 4, ep=(rd, bufs.res[1], bufs.ss[1], bufs.cnt))
+    assert int(bufs.cnt.abs().sum()) == 0
+    del g
+
+
+def test_packed_weights(dev):
+    """gemv.pack (tiled bf16 copy) is read by the fused kernels too."""
+    M = 1
+    w, x = bf((NQKV, H), 50, 0.02), bf((M, H), 51)
+    ref = O.bf16_matmul(u16(x), u16(w))
+    wd = G.pack(w.to(dev))
+    assert rel_err(gemv_fused(x.to(dev), wd, 1).float().cpu().numpy(), ref) <= TOL

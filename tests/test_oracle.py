@@ -314,3 +314,31 @@ def test_golden_small_cases():
     assert np.array_equal(w8, data["w8"]) and np.array_equal(ws, data["ws"])
     _, y = O.fp8_matmul(x8, xs, w8, ws)
     assert np.array_equal(O.f32_to_bf16(y.astype(np.float32)), data["y_bf16"])
+
+
+def test_rmsnorm_and_residual_epilogue():
+    """The fused GEMV's prologue / epilogue arithmetic against torch evaluating Qwen3RMSNorm's own
+    expression and a bf16 residual add (CPU)."""
+    g = torch.Generator().manual_seed(13)
+    M, K = 3, 2560
+    res = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    y = torch.randn(M, K, generator=g) * 0.5
+    ln = (1 + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16)
+    xn = O.residual_add(y.numpy(), bf16_bits(res))
+    ref_xn = (res.float() + y.to(torch.bfloat16).float()).to(torch.bfloat16)
+    assert np.array_equal(xn, bf16_bits(ref_xn))
+    ss_t = O.tile_sumsq(xn)
+    assert ss_t.shape == (M, K // 16)
+    xf = ref_xn.double()
+    assert np.allclose(ss_t.sum(1), (xf * xf).sum(1).numpy(), rtol=1e-12)
+    eps = 1e-6
+    h = O.rmsnorm_rows(xn, ss_t.sum(1), bf16_bits(ln), eps)
+    xt = ref_xn.float()
+    var = xt.pow(2).mean(-1, keepdim=True)
+    ref_h = ln * (xt * torch.rsqrt(var + eps)).to(torch.bfloat16)
+    got, ref = O.bf16_to_f32(h), ref_h.float().numpy()
+    assert np.mean(got != ref) < 1e-3   # rsqrt / mean rounding may move a value by one bf16 step
+    assert np.abs(got - ref).max() <= 2 ** -7 * np.abs(ref).max()
+    # a dropped weight or a wrong mean divisor is caught
+    assert not np.allclose(O.bf16_to_f32(O.rmsnorm_rows(xn, ss_t.sum(1), bf16_bits(torch.ones(K, dtype=torch.bfloat16)), eps)), ref, rtol=1e-2)
+    assert not np.allclose(O.bf16_to_f32(O.rmsnorm_rows(xn, 2 * ss_t.sum(1), bf16_bits(ln), eps)), ref, rtol=1e-2)
