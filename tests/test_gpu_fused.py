@@ -164,3 +164,16 @@ def test_packed_weights(dev):
     ref = O.bf16_matmul(u16(x), u16(w))
     wd = G.pack(w.to(dev))
     assert rel_err(gemv_fused(x.to(dev), wd, 1).float().cpu().numpy(), ref) <= TOL
+
+
+def test_packfile_rebuilds_tiled_copy_on_device(dev, tmp_path):
+    """fp8.quantize on the GPU -> packfile (row-major bytes only) -> load onto the GPU: the tiled
+    copy rebuilt by krq_pack_fp8 equals the quantizer's, and the GEMV gives identical bits."""
+    from kernels import fp8, packfile
+    w, x = bf((NQKV, H), 60, 0.02), bf((1, H), 61)
+    q = fp8.quantize(w.to(dev))
+    p = str(tmp_path / "w.safetensors")
+    packfile.save_fp8(p, {"qkv": q})
+    r = packfile.load_fp8(p, device=dev)["qkv"]
+    assert torch.equal(r.tiled, q.tiled) and torch.equal(r[1], q[1])
+    assert torch.equal(fp8.gemv_fp8(x.to(dev), r, 2), fp8.gemv_fp8(x.to(dev), q, 2))
