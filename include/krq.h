@@ -202,6 +202,33 @@ int64_t krq_gemv_fused_fits(int64_t M, int64_t K, int split, int mode, int norm)
 int krq_rmsnorm_rows(const void* x, const float* ss_in, const void* ln, float eps, int64_t M, int64_t K,
                      void* h, void* stream);
 
+/*
+ * FP8 counterpart of krq_gemv_bf16_fused: the fused-GEMV semantics above (reference
+ * engine/kernels/fused_gemv.py:48-167) on the FP8 weights and activation kinds of krq_gemv_fp8
+ * (reference engine/kernels/fp8.py:17-106, the linear_fp8 call sites engine/engine.py:649-677).
+ *   ln != NULL (RMSNorm; x_kind KRQ_X_BF16_DYN or KRQ_X_BF16_STATIC; modes BF16 / PARTIAL /
+ *                 SWIGLU): h = bf16(bf16(x * rstd) * ln) as above, then h is scaled as the
+ *                 x_kind says (DYN: per token over the whole normalized row, M == 1; STATIC:
+ *                 x_inv / x_scale) and quantized to e4m3 in the kernel.
+ *   mode KRQ_OUT_RESIDUAL (ln == NULL; any x_kind): one split's value is the scaled product
+ *                 (x8 . w8) * x_scale[m] * w_scale[n], as the partials output holds it; then
+ *                 y = bf16(sum over splits in split order) and res_out / ss_out / cnt / out as in
+ *                 krq_gemv_bf16_fused.
+ * krq_gemv_fp8_fused_fits() tells whether the in-kernel staging holds the launch; otherwise use
+ * krq_rmsnorm_quant_rows (per token) or krq_rmsnorm_rows + a static cast, then krq_gemv_fp8 /
+ * the residual mode with x_kind KRQ_X_FP8. Calls sharing cnt must not overlap.
+ */
+int krq_gemv_fp8_fused(const void* x, int x_kind, const float* x_scale, const float* x_inv, int x_per_row,
+                       const void* w8, int w_layout, const float* w_scale, int w_per_row, int64_t M,
+                       int64_t N, int64_t K, int split, int mode, const void* ln, const float* ss_in,
+                       float eps, const void* res_in, void* res_out, float* ss_out, uint32_t* cnt,
+                       void* out, void* stream);
+int64_t krq_gemv_fp8_fused_fits(int64_t M, int64_t K, int split, int mode, int x_kind, int norm);
+/* RMSNorm then per-token e4m3 quantization of whole rows: x8 [M][K] e4m3 and x_scale [M] equal
+ * krq_quant_rows applied to krq_rmsnorm_rows' output (K <= 16384). */
+int krq_rmsnorm_quant_rows(const void* x, const float* ss_in, const void* ln, float eps, int64_t M,
+                           int64_t K, void* x8, float* x_scale, void* stream);
+
 /* Tiled <-> row-major weight copies (byte permutations; see "tiled" above). For a bf16 [N, K]
  * matrix pass its [N, 2K] byte view (K -> 2K). */
 int krq_pack_fp8(const void* w8_rowmajor, int64_t N, int64_t K, void* w8_tiled, void* stream);

@@ -1,0 +1,193 @@
+// FP8 decode GEMVs with the RMSNorm prologue and the residual epilogue of the fused BF16 GEMVs
+// (reference engine/kernels/fused_gemv.py:1-17, :48-167, carried over to the FP8 weights of
+// engine/kernels/fp8.py): a decoder layer on FP8 weights is four GEMV launches plus attention.
+//
+//   qkv, gate_up   bf16 residual rows in, RMSNorm in the prologue, then the activation scaling of
+//                  the plain FP8 GEMV (per token over the normalized row at M = 1, or a static
+//                  SharedScale inverse at any M), e4m3 slice in LDS, matrix cores;
+//   o, down        any activation kind, residual epilogue: x_new = bf16(res_in + bf16(y)) with y
+//                  the in-order sum of the scaled split partials, plus per-tile sums of squares.
+// Rows that do not fit the in-kernel staging (M > 1 with per-token scales) are normalized and
+// quantized by k_rmsnorm_quant_rows first: one launch, the same values as quant_rows(rmsnorm(x)).
+// The kernel template is gemv_fp8_kernel.h's; the fused variants always use the matrix cores.
+#include "gemv_fp8_kernel.h"
+
+using namespace krq;
+
+namespace {
+
+constexpr size_t kMaxSmem = 60 * 1024;
+constexpr int kRowThreads = 256;
+constexpr int kRowChunks = 8;  // 16-byte chunks per thread: rows of up to 16,384 elements
+
+// RMSNorm + per-token e4m3 quantization of whole rows (one block per row): x8 = e4m3(h * inv),
+// xs = amax(h) / 448 with the ActScale arithmetic of quant_rows (amax floored at 1e-6).
+__global__ __launch_bounds__(kRowThreads) void k_rmsnorm_quant_rows(const uint16_t* __restrict__ x,
+                                                                    const float* __restrict__ ss_in,
+                                                                    const uint16_t* __restrict__ ln, float eps,
+                                                                    int64_t K, uint8_t* __restrict__ x8,
+                                                                    float* __restrict__ xs) {
+  __shared__ float rstd;
+  const int m = blockIdx.x, T = (int)(K >> 4);
+  row_rstd(ss_in + (int64_t)m * T, 1, T, K, eps, &rstd);
+  __syncthreads();
+  const uint8_t* xr = reinterpret_cast<const uint8_t*>(x + m * K);
+  const uint8_t* lr = reinterpret_cast<const uint8_t*>(ln);
+  uint4 v[kRowChunks];
+  float am = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int64_t e = 8 * (int64_t)(threadIdx.x + c * kRowThreads);
+    v[c] = e < K ? norm8(ld16(xr + 2 * e), ld16(lr + 2 * e), rstd) : zero4();
+    am = absmax8(v[c], am);
+  }
+  am = block_max<kRowThreads>(am);
+  const float a = fmaxf(am, 1e-6f);
+  const float iv = inv_from_amax(a);
+  if (threadIdx.x == 0) xs[m] = scale_from_amax(a);
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int64_t e = 8 * (int64_t)(threadIdx.x + c * kRowThreads);
+    if (e < K) *reinterpret_cast<uint2*>(x8 + m * K + e) = quant8(v[c], iv);
+  }
+}
+
+#define KRQ_FUSED_FP8_ARGS xb, x_scale, x_inv, x_per_row, wb, w_scale, w_per_row, m, NO, K, kts, out, nullptr, fa
+
+template <int MODE, int LAYOUT, int XK, bool NORM>
+void launch(int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb, const float* x_scale,
+            const float* x_inv, int x_per_row, const uint8_t* wb, const float* w_scale, int w_per_row, int m,
+            int64_t NO, int64_t K, int kts, void* out, const FusedArgs& fa) {
+  const dim3 block(nw * 64);
+  if (M <= 4)
+    hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, 4, NORM>), grid, block, smem, s, KRQ_FUSED_FP8_ARGS);
+  else if (M <= 16)
+    hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, 2, NORM>), grid, block, smem, s, KRQ_FUSED_FP8_ARGS);
+  else
+    hipLaunchKernelGGL((k_gemv_fp8_fused<2, MODE, LAYOUT, XK, 1, 2, NORM>), grid, block, smem, s, KRQ_FUSED_FP8_ARGS);
+}
+
+template <int MODE, int XK, bool NORM>
+void launch_layout(int layout, int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb,
+                   const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
+                   const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out,
+                   const FusedArgs& fa) {
+  if (layout == KRQ_W_TILED)
+    launch<MODE, KRQ_W_TILED, XK, NORM>(M, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, w_scale,
+                                         w_per_row, m, NO, K, kts, out, fa);
+  else
+    launch<MODE, KRQ_W_ROWMAJOR, XK, NORM>(M, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, w_scale,
+                                            w_per_row, m, NO, K, kts, out, fa);
+}
+
+// Waves and LDS bytes of a fused FP8 launch; false if the prologue's staging does not fit.
+bool plan(int64_t M, int64_t K, int split, int mode, int x_kind, bool norm, int* nw_out, size_t* smem_out) {
+  if (M < 1 || M > 32 || split < 1 || K < 64 || K % split || (K / split) % 64) return false;
+  if (norm && x_kind == KRQ_X_FP8) return false;
+  if (x_kind == KRQ_X_BF16_DYN && M != 1) return false;
+  const int64_t ks = K / split;
+  const int kts = static_cast<int>(ks / 64);
+  const int P = mode == KRQ_OUT_SWIGLU ? 2 : 1;
+  const int MT = M <= 16 ? 1 : 2;
+  int nw = plan_waves((kts + 1) / 2, P, M <= 4 ? 4 : 2);
+  const int64_t xchunks = x_kind == KRQ_X_BF16_DYN ? (K + 7) / 8 : x_kind == KRQ_X_BF16_STATIC ? M * (ks / 8) : 0;
+  const int xc = x_kind == KRQ_X_BF16_DYN ? kXChunksDyn : kXChunks;
+  const int sc = x_kind == KRQ_X_BF16_DYN ? kSsChunksDyn : kSsChunks;
+  auto short_of = [&](int w) {
+    return (int64_t)w * 64 * xc < xchunks || (norm && (int64_t)w * 64 * sc * 4 < M * (K / 16));
+  };
+  while (short_of(nw) && nw < kMaxThreads / 64) ++nw;
+  if (short_of(nw)) return false;
+  const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) + (x_kind == KRQ_X_FP8 ? 0 : (size_t)M * ks) +
+                      (norm ? (size_t)M * (K / 16) * sizeof(float) : 0);
+  if (smem > kMaxSmem) return false;
+  *nw_out = nw;
+  *smem_out = smem;
+  return true;
+}
+
+}  // namespace
+
+extern "C" int64_t krq_gemv_fp8_fused_fits(int64_t M, int64_t K, int split, int mode, int x_kind, int norm) {
+  int nw = 0;
+  size_t smem = 0;
+  return plan(M, K, split, mode, x_kind, norm != 0, &nw, &smem) ? 1 : 0;
+}
+
+extern "C" int krq_gemv_fp8_fused(const void* x, int x_kind, const float* x_scale, const float* x_inv,
+                                  int x_per_row, const void* w8, int w_layout, const float* w_scale,
+                                  int w_per_row, int64_t M, int64_t N, int64_t K, int split, int mode,
+                                  const void* ln, const float* ss_in, float eps, const void* res_in,
+                                  void* res_out, float* ss_out, uint32_t* cnt, void* out, void* stream) {
+  KRQ_REQUIRE(x && w8 && w_scale, "gemv_fp8_fused: null pointer");
+  KRQ_REQUIRE(aligned16(x) && aligned16(w8), "gemv_fp8_fused: x and w8 must be 16-byte aligned");
+  KRQ_REQUIRE(x_kind >= KRQ_X_FP8 && x_kind <= KRQ_X_BF16_STATIC, "gemv_fp8_fused: bad x_kind %d", x_kind);
+  KRQ_REQUIRE(x_kind == KRQ_X_BF16_DYN || x_scale, "gemv_fp8_fused: x_scale is required");
+  KRQ_REQUIRE(x_kind != KRQ_X_BF16_STATIC || x_inv, "gemv_fp8_fused: x_inv is required");
+  KRQ_REQUIRE(M >= 1 && M <= 32, "gemv_fp8_fused: M=%lld outside 1..32", (long long)M);
+  KRQ_REQUIRE(x_kind != KRQ_X_BF16_DYN || M == 1, "gemv_fp8_fused: in-kernel per-token scaling takes M == 1");
+  KRQ_REQUIRE(N > 0 && K >= 64 && split >= 1 && split <= 65535 && K % split == 0 && (K / split) % 64 == 0,
+              "gemv_fp8_fused: no tiling divides K_SPLIT (K=%lld split=%d; K/split must be a multiple of 64)",
+              (long long)K, split);
+  KRQ_REQUIRE(w_layout == KRQ_W_ROWMAJOR || w_layout == KRQ_W_TILED, "gemv_fp8_fused: bad layout %d", w_layout);
+  KRQ_REQUIRE(mode == KRQ_OUT_BF16 || mode == KRQ_OUT_PARTIAL || mode == KRQ_OUT_SWIGLU || mode == kOutResidual,
+              "gemv_fp8_fused: bad mode %d", mode);
+  KRQ_REQUIRE(mode == KRQ_OUT_PARTIAL || mode == kOutResidual || split == 1,
+              "gemv_fp8_fused: split %d needs the partials or residual output", split);
+  const bool norm = ln != nullptr;
+  KRQ_REQUIRE(norm || mode == kOutResidual,
+              "gemv_fp8_fused: neither RMSNorm (ln) nor the residual epilogue; call krq_gemv_fp8");
+  KRQ_REQUIRE(!(norm && mode == kOutResidual), "gemv_fp8_fused: RMSNorm and the residual epilogue in one call");
+  KRQ_REQUIRE(!norm || (ss_in && aligned16(ln) && aligned16(ss_in) && x_kind != KRQ_X_FP8),
+              "gemv_fp8_fused: RMSNorm needs bf16 activations, ss_in and aligned ln / ss_in");
+  KRQ_REQUIRE(mode != kOutResidual || (res_in && res_out && ss_out && (split == 1 || (cnt && out))),
+              "gemv_fp8_fused: the residual epilogue needs res_in, res_out, ss_out and, for split > 1, "
+              "cnt and the partials buffer");
+  KRQ_REQUIRE(mode == kOutResidual || out, "gemv_fp8_fused: null output");
+  const int64_t NO = mode == KRQ_OUT_SWIGLU ? N / 2 : N;
+  KRQ_REQUIRE(NO % 16 == 0 && (mode != KRQ_OUT_SWIGLU || N % 2 == 0) && NO / 16 <= 0x7fffffff,
+              "gemv_fp8_fused: no tiling divides N=%lld", (long long)N);
+  int nw = 0;
+  size_t smem = 0;
+  KRQ_REQUIRE(plan(M, K, split, mode, x_kind, norm, &nw, &smem),
+              "gemv_fp8_fused: M=%lld x K/split=%lld does not fit the in-kernel staging; normalize and "
+              "quantize rows first (krq_rmsnorm_quant_rows)", (long long)M, (long long)(K / split));
+  const int kts = static_cast<int>(K / split / 64);
+  const dim3 grid(static_cast<unsigned>(NO / 16), static_cast<unsigned>(split));
+  const FusedArgs fa{reinterpret_cast<const uint16_t*>(ln), ss_in, eps, reinterpret_cast<const uint16_t*>(res_in),
+                     reinterpret_cast<uint16_t*>(res_out), ss_out, cnt};
+  const uint8_t* xb = (const uint8_t*)x;
+  const uint8_t* wb = (const uint8_t*)w8;
+  const int m = static_cast<int>(M);
+  hipStream_t s = (hipStream_t)stream;
+#define KRQ_CASE(MODE, XK, NORM)                                                                          \
+  launch_layout<MODE, XK, NORM>(w_layout, m, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, w_scale, \
+                                w_per_row, m, NO, K, kts, out, fa)
+  if (mode == kOutResidual) {
+    if (x_kind == KRQ_X_FP8) KRQ_CASE(kOutResidual, KRQ_X_FP8, false);
+    else if (x_kind == KRQ_X_BF16_DYN) KRQ_CASE(kOutResidual, KRQ_X_BF16_DYN, false);
+    else KRQ_CASE(kOutResidual, KRQ_X_BF16_STATIC, false);
+  } else if (x_kind == KRQ_X_BF16_DYN) {
+    if (mode == KRQ_OUT_BF16) KRQ_CASE(KRQ_OUT_BF16, KRQ_X_BF16_DYN, true);
+    else if (mode == KRQ_OUT_PARTIAL) KRQ_CASE(KRQ_OUT_PARTIAL, KRQ_X_BF16_DYN, true);
+    else KRQ_CASE(KRQ_OUT_SWIGLU, KRQ_X_BF16_DYN, true);
+  } else {
+    if (mode == KRQ_OUT_BF16) KRQ_CASE(KRQ_OUT_BF16, KRQ_X_BF16_STATIC, true);
+    else if (mode == KRQ_OUT_PARTIAL) KRQ_CASE(KRQ_OUT_PARTIAL, KRQ_X_BF16_STATIC, true);
+    else KRQ_CASE(KRQ_OUT_SWIGLU, KRQ_X_BF16_STATIC, true);
+  }
+#undef KRQ_CASE
+  return krq_check_launch("gemv_fp8_fused");
+}
+
+extern "C" int krq_rmsnorm_quant_rows(const void* x, const float* ss_in, const void* ln, float eps, int64_t M,
+                                      int64_t K, void* x8, float* x_scale, void* stream) {
+  KRQ_REQUIRE(x && ss_in && ln && x8 && x_scale, "rmsnorm_quant_rows: null pointer");
+  KRQ_REQUIRE(aligned16(x) && aligned16(ln) && aligned16(x8), "rmsnorm_quant_rows: x, ln and x8 must be 16-byte aligned");
+  KRQ_REQUIRE(M >= 1 && M <= 0x7fffffff && K > 0 && K % 16 == 0 && K <= 8 * kRowThreads * kRowChunks,
+              "rmsnorm_quant_rows: bad shape M=%lld K=%lld (K a multiple of 16, at most %d)", (long long)M,
+              (long long)K, 8 * kRowThreads * kRowChunks);
+  hipLaunchKernelGGL(k_rmsnorm_quant_rows, dim3(static_cast<unsigned>(M)), dim3(kRowThreads), 0, (hipStream_t)stream,
+                     (const uint16_t*)x, ss_in, (const uint16_t*)ln, eps, K, (uint8_t*)x8, x_scale);
+  return krq_check_launch("rmsnorm_quant_rows");
+}

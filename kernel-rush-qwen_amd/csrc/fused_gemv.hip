@@ -28,32 +28,9 @@ using namespace krq;
 
 namespace {
 
-constexpr int kOutResidual = KRQ_OUT_RESIDUAL;  // residual epilogue (res_out, ss_out), no output
 constexpr int kXC = 8;           // 16-byte x chunks per thread in the prologue
 constexpr int kSC = 8;           // sum-of-squares partials per thread in the prologue
 constexpr int kMaxNT = 512;
-
-struct FusedArgs {
-  const uint16_t* ln;  // NORM: RMSNorm weight [K] bf16
-  const float* ss_in;  // NORM: [M][K/16] per-tile sums of squares of x
-  float eps;
-  const uint16_t* res_in;  // residual epilogue: bf16 [M][N] residual rows
-  uint16_t* res_out;       // bf16 [M][N] new residual rows
-  float* ss_out;           // [M][N/16] per-tile sums of squares of res_out
-  uint32_t* cnt;           // [N/16] split-arrival counters (zero between launches)
-};
-
-KRQ_DEV uint4 norm8(uint4 xv, uint4 lv, float rstd) {
-  const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w}, la[4] = {lv.x, lv.y, lv.z, lv.w};
-  uint32_t o[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const float x0 = round_bf16(as_f32(xa[q] << 16) * rstd), x1 = round_bf16(as_f32(xa[q] & 0xffff0000u) * rstd);
-    const uint32_t h0 = f32_to_bf16(x0 * as_f32(la[q] << 16)), h1 = f32_to_bf16(x1 * as_f32(la[q] & 0xffff0000u));
-    o[q] = h0 | (h1 << 16);
-  }
-  return make_uint4(o[0], o[1], o[2], o[3]);
-}
 
 template <int MT, int MODE, int LAYOUT, int ALGO, int U, bool NORM>
 __global__ __launch_bounds__(kMaxNT) void k_gemv_fused(const uint8_t* __restrict__ x,
@@ -137,12 +114,7 @@ __global__ __launch_bounds__(kMaxNT) void k_gemv_fused(const uint8_t* __restrict
       if (i < M * T) sst[i] = sv[c];
     }
     __syncthreads();
-    for (int m = wave; m < M; m += nw) {  // one wave per row, fixed summation order
-      float a = 0.0f;
-      for (int t = lane; t < T; t += 64) a += sst[m * T + t];
-      a = wave_sum(a);
-      if (lane == 0) rstd_s[m] = rsqrtf(a / (float)K + fa.eps);
-    }
+    row_rstd(sst, M, T, K, fa.eps, rstd_s);
     __syncthreads();
   }
   if (NORM) {
@@ -224,57 +196,7 @@ __global__ __launch_bounds__(kMaxNT) void k_gemv_fused(const uint8_t* __restrict
     return;
   }
 
-  // ---- residual epilogue ----
-  constexpr int NV = MT * 256;
-  constexpr int VPT = NV / 64;  // values per thread at most (NT >= 64)
-  float av[VPT];
-#pragma unroll
-  for (int q = 0; q < VPT; ++q) {
-    const int v = threadIdx.x + q * NT;
-    float a = 0.0f;
-    if (v < NV)
-      for (int w2 = 0; w2 < nw; ++w2) a += red[w2 * NV + v];
-    av[q] = a;
-  }
-  float* part = reinterpret_cast<float*>(out);  // [S][M][NO] split partials
-  if (S > 1) {
-#pragma unroll
-    for (int q = 0; q < VPT; ++q) {
-      const int v = threadIdx.x + q * NT;
-      if (v >= NV) continue;
-      const int mt = v >> 8, i = (v >> 6) & 3, ln = v & 63;
-      const int m = mt * 16 + 4 * (ln >> 4) + i;
-      if (m < M)
-        cstore(reinterpret_cast<uint32_t*>(part + ((int64_t)sidx * M + m) * NO + rb * 16 + (ln & 15)), as_u32(av[q]));
-    }
-    stores_done();
-    __syncthreads();
-    if (threadIdx.x == 0) last_s = cadd(&fa.cnt[rb], 1u) == (uint32_t)(S - 1);
-    __syncthreads();
-    if (!last_s) return;
-  }
-#pragma unroll
-  for (int q = 0; q < VPT; ++q) {
-    const int v = threadIdx.x + q * NT;  // uniform per wave: NT and NV are multiples of 64
-    if (v >= NV) continue;
-    const int mt = v >> 8, i = (v >> 6) & 3, ln = v & 63;
-    const int m = mt * 16 + 4 * (ln >> 4) + i;
-    const int mm = min(m, M - 1);
-    const int64_t n = rb * 16 + (ln & 15);
-    float y = av[q];
-    if (S > 1) {
-      y = 0.0f;
-      for (int s2 = 0; s2 < S; ++s2)
-        y += s2 == sidx ? av[q] : as_f32(cload(reinterpret_cast<const uint32_t*>(part + ((int64_t)s2 * M + mm) * NO + n)));
-    }
-    const float xn = round_bf16(bf16_to_f32(fa.res_in[(int64_t)mm * NO + n]) + round_bf16(y));
-    if (m < M) fa.res_out[(int64_t)m * NO + n] = f32_to_bf16(xn);
-    float sq = xn * xn;  // the 16 lanes sharing (mt, i, g) hold the 16 columns of one row
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) sq += __shfl_xor(sq, o, kWave);
-    if (m < M && (ln & 15) == 0) fa.ss_out[(int64_t)m * (NO >> 4) + rb] = sq;
-  }
-  if (S > 1 && threadIdx.x == 0) cstore(&fa.cnt[rb], 0u);
+  residual_epilogue<MT>(red, nw, M, NO, rb, sidx, S, ones, 1.0f, reinterpret_cast<float*>(out), fa, &last_s);
 }
 
 // RMSNorm of whole rows for shapes whose slice does not fit the GEMV's LDS staging:
@@ -284,12 +206,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const uint16_t* __restrict
                                                       uint16_t* __restrict__ h) {
   __shared__ float rstd;
   const int m = blockIdx.x, T = (int)(K >> 4);
-  if (threadIdx.x < 64) {  // one wave, the fused prologue's summation order
-    float a = 0.0f;
-    for (int t = threadIdx.x; t < T; t += 64) a += ss_in[(int64_t)m * T + t];
-    a = wave_sum(a);
-    if (threadIdx.x == 0) rstd = rsqrtf(a / (float)K + eps);
-  }
+  row_rstd(ss_in + (int64_t)m * T, 1, T, K, eps, &rstd);  // the fused prologues' summation order
   __syncthreads();
   const uint8_t* xr = reinterpret_cast<const uint8_t*>(x + m * K);
   for (int64_t c = threadIdx.x; c < K / 8; c += blockDim.x) {

@@ -276,6 +276,111 @@ KRQ_DEV void cmax(uint32_t* p, uint32_t v) {
 // waits until every store and atomic this thread issued has completed
 KRQ_DEV void stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// ---------------------------------------------------------------------------------------------
+// RMSNorm prologue and residual epilogue of the fused GEMVs (reference engine/kernels/
+// fused_gemv.py:48-120): h = bf16(bf16(x * rstd) * w_ln), rstd = rsqrt(ss / K + eps) with ss the
+// sum of the row's [K/16] per-tile partials; x_new = bf16(res_in + bf16(y)) with per-tile sums of
+// squares of x_new.
+// ---------------------------------------------------------------------------------------------
+constexpr int kOutResidual = KRQ_OUT_RESIDUAL;
+
+struct FusedArgs {
+  const uint16_t* ln;  // RMSNorm weight [K] bf16 (null: no RMSNorm prologue)
+  const float* ss_in;  // [M][K/16] per-tile sums of squares of x
+  float eps;
+  const uint16_t* res_in;  // residual epilogue: bf16 [M][N] residual rows
+  uint16_t* res_out;       // bf16 [M][N] new residual rows
+  float* ss_out;           // [M][N/16] per-tile sums of squares of res_out
+  uint32_t* cnt;           // [N/16] split-arrival counters (zero between launches)
+};
+
+KRQ_DEV uint4 norm8(uint4 xv, uint4 lv, float rstd) {
+  const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w}, la[4] = {lv.x, lv.y, lv.z, lv.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float x0 = round_bf16(as_f32(xa[q] << 16) * rstd), x1 = round_bf16(as_f32(xa[q] & 0xffff0000u) * rstd);
+    const uint32_t h0 = f32_to_bf16(x0 * as_f32(la[q] << 16)), h1 = f32_to_bf16(x1 * as_f32(la[q] & 0xffff0000u));
+    o[q] = h0 | (h1 << 16);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// rstd[m] for m < M from the [M][T] partials staged in LDS (sst): one wave per row, lanes take
+// t = lane, lane + 64, ... and the wave sum folds them, the same order in every kernel that
+// normalizes (so the fused prologues and k_rmsnorm_rows agree bit for bit).
+KRQ_DEV void row_rstd(const float* sst, int M, int T, int64_t K, float eps, float* rstd) {
+  const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+  for (int m = threadIdx.x >> 6; m < M; m += nw) {
+    float a = 0.0f;
+    for (int t = lane; t < T; t += 64) a += sst[m * T + t];
+    a = wave_sum(a);
+    if (lane == 0) rstd[m] = rsqrtf(a / (float)K + eps);
+  }
+}
+
+// Residual epilogue of one row block rb (P == 1 accumulators in red). One split's value is
+// (sum over waves) * xs[m] * wsc, as the partials epilogue writes it. With S > 1 splits each split
+// writes its partial tile to part [S][M][NO] with write-through stores, waits for them, and bumps
+// cnt[rb]; the split that brings the count to S sums the S partials in split order, finishes the
+// tile and zeroes the counter. last_s: a shared word. Called by every thread of the block.
+template <int MT>
+KRQ_DEV void residual_epilogue(const float* red, int nw, int M, int64_t NO, int64_t rb, int sidx, int S,
+                               const float* xs, float wsc, float* part, const FusedArgs& fa,
+                               uint32_t* last_s) {
+  constexpr int NV = MT * 256;
+  constexpr int VPT = NV / 64;  // values per thread at most (blockDim.x >= 64)
+  const int NT = blockDim.x;
+  float av[VPT];
+#pragma unroll
+  for (int q = 0; q < VPT; ++q) {
+    const int v = threadIdx.x + q * NT;
+    float a = 0.0f;
+    if (v < NV) {
+      for (int w2 = 0; w2 < nw; ++w2) a += red[w2 * NV + v];
+      const int ln = v & 63, m = (v >> 8) * 16 + 4 * (ln >> 4) + ((v >> 6) & 3);
+      a = a * xs[m] * wsc;
+    }
+    av[q] = a;
+  }
+  if (S > 1) {
+#pragma unroll
+    for (int q = 0; q < VPT; ++q) {
+      const int v = threadIdx.x + q * NT;
+      if (v >= NV) continue;
+      const int ln = v & 63, m = (v >> 8) * 16 + 4 * (ln >> 4) + ((v >> 6) & 3);
+      if (m < M)
+        cstore(reinterpret_cast<uint32_t*>(part + ((int64_t)sidx * M + m) * NO + rb * 16 + (ln & 15)), as_u32(av[q]));
+    }
+    stores_done();
+    __syncthreads();
+    if (threadIdx.x == 0) *last_s = cadd(&fa.cnt[rb], 1u) == (uint32_t)(S - 1);
+    __syncthreads();
+    if (!*last_s) return;
+  }
+#pragma unroll
+  for (int q = 0; q < VPT; ++q) {
+    const int v = threadIdx.x + q * NT;  // uniform per wave: NT and NV are multiples of 64
+    if (v >= NV) continue;
+    const int ln = v & 63, m = (v >> 8) * 16 + 4 * (ln >> 4) + ((v >> 6) & 3);
+    const int mm = min(m, M - 1);
+    const int64_t n = rb * 16 + (ln & 15);
+    float y = av[q];
+    if (S > 1) {
+      y = 0.0f;
+      for (int s2 = 0; s2 < S; ++s2)
+        y += s2 == sidx ? av[q] : as_f32(cload(reinterpret_cast<const uint32_t*>(part + ((int64_t)s2 * M + mm) * NO + n)));
+    }
+    const float xn = round_bf16(bf16_to_f32(fa.res_in[(int64_t)mm * NO + n]) + round_bf16(y));
+    if (m < M) fa.res_out[(int64_t)m * NO + n] = f32_to_bf16(xn);
+    float sq = xn * xn;  // the 16 lanes sharing (mt, i, g) hold the 16 columns of one row
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) sq += __shfl_xor(sq, o, kWave);
+    if (m < M && (ln & 15) == 0) fa.ss_out[(int64_t)m * (NO >> 4) + rb] = sq;
+  }
+  if (S > 1 && threadIdx.x == 0) cstore(&fa.cnt[rb], 0u);
+}
+
 // block of launch planning shared by the GEMV entry points
 struct Plan {
   int nw;  // waves per block

@@ -1,0 +1,289 @@
+// The FP8 skinny GEMM / GEMV kernel template, shared by the plain entry points (gemv_fp8.hip) and
+// the fused ones (fused_fp8.hip): y = (x8 . w8^T) * x_scale[m] * w_scale[n], fp32 accumulate.
+// Layout, step and epilogue conventions: gemv_common.h.
+//
+// Activation kinds (template XK):
+//   KRQ_X_FP8          x is e4m3 [M, K] with its scale; matrix-core A operands are loaded from
+//                      global memory by the lanes whose row m < M.
+//   KRQ_X_BF16_DYN     x is bf16 [1, K]; the block computes the per-token scale itself
+//                      (amax over all of K, ActScale arithmetic), quantizes its K slice into LDS.
+//   KRQ_X_BF16_STATIC  x is bf16 [M, K] with a given inverse scale (SharedScale / ActScale
+//                      inv, per tensor or per row); the block quantizes its K slice into LDS.
+// NORM (bf16 kinds only): the bf16 rows are first normalized, h = bf16(bf16(x * rstd) * w_ln)
+// with rstd from the [M][K/16] sum-of-squares partials, and h is what gets scaled and quantized
+// (the per-token amax of KRQ_X_BF16_DYN is taken over h).
+// The activation loads of the fused kinds are issued before the first weight batch, so their
+// latency (L2 hits) overlaps the weight stream's; quantization uses the hardware e4m3 convert
+// after the reference's clamp, which is bit-identical to the software encoder.
+#pragma once
+
+#include "gemv_common.h"
+
+namespace {
+using namespace krq;
+
+// 16-byte activation chunks per thread in the fused prologues: every chunk load is issued (see
+// the kernel), so the one-row prologue, which reads the whole row for its amax, keeps the count
+// small and takes more waves for long rows instead
+constexpr int kXChunks = 8;
+constexpr int kXChunksDyn = 4;
+// 16-byte (four-partial) sum-of-squares chunks per thread in the RMSNorm prologue
+constexpr int kSsChunks = 4;
+constexpr int kSsChunksDyn = 1;
+constexpr int kMaxThreads = 512;
+
+// PB = 2 (MFMA kernels, modes other than SwiGLU): the block owns two adjacent row blocks, so each
+// activation load feeds two matrix-core products (at M > 1 the activation slices are as large as
+// the weight steps, and every row block re-reads them).
+template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, int PB, bool NORM>
+KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restrict__ xsc,
+                           const float* __restrict__ xinv, int x_per_row, const uint8_t* __restrict__ w8,
+                           const float* __restrict__ wsc, int w_per_row, int M, int64_t NO, int64_t K,
+                           int kts, void* __restrict__ out, void* __restrict__ aux, const FusedArgs& fa) {
+  // nw*P*MT*256 partial sums | e4m3 activation slice [M][ks] | (NORM) sum-of-squares [M][K/16]
+  extern __shared__ float red[];
+  __shared__ float xs_l[32], rstd_s[32];
+  __shared__ float amax_w[kMaxThreads / 64];
+  __shared__ uint32_t last_s;
+  static_assert(PB == 1 || (MODE != KRQ_OUT_SWIGLU && MODE != kOutResidual && ALGO != 2),
+                "paired row blocks: MFMA, no SwiGLU or residual epilogue");
+  static_assert(!NORM || XK != KRQ_X_FP8, "the RMSNorm prologue takes bf16 activations");
+  constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : PB;  // weight row blocks streamed per step
+  constexpr bool FUSED = XK != KRQ_X_FP8;
+  constexpr int SC = XK == KRQ_X_BF16_DYN ? kSsChunksDyn : kSsChunks;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t rb = (int64_t)blockIdx.x * PB, rbu = MODE == KRQ_OUT_SWIGLU ? rb + (NO >> 4) : rb + 1;
+  const int sidx = blockIdx.y;
+  const int nsteps = (kts + 1) >> 1;
+  const int64_t tbase = (int64_t)sidx * kts;
+  const int64_t k0 = tbase * 64;  // first K element of this split
+  const int ks = kts * 64;        // K elements of this split
+  const int T = (int)(K >> 4);    // sum-of-squares partials per row
+  uint8_t* xq = reinterpret_cast<uint8_t*>(red + nw * P * MT * 256);
+  const int jcount = wave < nsteps ? (nsteps - wave + nw - 1) / nw : 0;
+  const ColScales cs = load_col_scales<MODE, PB>(wsc, w_per_row, NO, rb);
+
+  // ---- fused activation prologue, part 1: activation loads ahead of the weight stream ----
+  // Every load of the prologue and of the step ring is issued unconditionally, at a clamped (valid)
+  // address where it is not needed: a branch around a load makes the compiler's wait counts
+  // conservative (a full drain, vmcnt(0)) at the join, which serializes the weight stream.
+  uint4 xv[kXChunks], lv[kXChunks], sv[SC];
+  const uint8_t* lnb = reinterpret_cast<const uint8_t*>(fa.ln);
+  if (XK == KRQ_X_BF16_DYN) {
+#pragma unroll
+    for (int c = 0; c < kXChunksDyn; ++c) {
+      const int64_t e = min(8 * (int64_t)(threadIdx.x + c * blockDim.x), K - 8);
+      xv[c] = ld16(x + 2 * e);  // chunks past K repeat the last one (same amax)
+      if (NORM) lv[c] = ld16(lnb + 2 * e);
+    }
+  } else if (XK == KRQ_X_BF16_STATIC) {
+    const int cpr = ks >> 3;  // chunks per row of the slice
+#pragma unroll
+    for (int c = 0; c < kXChunks; ++c) {
+      const int idx = threadIdx.x + c * blockDim.x, m = idx / cpr;
+      const int64_t e = k0 + 8 * (idx - m * cpr);
+      xv[c] = ld16(x + 2 * ((int64_t)min(m, M - 1) * K + e));
+      if (NORM) lv[c] = ld16(lnb + 2 * e);
+    }
+  }
+  if (NORM) {
+    const int nss = M * T / 4;  // 16-byte chunks of the partials
+#pragma unroll
+    for (int c = 0; c < SC; ++c)
+      sv[c] = ld16(reinterpret_cast<const uint8_t*>(fa.ss_in) + 16 * min((int)threadIdx.x + c * (int)blockDim.x, nss - 1));
+  }
+
+  // scale of this thread's activation row, read now so its latency hides under the weight stream
+  // (every thread loads and stores it, threads t and t + 32 the same value, so the load is not
+  // sunk into a branch after the weight loads)
+  const int xrow = min((int)(threadIdx.x & 31), M - 1);
+  const float xs_reg = XK != KRQ_X_BF16_DYN ? xsc[x_per_row ? xrow : 0] : 1.0f;
+
+  // ---- weight (and, for e4m3 activations, A operand) loads: a ring of U step slots ----
+  uint4 wl[U], wh[U], ul[U], uh[U], xl[U][MT], xh[U][MT];
+  // A slot past this wave's last step reloads that step (an address already in flight or cached,
+  // so no extra HBM traffic) and is masked where consumed. Rows m >= M read row M - 1: their
+  // products land in accumulator rows the epilogue never writes.
+  auto load_slot = [&](int u, int cc) {
+    const int j = jcount > 0 ? wave + min(cc, jcount - 1) * nw : 0;
+    const int64_t t0 = tbase + 2 * j;
+    const int64_t t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
+    wl[u] = ld16nt(w_addr<LAYOUT>(w8, rb, t0, K, lane));
+    wh[u] = ld16nt(w_addr<LAYOUT>(w8, rb, t1, K, lane));
+    if (P == 2) {
+      ul[u] = ld16nt(w_addr<LAYOUT>(w8, rbu, t0, K, lane));
+      uh[u] = ld16nt(w_addr<LAYOUT>(w8, rbu, t1, K, lane));
+    }
+    if (!FUSED) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = ALGO == 2 ? 0 : min(mt * 16 + r, M - 1);
+        const uint8_t* xr = x + (int64_t)m * K + g * 16;
+        xl[u][mt] = ld16(xr + t0 * 64);
+        xh[u][mt] = ld16(xr + t1 * 64);
+      }
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < U; ++u) load_slot(u, u);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- RMSNorm (NORM): row rstd from the partials, then normalize the loaded chunks ----
+  if (NORM) {
+    float* sst = reinterpret_cast<float*>(xq + (size_t)M * ks);
+    const int nss = M * T / 4;
+#pragma unroll
+    for (int c = 0; c < SC; ++c) {
+      const int i = threadIdx.x + c * blockDim.x;
+      if (i < nss) *reinterpret_cast<uint4*>(sst + 4 * i) = sv[c];
+    }
+    __syncthreads();
+    row_rstd(sst, M, T, K, fa.eps, rstd_s);
+    __syncthreads();
+    if (XK == KRQ_X_BF16_DYN) {
+#pragma unroll
+      for (int c = 0; c < kXChunksDyn; ++c) xv[c] = norm8(xv[c], lv[c], rstd_s[0]);
+    } else {
+      const int cpr = ks >> 3;
+#pragma unroll
+      for (int c = 0; c < kXChunks; ++c) {
+        const int m = (threadIdx.x + c * blockDim.x) / cpr;
+        xv[c] = norm8(xv[c], lv[c], rstd_s[min(m, M - 1)]);
+      }
+    }
+  }
+
+  // ---- fused activation prologue, part 2: scale, quantize the slice into LDS ----
+  if (XK == KRQ_X_FP8) {
+    xs_l[threadIdx.x & 31] = xs_reg;
+  } else if (XK == KRQ_X_BF16_DYN) {
+    float am = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kXChunksDyn; ++c) am = absmax8(xv[c], am);
+    am = wave_max(am);
+    if (lane == 0) amax_w[wave] = am;
+    __syncthreads();
+    float a = amax_w[0];
+    for (int w = 1; w < nw; ++w) a = fmaxf(a, amax_w[w]);
+    a = fmaxf(a, 1e-6f);
+    const float inv = inv_from_amax(a);
+    if (threadIdx.x == 0) xs_l[0] = scale_from_amax(a);
+#pragma unroll
+    for (int c = 0; c < kXChunksDyn; ++c) {
+      const int64_t e = 8 * (int64_t)(threadIdx.x + c * blockDim.x);
+      if (e >= k0 && e < k0 + ks) *reinterpret_cast<uint2*>(xq + (e - k0)) = quant8(xv[c], inv);
+    }
+  } else {
+    const int cpr = ks >> 3;
+#pragma unroll
+    for (int c = 0; c < kXChunks; ++c) {
+      const int idx = threadIdx.x + c * blockDim.x, m = idx / cpr;
+      if (m < M)
+        *reinterpret_cast<uint2*>(xq + (int64_t)m * ks + 8 * (idx - m * cpr)) =
+            quant8(xv[c], xinv[x_per_row ? m : 0]);
+    }
+    xs_l[threadIdx.x & 31] = xs_reg;
+  }
+  if (FUSED) __syncthreads();
+
+  // ---- main loop: consume slot u (step cc), then refill it with step cc + U ----
+  v4f acc[MT], accu[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+    accu[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+  }
+  float s0 = 0.f, s1 = 0.f, q0 = 0.f, q1 = 0.f;  // vector-ALU partial sums
+  auto consume_slot = [&](int u, int cc) {
+    const int j = jcount > 0 ? wave + min(cc, jcount - 1) * nw : 0;
+    const bool ok = cc < jcount, hi = ok && (2 * j + 1 < kts);
+    if (FUSED) {
+      // the quantized slice ends at ks: the high tile of an odd last step is zero (not stale LDS)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = ALGO == 2 ? 0 : min(mt * 16 + r, M - 1);
+        const uint8_t* xr = xq + (int64_t)m * ks + g * 16;
+        xl[u][mt] = *reinterpret_cast<const uint4*>(xr + (2 * j) * 64);
+        xh[u][mt] = sel4(2 * j + 1 < kts, *reinterpret_cast<const uint4*>(xr + min(2 * j + 1, kts - 1) * 64));
+      }
+    }
+    const uint4 bl = sel4(ok, wl[u]), bh = sel4(hi, wh[u]);
+    if (ALGO == 2) {
+      s0 = dot16_fp8(bl, xl[u][0], s0);
+      s1 = dot16_fp8(bh, xh[u][0], s1);
+      if (P == 2) {
+        q0 = dot16_fp8(sel4(ok, ul[u]), xl[u][0], q0);
+        q1 = dot16_fp8(sel4(hi, uh[u]), xh[u][0], q1);
+      }
+    } else {
+      const v8i B = pack_v8i(bl, bh);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const v8i A = pack_v8i(xl[u][mt], xh[u][mt]);
+        acc[mt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc[mt], 0, 0, 0, 0, 0, 0);
+      }
+      if (P == 2) {
+        const v8i Bu = pack_v8i(sel4(ok, ul[u]), sel4(hi, uh[u]));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const v8i A = pack_v8i(xl[u][mt], xh[u][mt]);
+          accu[mt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, Bu, accu[mt], 0, 0, 0, 0, 0, 0);
+        }
+      }
+    }
+  };
+  // the last batch is peeled off (consume only), so no load sits behind a branch and the first
+  // batch's loads stay ahead of everything else
+  int base = 0;
+  for (; base + U < jcount; base += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      consume_slot(u, base + u);
+      load_slot(u, base + u + U);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) consume_slot(u, base + u);
+  if (ALGO == 2) {
+    // the four lanes of row r (g = 0..3) hold partial sums of disjoint k: add them; lanes 0..15
+    // then carry columns 16*rb + lane in MFMA slot (mt 0, i 0), i.e. output row m = 0
+    float a = s0 + s1, au = q0 + q1;
+    a += __shfl_xor(a, 16, kWave);
+    a += __shfl_xor(a, 32, kWave);
+    au += __shfl_xor(au, 16, kWave);
+    au += __shfl_xor(au, 32, kWave);
+    acc[0] = v4f{g == 0 ? a : 0.f, 0.f, 0.f, 0.f};
+    accu[0] = v4f{g == 0 ? au : 0.f, 0.f, 0.f, 0.f};
+  }
+  stash<MT, P>(red, wave, lane, acc, accu);
+  __syncthreads();
+  if constexpr (MODE == kOutResidual) {
+    residual_epilogue<MT>(red, nw, M, NO, rb, sidx, gridDim.y, xs_l, cs.g, reinterpret_cast<float*>(out), fa,
+                          &last_s);
+  } else {
+    epilogue<MT, MODE, P>(red, 0, nw, M, NO, rb, sidx, xs_l, cs, out, aux);
+    if (PB == 2) epilogue<MT, MODE, P>(red, 1, nw, M, NO, rbu, sidx, xs_l, ColScales{cs.u, 1.0f}, out, aux);
+  }
+}
+
+#define KRQ_FP8_KERNEL_PARAMS                                                                             \
+  const uint8_t *__restrict__ x, const float *__restrict__ xsc, const float *__restrict__ xinv, int x_per_row, \
+      const uint8_t *__restrict__ w8, const float *__restrict__ wsc, int w_per_row, int M, int64_t NO,        \
+      int64_t K, int kts, void *__restrict__ out, void *__restrict__ aux
+
+// the plain kernel (gemv_fp8.hip)
+template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, int PB>
+__global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(KRQ_FP8_KERNEL_PARAMS) {
+  gemv_fp8_body<MT, MODE, LAYOUT, XK, ALGO, U, PB, false>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M, NO, K,
+                                                          kts, out, aux, FusedArgs{});
+}
+
+// the fused kernel (fused_fp8.hip): RMSNorm prologue and / or residual epilogue
+template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, bool NORM>
+__global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8_fused(KRQ_FP8_KERNEL_PARAMS, FusedArgs fa) {
+  gemv_fp8_body<MT, MODE, LAYOUT, XK, ALGO, U, 1, NORM>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M, NO, K,
+                                                        kts, out, aux, fa);
+}
+
+}  // namespace

@@ -20,11 +20,19 @@ accepted and has nothing to do.
 When a block's normalized K slice does not fit the kernel's LDS staging (large M x K/split), the
 rows are normalized by krq_rmsnorm_rows first and the GEMV runs on the result: two launches, same
 arithmetic.
+
+FP8 weights (an FP8Weight from kernels.fp8.quantize / quantize_weight, as the reference's FP8 engine
+holds them) take the FP8 form of the same kernels (krq_gemv_fp8_fused): the normalized rows are
+scaled and quantized in the prologue - per token over the normalized row at M = 1, or with the
+static inverse scale of a SharedScale / ActScale `a` at any M - and the residual epilogue sums the
+scaled split partials. Rows the prologue cannot stage (M > 1 with per-token scales) go through
+krq_rmsnorm_quant_rows first (the values of quant_rows(rmsnorm(x))).
 """
 
 import torch
 
 from . import _lib as L
+from . import fp8 as _fp8
 from . import gemv as _gemv
 
 MAX_ROWS = 32
@@ -54,11 +62,8 @@ def _norm_args(x, norm, mode, split):
     normalized by a separate launch and no norm in the GEMV."""
     if norm is None:
         return x, None, None
-    ln, ss = norm
+    ln, ss = _check_norm(x, norm)
     M, K = x.shape
-    L.require_device(ln, ss)
-    if ln.dtype != torch.bfloat16 or ln.numel() != K or ss.dtype != torch.float32 or ss.numel() != M * (K // 16):
-        raise ValueError("norm=(ln [K] bf16, ss [M, K/16] fp32 from FusedLayerBuffers.ss)")
     if L.lib().krq_gemv_fused_fits(M, K, split, mode, 1):
         return x, ln, ss
     return None, ln, ss
@@ -79,23 +84,114 @@ def _launch(x, w, split, mode, norm, ep, eps, out):
     wt, layout = _gemv._weight(w)
     res_in = res_out = ss_out = cnt = None
     if ep is not None:
-        res_in, res_out, ss_out, cnt = ep
-        L.require_device(res_in, res_out, ss_out, cnt)
-        if ss_out.numel() != M * (N // 16) or res_in.numel() != M * N or res_out.numel() != M * N:
-            raise ValueError("ep=(res_in [M, N], res_out [M, N], ss_out [M, N/16], cnt) from FusedLayerBuffers")
-        if split > 1 and cnt.numel() < N // 16:
-            raise ValueError(f"cnt holds {cnt.numel()} counters, needs {N // 16}")
+        res_in, res_out, ss_out, cnt = _check_ep(ep, M, N, split)
     L.call("krq_gemv_bf16_fused", L.ptr(xin), L.ptr(wt), layout, M, N, K, split, mode, L.ptr(ln), L.ptr(ss),
            float(eps), L.ptr(res_in), L.ptr(res_out), L.ptr(ss_out), L.ptr(cnt), L.ptr(out), L.stream(x))
     return out
 
 
-def gemv_fused(x, w, split, *, norm=None, zero_ss=None, ep=None, eps=1e-6):
-    """x [M, K] bf16, w [N, K] bf16.
+def _is_fp8(w):
+    return isinstance(w, tuple) and len(w) >= 2 and w[0].dtype == torch.float8_e4m3fn
+
+
+def _check_ep(ep, M, N, split):
+    res_in, res_out, ss_out, cnt = ep
+    L.require_device(res_in, res_out, ss_out, cnt)
+    if ss_out.numel() != M * (N // 16) or res_in.numel() != M * N or res_out.numel() != M * N:
+        raise ValueError("ep=(res_in [M, N], res_out [M, N], ss_out [M, N/16], cnt) from FusedLayerBuffers")
+    if split > 1 and cnt.numel() < N // 16:
+        raise ValueError(f"cnt holds {cnt.numel()} counters, needs {N // 16}")
+    return ep
+
+
+def _check_norm(x, norm):
+    ln, ss = norm
+    M, K = x.shape
+    L.require_device(ln, ss)
+    if ln.dtype != torch.bfloat16 or ln.numel() != K or ss.dtype != torch.float32 or ss.numel() != M * (K // 16):
+        raise ValueError("norm=(ln [K] bf16, ss [M, K/16] fp32 from FusedLayerBuffers.ss)")
+    return ln, ss
+
+
+def _launch_fp8(x, q, split, mode, norm, ep, eps, a, out):
+    """One krq_gemv_fp8_fused launch, or the two-launch forms when the prologue cannot stage x."""
+    w, layout, ws, (N, K) = _fp8._weight_operand(q)
+    M = x.shape[0]
+    wpr = 1 if ws.numel() > 1 else 0
+    if norm is not None and ep is not None:
+        raise ValueError("FP8 fused GEMVs take the RMSNorm prologue or the residual epilogue, not both")
+    ln = ss = None
+    if norm is not None:
+        ln, ss = _check_norm(x, norm)
+    res_in = res_out = ss_out = cnt = None
+    if ep is not None:
+        res_in, res_out, ss_out, cnt = _check_ep(ep, M, N, split)
+    fits = L.lib().krq_gemv_fp8_fused_fits
+    kind = L.X_BF16_STATIC if a is not None else L.X_BF16_DYN
+    if not fits(M, K, split, mode, kind, 1 if norm is not None else 0):
+        # stage outside: normalize (and quantize) the rows first, then e4m3 activations
+        if norm is not None:
+            if a is None:
+                x8 = torch.empty((M, K), device=x.device, dtype=torch.float8_e4m3fn)
+                xs = torch.empty((M,), device=x.device, dtype=torch.float32)
+                L.call("krq_rmsnorm_quant_rows", L.ptr(x), L.ptr(ss), L.ptr(ln), float(eps), M, K, L.ptr(x8),
+                       L.ptr(xs), L.stream(x))
+            else:
+                x8, xs = _fp8._cast(_rmsnorm(x, ln, ss, eps), a), a.scale.reshape(1)
+            return _fp8.gemv_fp8_launch(x8, xs, q, split, mode, L.ALGO_MFMA, out)
+        x8, xs = _fp8._activation_fp8(x, a, None)
+        kind, xin, x_scale, x_inv = L.X_FP8, x8, xs, None
+    elif a is not None:
+        xin, x_scale, x_inv = x, a.scale.reshape(1), a.inv.reshape(1)
+    else:
+        xin, x_scale, x_inv = x, None, None
+    xpr = 1 if (x_scale is not None and x_scale.numel() == M and M > 1) else 0
+    L.require_device(x_scale, x_inv)
+    L.call("krq_gemv_fp8_fused", L.ptr(xin), kind, L.ptr(x_scale), L.ptr(x_inv), xpr, L.ptr(w), layout, L.ptr(ws),
+           wpr, M, N, K, split, mode, L.ptr(ln), L.ptr(ss), float(eps), L.ptr(res_in), L.ptr(res_out),
+           L.ptr(ss_out), L.ptr(cnt), L.ptr(out), L.stream(x))
+    return out
+
+
+def _fp8_fused(x, q, split, mode, norm, ep, eps, a):
+    if x.dtype != torch.bfloat16 or x.dim() != 2:
+        raise ValueError("fused FP8 GEMVs expect bf16 x [M, K]")
+    L.require_device(x)
+    x = x.contiguous()
+    M, K = x.shape
+    N = q[0].shape[0]
+    if q[0].shape[1] != K:
+        raise ValueError(f"x {tuple(x.shape)} and w {tuple(q[0].shape)} do not match")
+    if M > MAX_ROWS:
+        raise ValueError(f"fused GEMVs take at most {MAX_ROWS} rows, got {M}")
+    if norm is None and ep is None:  # nothing to fuse: the plain FP8 GEMV
+        if mode == L.OUT_SWIGLU:
+            return _fp8.gemv_swiglu_fp8(x, q, a)
+        return _fp8.gemv_fp8(x, q, split, a)
+    if mode == L.OUT_RESIDUAL:
+        part = torch.empty((split, M, N), device=x.device, dtype=torch.float32) if split > 1 else None
+        _launch_fp8(x, q, split, mode, norm, ep, eps, a, part)
+        return None
+    if mode == L.OUT_PARTIAL:
+        out = torch.empty((split, M, N), device=x.device, dtype=torch.float32)
+    else:
+        out = torch.empty((M, N // 2 if mode == L.OUT_SWIGLU else N), device=x.device, dtype=torch.bfloat16)
+    return _launch_fp8(x, q, split, mode, norm, ep, eps, a, out)
+
+
+def gemv_fused(x, w, split, *, norm=None, zero_ss=None, ep=None, eps=1e-6, a=None):
+    """x [M, K] bf16, w [N, K] bf16 or an FP8Weight.
     norm=(ln_w, ss_in): normalise x rows on the fly.
     zero_ss: accepted; the per-tile sums need no reset (every producer overwrites them).
     ep=(res_in, res_out, ss_out, cnt): residual epilogue; returns None.
+    a (FP8 weights only): ActScale / SharedScale for static activation scaling; per token if None.
     Otherwise returns bf16 [M, N] (split 1) or fp32 partials [split, M, N]."""
+    if _is_fp8(w):
+        assert x.shape[-1] % split == 0
+        mode = L.OUT_RESIDUAL if ep is not None else (L.OUT_PARTIAL if split > 1 else L.OUT_BF16)
+        return _fp8_fused(x, w, split, mode, norm, ep, eps, a)
+    if a is not None:
+        raise ValueError("activation scales apply to FP8 weights only")
     _check(x, w)
     M, K = x.shape
     N = w.shape[0]
@@ -111,9 +207,13 @@ def gemv_fused(x, w, split, *, norm=None, zero_ss=None, ep=None, eps=1e-6):
     return _launch(x, w, 1, L.OUT_BF16, norm, None, eps, out)
 
 
-def gemv_swiglu_fused(x, w_gu, *, norm=None, zero_ss=None, eps=1e-6):
-    """x [M, K], w_gu [2I, K] = [gate; up] -> bf16(silu(gate) * up) [M, I], with the optional
-    RMSNorm prologue of gemv_fused."""
+def gemv_swiglu_fused(x, w_gu, *, norm=None, zero_ss=None, eps=1e-6, a=None):
+    """x [M, K], w_gu [2I, K] = [gate; up] (bf16 or an FP8Weight) -> bf16(silu(gate) * up) [M, I],
+    with the optional RMSNorm prologue (and, for FP8 weights, activation scaling) of gemv_fused."""
+    if _is_fp8(w_gu):
+        return _fp8_fused(x, w_gu, 1, L.OUT_SWIGLU, norm, None, eps, a)
+    if a is not None:
+        raise ValueError("activation scales apply to FP8 weights only")
     _check(x, w_gu)
     M = x.shape[0]
     out = torch.empty((M, w_gu.shape[0] // 2), device=x.device, dtype=torch.bfloat16)

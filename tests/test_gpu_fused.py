@@ -177,3 +177,208 @@ def test_packfile_rebuilds_tiled_copy_on_device(dev, tmp_path):
     r = packfile.load_fp8(p, device=dev)["qkv"]
     assert torch.equal(r.tiled, q.tiled) and torch.equal(r[1], q[1])
     assert torch.equal(fp8.gemv_fp8(x.to(dev), r, 2), fp8.gemv_fp8(x.to(dev), q, 2))
+
+
+# ---------------------------------------------------------------------------------------------
+# FP8 weights (krq_gemv_fp8_fused, krq_rmsnorm_quant_rows)
+# ---------------------------------------------------------------------------------------------
+def _fp8_oracle(h_u16, q, split=1, inv=None, scale=None):
+    """Oracle of one FP8 GEMV on bf16 rows h: per-token quant_rows (inv None) or the static cast,
+    then the exact product; returns the float64 [split, M, N] scaled partials."""
+    w8 = q[0].cpu().view(torch.uint8).numpy()
+    ws = q[1].cpu().numpy()
+    if inv is None:
+        x8, xs = O.quant_rows(h_u16)
+    else:
+        x8, xs = O.cast(h_u16, np.float32(inv)), np.float32(scale)
+    K = h_u16.shape[1]
+    ks = K // split
+    return np.stack([O.fp8_matmul(x8[:, s * ks:(s + 1) * ks], xs, w8[:, s * ks:(s + 1) * ks], ws)[1]
+                     for s in range(split)])
+
+
+def _norm_inputs(M, K, seed):
+    x = bf((M, K), seed)
+    ln = (1 + 0.1 * torch.randn(K, generator=torch.Generator().manual_seed(seed + 1))).to(torch.bfloat16)
+    ss = O.tile_sumsq(u16(x)).astype(np.float32)
+    h = O.rmsnorm_rows(u16(x), ss.astype(np.float64).sum(1), u16(ln), EPS)
+    return x, ln, ss, h
+
+
+@pytest.mark.parametrize("M,N,split,swiglu", [(1, NQKV, 2, False), (1, 2 * I, 1, True), (16, NQKV, 2, False),
+                                              (16, 2 * I, 1, True), (32, NQKV, 1, False)])
+def test_fp8_rmsnorm_prologue_per_token(dev, M, N, split, swiglu):
+    """norm=(ln, ss) with per-token scales: in the GEMV prologue at M = 1, krq_rmsnorm_quant_rows
+    first at M > 1. Bit-identical to rmsnorm_rows -> the plain FP8 GEMV, and within the bar of the
+    oracle (quant_rows of the normalized rows, exact FP8 product)."""
+    from kernels import fp8 as F
+    from kernels import fused_gemv as FG
+    x, ln, ss, h = _norm_inputs(M, H, 70 + M)
+    q = F.quantize(bf((N, H), 71, 0.02).to(dev))
+    xd, lnd, ssd = x.to(dev), ln.to(dev), torch.from_numpy(ss).to(dev)
+    hd = FG._rmsnorm(xd, lnd, ssd, EPS)
+    if swiglu:
+        got = gemv_swiglu_fused(xd, q, norm=(lnd, ssd), eps=EPS)
+        two = F.gemv_swiglu_fp8(hd, q)
+        full = _fp8_oracle(h, q)[0]
+        ref = O.bf16_to_f32(O.swiglu(full[:, :N // 2].astype(np.float32), full[:, N // 2:].astype(np.float32)))
+        gotn = got.float().cpu().numpy()
+    else:
+        got = gemv_fused(xd, q, split, norm=(lnd, ssd), eps=EPS)
+        two = F.gemv_fp8(hd, q, split)
+        ref = _fp8_oracle(h, q, split).sum(0)
+        gotn = sum_partials(got) if split > 1 else got.float().cpu().numpy()
+    assert torch.equal(got, two), "fused prologue differs from rmsnorm_rows + gemv_fp8"
+    e = rel_err(gotn, ref)
+    print(f"fp8 norm M={M} N={N} split={split}: max-rel {e:.2e}")
+    assert e <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 3, 32])
+def test_rmsnorm_quant_rows_is_quant_rows_of_rmsnorm(dev, M):
+    from kernels import fp8 as F
+    from kernels import fused_gemv as FG
+    from kernels import _lib as L
+    x, ln, ss, _ = _norm_inputs(M, H, 80 + M)
+    xd, lnd, ssd = x.to(dev), ln.to(dev), torch.from_numpy(ss).to(dev)
+    x8 = torch.empty((M, H), device=dev, dtype=torch.float8_e4m3fn)
+    xs = torch.empty((M,), device=dev, dtype=torch.float32)
+    L.call("krq_rmsnorm_quant_rows", L.ptr(xd), L.ptr(ssd), L.ptr(lnd), EPS, M, H, L.ptr(x8), L.ptr(xs), L.stream(xd))
+    r8, rs = F.quant_rows(FG._rmsnorm(xd, lnd, ssd, EPS))
+    assert torch.equal(x8.view(torch.uint8), r8.view(torch.uint8)) and torch.equal(xs, rs.reshape(-1))
+
+
+@pytest.mark.parametrize("M,N,split,swiglu", [(1, NQKV, 2, False), (16, NQKV, 2, False), (32, 2 * I, 1, True)])
+def test_fp8_rmsnorm_prologue_static_scale(dev, M, N, split, swiglu):
+    """norm with a static SharedScale a (the reference engine's decode-FP8 form): normalized rows
+    cast with a.inv in the prologue; against the oracle's cast of the normalized rows."""
+    from kernels import fp8 as F
+    x, ln, ss, h = _norm_inputs(M, H, 90 + M)
+    q = F.quantize(bf((N, H), 91, 0.02).to(dev))
+    xd, lnd, ssd = x.to(dev), ln.to(dev), torch.from_numpy(ss).to(dev)
+    amax = float(np.abs(O.bf16_to_f32(h)).max()) * 1.5
+    inv = torch.tensor([448.0 / amax], device=dev)
+    scale = torch.tensor(amax / 448.0, device=dev)
+    a = F.SharedScale(inv, scale)
+    if swiglu:
+        got = gemv_swiglu_fused(xd, q, norm=(lnd, ssd), eps=EPS, a=a).float().cpu().numpy()
+        full = _fp8_oracle(h, q, 1, inv.item(), scale.item())[0]
+        ref = O.bf16_to_f32(O.swiglu(full[:, :N // 2].astype(np.float32), full[:, N // 2:].astype(np.float32)))
+    else:
+        y = gemv_fused(xd, q, split, norm=(lnd, ssd), eps=EPS, a=a)
+        got = sum_partials(y) if split > 1 else y.float().cpu().numpy()
+        ref = _fp8_oracle(h, q, split, inv.item(), scale.item()).sum(0)
+    e = rel_err(got, ref)
+    print(f"fp8 norm static M={M} N={N}: max-rel {e:.2e}")
+    assert e <= TOL
+
+
+@pytest.mark.parametrize("M,split,static", [(1, 4, False), (1, 1, False), (16, 4, False), (32, 2, False),
+                                            (4, 4, True)])
+def test_fp8_residual_epilogue(dev, M, split, static):
+    """ep=(res_in, res_out, ss_out, cnt) on FP8 weights: res_out equals bf16(res_in + bf16(in-order
+    sum of the plain GEMV's scaled partials)) bit for bit, ss_out its per-tile sums of squares, and
+    the counters are zero again (twice in a row); the oracle bounds the whole."""
+    from kernels import fp8 as F
+    K = 4096
+    a_, res = bf((M, K), 100 + M), bf((M, H), 101)
+    q = F.quantize(bf((H, K), 102, 0.02).to(dev))
+    ad, rd = a_.to(dev), res.to(dev)
+    sa = None
+    if static:
+        sa = F.ActScale(ad)
+    bufs = FusedLayerBuffers(M, H, V, dev)
+    p = F.gemv_fp8(ad, q, split, sa)
+    if split > 1:  # the partials summed in split order, then rounded
+        y = p[0].clone()
+        for s in range(1, split):
+            y += p[s]
+        p = y.to(torch.bfloat16)
+    want = (rd.float() + p.float()).to(torch.bfloat16)
+    for _ in range(2):
+        assert gemv_fused(ad, q, split, ep=(rd, bufs.res[1], bufs.ss[1], bufs.cnt), a=sa) is None
+        torch.cuda.synchronize()
+        assert torch.equal(bufs.res[1], want), "residual epilogue differs from the partials path"
+        assert rel_err(bufs.ss[1].cpu().numpy(), O.tile_sumsq(u16(want))) <= 1e-5
+        assert int(bufs.cnt.abs().sum()) == 0
+    if static:
+        ref_y = _fp8_oracle(u16(a_), q, 1, sa.inv.item(), sa.scale.item()).sum(0)
+    else:
+        ref_y = _fp8_oracle(u16(a_), q).sum(0)
+    ref = O.bf16_to_f32(O.residual_add(ref_y, u16(res)))
+    assert rel_err(bufs.res[1].float().cpu().numpy(), ref) <= TOL
+
+
+def test_fp8_layer_fragment_like_the_engine(dev):
+    """o (ep) -> gate_up (norm, SwiGLU) -> down (ep) -> next qkv (norm) on FP8 weights with
+    per-token scales at M = 1. Each stage is checked against the oracle on the inputs that stage
+    actually received (the previous stage's GPU output): chaining two independent runs would
+    compound re-quantization, since a one-ulp change of a residual element can move the per-token
+    amax and with it every e4m3 code of the next stage."""
+    from kernels import fp8 as F
+    M = 1
+    cur, a_ = bf((M, H), 110), bf((M, 4096), 111)
+    ws = {n: bf(s, 112 + i, 0.02) for i, (n, s) in enumerate([("o", (H, 4096)), ("gu", (2 * I, H)),
+                                                               ("down", (H, I)), ("qkv", (NQKV, H))])}
+    q = {n: F.quantize(w.to(dev)) for n, w in ws.items()}
+    ln2 = (1 + 0.1 * torch.randn(H, generator=torch.Generator().manual_seed(120))).to(torch.bfloat16)
+    ln1 = (1 + 0.1 * torch.randn(H, generator=torch.Generator().manual_seed(121))).to(torch.bfloat16)
+    bufs = FusedLayerBuffers(M, H, V, dev)
+    d = lambda t: t.to(dev)
+    gemv_fused(d(a_), q["o"], 4, ep=(d(cur), bufs.res[1], bufs.ss[1], bufs.cnt))
+    act_d = gemv_swiglu_fused(bufs.res[1], q["gu"], norm=(d(ln2), bufs.ss[1]), eps=EPS)
+    gemv_fused(act_d, q["down"], 4, ep=(bufs.res[1], bufs.res[0], bufs.ss[0], bufs.cnt))
+    qkv = gemv_fused(bufs.res[0], q["qkv"], 2, norm=(d(ln1), bufs.ss[0]), eps=EPS)
+    res_b, act, res_a = u16(bufs.res[1]), u16(act_d), u16(bufs.res[0])
+    # stage by stage
+    ref_b = O.residual_add(_fp8_oracle(u16(a_), q["o"]).sum(0), u16(cur))
+    h2 = O.rmsnorm_rows(res_b, O.tile_sumsq(res_b).sum(1), u16(ln2), EPS)
+    full = _fp8_oracle(h2, q["gu"])[0]
+    ref_act = O.swiglu(full[:, :I].astype(np.float32), full[:, I:].astype(np.float32))
+    ref_a = O.residual_add(_fp8_oracle(act, q["down"]).sum(0), res_b)
+    h1 = O.rmsnorm_rows(res_a, O.tile_sumsq(res_a).sum(1), u16(ln1), EPS)
+    qkv_ref = _fp8_oracle(h1, q["qkv"], 2).sum(0)
+    errs = [rel_err(O.bf16_to_f32(res_b), O.bf16_to_f32(ref_b)), rel_err(O.bf16_to_f32(act), O.bf16_to_f32(ref_act)),
+            rel_err(O.bf16_to_f32(res_a), O.bf16_to_f32(ref_a)), rel_err(sum_partials(qkv), qkv_ref)]
+    print("fp8 layer fragment, per stage max-rel: " + " ".join(f"{e:.2e}" for e in errs))
+    assert max(errs) <= TOL
+    assert rel_err(bufs.ss[0].cpu().numpy(), O.tile_sumsq(res_a)) <= 1e-5
+
+
+def test_fp8_fused_graph_replays(dev):
+    """FP8 residual epilogue and RMSNorm prologue captured in a graph: replays equal eager, with
+    eager calls in between, and the counters stay zero."""
+    from kernels import fp8 as F
+    M = 1
+    a_, res = bf((M, 4096), 130), bf((M, H), 131)
+    q_o = F.quantize(bf((H, 4096), 132, 0.02).to(dev))
+    q_qkv = F.quantize(bf((NQKV, H), 133, 0.02).to(dev))
+    ln = torch.ones(H, dtype=torch.bfloat16, device=dev)
+    ad, rd = a_.to(dev), res.to(dev)
+    bufs = FusedLayerBuffers(M, H, V, dev)
+    out = {}
+
+    def step():
+        gemv_fused(ad, q_o, 4, ep=(rd, bufs.res[1], bufs.ss[1], bufs.cnt))
+        out["qkv"] = gemv_fused(bufs.res[1], q_qkv, 2, norm=(ln, bufs.ss[1]), eps=EPS)
+
+    step()
+    torch.cuda.synchronize()
+    eager_res, eager_qkv = bufs.res[1].clone(), out["qkv"].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    graph_qkv = out["qkv"]
+    for _ in range(3):
+        bufs.res[1].zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(bufs.res[1], eager_res) and torch.equal(graph_qkv, eager_qkv)
+        step()
+    assert int(bufs.cnt.abs().sum()) == 0
+    del g
