@@ -197,7 +197,7 @@ int krq_gemv_bf16_fused(const void* x, const void* w, int w_layout, int64_t M, i
                         int split, int mode, const void* ln, const float* ss_in, float eps,
                         const void* res_in, void* res_out, float* ss_out, uint32_t* cnt, void* out,
                         void* stream);
-int64_t krq_gemv_fused_fits(int64_t M, int64_t K, int split, int mode, int norm);
+int64_t krq_gemv_fused_fits(int64_t M, int64_t N, int64_t K, int split, int mode, int norm);
 /* h = bf16(bf16(x * rstd) * ln) for whole bf16 rows x [M][K], rstd as above. */
 int krq_rmsnorm_rows(const void* x, const float* ss_in, const void* ln, float eps, int64_t M, int64_t K,
                      void* h, void* stream);
@@ -223,7 +223,7 @@ int krq_gemv_fp8_fused(const void* x, int x_kind, const float* x_scale, const fl
                        int64_t N, int64_t K, int split, int mode, const void* ln, const float* ss_in,
                        float eps, const void* res_in, void* res_out, float* ss_out, uint32_t* cnt,
                        void* out, void* stream);
-int64_t krq_gemv_fp8_fused_fits(int64_t M, int64_t K, int split, int mode, int x_kind, int norm);
+int64_t krq_gemv_fp8_fused_fits(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind, int norm);
 /* RMSNorm then per-token e4m3 quantization of whole rows: x8 [M][K] e4m3 and x_scale [M] equal
  * krq_quant_rows applied to krq_rmsnorm_rows' output (K <= 16384). */
 int krq_rmsnorm_quant_rows(const void* x, const float* ss_in, const void* ln, float eps, int64_t M,

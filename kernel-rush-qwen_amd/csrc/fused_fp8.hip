@@ -81,7 +81,8 @@ void launch_layout(int layout, int M, dim3 grid, int nw, size_t smem, hipStream_
 }
 
 // Waves and LDS bytes of a fused FP8 launch; false if the prologue's staging does not fit.
-bool plan(int64_t M, int64_t K, int split, int mode, int x_kind, bool norm, int* nw_out, size_t* smem_out) {
+bool plan(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind, bool norm, int* nw_out,
+          size_t* smem_out) {
   if (M < 1 || M > 32 || split < 1 || K < 64 || K % split || (K / split) % 64) return false;
   if (norm && x_kind == KRQ_X_FP8) return false;
   if (x_kind == KRQ_X_BF16_DYN && M != 1) return false;
@@ -89,7 +90,8 @@ bool plan(int64_t M, int64_t K, int split, int mode, int x_kind, bool norm, int*
   const int kts = static_cast<int>(ks / 64);
   const int P = mode == KRQ_OUT_SWIGLU ? 2 : 1;
   const int MT = M <= 16 ? 1 : 2;
-  int nw = plan_waves((kts + 1) / 2, P, M <= 4 ? 4 : 2);
+  const int64_t NO = mode == KRQ_OUT_SWIGLU ? N / 2 : N;
+  int nw = plan_waves((kts + 1) / 2, P, M <= 4 ? 4 : 2, NO / 16 * split);
   const int64_t xchunks = x_kind == KRQ_X_BF16_DYN ? (K + 7) / 8 : x_kind == KRQ_X_BF16_STATIC ? M * (ks / 8) : 0;
   const int xc = x_kind == KRQ_X_BF16_DYN ? kXChunksDyn : kXChunks;
   const int sc = x_kind == KRQ_X_BF16_DYN ? kSsChunksDyn : kSsChunks;
@@ -108,10 +110,11 @@ bool plan(int64_t M, int64_t K, int split, int mode, int x_kind, bool norm, int*
 
 }  // namespace
 
-extern "C" int64_t krq_gemv_fp8_fused_fits(int64_t M, int64_t K, int split, int mode, int x_kind, int norm) {
+extern "C" int64_t krq_gemv_fp8_fused_fits(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind,
+                                           int norm) {
   int nw = 0;
   size_t smem = 0;
-  return plan(M, K, split, mode, x_kind, norm != 0, &nw, &smem) ? 1 : 0;
+  return plan(M, N, K, split, mode, x_kind, norm != 0, &nw, &smem) ? 1 : 0;
 }
 
 extern "C" int krq_gemv_fp8_fused(const void* x, int x_kind, const float* x_scale, const float* x_inv,
@@ -149,7 +152,7 @@ extern "C" int krq_gemv_fp8_fused(const void* x, int x_kind, const float* x_scal
               "gemv_fp8_fused: no tiling divides N=%lld", (long long)N);
   int nw = 0;
   size_t smem = 0;
-  KRQ_REQUIRE(plan(M, K, split, mode, x_kind, norm, &nw, &smem),
+  KRQ_REQUIRE(plan(M, N, K, split, mode, x_kind, norm, &nw, &smem),
               "gemv_fp8_fused: M=%lld x K/split=%lld does not fit the in-kernel staging; normalize and "
               "quantize rows first (krq_rmsnorm_quant_rows)", (long long)M, (long long)(K / split));
   const int kts = static_cast<int>(K / split / 64);

@@ -241,13 +241,14 @@ void launch_layout(int layout, int M, dim3 grid, int nw, size_t smem, hipStream_
 constexpr size_t kMaxSmem = 60 * 1024;
 
 // Waves and LDS bytes of a launch; false if the slice (or the sum-of-squares partials) does not fit.
-bool plan_fused(int64_t M, int64_t K, int split, int mode, bool norm, int* nw_out, size_t* smem_out) {
+bool plan_fused(int64_t M, int64_t N, int64_t K, int split, int mode, bool norm, int* nw_out, size_t* smem_out) {
   if (M < 1 || M > 32 || split < 1 || K % 16 || K % split || (K / split) % 32) return false;
   const int64_t ks = K / split;
   const int kts = static_cast<int>(ks / 32);
   const int P = mode == KRQ_OUT_SWIGLU ? 2 : 1;
   const int MT = M <= 16 ? 1 : 2;
-  int nw = plan_waves((kts + 1) / 2, P, M <= 4 ? 4 : 2);
+  const int64_t NO = mode == KRQ_OUT_SWIGLU ? N / 2 : N;
+  int nw = plan_waves((kts + 1) / 2, P, M <= 4 ? 4 : 2, NO / 16 * split);
   auto short_of = [&](int w) {
     return norm && ((int64_t)w * 64 * kXC < M * (ks / 8) || (int64_t)w * 64 * kSC < M * (K / 16));
   };
@@ -263,10 +264,10 @@ bool plan_fused(int64_t M, int64_t K, int split, int mode, bool norm, int* nw_ou
 
 }  // namespace
 
-extern "C" int64_t krq_gemv_fused_fits(int64_t M, int64_t K, int split, int mode, int norm) {
+extern "C" int64_t krq_gemv_fused_fits(int64_t M, int64_t N, int64_t K, int split, int mode, int norm) {
   int nw = 0;
   size_t smem = 0;
-  return plan_fused(M, K, split, mode, norm != 0, &nw, &smem) ? 1 : 0;
+  return plan_fused(M, N, K, split, mode, norm != 0, &nw, &smem) ? 1 : 0;
 }
 
 extern "C" int krq_gemv_bf16_fused(const void* x, const void* w, int w_layout, int64_t M, int64_t N,
@@ -294,7 +295,7 @@ extern "C" int krq_gemv_bf16_fused(const void* x, const void* w, int w_layout, i
               "gemv_bf16_fused: no tiling divides N=%lld", (long long)N);
   int nw = 0;
   size_t smem = 0;
-  KRQ_REQUIRE(plan_fused(M, K, split, mode, norm, &nw, &smem),
+  KRQ_REQUIRE(plan_fused(M, N, K, split, mode, norm, &nw, &smem),
               "gemv_bf16_fused: M=%lld x K/split=%lld does not fit the staged slice; normalize rows first "
               "(krq_rmsnorm_rows) and call the plain GEMV", (long long)M, (long long)(K / split));
   const int kts = static_cast<int>(K / split / 32);

@@ -176,7 +176,7 @@ int krq::gemv_bf16_run(const void* x, const void* w, int w_layout, int64_t M, in
                   (NO / 16) * split >= 4096) ? 2 : 1;
   const int P = mode == KRQ_OUT_SWIGLU ? 2 : pb;
   const int MT = M <= 16 ? 1 : 2;
-  const int nw = plan_waves((kts + 1) / 2, P, M <= 4 ? 4 : 2);  // U of the variant launch() picks
+  const int nw = plan_waves((kts + 1) / 2, P, M <= 4 ? 4 : 2, NO / 16 / pb * split);  // U of launch()'s variant
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float);
   const dim3 grid(static_cast<unsigned>(NO / 16 / pb), static_cast<unsigned>(split));
   const uint8_t* xb = (const uint8_t*)x;

@@ -388,9 +388,10 @@ struct Plan {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Waves per block for a block of nsteps steps over P weight matrices with U step slots per wave.
-// Overridable (for launch-shape sweeps) by the environment variable KRQ_GEMV_WAVES.
-int plan_waves(int nsteps, int P, int U);
+// Waves per block for a block of nsteps steps over P weight matrices with U step slots per wave,
+// in a grid of `blocks` blocks. Overridable (for launch-shape sweeps) by the environment variable
+// KRQ_GEMV_WAVES.
+int plan_waves(int nsteps, int P, int U, int64_t blocks);
 
 // Validated launches shared by the C ABI entry points (gemv_fp8.hip, gemv_bf16.hip); mode may
 // also be kOutArgmax (then split == 1, aux = [N/16][M] Best, out = optional bf16 logits).

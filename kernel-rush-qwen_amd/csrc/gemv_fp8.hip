@@ -8,7 +8,7 @@
 using namespace krq;
 
 namespace krq {
-int plan_waves(int nsteps, int P, int U) {
+int plan_waves(int nsteps, int P, int U, int64_t blocks) {
   static const int env = [] {
     const char* s = getenv("KRQ_GEMV_WAVES");
     return s ? atoi(s) : 0;
@@ -16,10 +16,14 @@ int plan_waves(int nsteps, int P, int U) {
   if (env >= 1 && env <= 8) return env;
   if (nsteps < 2) return 1;
   // measured on MI355X at the Qwen3-4B shapes: a single-matrix block takes just enough waves for
-  // all of its steps to be in flight at once (one memory round trip), up to 4; past that, and for
-  // the two-matrix SwiGLU block, two waves
+  // all of its steps to be in flight at once (one memory round trip), up to 4; when that is not
+  // enough, two waves, unless the grid has fewer blocks than the chip has CUs x 2 (the single-pass
+  // O and down, 160 blocks: 5.07 / 8.74 us with 4 waves against 6.50 / 8.75 with 2 at M = 1),
+  // where four keep more loads in flight. The two-matrix SwiGLU block takes two waves.
   const int w = (nsteps + U - 1) / U;
-  return (P == 1 && w <= 4) ? w : 2;
+  if (P != 1) return 2;
+  if (w <= 4) return w;
+  return blocks < 512 ? 4 : 2;
 }
 }  // namespace krq
 
@@ -107,7 +111,7 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   const int MT = (algo == 2 || M <= 16) ? 1 : 2;
   // step slots per wave of the variant launch() picks
   const int U = (algo == 2 || M <= 4) ? 4 : 2;
-  int nw = plan_waves((kts + 1) / 2, P, U);
+  int nw = plan_waves((kts + 1) / 2, P, U, NO / 16 / pb * split);
   // fused prologues hold at most kXChunks 16-byte chunks per thread
   int64_t xchunks = 0;
   if (x_kind == KRQ_X_BF16_DYN) xchunks = (K + 7) / 8;

@@ -142,8 +142,11 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
     row_rstd(sst, M, T, K, fa.eps, rstd_s);
     __syncthreads();
     if (XK == KRQ_X_BF16_DYN) {
+      // only chunks inside the row: the clamped repeats past K are left raw and kept out of the
+      // amax below (they are never quantized into the slice)
 #pragma unroll
-      for (int c = 0; c < kXChunksDyn; ++c) xv[c] = norm8(xv[c], lv[c], rstd_s[0]);
+      for (int c = 0; c < kXChunksDyn; ++c)
+        if (8 * (int64_t)(threadIdx.x + c * blockDim.x) < K) xv[c] = norm8(xv[c], lv[c], rstd_s[0]);
     } else {
       const int cpr = ks >> 3;
 #pragma unroll
@@ -160,7 +163,8 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   } else if (XK == KRQ_X_BF16_DYN) {
     float am = 0.0f;
 #pragma unroll
-    for (int c = 0; c < kXChunksDyn; ++c) am = absmax8(xv[c], am);
+    for (int c = 0; c < kXChunksDyn; ++c)
+      if (!NORM || 8 * (int64_t)(threadIdx.x + c * blockDim.x) < K) am = absmax8(xv[c], am);
     am = wave_max(am);
     if (lane == 0) amax_w[wave] = am;
     __syncthreads();

@@ -41,11 +41,11 @@ EXPORTS = {
     "krq_mlp_ctl_words": (_i64, []),
     "krq_gemv_bf16_fused": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _f32, _vp,
                                    _vp, _vp, _vp, _vp, _vp]),
-    "krq_gemv_fused_fits": (_i64, [_i64, _i64, _i32, _i32, _i32]),
+    "krq_gemv_fused_fits": (_i64, [_i64, _i64, _i64, _i32, _i32, _i32]),
     "krq_rmsnorm_rows": (_i32, [_vp, _vp, _vp, _f32, _i64, _i64, _vp, _vp]),
     "krq_gemv_fp8_fused": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _i32,
                                   _i32, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "krq_gemv_fp8_fused_fits": (_i64, [_i64, _i64, _i32, _i32, _i32, _i32]),
+    "krq_gemv_fp8_fused_fits": (_i64, [_i64, _i64, _i64, _i32, _i32, _i32, _i32]),
     "krq_rmsnorm_quant_rows": (_i32, [_vp, _vp, _vp, _f32, _i64, _i64, _vp, _vp, _vp]),
     "krq_pack_fp8": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "krq_unpack_fp8": (_i32, [_vp, _i64, _i64, _vp, _vp]),

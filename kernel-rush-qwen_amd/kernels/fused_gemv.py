@@ -36,6 +36,11 @@ from . import fp8 as _fp8
 from . import gemv as _gemv
 
 MAX_ROWS = 32
+# K splits the residual epilogue runs with (None: the caller's split). Its output has no split
+# partials, so the decomposition is free; on MI355X one K pass with four waves per block costs at
+# most ~0.8 us more than split 4 (O: the same), while the split-K last-arriver reduction costs
+# three memory round trips (~3 us) at the tail of the launch.
+EP_SPLIT = 1
 
 
 class FusedLayerBuffers:
@@ -57,14 +62,14 @@ def _check(x, w):
         raise ValueError(f"fused GEMVs take at most {MAX_ROWS} rows, got {x.shape[0]}")
 
 
-def _norm_args(x, norm, mode, split):
+def _norm_args(x, N, norm, mode, split):
     """(x, ln, ss) for the launch: the RMSNorm in the kernel when its slice fits, else rows
     normalized by a separate launch and no norm in the GEMV."""
     if norm is None:
         return x, None, None
     ln, ss = _check_norm(x, norm)
     M, K = x.shape
-    if L.lib().krq_gemv_fused_fits(M, K, split, mode, 1):
+    if L.lib().krq_gemv_fused_fits(M, N, K, split, mode, 1):
         return x, ln, ss
     return None, ln, ss
 
@@ -78,7 +83,7 @@ def _rmsnorm(x, ln, ss, eps):
 def _launch(x, w, split, mode, norm, ep, eps, out):
     M, K = x.shape
     N = w.shape[0]
-    xin, ln, ss = _norm_args(x, norm, mode, split)
+    xin, ln, ss = _norm_args(x, N, norm, mode, split)
     if xin is None:  # normalize first, then the plain fused launch
         xin, ln, ss = _rmsnorm(x, ln, ss, eps), None, None
     wt, layout = _gemv._weight(w)
@@ -128,7 +133,7 @@ def _launch_fp8(x, q, split, mode, norm, ep, eps, a, out):
         res_in, res_out, ss_out, cnt = _check_ep(ep, M, N, split)
     fits = L.lib().krq_gemv_fp8_fused_fits
     kind = L.X_BF16_STATIC if a is not None else L.X_BF16_DYN
-    if not fits(M, K, split, mode, kind, 1 if norm is not None else 0):
+    if not fits(M, N, K, split, mode, kind, 1 if norm is not None else 0):
         # stage outside: normalize (and quantize) the rows first, then e4m3 activations
         if norm is not None:
             if a is None:
@@ -183,11 +188,14 @@ def gemv_fused(x, w, split, *, norm=None, zero_ss=None, ep=None, eps=1e-6, a=Non
     """x [M, K] bf16, w [N, K] bf16 or an FP8Weight.
     norm=(ln_w, ss_in): normalise x rows on the fly.
     zero_ss: accepted; the per-tile sums need no reset (every producer overwrites them).
-    ep=(res_in, res_out, ss_out, cnt): residual epilogue; returns None.
+    ep=(res_in, res_out, ss_out, cnt): residual epilogue; returns None. Runs with EP_SPLIT K
+    splits (default one pass) whatever `split` says: y is the full fp32 sum either way.
     a (FP8 weights only): ActScale / SharedScale for static activation scaling; per token if None.
     Otherwise returns bf16 [M, N] (split 1) or fp32 partials [split, M, N]."""
+    assert x.shape[-1] % split == 0
+    if ep is not None and EP_SPLIT is not None:
+        split = EP_SPLIT
     if _is_fp8(w):
-        assert x.shape[-1] % split == 0
         mode = L.OUT_RESIDUAL if ep is not None else (L.OUT_PARTIAL if split > 1 else L.OUT_BF16)
         return _fp8_fused(x, w, split, mode, norm, ep, eps, a)
     if a is not None:
@@ -195,7 +203,6 @@ def gemv_fused(x, w, split, *, norm=None, zero_ss=None, ep=None, eps=1e-6, a=Non
     _check(x, w)
     M, K = x.shape
     N = w.shape[0]
-    assert K % split == 0
     if ep is not None:
         part = torch.empty((split, M, N), device=x.device, dtype=torch.float32) if split > 1 else None
         _launch(x, w, split, L.OUT_RESIDUAL, norm, ep, eps, part)

@@ -76,8 +76,8 @@ def test_invalid_arguments_fail_before_any_launch():
     rc = lib.krq_gemv_bf16_fused(p, p, 0, 16, 19456, 2560, 1, L.OUT_SWIGLU, p, p, 1e-6,
                                  None, None, None, None, p, _null())
     assert rc == L.KRQ_EINVAL and b"krq_rmsnorm_rows" in lib.krq_last_error()
-    assert lib.krq_gemv_fused_fits(1, 2560, 2, L.OUT_PARTIAL, 1) == 1
-    assert lib.krq_gemv_fused_fits(16, 2560, 1, L.OUT_SWIGLU, 1) == 0
+    assert lib.krq_gemv_fused_fits(1, 6144, 2560, 2, L.OUT_PARTIAL, 1) == 1
+    assert lib.krq_gemv_fused_fits(16, 19456, 2560, 1, L.OUT_SWIGLU, 1) == 0
     # fused FP8 GEMV: something to fuse; RMSNorm needs bf16 activations; per-token in-kernel
     # scaling takes one row; the residual epilogue needs its buffers
     args = (p, 1, None, None, 0, p, 1, p, 1)
@@ -95,11 +95,11 @@ def test_invalid_arguments_fail_before_any_launch():
     assert rc == L.KRQ_EINVAL and b"cnt" in lib.krq_last_error()
     rc = lib.krq_gemv_fp8_fused(*args, 1, 2560, 4096, 4, L.OUT_RESIDUAL, p, p, 1e-6, p, p, p, p, p, _null())
     assert rc == L.KRQ_EINVAL and b"in one call" in lib.krq_last_error()
-    assert lib.krq_gemv_fp8_fused_fits(1, 2560, 2, L.OUT_PARTIAL, L.X_BF16_DYN, 1) == 1
-    assert lib.krq_gemv_fp8_fused_fits(16, 2560, 2, L.OUT_PARTIAL, L.X_BF16_DYN, 1) == 0
-    assert lib.krq_gemv_fp8_fused_fits(16, 2560, 2, L.OUT_PARTIAL, L.X_BF16_STATIC, 1) == 1
-    assert lib.krq_gemv_fp8_fused_fits(32, 2560, 1, L.OUT_SWIGLU, L.X_BF16_STATIC, 1) == 0
-    assert lib.krq_gemv_fp8_fused_fits(1, 9728, 4, L.OUT_RESIDUAL, L.X_FP8, 0) == 1
+    assert lib.krq_gemv_fp8_fused_fits(1, 6144, 2560, 2, L.OUT_PARTIAL, L.X_BF16_DYN, 1) == 1
+    assert lib.krq_gemv_fp8_fused_fits(16, 6144, 2560, 2, L.OUT_PARTIAL, L.X_BF16_DYN, 1) == 0
+    assert lib.krq_gemv_fp8_fused_fits(16, 6144, 2560, 2, L.OUT_PARTIAL, L.X_BF16_STATIC, 1) == 1
+    assert lib.krq_gemv_fp8_fused_fits(32, 19456, 2560, 1, L.OUT_SWIGLU, L.X_BF16_STATIC, 1) == 0
+    assert lib.krq_gemv_fp8_fused_fits(1, 2560, 9728, 4, L.OUT_RESIDUAL, L.X_FP8, 0) == 1
     rc = lib.krq_rmsnorm_quant_rows(p, p, p, 1e-6, 1, 16384 + 16, p, p, _null())
     assert rc == L.KRQ_EINVAL and b"at most 16384" in lib.krq_last_error()
 

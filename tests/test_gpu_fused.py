@@ -75,10 +75,15 @@ def test_rmsnorm_prologue(dev, M, K, N, split, swiglu):
     assert e <= TOL
 
 
-@pytest.mark.parametrize("M,split", [(1, 4), (16, 4), (1, 1), (32, 2)])
-def test_residual_epilogue(dev, M, split):
+@pytest.mark.parametrize("M,split,protocol", [(1, 4, True), (16, 4, True), (1, 1, False), (32, 2, True),
+                                              (16, 4, False)])
+def test_residual_epilogue(dev, monkeypatch, M, split, protocol):
     """ep=(res_in, res_out, ss_out, cnt): res_out = bf16(res_in + bf16(y)), ss_out per 16-column
-    tile; the split counters are back at zero afterwards (twice in a row)."""
+    tile; the split counters are back at zero afterwards (twice in a row). protocol: the caller's
+    split with the last-arriver reduction (EP_SPLIT None) instead of the default single K pass."""
+    from kernels import fused_gemv as FG
+    if protocol:
+        monkeypatch.setattr(FG, "EP_SPLIT", None)
     K = 4096
     a, w, res = bf((M, K), 20), bf((H, K), 21, 0.02), bf((M, H), 22)
     y = O.bf16_matmul(u16(a), u16(w))
@@ -130,9 +135,11 @@ def test_layer_fragment_like_the_engine(dev):
     assert e <= TOL
 
 
-def test_fused_graph_replays(dev):
+def test_fused_graph_replays(dev, monkeypatch):
     """The residual epilogue's counters reset themselves: replays match eager, with eager calls
-    in between."""
+    in between (split-K protocol: EP_SPLIT None)."""
+    from kernels import fused_gemv as FG
+    monkeypatch.setattr(FG, "EP_SPLIT", None)
     M = 4
     a, w, res = bf((M, 4096), 40), bf((H, 4096), 41, 0.02), bf((M, H), 42)
     ad, wd, rd = a.to(dev), w.to(dev), res.to(dev)
@@ -273,13 +280,20 @@ def test_fp8_rmsnorm_prologue_static_scale(dev, M, N, split, swiglu):
     assert e <= TOL
 
 
-@pytest.mark.parametrize("M,split,static", [(1, 4, False), (1, 1, False), (16, 4, False), (32, 2, False),
-                                            (4, 4, True)])
-def test_fp8_residual_epilogue(dev, M, split, static):
-    """ep=(res_in, res_out, ss_out, cnt) on FP8 weights: res_out equals bf16(res_in + bf16(in-order
-    sum of the plain GEMV's scaled partials)) bit for bit, ss_out its per-tile sums of squares, and
-    the counters are zero again (twice in a row); the oracle bounds the whole."""
+@pytest.mark.parametrize("M,split,static,protocol", [(1, 4, False, True), (1, 4, False, False), (1, 1, False, True),
+                                                     (16, 4, False, True), (16, 4, False, False),
+                                                     (32, 2, False, True), (4, 4, True, True), (4, 1, True, False)])
+def test_fp8_residual_epilogue(dev, monkeypatch, M, split, static, protocol):
+    """ep=(res_in, res_out, ss_out, cnt) on FP8 weights: res_out equals bf16(res_in + bf16(y)) bit
+    for bit, y being the plain GEMV's output for the same K decomposition (the in-order sum of its
+    scaled split partials with the split-K protocol, EP_SPLIT None; its one-pass output with the
+    default single pass), ss_out its per-tile sums of squares, and the counters are zero again
+    (twice in a row); the oracle bounds the whole."""
     from kernels import fp8 as F
+    from kernels import fused_gemv as FG
+    if protocol:
+        monkeypatch.setattr(FG, "EP_SPLIT", None)
+    ref_split = split if protocol else 1  # the call below passes `split` either way
     K = 4096
     a_, res = bf((M, K), 100 + M), bf((M, H), 101)
     q = F.quantize(bf((H, K), 102, 0.02).to(dev))
@@ -288,10 +302,10 @@ def test_fp8_residual_epilogue(dev, M, split, static):
     if static:
         sa = F.ActScale(ad)
     bufs = FusedLayerBuffers(M, H, V, dev)
-    p = F.gemv_fp8(ad, q, split, sa)
-    if split > 1:  # the partials summed in split order, then rounded
+    p = F.gemv_fp8(ad, q, ref_split, sa)
+    if ref_split > 1:  # the partials summed in split order, then rounded
         y = p[0].clone()
-        for s in range(1, split):
+        for s in range(1, ref_split):
             y += p[s]
         p = y.to(torch.bfloat16)
     want = (rd.float() + p.float()).to(torch.bfloat16)
@@ -345,10 +359,14 @@ def test_fp8_layer_fragment_like_the_engine(dev):
     assert rel_err(bufs.ss[0].cpu().numpy(), O.tile_sumsq(res_a)) <= 1e-5
 
 
-def test_fp8_fused_graph_replays(dev):
+@pytest.mark.parametrize("protocol", [True, False])
+def test_fp8_fused_graph_replays(dev, monkeypatch, protocol):
     """FP8 residual epilogue and RMSNorm prologue captured in a graph: replays equal eager, with
-    eager calls in between, and the counters stay zero."""
+    eager calls in between, and the counters stay zero (with and without the split-K protocol)."""
     from kernels import fp8 as F
+    from kernels import fused_gemv as FG
+    if protocol:
+        monkeypatch.setattr(FG, "EP_SPLIT", None)
     M = 1
     a_, res = bf((M, 4096), 130), bf((M, H), 131)
     q_o = F.quantize(bf((H, 4096), 132, 0.02).to(dev))
