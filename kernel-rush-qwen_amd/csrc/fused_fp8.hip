@@ -17,36 +17,36 @@ using namespace krq;
 namespace {
 
 constexpr size_t kMaxSmem = 60 * 1024;
-constexpr int kRowThreads = 256;
-constexpr int kRowChunks = 8;  // 16-byte chunks per thread: rows of up to 16,384 elements
+// largest bf16 x slice (bytes) a block normalizes in its prologue (as in fused_gemv.hip)
+constexpr int64_t kNormStageMax = 24 * 1024;
 
 // RMSNorm + per-token e4m3 quantization of whole rows (one block per row): x8 = e4m3(h * inv),
 // xs = amax(h) / 448 with the ActScale arithmetic of quant_rows (amax floored at 1e-6).
+template <int C>
 __global__ __launch_bounds__(kRowThreads) void k_rmsnorm_quant_rows(const uint16_t* __restrict__ x,
                                                                     const float* __restrict__ ss_in,
                                                                     const uint16_t* __restrict__ ln, float eps,
                                                                     int64_t K, uint8_t* __restrict__ x8,
                                                                     float* __restrict__ xs) {
-  __shared__ float rstd;
-  const int m = blockIdx.x, T = (int)(K >> 4);
-  row_rstd(ss_in + (int64_t)m * T, 1, T, K, eps, &rstd);
-  __syncthreads();
-  const uint8_t* xr = reinterpret_cast<const uint8_t*>(x + m * K);
-  const uint8_t* lr = reinterpret_cast<const uint8_t*>(ln);
-  uint4 v[kRowChunks];
+  __shared__ float sst[kRowThreads * C / 2];
+  __shared__ float rstd_sh;
+  const int m = blockIdx.x;
+  uint4 v[C], lv[C];
+  const float rstd = row_prologue<C>(x, ss_in, ln, eps, K, m, sst, &rstd_sh, v, lv);
   float am = 0.0f;
 #pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
-    const int64_t e = 8 * (int64_t)(threadIdx.x + c * kRowThreads);
-    v[c] = e < K ? norm8(ld16(xr + 2 * e), ld16(lr + 2 * e), rstd) : zero4();
-    am = absmax8(v[c], am);
+  for (int c = 0; c < C; ++c) {
+    if (8 * (int64_t)(threadIdx.x + c * kRowThreads) < K) {
+      v[c] = norm8(v[c], lv[c], rstd);
+      am = absmax8(v[c], am);
+    }
   }
   am = block_max<kRowThreads>(am);
   const float a = fmaxf(am, 1e-6f);
   const float iv = inv_from_amax(a);
   if (threadIdx.x == 0) xs[m] = scale_from_amax(a);
 #pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
+  for (int c = 0; c < C; ++c) {
     const int64_t e = 8 * (int64_t)(threadIdx.x + c * kRowThreads);
     if (e < K) *reinterpret_cast<uint2*>(x8 + m * K + e) = quant8(v[c], iv);
   }
@@ -87,6 +87,7 @@ bool plan(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind, bool
   if (norm && x_kind == KRQ_X_FP8) return false;
   if (x_kind == KRQ_X_BF16_DYN && M != 1) return false;
   const int64_t ks = K / split;
+  if (norm && x_kind == KRQ_X_BF16_STATIC && M * ks * 2 > kNormStageMax) return false;
   const int kts = static_cast<int>(ks / 64);
   const int P = mode == KRQ_OUT_SWIGLU ? 2 : 1;
   const int MT = M <= 16 ? 1 : 2;
@@ -94,14 +95,15 @@ bool plan(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind, bool
   int nw = plan_waves((kts + 1) / 2, P, M <= 4 ? 4 : 2, NO / 16 * split);
   const int64_t xchunks = x_kind == KRQ_X_BF16_DYN ? (K + 7) / 8 : x_kind == KRQ_X_BF16_STATIC ? M * (ks / 8) : 0;
   const int xc = x_kind == KRQ_X_BF16_DYN ? kXChunksDyn : kXChunks;
-  const int sc = x_kind == KRQ_X_BF16_DYN ? kSsChunksDyn : kSsChunks;
+  if (norm && x_kind == KRQ_X_BF16_DYN && K / 16 > 64 * kSsPerLane) return false;
   auto short_of = [&](int w) {
-    return (int64_t)w * 64 * xc < xchunks || (norm && (int64_t)w * 64 * sc * 4 < M * (K / 16));
+    return (int64_t)w * 64 * xc < xchunks ||
+           (norm && x_kind == KRQ_X_BF16_STATIC && (int64_t)w * 64 * kSsChunks * 4 < M * (K / 16));
   };
   while (short_of(nw) && nw < kMaxThreads / 64) ++nw;
   if (short_of(nw)) return false;
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) + (x_kind == KRQ_X_FP8 ? 0 : (size_t)M * ks) +
-                      (norm ? (size_t)M * (K / 16) * sizeof(float) : 0);
+                      (norm && x_kind == KRQ_X_BF16_STATIC ? (size_t)M * (K / 16) * sizeof(float) : 0);
   if (smem > kMaxSmem) return false;
   *nw_out = nw;
   *smem_out = smem;
@@ -187,10 +189,11 @@ extern "C" int krq_rmsnorm_quant_rows(const void* x, const float* ss_in, const v
                                       int64_t K, void* x8, float* x_scale, void* stream) {
   KRQ_REQUIRE(x && ss_in && ln && x8 && x_scale, "rmsnorm_quant_rows: null pointer");
   KRQ_REQUIRE(aligned16(x) && aligned16(ln) && aligned16(x8), "rmsnorm_quant_rows: x, ln and x8 must be 16-byte aligned");
-  KRQ_REQUIRE(M >= 1 && M <= 0x7fffffff && K > 0 && K % 16 == 0 && K <= 8 * kRowThreads * kRowChunks,
+  KRQ_REQUIRE(M >= 1 && M <= 0x7fffffff && K > 0 && K % 16 == 0 && K <= kRowMaxK,
               "rmsnorm_quant_rows: bad shape M=%lld K=%lld (K a multiple of 16, at most %d)", (long long)M,
-              (long long)K, 8 * kRowThreads * kRowChunks);
-  hipLaunchKernelGGL(k_rmsnorm_quant_rows, dim3(static_cast<unsigned>(M)), dim3(kRowThreads), 0, (hipStream_t)stream,
+              (long long)K, kRowMaxK);
+  hipLaunchKernelGGL(K <= kRowSmallK ? k_rmsnorm_quant_rows<2> : k_rmsnorm_quant_rows<kRowChunks>,
+                     dim3(static_cast<unsigned>(M)), dim3(kRowThreads), 0, (hipStream_t)stream,
                      (const uint16_t*)x, ss_in, (const uint16_t*)ln, eps, K, (uint8_t*)x8, x_scale);
   return krq_check_launch("rmsnorm_quant_rows");
 }

@@ -201,17 +201,21 @@ __global__ __launch_bounds__(kMaxNT) void k_gemv_fused(const uint8_t* __restrict
 
 // RMSNorm of whole rows for shapes whose slice does not fit the GEMV's LDS staging:
 // h = bf16(bf16(x * rstd) * w_ln), rstd from the [M][K/16] sum-of-squares partials.
-__global__ __launch_bounds__(256) void k_rmsnorm_rows(const uint16_t* __restrict__ x, const float* __restrict__ ss_in,
-                                                      const uint16_t* __restrict__ ln, float eps, int64_t K,
-                                                      uint16_t* __restrict__ h) {
-  __shared__ float rstd;
-  const int m = blockIdx.x, T = (int)(K >> 4);
-  row_rstd(ss_in + (int64_t)m * T, 1, T, K, eps, &rstd);  // the fused prologues' summation order
-  __syncthreads();
-  const uint8_t* xr = reinterpret_cast<const uint8_t*>(x + m * K);
-  for (int64_t c = threadIdx.x; c < K / 8; c += blockDim.x) {
-    const uint4 v = norm8(ld16(xr + 16 * c), ld16(reinterpret_cast<const uint8_t*>(ln) + 16 * c), rstd);
-    *reinterpret_cast<uint4*>(reinterpret_cast<uint8_t*>(h + m * K) + 16 * c) = v;
+template <int C>
+__global__ __launch_bounds__(kRowThreads) void k_rmsnorm_rows(const uint16_t* __restrict__ x,
+                                                              const float* __restrict__ ss_in,
+                                                              const uint16_t* __restrict__ ln, float eps, int64_t K,
+                                                              uint16_t* __restrict__ h) {
+  __shared__ float sst[kRowThreads * C / 2];
+  __shared__ float rstd_sh;
+  const int m = blockIdx.x;
+  uint4 xv[C], lv[C];
+  const float rstd = row_prologue<C>(x, ss_in, ln, eps, K, m, sst, &rstd_sh, xv, lv);
+  uint8_t* hr = reinterpret_cast<uint8_t*>(h + m * K);
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int64_t e = 8 * (int64_t)(threadIdx.x + c * kRowThreads);
+    if (e < K) *reinterpret_cast<uint4*>(hr + 2 * e) = norm8(xv[c], lv[c], rstd);
   }
 }
 
@@ -239,11 +243,16 @@ void launch_layout(int layout, int M, dim3 grid, int nw, size_t smem, hipStream_
 }
 
 constexpr size_t kMaxSmem = 60 * 1024;
+// Largest bf16 x slice (bytes) a block normalizes in its prologue. Measured on MI355X: at M = 16
+// the QKV slice (40 KB) takes 19.0 us in-kernel against 2.6 + 8.4 us for krq_rmsnorm_rows and the
+// plain launch; the M = 4 gate/up slice (20 KB) is faster in-kernel (21.4 against 22.0 us).
+constexpr int64_t kNormStageMax = 24 * 1024;
 
 // Waves and LDS bytes of a launch; false if the slice (or the sum-of-squares partials) does not fit.
 bool plan_fused(int64_t M, int64_t N, int64_t K, int split, int mode, bool norm, int* nw_out, size_t* smem_out) {
   if (M < 1 || M > 32 || split < 1 || K % 16 || K % split || (K / split) % 32) return false;
   const int64_t ks = K / split;
+  if (norm && M * ks * 2 > kNormStageMax) return false;
   const int kts = static_cast<int>(ks / 32);
   const int P = mode == KRQ_OUT_SWIGLU ? 2 : 1;
   const int MT = M <= 16 ? 1 : 2;
@@ -323,9 +332,11 @@ extern "C" int krq_rmsnorm_rows(const void* x, const float* ss_in, const void* l
                                 int64_t K, void* h, void* stream) {
   KRQ_REQUIRE(x && ss_in && ln && h, "rmsnorm_rows: null pointer");
   KRQ_REQUIRE(aligned16(x) && aligned16(ln) && aligned16(h), "rmsnorm_rows: x, ln and h must be 16-byte aligned");
-  KRQ_REQUIRE(M >= 1 && M <= 65535 && K > 0 && K % 16 == 0, "rmsnorm_rows: bad shape M=%lld K=%lld",
-              (long long)M, (long long)K);
-  hipLaunchKernelGGL(k_rmsnorm_rows, dim3(static_cast<unsigned>(M)), dim3(256), 0, (hipStream_t)stream,
+  KRQ_REQUIRE(M >= 1 && M <= 0x7fffffff && K > 0 && K % 16 == 0 && K <= kRowMaxK,
+              "rmsnorm_rows: bad shape M=%lld K=%lld (K a multiple of 16, at most %d)", (long long)M, (long long)K,
+              kRowMaxK);
+  hipLaunchKernelGGL(K <= kRowSmallK ? k_rmsnorm_rows<2> : k_rmsnorm_rows<kRowChunks>, dim3(static_cast<unsigned>(M)),
+                     dim3(kRowThreads), 0, (hipStream_t)stream,
                      (const uint16_t*)x, ss_in, (const uint16_t*)ln, eps, K, (uint16_t*)h);
   return krq_check_launch("rmsnorm_rows");
 }

@@ -294,29 +294,81 @@ struct FusedArgs {
   uint32_t* cnt;           // [N/16] split-arrival counters (zero between launches)
 };
 
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+// Two fp32 values rounded to bf16 (nearest even) and packed lo | hi << 16: one hardware convert
+// (v_cvt_pk_bf16_f32). Equal to f32_to_bf16 on every non-NaN input; a NaN stays a NaN.
+KRQ_DEV uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{lo, hi}, v2bf));
+}
+
 KRQ_DEV uint4 norm8(uint4 xv, uint4 lv, float rstd) {
   const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w}, la[4] = {lv.x, lv.y, lv.z, lv.w};
   uint32_t o[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const float x0 = round_bf16(as_f32(xa[q] << 16) * rstd), x1 = round_bf16(as_f32(xa[q] & 0xffff0000u) * rstd);
-    const uint32_t h0 = f32_to_bf16(x0 * as_f32(la[q] << 16)), h1 = f32_to_bf16(x1 * as_f32(la[q] & 0xffff0000u));
-    o[q] = h0 | (h1 << 16);
+    const uint32_t r = pack_bf16x2(as_f32(xa[q] << 16) * rstd, as_f32(xa[q] & 0xffff0000u) * rstd);
+    o[q] = pack_bf16x2(as_f32(r << 16) * as_f32(la[q] << 16), as_f32(r & 0xffff0000u) * as_f32(la[q] & 0xffff0000u));
   }
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
-// rstd[m] for m < M from the [M][T] partials staged in LDS (sst): one wave per row, lanes take
-// t = lane, lane + 64, ... and the wave sum folds them, the same order in every kernel that
-// normalizes (so the fused prologues and k_rmsnorm_rows agree bit for bit).
+// The canonical row sum of T sum-of-squares partials, used by every kernel that normalizes (so the
+// fused prologues, k_rmsnorm_rows and k_rmsnorm_quant_rows agree bit for bit): lane l adds
+// partials t = l, l + 64, l + 128, ... in that order, then the butterfly wave sum (every lane ends
+// with the same total). rstd = rsqrt(sum / K + eps).
+KRQ_DEV float rstd_of(float lane_sum, int64_t K, float eps) {
+  return rsqrtf(wave_sum(lane_sum) / (float)K + eps);
+}
+
+// Row kernels (one block of kRowThreads per row, rows of up to kRowMaxK elements): the x and ln
+// chunks are loaded into registers first and the row's partials staged in LDS with independent
+// loads, so the whole prologue is one memory round trip. C = 16-byte chunks per thread (2 for
+// rows of up to 4,096 elements, else kRowChunks).
+constexpr int kRowThreads = 256;
+constexpr int kRowChunks = 8;
+constexpr int kRowMaxK = 8 * kRowThreads * kRowChunks;  // 16,384
+constexpr int kRowSmallK = 8 * kRowThreads * 2;         // 4,096
+
+// rstd[m] for m < M from the [M][T] partials staged in LDS (sst): one wave per row.
 KRQ_DEV void row_rstd(const float* sst, int M, int T, int64_t K, float eps, float* rstd) {
   const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
   for (int m = threadIdx.x >> 6; m < M; m += nw) {
     float a = 0.0f;
     for (int t = lane; t < T; t += 64) a += sst[m * T + t];
-    a = wave_sum(a);
-    if (lane == 0) rstd[m] = rsqrtf(a / (float)K + eps);
+    const float r = rstd_of(a, K, eps);
+    if (lane == 0) rstd[m] = r;
   }
+}
+
+// Row prologue of the row kernels: loads row m's x and ln chunks (chunk c of this thread covers
+// elements 8 * (threadIdx.x + c * kRowThreads)), stages the row's T partials in sst and returns
+// rstd (every thread). Chunks past K hold a repeat of the last one.
+template <int C>
+KRQ_DEV float row_prologue(const uint16_t* __restrict__ x, const float* __restrict__ ss_in,
+                           const uint16_t* __restrict__ ln, float eps, int64_t K, int m, float* sst,
+                           float* rstd_sh, uint4* xv, uint4* lv) {
+  const int T = (int)(K >> 4);
+  const uint8_t* xr = reinterpret_cast<const uint8_t*>(x + m * K);
+  const uint8_t* lr = reinterpret_cast<const uint8_t*>(ln);
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int64_t e = min(8 * (int64_t)(threadIdx.x + c * kRowThreads), K - 8);
+    xv[c] = ld16(xr + 2 * e);
+    lv[c] = ld16(lr + 2 * e);
+  }
+  constexpr int kSp = C / 2;  // partials per thread: T = K / 16 <= kRowThreads * C / 2
+  float sp[kSp];
+#pragma unroll
+  for (int j = 0; j < kSp; ++j) sp[j] = ss_in[(int64_t)m * T + min((int)threadIdx.x + j * kRowThreads, T - 1)];
+#pragma unroll
+  for (int j = 0; j < kSp; ++j)
+    if ((int)threadIdx.x + j * kRowThreads < T) sst[threadIdx.x + j * kRowThreads] = sp[j];
+  __syncthreads();
+  row_rstd(sst, 1, T, K, eps, rstd_sh);
+  __syncthreads();
+  return *rstd_sh;
 }
 
 // Residual epilogue of one row block rb (P == 1 accumulators in red). One split's value is

@@ -27,9 +27,11 @@ using namespace krq;
 // small and takes more waves for long rows instead
 constexpr int kXChunks = 8;
 constexpr int kXChunksDyn = 4;
-// 16-byte (four-partial) sum-of-squares chunks per thread in the RMSNorm prologue
+// 16-byte (four-partial) sum-of-squares chunks per thread in the RMSNorm prologue (staged rows)
 constexpr int kSsChunks = 4;
-constexpr int kSsChunksDyn = 1;
+// sum-of-squares partials per lane in the one-row RMSNorm prologue, where every wave sums the row
+// itself (T = K / 16 <= 64 * kSsPerLane, i.e. K <= 4096)
+constexpr int kSsPerLane = 4;
 constexpr int kMaxThreads = 512;
 
 // PB = 2 (MFMA kernels, modes other than SwiGLU): the block owns two adjacent row blocks, so each
@@ -50,7 +52,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   static_assert(!NORM || XK != KRQ_X_FP8, "the RMSNorm prologue takes bf16 activations");
   constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : PB;  // weight row blocks streamed per step
   constexpr bool FUSED = XK != KRQ_X_FP8;
-  constexpr int SC = XK == KRQ_X_BF16_DYN ? kSsChunksDyn : kSsChunks;
+  constexpr int SC = XK == KRQ_X_BF16_DYN ? kSsPerLane : kSsChunks;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int64_t rb = (int64_t)blockIdx.x * PB, rbu = MODE == KRQ_OUT_SWIGLU ? rb + (NO >> 4) : rb + 1;
@@ -69,6 +71,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   // address where it is not needed: a branch around a load makes the compiler's wait counts
   // conservative (a full drain, vmcnt(0)) at the join, which serializes the weight stream.
   uint4 xv[kXChunks], lv[kXChunks], sv[SC];
+  float sp[SC];
   const uint8_t* lnb = reinterpret_cast<const uint8_t*>(fa.ln);
   if (XK == KRQ_X_BF16_DYN) {
 #pragma unroll
@@ -87,7 +90,10 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
       if (NORM) lv[c] = ld16(lnb + 2 * e);
     }
   }
-  if (NORM) {
+  if (NORM && XK == KRQ_X_BF16_DYN) {  // every wave reads the row's partials itself
+#pragma unroll
+    for (int c = 0; c < SC; ++c) sp[c] = fa.ss_in[min(lane + 64 * c, T - 1)];
+  } else if (NORM) {
     const int nss = M * T / 4;  // 16-byte chunks of the partials
 #pragma unroll
     for (int c = 0; c < SC; ++c)
@@ -130,7 +136,18 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- RMSNorm (NORM): row rstd from the partials, then normalize the loaded chunks ----
-  if (NORM) {
+  if (NORM && XK == KRQ_X_BF16_DYN) {
+    float a = 0.0f;
+#pragma unroll
+    for (int c = 0; c < SC; ++c)
+      if (lane + 64 * c < T) a += sp[c];
+    const float rstd = rstd_of(a, K, fa.eps);
+    // only chunks inside the row: the clamped repeats past K are left raw and kept out of the
+    // amax below (they are never quantized into the slice)
+#pragma unroll
+    for (int c = 0; c < kXChunksDyn; ++c)
+      if (8 * (int64_t)(threadIdx.x + c * blockDim.x) < K) xv[c] = norm8(xv[c], lv[c], rstd);
+  } else if (NORM) {
     float* sst = reinterpret_cast<float*>(xq + (size_t)M * ks);
     const int nss = M * T / 4;
 #pragma unroll
@@ -141,13 +158,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
     __syncthreads();
     row_rstd(sst, M, T, K, fa.eps, rstd_s);
     __syncthreads();
-    if (XK == KRQ_X_BF16_DYN) {
-      // only chunks inside the row: the clamped repeats past K are left raw and kept out of the
-      // amax below (they are never quantized into the slice)
-#pragma unroll
-      for (int c = 0; c < kXChunksDyn; ++c)
-        if (8 * (int64_t)(threadIdx.x + c * blockDim.x) < K) xv[c] = norm8(xv[c], lv[c], rstd_s[0]);
-    } else {
+    {
       const int cpr = ks >> 3;
 #pragma unroll
       for (int c = 0; c < kXChunks; ++c) {

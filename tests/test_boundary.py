@@ -97,7 +97,8 @@ def test_invalid_arguments_fail_before_any_launch():
     assert rc == L.KRQ_EINVAL and b"in one call" in lib.krq_last_error()
     assert lib.krq_gemv_fp8_fused_fits(1, 6144, 2560, 2, L.OUT_PARTIAL, L.X_BF16_DYN, 1) == 1
     assert lib.krq_gemv_fp8_fused_fits(16, 6144, 2560, 2, L.OUT_PARTIAL, L.X_BF16_DYN, 1) == 0
-    assert lib.krq_gemv_fp8_fused_fits(16, 6144, 2560, 2, L.OUT_PARTIAL, L.X_BF16_STATIC, 1) == 1
+    assert lib.krq_gemv_fp8_fused_fits(4, 6144, 2560, 2, L.OUT_PARTIAL, L.X_BF16_STATIC, 1) == 1
+    assert lib.krq_gemv_fp8_fused_fits(16, 6144, 2560, 2, L.OUT_PARTIAL, L.X_BF16_STATIC, 1) == 0
     assert lib.krq_gemv_fp8_fused_fits(32, 19456, 2560, 1, L.OUT_SWIGLU, L.X_BF16_STATIC, 1) == 0
     assert lib.krq_gemv_fp8_fused_fits(1, 2560, 9728, 4, L.OUT_RESIDUAL, L.X_FP8, 0) == 1
     rc = lib.krq_rmsnorm_quant_rows(p, p, p, 1e-6, 1, 16384 + 16, p, p, _null())

@@ -50,7 +50,8 @@ def test_plain_outputs_match_gemv(dev, M):
 
 
 @pytest.mark.parametrize("M,K,N,split,swiglu", [(1, H, NQKV, 2, False), (16, H, NQKV, 2, False),
-                                                (1, H, 2 * I, 1, True), (16, H, 2 * I, 1, True),
+                                                (4, H, NQKV, 2, False), (1, H, 2 * I, 1, True),
+                                                (4, H, 2 * I, 1, True), (16, H, 2 * I, 1, True),
                                                 (4, H, V, 1, False)])
 def test_rmsnorm_prologue(dev, M, K, N, split, swiglu):
     """norm=(ln, ss): includes shapes whose normalized slice fits the in-kernel staging and ones that
@@ -241,21 +242,30 @@ def test_fp8_rmsnorm_prologue_per_token(dev, M, N, split, swiglu):
     assert e <= TOL
 
 
-@pytest.mark.parametrize("M", [1, 3, 32])
-def test_rmsnorm_quant_rows_is_quant_rows_of_rmsnorm(dev, M):
+@pytest.mark.parametrize("M,K", [(1, H), (3, H), (32, H), (2, I), (5, 16384)])
+def test_rmsnorm_quant_rows_is_quant_rows_of_rmsnorm(dev, M, K):
+    """krq_rmsnorm_quant_rows = quant_rows(krq_rmsnorm_rows(x)) bit for bit (both row-kernel
+    variants: K <= 4096 and longer rows); krq_rmsnorm_rows within one bf16 rounding of the
+    oracle's RMSNorm (rsqrt against 1 / sqrt)."""
     from kernels import fp8 as F
     from kernels import fused_gemv as FG
     from kernels import _lib as L
-    x, ln, ss, _ = _norm_inputs(M, H, 80 + M)
+    x, ln, ss, h = _norm_inputs(M, K, 80 + M)
     xd, lnd, ssd = x.to(dev), ln.to(dev), torch.from_numpy(ss).to(dev)
-    x8 = torch.empty((M, H), device=dev, dtype=torch.float8_e4m3fn)
+    x8 = torch.empty((M, K), device=dev, dtype=torch.float8_e4m3fn)
     xs = torch.empty((M,), device=dev, dtype=torch.float32)
-    L.call("krq_rmsnorm_quant_rows", L.ptr(xd), L.ptr(ssd), L.ptr(lnd), EPS, M, H, L.ptr(x8), L.ptr(xs), L.stream(xd))
-    r8, rs = F.quant_rows(FG._rmsnorm(xd, lnd, ssd, EPS))
+    L.call("krq_rmsnorm_quant_rows", L.ptr(xd), L.ptr(ssd), L.ptr(lnd), EPS, M, K, L.ptr(x8), L.ptr(xs), L.stream(xd))
+    hd = FG._rmsnorm(xd, lnd, ssd, EPS)
+    r8, rs = F.quant_rows(hd)
     assert torch.equal(x8.view(torch.uint8), r8.view(torch.uint8)) and torch.equal(xs, rs.reshape(-1))
+    got = O.bf16_to_f32(u16(hd)).astype(np.float64)
+    want = O.bf16_to_f32(h).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-30)
+    assert np.mean(got != want) < 0.05
 
 
-@pytest.mark.parametrize("M,N,split,swiglu", [(1, NQKV, 2, False), (16, NQKV, 2, False), (32, 2 * I, 1, True)])
+@pytest.mark.parametrize("M,N,split,swiglu", [(1, NQKV, 2, False), (4, NQKV, 2, False), (4, 2 * I, 1, True),
+                                              (16, NQKV, 2, False), (32, 2 * I, 1, True)])
 def test_fp8_rmsnorm_prologue_static_scale(dev, M, N, split, swiglu):
     """norm with a static SharedScale a (the reference engine's decode-FP8 form): normalized rows
     cast with a.inv in the prologue; against the oracle's cast of the normalized rows."""
@@ -400,3 +410,29 @@ def test_fp8_fused_graph_replays(dev, monkeypatch, protocol):
         step()
     assert int(bufs.cnt.abs().sum()) == 0
     del g
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_rmsnorm_rounding_all_bf16_products(dev, seed):
+    """The RMSNorm's bf16 roundings (a hardware fp32 -> bf16 convert) against the oracle's round to
+    nearest even: with partials summing to exactly K and eps = 0, rstd = 1 and h = bf16(x * ln), an
+    exact fp32 product rounded once; x runs over all 65,536 bf16 patterns (ties, overflow to inf,
+    subnormal products), ln over random finite patterns. NaN inputs only need to stay NaN."""
+    from kernels import _lib as L
+    M, K = 16, 4096
+    x = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).reshape(M, K)
+    g = torch.Generator().manual_seed(300 + seed)
+    lnb = torch.randint(0, 65536, (K,), generator=g, dtype=torch.int32).to(torch.int16)
+    lnb = torch.where((lnb.int() & 0x7F80) == 0x7F80, lnb & 0x3FFF, lnb)  # finite ln
+    ln = lnb.view(torch.bfloat16)
+    ss = torch.full((M, K // 16), 16.0, dtype=torch.float32)
+    xd, lnd, ssd = x.to(dev), ln.to(dev), ss.to(dev)
+    h = torch.empty_like(xd)
+    L.call("krq_rmsnorm_rows", L.ptr(xd), L.ptr(ssd), L.ptr(lnd), 0.0, M, K, L.ptr(h), L.stream(xd))
+    got = u16(h)
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = O.f32_to_bf16((O.bf16_to_f32(u16(x)) * O.bf16_to_f32(u16(ln))[None, :]).astype(np.float32))
+    nan_w = np.isnan(O.bf16_to_f32(want))
+    assert np.array_equal(np.isnan(O.bf16_to_f32(got)), nan_w)
+    bad = (got != want) & ~nan_w
+    assert not bad.any(), f"{int(bad.sum())} mismatches, first x={u16(x)[bad][:4]} got={got[bad][:4]} want={want[bad][:4]}"
