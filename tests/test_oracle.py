@@ -331,6 +331,8 @@ def test_rmsnorm_and_residual_epilogue():
     assert ss_t.shape == (M, K // 16)
     xf = ref_xn.double()
     assert np.allclose(ss_t.sum(1), (xf * xf).sum(1).numpy(), rtol=1e-12)
+    for m, t in ((0, 0), (1, 7), (2, K // 16 - 1)):  # tile t = columns 16t .. 16t + 15 of row m
+        assert ss_t[m, t] == float((xf[m, 16 * t:16 * t + 16] ** 2).sum())
     eps = 1e-6
     h = O.rmsnorm_rows(xn, ss_t.sum(1), bf16_bits(ln), eps)
     xt = ref_xn.float()
