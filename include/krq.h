@@ -229,6 +229,17 @@ int64_t krq_gemv_fp8_fused_fits(int64_t M, int64_t N, int64_t K, int split, int 
 int krq_rmsnorm_quant_rows(const void* x, const float* ss_in, const void* ln, float eps, int64_t M,
                            int64_t K, void* x8, float* x_scale, void* stream);
 
+/*
+ * FP8 prefill GEMM (M > 32): out bf16 [M, N] = bf16((x8 . w8^T) * x_scale[m or 0] * w_scale[n or 0]),
+ * fp32 accumulate - the torch._scaled_mm product of linear_fp8 (reference engine/kernels/fp8.py:
+ * 97-106, prefill call site engine/engine.py:670-677). x_kind KRQ_X_FP8: x is e4m3 [M, K];
+ * KRQ_X_BF16_STATIC: x is bf16 [M, K], quantized in the kernel as e4m3(clamp(x * x_inv)) (x_inv per
+ * tensor, or per row with x_per_row). w8 row-major e4m3 [N, K]. N and K multiples of 128.
+ */
+int krq_gemm_fp8(const void* x, int x_kind, const float* x_scale, const float* x_inv, int x_per_row,
+                 const void* w8, const float* w_scale, int w_per_row, int64_t M, int64_t N, int64_t K,
+                 void* out, void* stream);
+
 /* Tiled <-> row-major weight copies (byte permutations; see "tiled" above). For a bf16 [N, K]
  * matrix pass its [N, 2K] byte view (K -> 2K). */
 int krq_pack_fp8(const void* w8_rowmajor, int64_t N, int64_t K, void* w8_tiled, void* stream);

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "kernels", "libkrq.so")
-SOURCES = ["quant.hip", "gemv_fp8.hip", "gemv_bf16.hip", "lmhead.hip", "mlp.hip", "fused_gemv.hip", "fused_fp8.hip"]
+SOURCES = ["quant.hip", "gemv_fp8.hip", "gemv_bf16.hip", "lmhead.hip", "mlp.hip", "fused_gemv.hip", "fused_fp8.hip", "gemm_fp8.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in the generated code.
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17",

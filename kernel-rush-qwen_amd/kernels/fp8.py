@@ -292,11 +292,42 @@ def gemv_swiglu_fp8(x, q, a=None, xs=None, algo=L.ALGO_AUTO):
     return _chunked(x8, s, lambda xc, sc: gemv_fp8_launch(xc, sc, q, 1, L.OUT_SWIGLU, algo))
 
 
+def gemm_fp8(x, q, a=None, xs=None):
+    """Prefill FP8 GEMM (krq_gemm_fp8): bf16 [M, N] = bf16(x8 . w8^T * x_scale[m] * w_scale[n]),
+    the product torch._scaled_mm gives linear_fp8 (engine/kernels/fp8.py:105-106).
+    x is bf16 [M, K] with an ActScale / SharedScale `a` (the cast is fused into the GEMM's A-tile
+    staging) or float8_e4m3fn [M, K] with its scale xs (1 or M values); q from quantize_weight /
+    quantize, N and K multiples of 128."""
+    w8, ws = q[0], q[1]
+    L.require_device(x, w8, ws)
+    if w8.dtype != torch.float8_e4m3fn or w8.dim() != 2 or not w8.is_contiguous():
+        raise ValueError("expected a contiguous float8_e4m3fn [N, K] weight")
+    N, K = w8.shape
+    if x.dim() != 2 or x.shape[1] != K:
+        raise ValueError(f"x {tuple(x.shape)} does not match w8 {tuple(w8.shape)}")
+    M = x.shape[0]
+    if x.dtype == torch.float8_e4m3fn:
+        if xs is None or xs.dtype != torch.float32 or xs.numel() not in (1, M):
+            raise ValueError("float8 activations need their fp32 scale xs (1 or M values)")
+        kind, xin, x_scale, x_inv = L.X_FP8, x.contiguous(), xs.reshape(-1).contiguous(), None
+    else:
+        if a is None:
+            raise ValueError("bf16 activations need an ActScale / SharedScale a")
+        kind, xin, x_scale, x_inv = L.X_BF16_STATIC, _rows(x), a.scale.reshape(1), a.inv.reshape(1)
+    L.require_device(x_scale, x_inv)
+    xpr = 1 if (x_scale.numel() == M and M > 1) else 0
+    out = torch.empty((M, N), device=x.device, dtype=torch.bfloat16)
+    L.call("krq_gemm_fp8", L.ptr(xin), kind, L.ptr(x_scale), L.ptr(x_inv), xpr, L.ptr(w8), L.ptr(ws),
+           1 if ws.numel() > 1 else 0, M, N, K, L.ptr(out), L.stream(xin))
+    return out
+
+
 def linear_fp8(x, q, a=None, amax_out=None):
     """bf16 [M, N] ~= x @ W^T with q = quantize_weight(W); a = given scale, or
     None to scale by this tensor's own range (running max kept in amax_out).
     Reference: engine/kernels/fp8.py:97-106. Decode sizes (M <= 32) run the HIP GEMV; larger M
-    (prefill) keep the reference's library GEMM, torch._scaled_mm (hipBLASLt on ROCm)."""
+    (prefill) keep the reference's library GEMM, torch._scaled_mm (hipBLASLt on ROCm), which is
+    2-5x faster on MI355X than this library's MFMA tile GEMM (gemm_fp8) at the Qwen3-4B shapes."""
     w8, ws = q[0], q[1]
     if a is None:
         a = ActScale(x)

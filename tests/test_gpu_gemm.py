@@ -1,0 +1,80 @@
+"""FP8 prefill GEMM (krq_gemm_fp8, kernels.fp8.gemm_fp8) against the exact oracle product of the
+same e4m3 operands: max|y - ref| <= 1e-2 * max|ref| (the path's tolerance), for ragged M, per
+tensor / per row scales, e4m3 activations and bf16 activations quantized in the kernel; the fused
+cast is bit-identical to the reference's cast followed by the GEMM."""
+
+import numpy as np
+import pytest
+import torch
+
+from kernels import fp8 as F
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def rel_err(y, ref):
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.abs(y - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def codes(t):
+    return t.cpu().view(torch.uint8).numpy()
+
+
+def bf(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("M,N,K,per_row", [(33, 128, 128, True), (128, 256, 256, False), (300, 384, 640, True),
+                                           (257, 6144, 2560, True), (256, 2560, 9728, False)])
+def test_gemm_fp8_matches_oracle(dev, M, N, K, per_row):
+    w = bf((N, K), 1, 0.02).to(dev)
+    q = F.quantize(w) if per_row else F.quantize_weight(w)
+    x = bf((M, K), 2).to(dev)
+    x8, xs = F.quant_rows(x)                      # e4m3 activations, per-token scales
+    y = F.gemm_fp8(x8, q, xs=xs)
+    _, ref = O.fp8_matmul(codes(x8), xs.cpu().numpy().reshape(-1), codes(q[0]), q[1].cpu().numpy())
+    e = rel_err(y.float().cpu().numpy(), ref)
+    print(f"gemm M={M} N={N} K={K}: max-rel {e:.2e}")
+    assert e <= TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(200, 256, 384), (512, 2560, 4096)])
+def test_gemm_fused_cast_is_cast_then_gemm(dev, M, N, K):
+    """bf16 x with an ActScale: the in-kernel cast equals fp8._cast + the e4m3 GEMM bit for bit,
+    and linear_fp8 (prefill) is within the bar of the oracle."""
+    w = bf((N, K), 3, 0.02).to(dev)
+    q = F.quantize_weight(w)
+    x = bf((M, K), 4).to(dev)
+    a = F.ActScale(x)
+    y = F.gemm_fp8(x, q, a)
+    y2 = F.gemm_fp8(F._cast(x, a), q, xs=a.scale.reshape(1))
+    assert torch.equal(y, y2)
+    _, ref = O.fp8_matmul(codes(F._cast(x, a)), a.scale.cpu().numpy(), codes(q[0]), q[1].cpu().numpy())
+    assert rel_err(F.linear_fp8(x, q).float().cpu().numpy(), ref) <= TOL
+    assert rel_err(y.float().cpu().numpy(), ref) <= TOL
+
+
+def test_gemm_matches_library_gemm(dev):
+    """Against torch._scaled_mm (hipBLASLt) on the same operands: both within the bar of the oracle,
+    and within a few bf16 ulps of each other."""
+    M, N, K = 384, 2560, 2560
+    q = F.quantize_weight(bf((N, K), 5, 0.02).to(dev))
+    x = bf((M, K), 6).to(dev)
+    a = F.ActScale(x)
+    x8 = F._cast(x, a)
+    ours = F.gemm_fp8(x8, q, xs=a.scale.reshape(1)).float()
+    lib = torch._scaled_mm(x8, q[0].t(), scale_a=a.scale, scale_b=q[1], out_dtype=torch.bfloat16).float()
+    assert rel_err(ours.cpu().numpy(), lib.cpu().numpy()) <= 2 * 2.0 ** -8
+
+
+def test_gemm_rejects_bad_shapes(dev):
+    q = F.quantize_weight(bf((200, 256), 7).to(dev))  # N not a multiple of 128
+    x8, xs = F.quant_rows(bf((64, 256), 8).to(dev))
+    with pytest.raises(ValueError):
+        F.gemm_fp8(x8, q, xs=xs)
