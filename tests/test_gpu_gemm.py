@@ -31,7 +31,8 @@ def bf(shape, seed, scale=1.0):
 
 
 @pytest.mark.parametrize("M,N,K,per_row", [(33, 128, 128, True), (128, 256, 256, False), (300, 384, 640, True),
-                                           (257, 6144, 2560, True), (256, 2560, 9728, False)])
+                                           (257, 6144, 2560, True), (256, 2560, 9728, False),
+                                           (600, 512, 384, True), (1024, 2560, 9728, False), (777, 6144, 2560, True)])
 def test_gemm_fp8_matches_oracle(dev, M, N, K, per_row):
     w = bf((N, K), 1, 0.02).to(dev)
     q = F.quantize(w) if per_row else F.quantize_weight(w)
