@@ -19,6 +19,10 @@ Also printed (stderr): per-kernel table from graph-replayed back-to-back launche
 and the roofline of the dominant kernel (the gate_up GEMV; its HBM traffic from the committed
 rocprofv3 counter summary). --config c3 runs M = 16, --config c3m32 M = 32, --config c4 the
 lm_head + argmax (--lm bf16|fp8, --m 1|16), --config c5 the full decode step (36 layers + lm_head).
+--config layer runs the fused FP8 decoder layer (kernels.fused_gemv: O with the residual epilogue,
+gate_up with the RMSNorm prologue, down with the residual epilogue, the next QKV with the RMSNorm
+prologue, chained as engine/engine.py:953-961 chains them; --m rows), --config prefill the FP8
+prefill GEMM against the library GEMM (--m rows, default 1024).
 """
 
 import argparse
@@ -40,6 +44,89 @@ METRIC = "FP8 skinny-GEMM HBM GB/s (% of 8 TB/s peak) at Qwen3-4B shapes, M=1 an
 # (name, N rows of W, K, split, mode)
 PROJ = [("qkv", NQKV, H, 2, "partial"), ("o", H, NQD, 4, "partial"),
         ("gate_up", 2 * I, H, 1, "swiglu"), ("down", H, I, 4, "partial")]
+
+
+def fused_layer(torch, dev, layers, xs, M):
+    """The fused FP8 decoder layer (engine/engine.py:953-961 order): x = cur + O(attn);
+    act = SwiGLU(rmsnorm(x) W_gu); x = x + down(act); qkv = rmsnorm(x) W_qkv (split-2 partials).
+    Returns (step, algorithmic bytes per step, [(stage name, fn, bytes)])."""
+    from kernels.fused_gemv import FusedLayerBuffers, gemv_fused, gemv_swiglu_fused
+    bufs = FusedLayerBuffers(M, H, V, dev)
+    g = torch.Generator().manual_seed(3000)
+    bufs.res[0].copy_(torch.randn(M, H, generator=g).to(torch.bfloat16))
+    ln = [(1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev) for _ in range(2)]
+    attn = xs["o"]
+    # seed the partials of the first consumers from the starting residual rows
+    sq = bufs.res[0].float().pow(2).reshape(M, H // 16, 16).sum(-1)
+    bufs.ss[0].copy_(sq)
+    bufs.ss[1].copy_(sq)
+
+    def o(i):
+        gemv_fused(attn, layers[i % LAYERS]["o"], 4, ep=(bufs.res[0], bufs.res[1], bufs.ss[1], bufs.cnt))
+
+    act = {}
+
+    def gu(i):
+        act["a"] = gemv_swiglu_fused(bufs.res[1], layers[i % LAYERS]["gate_up"], norm=(ln[1], bufs.ss[1]))
+
+    gu(0)
+
+    def down(i):
+        gemv_fused(act["a"], layers[i % LAYERS]["down"], 4, ep=(bufs.res[1], bufs.res[0], bufs.ss[0], bufs.cnt))
+
+    def qkv(i):
+        gemv_fused(bufs.res[0], layers[(i + 1) % LAYERS]["qkv"], 2, norm=(ln[0], bufs.ss[0]))
+
+    def step(i):
+        o(i)
+        gu(i)
+        down(i)
+        qkv(i)
+
+    res = 2 * M * H + 2 * M * H + 4 * M * (H // 16)          # residual in / out, sums of squares out
+    nrm = 2 * H + 4 * M * (H // 16)                           # RMSNorm weight, sums of squares in
+    b_o = H * NQD + 4 * H + 2 * M * NQD + res
+    b_gu = 2 * I * H + 8 * I + 2 * M * H + nrm + 2 * M * I
+    b_dn = H * I + 4 * H + 2 * M * I + res
+    b_qkv = NQKV * H + 4 * NQKV + 2 * M * H + nrm + 4 * 2 * M * NQKV
+    stages = [("o+residual", o, b_o), ("gate_up+norm", gu, b_gu), ("down+residual", down, b_dn),
+              ("qkv+norm", qkv, b_qkv)]
+    return step, b_o + b_gu + b_dn + b_qkv, stages
+
+
+def prefill(torch, fp8, dev_rows):
+    """FP8 prefill GEMM at the four Qwen3-4B projections, M = dev_rows: krq_gemm_fp8 on e4m3
+    activations against torch._scaled_mm (hipBLASLt) on the same operands, and the reference's
+    whole linear_fp8 (ActScale + cast + library GEMM). Prints one JSON line for gate_up."""
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    M = dev_rows
+    out = {}
+    for p, (name, N, K, _, _) in enumerate(PROJ):
+        g = torch.Generator(device=dev).manual_seed(4000 + p)
+        q = fp8.quantize_weight((torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16))
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        a = fp8.ActScale(x)
+        x8, xs = fp8._cast(x, a), a.scale.reshape(1)
+        t_ours = graph_time(torch, lambda i: fp8.gemm_fp8(x8, q, xs=xs), 20)[0]
+        t_lib = graph_time(torch, lambda i: torch._scaled_mm(x8, q[0].t(), scale_a=a.scale, scale_b=q[1],
+                                                             out_dtype=torch.bfloat16), 20)[0]
+        t_lin = graph_time(torch, lambda i: fp8.linear_fp8(x, q), 20)[0]
+        fl = 2.0 * M * N * K
+        out[name] = (t_ours, t_lib, t_lin, fl)
+        log(f"[bench] prefill M={M} {name:<8} krq_gemm_fp8 {t_ours:8.1f} us ({fl / t_ours / 1e6:6.0f} TFLOP/s) | "
+            f"hipBLASLt {t_lib:8.1f} us ({fl / t_lib / 1e6:6.0f} TFLOP/s) | linear_fp8 {t_lin:8.1f} us")
+    t_ours, t_lib, t_lin, fl = out["gate_up"]
+    tf = fl / t_ours / 1e6
+    print(json.dumps({
+        "metric": "FP8 prefill GEMM TFLOP/s (gate_up [19456x2560])", "value": round(tf, 1), "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": 20, "warmup": 1, "ms_per_step": round(t_ours / 1e3, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp8_e4m3", "data": "synthetic",
+        "config": {"workload": f"prefill GEMM M={M}", "library_tflops": round(fl / t_lib / 1e6, 1),
+                   "linear_fp8_us": round(t_lin, 2)},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": 5000.0, "unit": "TFLOP/s",
+                     "frac": round(tf / 5000.0, 4), "traffic": None},
+        "cpu_baseline": None}), flush=True)
 
 
 def log(*a):
@@ -279,8 +366,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c3m32", "c4", "c5"])
-    ap.add_argument("--m", type=int, default=None, help="rows for --config c4 / c5 (default 1)")
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c3m32", "c4", "c5", "layer", "prefill"])
+    ap.add_argument("--m", type=int, default=None, help="rows for --config c4 / c5 / layer (default 1) "
+                    "and prefill (default 1024)")
     ap.add_argument("--lm", default="bf16", choices=["bf16", "fp8"], help="lm head weights (c4)")
     ap.add_argument("--layout", default="tiled", choices=["tiled", "rowmajor"],
                     help="FP8 weight layout read by the GEMV")
@@ -301,6 +389,8 @@ def main():
     from kernels import gemv as G
 
     cfg = args.config
+    if cfg == "prefill":
+        return prefill(torch, fp8, dev_rows=args.m or 1024)
     M = {"c2": 1, "c3": 16, "c3m32": 32}.get(cfg, args.m or 1)
     steps = args.steps or {"c4": 20, "c5": 5}.get(cfg, 360)
     warmup = args.warmup if args.warmup is not None else {"c4": 2, "c5": 1}.get(cfg, 36)
@@ -339,6 +429,10 @@ def main():
         step, step_bytes = layer_step, layer_bytes
         work = (f"{cfg.upper()}: one Qwen3-4B decoder layer's QKV/O/gate_up/down FP8 projections "
                 f"at M={M}, per-token dynamic scales, per-channel weights, cycling {LAYERS} layers")
+    elif cfg == "layer":
+        step, step_bytes, fused_stages = fused_layer(torch, dev, layers, xs, M)
+        work = (f"fused FP8 decoder layer at M={M}: O + residual, gate_up with RMSNorm, down + residual, "
+                f"next QKV with RMSNorm (kernels.fused_gemv), per-token scales, cycling {LAYERS} layers")
     elif cfg == "c4":
         w_lm = E if E is not None else q8
         step = lambda i: lmhead.lm_head_argmax(h, w_lm)
@@ -365,7 +459,20 @@ def main():
         log("[bench] calibration copy: 268435456 bytes read, 268435456 bytes written")
         del src, dst
 
-    if cfg in ("c2", "c3", "c3m32"):
+    if cfg == "layer":
+        rows = []
+        for name, fn, nbytes in fused_stages:
+            tmin, tmed = graph_time(torch, fn, args.reps)
+            rows.append({"name": name, "us_min": tmin, "us_med": tmed, "bytes": nbytes})
+        log(f"[bench] fused layer stages (graph of {args.reps} back-to-back launches, cycling {LAYERS} layers):")
+        for r in rows:
+            log(f"  {r['name']:<14} {r['us_min']:8.2f} us (median {r['us_med']:.2f})  {r['bytes']:>10} B  "
+                f"{r['bytes'] / r['us_min'] / 1e3:7.0f} GB/s")
+        dom = max(rows, key=lambda r: r["bytes"])
+        key = None
+        kern = f"fused {dom['name']} M={M}"
+        dom_bytes, dom_us = dom["bytes"], dom["us_min"]
+    elif cfg in ("c2", "c3", "c3m32"):
         rows = kernel_table(torch, fp8, L, layers, xs, M, args.reps)
         print_rows(rows, args.reps)
         dom = max(rows[:4], key=lambda r: r["bytes"])
