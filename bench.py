@@ -379,8 +379,8 @@ def main():
                     help="also run one 256 MiB device copy (known bytes) to scale HBM counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one GPU only (the path is single-GPU; see the "
-              "sharding notes in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py: this build measures one GPU only (the path runs on one GPU; sharding across "
+              "GPUs is a design note, not an implementation); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
