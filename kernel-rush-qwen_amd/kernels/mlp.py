@@ -11,12 +11,18 @@ first; the SwiGLU activations are re-quantized per token inside the kernel once 
 `programs` is the number of blocks, as in the reference; the library clamps it to the blocks the
 device holds at once (so spin-waits cannot deadlock), and `programs=None` takes one per CU. The
 control words are zeroed here once and left zeroed by every launch.
+
+BF16 weights (the reference engine's default, engine/engine.py:911-915) return the same contract
+through the two GEMV launches of kernels.gemv (SwiGLU, then the split-K down partials): on MI355X
+the one-launch form measured slower than the pair for FP8 weights (the cross-XCD handoff between
+the phases costs more than the launch boundary), so the BF16 path is the pair.
 """
 
 import torch
 
 from . import _lib as L
 from . import fp8 as _fp8
+from . import gemv as _gemv
 
 
 class PersistentMLP:
@@ -35,9 +41,25 @@ class PersistentMLP:
         self.ctl = torch.zeros((int(L.lib().krq_mlp_ctl_words()),), device=device, dtype=torch.int32)
         self.act = None   # bf16 [M, I] SwiGLU activations of the last call
 
+    def _bf16(self, h, w_gu, w_down):
+        H, I = self.H, self.I
+        if tuple(w_gu.shape) != (2 * I, H) or tuple(w_down.shape) != (H, I):
+            raise ValueError(f"PersistentMLP: weights {tuple(w_gu.shape)} / {tuple(w_down.shape)} do not "
+                             f"match H={H}, I={I}")
+        h2 = _fp8._rows(h)
+        if h2.shape[0] != self.M:
+            raise ValueError(f"PersistentMLP built for M={self.M}, called with M={h2.shape[0]}")
+        act = _gemv.gemv_swiglu(h2, w_gu)
+        self.act = act
+        return _gemv.gemv(act, w_down, self.split)
+
     def __call__(self, h, w_gu, w_down):
+        if isinstance(w_gu, torch.Tensor) and isinstance(w_down, torch.Tensor):
+            if w_gu.dtype != torch.bfloat16 or w_down.dtype != torch.bfloat16:
+                raise ValueError("PersistentMLP: weights are FP8Weight tuples or bf16 tensors")
+            return self._bf16(h, w_gu, w_down)
         if not (isinstance(w_gu, tuple) and isinstance(w_down, tuple)):
-            raise ValueError("PersistentMLP: the HIP kernel takes FP8 weights (fp8.quantize)")
+            raise ValueError("PersistentMLP: weights are FP8Weight tuples or bf16 tensors")
         H, I, S = self.H, self.I, self.split
         gu, lay_gu, gs, gshape = _fp8._weight_operand(w_gu)
         dn, lay_dn, ds, dshape = _fp8._weight_operand(w_down)

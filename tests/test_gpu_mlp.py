@@ -160,3 +160,28 @@ def test_mlp_counters_reset_across_calls_and_graph_replays(dev):
         assert torch.equal(pm(xd, qgu, qd), first)
     assert not pm.failed() and int(pm.ctl.abs().sum()) == 0
     del g
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_mlp_bf16_weights(dev, M):
+    """BF16 weights (the reference engine's call, engine/engine.py:911-915): the same contract,
+    fp32 partials [S, M, H] whose in-order sum is the product, against the oracle (bf16 matmul,
+    SwiGLU rounding chain, bf16 matmul)."""
+    from kernels import gemv as G
+    g = torch.Generator().manual_seed(500 + M)
+    h = torch.randn(M, H, generator=g).to(torch.bfloat16)
+    wgu = (torch.randn(2 * I, H, generator=g) * 0.02).to(torch.bfloat16)
+    wd = (torch.randn(H, I, generator=g) * 0.02).to(torch.bfloat16)
+    pm = PersistentMLP(M, H, I, dev)
+    out = pm(h.to(dev), wgu.to(dev), wd.to(dev))
+    assert out.shape == (4, M, H) and out.dtype == torch.float32
+    full = O.bf16_matmul(u16(h), u16(wgu))
+    act = O.swiglu(full[:, :I].astype(np.float32), full[:, I:].astype(np.float32))
+    ref = O.bf16_matmul(act, u16(wd))
+    assert rel_err(pm.act.float().cpu().numpy(), O.bf16_to_f32(act)) <= TOL
+    y = out[0].clone()
+    for s in range(1, 4):
+        y += out[s]
+    assert rel_err(y.cpu().numpy(), ref) <= TOL
+    # the same kernels as the two GEMV calls
+    assert torch.equal(out, G.gemv(G.gemv_swiglu(h.to(dev), wgu.to(dev)), wd.to(dev), 4))
