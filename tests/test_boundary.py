@@ -103,6 +103,15 @@ def test_invalid_arguments_fail_before_any_launch():
     assert lib.krq_gemv_fp8_fused_fits(1, 2560, 9728, 4, L.OUT_RESIDUAL, L.X_FP8, 0) == 1
     rc = lib.krq_rmsnorm_quant_rows(p, p, p, 1e-6, 1, 16384 + 16, p, p, _null())
     assert rc == L.KRQ_EINVAL and b"at most 16384" in lib.krq_last_error()
+    rc = lib.krq_rmsnorm_rows(p, p, p, 1e-6, 1, 20000, p, _null())
+    assert rc == L.KRQ_EINVAL and b"at most 16384" in lib.krq_last_error()
+    # prefill GEMM: N and K multiples of 128; bf16 activations need their inverse scale
+    rc = lib.krq_gemm_fp8(p, L.X_FP8, p, None, 0, p, p, 1, 256, 200, 256, p, _null())
+    assert rc == L.KRQ_EINVAL and b"multiples of 128" in lib.krq_last_error()
+    rc = lib.krq_gemm_fp8(p, L.X_BF16_STATIC, p, None, 0, p, p, 1, 256, 256, 256, p, _null())
+    assert rc == L.KRQ_EINVAL and b"x_inv" in lib.krq_last_error()
+    rc = lib.krq_gemm_fp8(p, L.X_BF16_DYN, p, p, 0, p, p, 1, 256, 256, 256, p, _null())
+    assert rc == L.KRQ_EINVAL and b"x_kind" in lib.krq_last_error()
 
 
 def test_fused_buffers_and_mlp_contracts():
@@ -140,3 +149,25 @@ def test_reference_helpers():
     q = fp8.FP8Weight(torch.zeros(1), torch.ones(()), None)
     w8, s = q
     assert isinstance(q, tuple) and q.tiled is None and s.item() == 1.0
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 exits with a message before touching a device."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_fused_and_gemm_wrappers_refuse_cpu_tensors():
+    from kernels import fused_gemv as FG
+    x = torch.zeros(1, 256, dtype=torch.bfloat16)
+    w = torch.zeros(32, 256, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        FG.gemv_fused(x, w, 1)
+    q = fp8.FP8Weight(torch.zeros(128, 256, dtype=torch.float8_e4m3fn), torch.ones(()), None)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        FG.gemv_fused(x, q, 1, ep=(x, x, x, x))
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        fp8.gemm_fp8(torch.zeros(64, 256, dtype=torch.float8_e4m3fn), q, xs=torch.ones(1))
