@@ -308,11 +308,11 @@ def lm_bytes(M, kind):
 
 def dominant_key(M, mode, fused, layout):
     """The template name rocprofv3 reports for the GEMV kernel of these arguments
-    (k_gemv_fp8<MT, MODE, LAYOUT, XK, ALGO, U, PB>; the SwiGLU kernel is never paired), to look
-    up its measured HBM traffic."""
+    (k_gemv_fp8<MT, MODE, LAYOUT, XK, ALGO, U, PB, AWC>; the SwiGLU kernel is never paired and
+    has no activation wave), to look up its measured HBM traffic."""
     mt = 1 if M <= 16 else 2
     u = 4 if M <= 4 else 2
-    return f"k_gemv_fp8<{mt}, {mode}, {layout}, {1 if fused else 0}, 1, {u}, 1>"
+    return f"k_gemv_fp8<{mt}, {mode}, {layout}, {1 if fused else 0}, 1, {u}, 1, 0>"
 
 
 def measured_traffic(cfg, key):

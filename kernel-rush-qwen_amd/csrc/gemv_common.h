@@ -126,6 +126,32 @@ KRQ_DEV uint2 quant8(uint4 v, float s) {
   return r;
 }
 
+// 8 bf16 times the inverse of their own row's amax -> 8 e4m3 bytes, without the clamp: |x * inv| is
+// at most 448.0001 (fp32 rounding of amax * fl(fl(1 / amax) * 448)), which the convert rounds to
+// 448 as the clamp would; a NaN element gives a NaN code (its sign does not reach the products)
+KRQ_DEV uint2 quant8_own_amax(uint4 v, float s) {
+  uint2 r;
+  int p = __builtin_amdgcn_cvt_pk_fp8_f32(as_f32(v.x << 16) * s, as_f32(v.x & 0xffff0000u) * s, 0, false);
+  r.x = static_cast<uint32_t>(
+      __builtin_amdgcn_cvt_pk_fp8_f32(as_f32(v.y << 16) * s, as_f32(v.y & 0xffff0000u) * s, p, true));
+  p = __builtin_amdgcn_cvt_pk_fp8_f32(as_f32(v.z << 16) * s, as_f32(v.z & 0xffff0000u) * s, 0, false);
+  r.y = static_cast<uint32_t>(
+      __builtin_amdgcn_cvt_pk_fp8_f32(as_f32(v.w << 16) * s, as_f32(v.w & 0xffff0000u) * s, p, true));
+  return r;
+}
+
+// |x| max of 8 bf16 on their bits: |x| orders as its bit pattern (sign cleared), so a packed
+// 16-bit integer max per 32-bit word suffices; m holds two running maxima. Integer work only, which
+// also keeps the compiler from holding fp32 copies of the row for the quantization that follows.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+KRQ_DEV u16x2 absmax8_bits(uint4 v, u16x2 m) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[q] & 0x7fff7fffu));
+  return m;
+}
+KRQ_DEV float bits_max_to_f32(u16x2 m) { return as_f32(static_cast<uint32_t>(m.x > m.y ? m.x : m.y) << 16); }
+
 KRQ_DEV float absmax8(uint4 v, float m) {
   const uint32_t a[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -441,9 +467,9 @@ struct Plan {
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Waves per block for a block of nsteps steps over P weight matrices with U step slots per wave,
-// in a grid of `blocks` blocks. Overridable (for launch-shape sweeps) by the environment variable
-// KRQ_GEMV_WAVES.
-int plan_waves(int nsteps, int P, int U, int64_t blocks);
+// in a grid of `blocks` blocks (act_wave: weight waves beside the one-row kernel's activation
+// wave). Overridable (for launch-shape sweeps) by the environment variable KRQ_GEMV_WAVES.
+int plan_waves(int nsteps, int P, int U, int64_t blocks, bool act_wave = false);
 
 // Validated launches shared by the C ABI entry points (gemv_fp8.hip, gemv_bf16.hip); mode may
 // also be kOutArgmax (then split == 1, aux = [N/16][M] Best, out = optional bf16 logits).

@@ -8,7 +8,7 @@
 using namespace krq;
 
 namespace krq {
-int plan_waves(int nsteps, int P, int U, int64_t blocks) {
+int plan_waves(int nsteps, int P, int U, int64_t blocks, bool act_wave) {
   static const int env = [] {
     const char* s = getenv("KRQ_GEMV_WAVES");
     return s ? atoi(s) : 0;
@@ -19,10 +19,13 @@ int plan_waves(int nsteps, int P, int U, int64_t blocks) {
   // all of its steps to be in flight at once (one memory round trip), up to 4; when that is not
   // enough, two waves, unless the grid has fewer blocks than the chip has CUs x 2 (the single-pass
   // O and down, 160 blocks: 5.07 / 8.74 us with 4 waves against 6.50 / 8.75 with 2 at M = 1),
-  // where four keep more loads in flight. The two-matrix SwiGLU block takes two waves.
+  // where four keep more loads in flight. The two-matrix SwiGLU block takes two waves. Beside an
+  // activation wave (one-row kernel), three (four waves in all): down 7.68 -> 7.16 us and the FP8
+  // lm_head 64.7 -> 63.1 us at M = 1.
   const int w = (nsteps + U - 1) / U;
   if (P != 1) return 2;
   if (w <= 4) return w;
+  if (act_wave) return 3;
   return blocks < 512 ? 4 : 2;
 }
 }  // namespace krq
@@ -31,39 +34,60 @@ namespace {
 
 #define KRQ_GEMV_ARGS xb, x_scale, x_inv, x_per_row, wb, w_scale, w_per_row, m, NO, K, kts, out, aux
 
+// one-row kind: MT 1, U 4, no pairing; awc = chunks per lane of the activation wave (0: none)
+template <int MODE, int LAYOUT, int ALGO>
+void launch_dyn(int awc, dim3 grid, dim3 block, size_t smem, hipStream_t s, const uint8_t* xb,
+                const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
+                const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out,
+                void* aux) {
+  constexpr int XK = KRQ_X_BF16_DYN;
+  if (awc == kAwSmall)
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, 4, 1, kAwSmall>), grid, block, smem, s, KRQ_GEMV_ARGS);
+  else if (awc == kAwLarge)
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, 4, 1, kAwLarge>), grid, block, smem, s, KRQ_GEMV_ARGS);
+  else
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, 4, 1, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
+}
+
 template <int MODE, int LAYOUT, int XK>
-int launch(int algo, int pb, int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb,
+int launch(int algo, int pb, int awc, int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb,
            const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
            const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out,
            void* aux) {
-  const dim3 block(nw * 64);
+  const dim3 block((nw + (awc > 0 ? 1 : 0)) * 64);
   constexpr int PB2 = MODE == KRQ_OUT_SWIGLU ? 1 : 2;  // no paired variant of the SwiGLU kernel
-  if (algo == 2)
-    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 2, 4, 1>), grid, block, smem, s, KRQ_GEMV_ARGS);
-  else if (M <= 4)
-    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, 4, 1>), grid, block, smem, s, KRQ_GEMV_ARGS);
-  else if (M <= 16 && pb == 2)
-    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, 2, PB2>), grid, block, smem, s, KRQ_GEMV_ARGS);
-  else if (M <= 16)
-    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, 2, 1>), grid, block, smem, s, KRQ_GEMV_ARGS);
-  else if (pb == 2)
-    hipLaunchKernelGGL((k_gemv_fp8<2, MODE, LAYOUT, XK, 1, 2, PB2>), grid, block, smem, s, KRQ_GEMV_ARGS);
-  else
-    hipLaunchKernelGGL((k_gemv_fp8<2, MODE, LAYOUT, XK, 1, 2, 1>), grid, block, smem, s, KRQ_GEMV_ARGS);
+  if constexpr (XK == KRQ_X_BF16_DYN) {
+    if (algo == 2)
+      launch_dyn<MODE, LAYOUT, 2>(awc, grid, block, smem, s, KRQ_GEMV_ARGS);
+    else
+      launch_dyn<MODE, LAYOUT, 1>(awc, grid, block, smem, s, KRQ_GEMV_ARGS);
+  } else if (algo == 2) {
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 2, 4, 1, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
+  } else if (M <= 4) {
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, 4, 1, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
+  } else if (M <= 16 && pb == 2) {
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, 2, PB2, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
+  } else if (M <= 16) {
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, 2, 1, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
+  } else if (pb == 2) {
+    hipLaunchKernelGGL((k_gemv_fp8<2, MODE, LAYOUT, XK, 1, 2, PB2, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
+  } else {
+    hipLaunchKernelGGL((k_gemv_fp8<2, MODE, LAYOUT, XK, 1, 2, 1, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
+  }
   return 0;
 }
 
 template <int MODE, int LAYOUT>
-void launch_xk(int xk, int algo, int pb, int M, dim3 grid, int nw, size_t smem, hipStream_t s,
+void launch_xk(int xk, int algo, int pb, int awc, int M, dim3 grid, int nw, size_t smem, hipStream_t s,
                const uint8_t* xb, const float* x_scale, const float* x_inv, int x_per_row,
                const uint8_t* wb, const float* w_scale, int w_per_row, int m, int64_t NO,
                int64_t K, int kts, void* out, void* aux) {
   if (xk == KRQ_X_FP8)
-    launch<MODE, LAYOUT, KRQ_X_FP8>(algo, pb, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
+    launch<MODE, LAYOUT, KRQ_X_FP8>(algo, pb, awc, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
   else if (xk == KRQ_X_BF16_DYN)
-    launch<MODE, LAYOUT, KRQ_X_BF16_DYN>(algo, pb, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
+    launch<MODE, LAYOUT, KRQ_X_BF16_DYN>(algo, pb, awc, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
   else
-    launch<MODE, LAYOUT, KRQ_X_BF16_STATIC>(algo, pb, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
+    launch<MODE, LAYOUT, KRQ_X_BF16_STATIC>(algo, pb, awc, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
 }
 
 }  // namespace
@@ -111,16 +135,28 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   const int MT = (algo == 2 || M <= 16) ? 1 : 2;
   // step slots per wave of the variant launch() picks
   const int U = (algo == 2 || M <= 4) ? 4 : 2;
-  int nw = plan_waves((kts + 1) / 2, P, U, NO / 16 / pb * split);
-  // fused prologues hold at most kXChunks 16-byte chunks per thread
+  // one-row kind: an activation wave holding the whole row (K <= 10240; KRQ_GEMV_AW=0 turns it off),
+  // else every wave takes part in the prologue. Measured at M = 1: QKV 5.92 -> 5.29 us, O 5.15 ->
+  // 4.41, down 7.91 -> 7.16, FP8 lm_head 64.9 -> 63.1; the SwiGLU GEMV, whose two-matrix block has
+  // a long main loop that hides the prologue, keeps the shared prologue (10.92 against 11.04 us).
+  static const bool aw_ok = [] {
+    const char* e = getenv("KRQ_GEMV_AW");
+    return !(e && atoi(e) == 0);
+  }();
+  int awc = 0;
+  if (x_kind == KRQ_X_BF16_DYN && aw_ok && mode != KRQ_OUT_SWIGLU)
+    awc = K <= 512 * kAwSmall ? kAwSmall : K <= 512 * kAwLarge ? kAwLarge : 0;
+  int nw = plan_waves((kts + 1) / 2, P, U, NO / 16 / pb * split, awc > 0);
+  // the other fused prologues hold at most kXChunks 16-byte chunks per thread
   int64_t xchunks = 0;
-  if (x_kind == KRQ_X_BF16_DYN) xchunks = (K + 7) / 8;
+  if (x_kind == KRQ_X_BF16_DYN && awc == 0) xchunks = (K + 7) / 8;
   if (x_kind == KRQ_X_BF16_STATIC) xchunks = M * (ks / 8);
   const int xc = x_kind == KRQ_X_BF16_DYN ? kXChunksDyn : kXChunks;
   while ((int64_t)nw * 64 * xc < xchunks && nw < kMaxThreads / 64) ++nw;
   KRQ_REQUIRE((int64_t)nw * 64 * xc >= xchunks,
               "gemv_fp8: activation slice of %lld elements too large for in-kernel quantization",
               (long long)(xchunks * 8));
+  if (awc > 0) nw = min(nw, kMaxThreads / 64 - 1);
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) +
                       (x_kind == KRQ_X_FP8 ? 0 : (size_t)M * ks);
   const dim3 grid(static_cast<unsigned>(NO / 16 / pb), static_cast<unsigned>(split));
@@ -129,7 +165,7 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   const int m = static_cast<int>(M);
   hipStream_t s = (hipStream_t)stream;
 #define KRQ_FP8_CASE(MODE, LAYOUT)                                                                   \
-  launch_xk<MODE, LAYOUT>(x_kind, algo, pb, m, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, \
+  launch_xk<MODE, LAYOUT>(x_kind, algo, pb, awc, m, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, \
                           w_scale, w_per_row, m, NO, K, kts, out, aux)
   if (w_layout == KRQ_W_TILED) {
     if (mode == KRQ_OUT_BF16) KRQ_FP8_CASE(KRQ_OUT_BF16, KRQ_W_TILED);

@@ -33,11 +33,45 @@ constexpr int kSsChunks = 4;
 // itself (T = K / 16 <= 64 * kSsPerLane, i.e. K <= 4096)
 constexpr int kSsPerLane = 4;
 constexpr int kMaxThreads = 512;
+// one-row activation wave: 16-byte chunks per lane (the whole row, K <= 64 * 8 * AWC)
+constexpr int kAwSmall = 8, kAwLarge = 20;
+
+// The activation wave of the one-row (KRQ_X_BF16_DYN) kernel: one extra wave per block that loads
+// the whole bf16 row, takes its amax (ActScale arithmetic), and quantizes the block's K slice
+// [k0, k0 + ks) into LDS, while the other waves only issue their weight loads. It issues no weight
+// loads itself, so its row loads are not queued behind its own weight stream, and it runs at
+// raised issue priority; the weight waves wait for it at one barrier.
+template <int AWC>
+KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, int64_t K, int64_t k0, int ks, int lane,
+                             uint8_t* xq, float* xs_l) {
+  __builtin_amdgcn_s_setprio(3);
+  // chunk i = lane + 64 c holds elements 8i .. 8i + 7; indices past the row repeat its last chunk
+  const int last = static_cast<int>(K >> 3) - 1, lo = static_cast<int>(k0 >> 3), n = ks >> 3;
+  uint4 v[AWC];
+#pragma unroll
+  for (int c = 0; c < AWC; ++c) v[c] = ld16(x + 16 * min(lane + 64 * c, last));
+  __builtin_amdgcn_sched_barrier(0);  // every row load in flight before the first wait
+  u16x2 mb = {0, 0};
+#pragma unroll
+  for (int c = 0; c < AWC; ++c) mb = absmax8_bits(v[c], mb);
+  const float am = fmaxf(wave_max_nonneg(bits_max_to_f32(mb)), 1e-6f);
+  const float inv = inv_from_amax(am);
+  if (lane == 0) xs_l[0] = scale_from_amax(am);
+#pragma unroll
+  for (int c = 0; c < AWC; ++c) {
+    const int i = lane + 64 * c - lo;  // chunk index inside the slice
+    if (static_cast<unsigned>(i) < static_cast<unsigned>(n))
+      *reinterpret_cast<uint2*>(xq + 8 * i) = quant8_own_amax(v[c], inv);
+  }
+  __builtin_amdgcn_s_setprio(0);
+}
 
 // PB = 2 (MFMA kernels, modes other than SwiGLU): the block owns two adjacent row blocks, so each
 // activation load feeds two matrix-core products (at M > 1 the activation slices are as large as
 // the weight steps, and every row block re-reads them).
-template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, int PB, bool NORM>
+// AWC > 0 (one-row kind without RMSNorm): the block's last wave is the activation wave above and
+// the others stream weights; AWC = 0: every wave takes part in the activation prologue.
+template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, int PB, bool NORM, int AWC>
 KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restrict__ xsc,
                            const float* __restrict__ xinv, int x_per_row, const uint8_t* __restrict__ w8,
                            const float* __restrict__ wsc, int w_per_row, int M, int64_t NO, int64_t K,
@@ -50,10 +84,13 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   static_assert(PB == 1 || (MODE != KRQ_OUT_SWIGLU && MODE != kOutResidual && ALGO != 2),
                 "paired row blocks: MFMA, no SwiGLU or residual epilogue");
   static_assert(!NORM || XK != KRQ_X_FP8, "the RMSNorm prologue takes bf16 activations");
+  constexpr bool AW = AWC > 0;
+  static_assert(!AW || (XK == KRQ_X_BF16_DYN && !NORM && MT == 1), "activation wave: one-row kind, no RMSNorm");
   constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : PB;  // weight row blocks streamed per step
   constexpr bool FUSED = XK != KRQ_X_FP8;
   constexpr int SC = XK == KRQ_X_BF16_DYN ? kSsPerLane : kSsChunks;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  // nw = the waves that stream weights (all but the activation wave)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x >> 6) - (AW ? 1 : 0);
   const int r = lane & 15, g = lane >> 4;
   const int64_t rb = (int64_t)blockIdx.x * PB, rbu = MODE == KRQ_OUT_SWIGLU ? rb + (NO >> 4) : rb + 1;
   const int sidx = blockIdx.y;
@@ -73,7 +110,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   uint4 xv[kXChunks], lv[kXChunks], sv[SC];
   float sp[SC];
   const uint8_t* lnb = reinterpret_cast<const uint8_t*>(fa.ln);
-  if (XK == KRQ_X_BF16_DYN) {
+  if (XK == KRQ_X_BF16_DYN && !AW) {
 #pragma unroll
     for (int c = 0; c < kXChunksDyn; ++c) {
       const int64_t e = min(8 * (int64_t)(threadIdx.x + c * blockDim.x), K - 8);
@@ -100,6 +137,11 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
       sv[c] = ld16(reinterpret_cast<const uint8_t*>(fa.ss_in) + 16 * min((int)threadIdx.x + c * (int)blockDim.x, nss - 1));
   }
 
+  // (wave index read as a scalar: the compiler then knows the branch is uniform per wave)
+  if (AW && __builtin_amdgcn_readfirstlane(wave) == nw) {
+    activation_wave<AW ? AWC : 1>(x, K, k0, ks, lane, xq, xs_l);
+    __syncthreads();  // the slice and its scale are in LDS
+  } else {
   // scale of this thread's activation row, read now so its latency hides under the weight stream
   // (every thread loads and stores it, threads t and t + 32 the same value, so the load is not
   // sunk into a branch after the weight loads)
@@ -172,22 +214,24 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   if (XK == KRQ_X_FP8) {
     xs_l[threadIdx.x & 31] = xs_reg;
   } else if (XK == KRQ_X_BF16_DYN) {
-    float am = 0.0f;
+    if constexpr (!AW) {  // (with the activation wave, the slice is already in LDS after the barrier below)
+      float am = 0.0f;
 #pragma unroll
-    for (int c = 0; c < kXChunksDyn; ++c)
-      if (!NORM || 8 * (int64_t)(threadIdx.x + c * blockDim.x) < K) am = absmax8(xv[c], am);
-    am = wave_max(am);
-    if (lane == 0) amax_w[wave] = am;
-    __syncthreads();
-    float a = amax_w[0];
-    for (int w = 1; w < nw; ++w) a = fmaxf(a, amax_w[w]);
-    a = fmaxf(a, 1e-6f);
-    const float inv = inv_from_amax(a);
-    if (threadIdx.x == 0) xs_l[0] = scale_from_amax(a);
+      for (int c = 0; c < kXChunksDyn; ++c)
+        if (!NORM || 8 * (int64_t)(threadIdx.x + c * blockDim.x) < K) am = absmax8(xv[c], am);
+      am = wave_max(am);
+      if (lane == 0) amax_w[wave] = am;
+      __syncthreads();
+      float a = amax_w[0];
+      for (int w = 1; w < nw; ++w) a = fmaxf(a, amax_w[w]);
+      a = fmaxf(a, 1e-6f);
+      const float inv = inv_from_amax(a);
+      if (threadIdx.x == 0) xs_l[0] = scale_from_amax(a);
 #pragma unroll
-    for (int c = 0; c < kXChunksDyn; ++c) {
-      const int64_t e = 8 * (int64_t)(threadIdx.x + c * blockDim.x);
-      if (e >= k0 && e < k0 + ks) *reinterpret_cast<uint2*>(xq + (e - k0)) = quant8(xv[c], inv);
+      for (int c = 0; c < kXChunksDyn; ++c) {
+        const int64_t e = 8 * (int64_t)(threadIdx.x + c * blockDim.x);
+        if (e >= k0 && e < k0 + ks) *reinterpret_cast<uint2*>(xq + (e - k0)) = quant8(xv[c], inv);
+      }
     }
   } else {
     const int cpr = ks >> 3;
@@ -272,6 +316,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
     accu[0] = v4f{g == 0 ? au : 0.f, 0.f, 0.f, 0.f};
   }
   stash<MT, P>(red, wave, lane, acc, accu);
+  }  // weight waves
   __syncthreads();
   if constexpr (MODE == kOutResidual) {
     residual_epilogue<MT>(red, nw, M, NO, rb, sidx, gridDim.y, xs_l, cs.g, reinterpret_cast<float*>(out), fa,
@@ -288,17 +333,17 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
       int64_t K, int kts, void *__restrict__ out, void *__restrict__ aux
 
 // the plain kernel (gemv_fp8.hip)
-template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, int PB>
+template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, int PB, int AWC>
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(KRQ_FP8_KERNEL_PARAMS) {
-  gemv_fp8_body<MT, MODE, LAYOUT, XK, ALGO, U, PB, false>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M, NO, K,
-                                                          kts, out, aux, FusedArgs{});
+  gemv_fp8_body<MT, MODE, LAYOUT, XK, ALGO, U, PB, false, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M, NO,
+                                                               K, kts, out, aux, FusedArgs{});
 }
 
 // the fused kernel (fused_fp8.hip): RMSNorm prologue and / or residual epilogue
 template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, bool NORM>
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8_fused(KRQ_FP8_KERNEL_PARAMS, FusedArgs fa) {
-  gemv_fp8_body<MT, MODE, LAYOUT, XK, ALGO, U, 1, NORM>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M, NO, K,
-                                                        kts, out, aux, fa);
+  gemv_fp8_body<MT, MODE, LAYOUT, XK, ALGO, U, 1, NORM, 0>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M, NO, K,
+                                                           kts, out, aux, fa);
 }
 
 }  // namespace

@@ -109,6 +109,26 @@ KRQ_DEV float wave_max(float v) {
   return v;
 }
 
+template <int CTRL>
+KRQ_DEV float dpp_max(float a) {
+  return fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), CTRL, 0xf, 0xf, false)));
+}
+
+// max over the wave of non-negative values, returned wave-uniform: DPP steps inside each row of 16
+// lanes (quad swaps, then the half-row and row mirrors), then the four row results read as
+// scalars; a few VALU cycles per step instead of an LDS-crossbar round trip per shuffle
+KRQ_DEV float wave_max_nonneg(float v) {
+  v = dpp_max<0xB1>(v);   // quad_perm(1,0,3,2): lane ^ 1
+  v = dpp_max<0x4E>(v);   // quad_perm(2,3,0,1): lane ^ 2
+  v = dpp_max<0x141>(v);  // row_half_mirror: the other quad of each 8
+  v = dpp_max<0x140>(v);  // row_mirror: the other half of each 16
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 KRQ_DEV float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);

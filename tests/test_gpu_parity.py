@@ -6,6 +6,8 @@ engine/engine.py:876) against the exact oracle of the same FP8 semantics; the me
 printed. Seeds follow the measurement plan: W ~ N(0, 0.02), x ~ N(0, 1), bf16.
 """
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -18,6 +20,13 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-2
+AW_ON = os.environ.get("KRQ_GEMV_AW") != "0"  # the one-row GEMV's activation wave (library default on)
+
+
+def _same_plan(K, split):
+    """The one-row kernel with its activation wave streams weights with the e4m3 kernel's waves
+    when a block's steps all fit in flight at once (at most 16 steps of 128 bytes)."""
+    return AW_ON and (K // split // 64 + 1) // 2 <= 16
 QKV, O_PROJ, GATE_UP, DOWN = (6144, 2560), (2560, 4096), (19456, 2560), (2560, 9728)
 
 
@@ -432,16 +441,46 @@ def test_fused_dynamic_quant_matches_two_kernel_path(dev, name, algo):
     x8, xs = fp8.quant_rows(xd)
     r8, rs = O.quantize(u16(w))
     _, yref = O.fp8_matmul(u8(x8), xs.cpu().numpy(), r8, rs)
-    for split in (1, 2, 4):
+    for split in (1, 2, 4, 8):
         mode = L.OUT_BF16 if split == 1 else L.OUT_PARTIAL
         fused = fp8.gemv_fp8_bf16_launch(xd, q, split, mode, None, algo)
         two = fp8.gemv_fp8_launch(x8, xs, q, split, mode, algo)
-        # same operands; the launch shape (and so the fp32 summation order) may differ
+        if _same_plan(K, split):
+            # the same operands in the same launch shape give the same bits
+            assert torch.equal(fused, two), (name, split)
+        # without it the launch shape (and so the fp32 summation order) may differ
         f = fused.float().cpu().numpy() if split == 1 else _sum_partials(fused)
         t = two.float().cpu().numpy() if split == 1 else _sum_partials(two)
         assert rel_err(f, t) <= 1e-2 and rel_err(f, yref) <= TOL, (name, split)
     sw = fp8.gemv_fp8_bf16_launch(xd, fp8.quantize(weight(2 * 1024, K, 5).to(dev)), 1, L.OUT_SWIGLU, None, algo)
     assert sw.shape == (1, 1024)
+
+
+@pytest.mark.parametrize("algo", [L.ALGO_MFMA, L.ALGO_VALU])
+def test_dynamic_quant_rounds_overshoot_to_448(dev, algo):
+    """fp32 amax * fl(fl(1 / amax) * 448) exceeds 448 for some bf16 amax values (by one ulp). The
+    one-row quantizer of the GEMV converts without the clamp, so the hardware convert must round
+    that to 448 (code 0x7E), as the reference's clamp-then-cast does: the GEMV equals the clamped
+    two-kernel path bit for bit, and nothing turns into NaN."""
+    u = (np.arange(0x3F80, 0x4100, dtype=np.uint32) << 16).view(np.float32)  # bf16 values in [1, 8)
+    inv = (np.float32(1) / u).astype(np.float32) * np.float32(448)
+    over = u[(u * inv).astype(np.float32) > np.float32(448)]
+    assert over.size > 0
+    a = float(over[len(over) // 2])
+    N, K = QKV
+    w, x = _fp8_case(N, K, 1, 23)
+    x = (x.float() * (a / 8)).to(torch.bfloat16)
+    x[0, 5], x[0, 1234] = a, -a
+    assert float(x.float().abs().max()) == a
+    q = fp8.quantize(w.to(dev))
+    xd = x.to(dev)
+    x8, xs = fp8.quant_rows(xd)
+    assert u8(x8)[0, 5] == 0x7E and u8(x8)[0, 1234] == 0xFE
+    for split, mode in ((1, L.OUT_BF16), (2, L.OUT_PARTIAL), (4, L.OUT_PARTIAL)):
+        fused = fp8.gemv_fp8_bf16_launch(xd, q, split, mode, None, algo)
+        assert bool(torch.isfinite(fused).all())
+        if _same_plan(K, split):
+            assert torch.equal(fused, fp8.gemv_fp8_launch(x8, xs, q, split, mode, algo)), split
 
 
 @pytest.mark.parametrize("M", [1, 4, 16])
