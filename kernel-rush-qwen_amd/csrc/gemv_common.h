@@ -152,6 +152,21 @@ KRQ_DEV u16x2 absmax8_bits(uint4 v, u16x2 m) {
 }
 KRQ_DEV float bits_max_to_f32(u16x2 m) { return as_f32(static_cast<uint32_t>(m.x > m.y ? m.x : m.y) << 16); }
 
+// 8 bf16 times a given inverse scale -> 8 e4m3 bytes, with the reference's clamp to +-448 (the
+// products can exceed it); NaN stays a NaN code (its sign does not reach the products)
+KRQ_DEV uint2 quant8_clamped(uint4 v, float s) {
+  uint2 r;
+  int p = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(as_f32(v.x << 16) * s), clamp448(as_f32(v.x & 0xffff0000u) * s), 0,
+                                          false);
+  r.x = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(as_f32(v.y << 16) * s),
+                                                              clamp448(as_f32(v.y & 0xffff0000u) * s), p, true));
+  p = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(as_f32(v.z << 16) * s), clamp448(as_f32(v.z & 0xffff0000u) * s), 0,
+                                      false);
+  r.y = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(as_f32(v.w << 16) * s),
+                                                              clamp448(as_f32(v.w & 0xffff0000u) * s), p, true));
+  return r;
+}
+
 KRQ_DEV float absmax8(uint4 v, float m) {
   const uint32_t a[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll

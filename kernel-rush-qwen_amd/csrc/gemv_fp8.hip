@@ -34,13 +34,12 @@ namespace {
 
 #define KRQ_GEMV_ARGS xb, x_scale, x_inv, x_per_row, wb, w_scale, w_per_row, m, NO, K, kts, out, aux
 
-// one-row kind: MT 1, U 4, no pairing; awc = chunks per lane of the activation wave (0: none)
-template <int MODE, int LAYOUT, int ALGO>
-void launch_dyn(int awc, dim3 grid, dim3 block, size_t smem, hipStream_t s, const uint8_t* xb,
+// one bf16 row: MT 1, U 4, no pairing; awc = chunks per lane of the activation wave (0: none)
+template <int MODE, int LAYOUT, int XK, int ALGO>
+void launch_row(int awc, dim3 grid, dim3 block, size_t smem, hipStream_t s, const uint8_t* xb,
                 const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
                 const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out,
                 void* aux) {
-  constexpr int XK = KRQ_X_BF16_DYN;
   if (awc == kAwSmall)
     hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, 4, 1, kAwSmall>), grid, block, smem, s, KRQ_GEMV_ARGS);
   else if (awc == kAwLarge)
@@ -56,12 +55,23 @@ int launch(int algo, int pb, int awc, int M, dim3 grid, int nw, size_t smem, hip
            void* aux) {
   const dim3 block((nw + (awc > 0 ? 1 : 0)) * 64);
   constexpr int PB2 = MODE == KRQ_OUT_SWIGLU ? 1 : 2;  // no paired variant of the SwiGLU kernel
-  if constexpr (XK == KRQ_X_BF16_DYN) {
+  if constexpr (XK == KRQ_X_BF16_DYN) {  // (M == 1)
     if (algo == 2)
-      launch_dyn<MODE, LAYOUT, 2>(awc, grid, block, smem, s, KRQ_GEMV_ARGS);
+      launch_row<MODE, LAYOUT, XK, 2>(awc, grid, block, smem, s, KRQ_GEMV_ARGS);
     else
-      launch_dyn<MODE, LAYOUT, 1>(awc, grid, block, smem, s, KRQ_GEMV_ARGS);
-  } else if (algo == 2) {
+      launch_row<MODE, LAYOUT, XK, 1>(awc, grid, block, smem, s, KRQ_GEMV_ARGS);
+    return 0;
+  }
+  if constexpr (XK == KRQ_X_BF16_STATIC) {
+    if (awc > 0) {  // (M == 1)
+      if (algo == 2)
+        launch_row<MODE, LAYOUT, XK, 2>(awc, grid, block, smem, s, KRQ_GEMV_ARGS);
+      else
+        launch_row<MODE, LAYOUT, XK, 1>(awc, grid, block, smem, s, KRQ_GEMV_ARGS);
+      return 0;
+    }
+  }
+  if (algo == 2) {
     hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 2, 4, 1, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
   } else if (M <= 4) {
     hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, 4, 1, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
@@ -143,14 +153,17 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
     const char* e = getenv("KRQ_GEMV_AW");
     return !(e && atoi(e) == 0);
   }();
+  // With static scales (M == 1) the wave quantizes the slice alone.
   int awc = 0;
   if (x_kind == KRQ_X_BF16_DYN && aw_ok && mode != KRQ_OUT_SWIGLU)
     awc = K <= 512 * kAwSmall ? kAwSmall : K <= 512 * kAwLarge ? kAwLarge : 0;
+  if (x_kind == KRQ_X_BF16_STATIC && aw_ok && M == 1)
+    awc = ks <= 512 * kAwSmall ? kAwSmall : ks <= 512 * kAwLarge ? kAwLarge : 0;
   int nw = plan_waves((kts + 1) / 2, P, U, NO / 16 / pb * split, awc > 0);
   // the other fused prologues hold at most kXChunks 16-byte chunks per thread
   int64_t xchunks = 0;
   if (x_kind == KRQ_X_BF16_DYN && awc == 0) xchunks = (K + 7) / 8;
-  if (x_kind == KRQ_X_BF16_STATIC) xchunks = M * (ks / 8);
+  if (x_kind == KRQ_X_BF16_STATIC && awc == 0) xchunks = M * (ks / 8);
   const int xc = x_kind == KRQ_X_BF16_DYN ? kXChunksDyn : kXChunks;
   while ((int64_t)nw * 64 * xc < xchunks && nw < kMaxThreads / 64) ++nw;
   KRQ_REQUIRE((int64_t)nw * 64 * xc >= xchunks,

@@ -36,32 +36,45 @@ constexpr int kMaxThreads = 512;
 // one-row activation wave: 16-byte chunks per lane (the whole row, K <= 64 * 8 * AWC)
 constexpr int kAwSmall = 8, kAwLarge = 20;
 
-// The activation wave of the one-row (KRQ_X_BF16_DYN) kernel: one extra wave per block that loads
-// the whole bf16 row, takes its amax (ActScale arithmetic), and quantizes the block's K slice
-// [k0, k0 + ks) into LDS, while the other waves only issue their weight loads. It issues no weight
-// loads itself, so its row loads are not queued behind its own weight stream, and it runs at
-// raised issue priority; the weight waves wait for it at one barrier.
-template <int AWC>
-KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, int64_t K, int64_t k0, int ks, int lane,
+// The activation wave of the one-row kernels: one extra wave per block that quantizes the block's
+// K slice [k0, k0 + ks) of the bf16 row into LDS, while the other waves only issue their weight
+// loads. It issues no weight loads itself, so its row loads are not queued behind its own weight
+// stream, and it runs at raised issue priority; the weight waves wait for it at one barrier.
+//   KRQ_X_BF16_DYN: loads the whole row, takes its amax (ActScale arithmetic), quantizes the slice.
+//   KRQ_X_BF16_STATIC (M = 1): loads the slice and quantizes it with the given inverse scale.
+template <int XK, int AWC>
+KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restrict__ xsc,
+                             const float* __restrict__ xinv, int64_t K, int64_t k0, int ks, int lane,
                              uint8_t* xq, float* xs_l) {
   __builtin_amdgcn_s_setprio(3);
-  // chunk i = lane + 64 c holds elements 8i .. 8i + 7; indices past the row repeat its last chunk
-  const int last = static_cast<int>(K >> 3) - 1, lo = static_cast<int>(k0 >> 3), n = ks >> 3;
+  // DYN: chunk i = lane + 64 c of the row holds elements 8i .. 8i + 7 (indices past the row repeat
+  // its last chunk); STATIC: the same over the slice
+  const int lo = static_cast<int>(k0 >> 3), n = ks >> 3;
+  const int last = XK == KRQ_X_BF16_DYN ? static_cast<int>(K >> 3) - 1 : n - 1;
+  const uint8_t* xb = XK == KRQ_X_BF16_DYN ? x : x + 2 * k0;
   uint4 v[AWC];
 #pragma unroll
-  for (int c = 0; c < AWC; ++c) v[c] = ld16(x + 16 * min(lane + 64 * c, last));
+  for (int c = 0; c < AWC; ++c) v[c] = ld16(xb + 16 * min(lane + 64 * c, last));
+  float inv = 0.0f;
+  if (XK == KRQ_X_BF16_STATIC) {
+    inv = xinv[0];
+    if (lane == 0) xs_l[0] = xsc[0];
+  }
   __builtin_amdgcn_sched_barrier(0);  // every row load in flight before the first wait
-  u16x2 mb = {0, 0};
+  if (XK == KRQ_X_BF16_DYN) {
+    u16x2 mb = {0, 0};
 #pragma unroll
-  for (int c = 0; c < AWC; ++c) mb = absmax8_bits(v[c], mb);
-  const float am = fmaxf(wave_max_nonneg(bits_max_to_f32(mb)), 1e-6f);
-  const float inv = inv_from_amax(am);
-  if (lane == 0) xs_l[0] = scale_from_amax(am);
+    for (int c = 0; c < AWC; ++c) mb = absmax8_bits(v[c], mb);
+    const float am = fmaxf(wave_max_nonneg(bits_max_to_f32(mb)), 1e-6f);
+    inv = inv_from_amax(am);
+    if (lane == 0) xs_l[0] = scale_from_amax(am);
+  }
 #pragma unroll
   for (int c = 0; c < AWC; ++c) {
-    const int i = lane + 64 * c - lo;  // chunk index inside the slice
+    const int i = lane + 64 * c - (XK == KRQ_X_BF16_DYN ? lo : 0);  // chunk index inside the slice
     if (static_cast<unsigned>(i) < static_cast<unsigned>(n))
-      *reinterpret_cast<uint2*>(xq + 8 * i) = quant8_own_amax(v[c], inv);
+      *reinterpret_cast<uint2*>(xq + 8 * i) =
+          XK == KRQ_X_BF16_DYN ? quant8_own_amax(v[c], inv) : quant8_clamped(v[c], inv);
   }
   __builtin_amdgcn_s_setprio(0);
 }
@@ -85,7 +98,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
                 "paired row blocks: MFMA, no SwiGLU or residual epilogue");
   static_assert(!NORM || XK != KRQ_X_FP8, "the RMSNorm prologue takes bf16 activations");
   constexpr bool AW = AWC > 0;
-  static_assert(!AW || (XK == KRQ_X_BF16_DYN && !NORM && MT == 1), "activation wave: one-row kind, no RMSNorm");
+  static_assert(!AW || (XK != KRQ_X_FP8 && !NORM && MT == 1), "activation wave: one bf16 row, no RMSNorm");
   constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : PB;  // weight row blocks streamed per step
   constexpr bool FUSED = XK != KRQ_X_FP8;
   constexpr int SC = XK == KRQ_X_BF16_DYN ? kSsPerLane : kSsChunks;
@@ -117,7 +130,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
       xv[c] = ld16(x + 2 * e);  // chunks past K repeat the last one (same amax)
       if (NORM) lv[c] = ld16(lnb + 2 * e);
     }
-  } else if (XK == KRQ_X_BF16_STATIC) {
+  } else if (XK == KRQ_X_BF16_STATIC && !AW) {
     const int cpr = ks >> 3;  // chunks per row of the slice
 #pragma unroll
     for (int c = 0; c < kXChunks; ++c) {
@@ -139,14 +152,14 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
 
   // (wave index read as a scalar: the compiler then knows the branch is uniform per wave)
   if (AW && __builtin_amdgcn_readfirstlane(wave) == nw) {
-    activation_wave<AW ? AWC : 1>(x, K, k0, ks, lane, xq, xs_l);
+    activation_wave<XK, AW ? AWC : 1>(x, xsc, xinv, K, k0, ks, lane, xq, xs_l);
     __syncthreads();  // the slice and its scale are in LDS
   } else {
   // scale of this thread's activation row, read now so its latency hides under the weight stream
   // (every thread loads and stores it, threads t and t + 32 the same value, so the load is not
   // sunk into a branch after the weight loads)
   const int xrow = min((int)(threadIdx.x & 31), M - 1);
-  const float xs_reg = XK != KRQ_X_BF16_DYN ? xsc[x_per_row ? xrow : 0] : 1.0f;
+  const float xs_reg = XK != KRQ_X_BF16_DYN && !AW ? xsc[x_per_row ? xrow : 0] : 1.0f;
 
   // ---- weight (and, for e4m3 activations, A operand) loads: a ring of U step slots ----
   uint4 wl[U], wh[U], ul[U], uh[U], xl[U][MT], xh[U][MT];
@@ -233,7 +246,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
         if (e >= k0 && e < k0 + ks) *reinterpret_cast<uint2*>(xq + (e - k0)) = quant8(xv[c], inv);
       }
     }
-  } else {
+  } else if constexpr (!AW) {
     const int cpr = ks >> 3;
 #pragma unroll
     for (int c = 0; c < kXChunks; ++c) {

@@ -500,6 +500,34 @@ def test_fused_static_quant_matches_cast_path(dev, M):
     assert rel_err(_sum_partials(fused), yref) <= TOL
 
 
+@pytest.mark.parametrize("name", ["qkv", "o", "down"])
+@pytest.mark.parametrize("algo", [L.ALGO_MFMA, L.ALGO_VALU])
+def test_one_row_static_quant_with_clamping(dev, name, algo):
+    """One row, static inverse scale small enough that ~5% of the products clamp at +-448: the
+    in-kernel quantization (the one-row activation wave) equals the reference's cast followed by
+    the e4m3 GEMV, bit for bit where the launch shapes match, and the SwiGLU variant too."""
+    N, K = SHAPES[name]
+    w, x = _fp8_case(N, K, 1, 40 + SEEDS[name])
+    q = fp8.quantize(w.to(dev))
+    xd = x.to(dev)
+    a = fp8.SharedScale(torch.tensor([448.0 / 2.0], device=dev), torch.tensor(2.0 / 448.0, device=dev))
+    x8 = fp8._cast_hip(xd, a)
+    assert (u8(x8) & 0x7F == 0x7E).mean() > 0.02  # many clamped codes
+    for split in (1, 2, 4, 8):
+        mode = L.OUT_BF16 if split == 1 else L.OUT_PARTIAL
+        fused = fp8.gemv_fp8_bf16_launch(xd, q, split, mode, a, algo)
+        two = fp8.gemv_fp8_launch(x8, a.scale.reshape(1), q, split, mode, algo)
+        if _same_plan(K, split):
+            assert torch.equal(fused, two), split
+        f = fused.float().cpu().numpy() if split == 1 else _sum_partials(fused)
+        t = two.float().cpu().numpy() if split == 1 else _sum_partials(two)
+        assert rel_err(f, t) <= 1e-2, split
+    qs = fp8.quantize(weight(2 * 1024, K, 6).to(dev))
+    sw = fp8.gemv_fp8_bf16_launch(xd, qs, 1, L.OUT_SWIGLU, a, algo)
+    sw2 = fp8.gemv_fp8_launch(x8, a.scale.reshape(1), qs, 1, L.OUT_SWIGLU, algo)
+    assert torch.equal(sw, sw2)  # the two-matrix block always streams with two weight waves
+
+
 def test_fused_quant_rejects_oversized_slices(dev):
     w = weight(64, 9728, 1).to(dev)
     q = fp8.quantize(w)
