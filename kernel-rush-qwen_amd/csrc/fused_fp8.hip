@@ -12,6 +12,8 @@
 // The kernel template is gemv_fp8_kernel.h's; the fused variants always use the matrix cores.
 #include "gemv_fp8_kernel.h"
 
+#include <stdlib.h>
+
 using namespace krq;
 
 namespace {
@@ -55,58 +57,96 @@ __global__ __launch_bounds__(kRowThreads) void k_rmsnorm_quant_rows(const uint16
 #define KRQ_FUSED_FP8_ARGS xb, x_scale, x_inv, x_per_row, wb, w_scale, w_per_row, m, NO, K, kts, out, nullptr, fa
 
 template <int MODE, int LAYOUT, int XK, bool NORM>
-void launch(int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb, const float* x_scale,
+void launch(int M, int awc, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb, const float* x_scale,
             const float* x_inv, int x_per_row, const uint8_t* wb, const float* w_scale, int w_per_row, int m,
             int64_t NO, int64_t K, int kts, void* out, const FusedArgs& fa) {
-  const dim3 block(nw * 64);
+  const dim3 block((nw + (awc > 0 ? 1 : 0)) * 64);
+  if constexpr (XK != KRQ_X_FP8) {
+    if (awc == kAwSmall) {
+      hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, 4, NORM, kAwSmall>), grid, block, smem, s,
+                         KRQ_FUSED_FP8_ARGS);
+      return;
+    }
+    if (!NORM && awc == kAwLarge) {  // (with RMSNorm the wave takes rows of at most 4,096)
+      hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, 4, NORM, kAwLarge>), grid, block, smem, s,
+                         KRQ_FUSED_FP8_ARGS);
+      return;
+    }
+  }
   if (M <= 4)
-    hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, 4, NORM>), grid, block, smem, s, KRQ_FUSED_FP8_ARGS);
+    hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, 4, NORM, 0>), grid, block, smem, s, KRQ_FUSED_FP8_ARGS);
   else if (M <= 16)
-    hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, 2, NORM>), grid, block, smem, s, KRQ_FUSED_FP8_ARGS);
+    hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, 2, NORM, 0>), grid, block, smem, s, KRQ_FUSED_FP8_ARGS);
   else
-    hipLaunchKernelGGL((k_gemv_fp8_fused<2, MODE, LAYOUT, XK, 1, 2, NORM>), grid, block, smem, s, KRQ_FUSED_FP8_ARGS);
+    hipLaunchKernelGGL((k_gemv_fp8_fused<2, MODE, LAYOUT, XK, 1, 2, NORM, 0>), grid, block, smem, s, KRQ_FUSED_FP8_ARGS);
 }
 
 template <int MODE, int XK, bool NORM>
-void launch_layout(int layout, int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb,
+void launch_layout(int layout, int M, int awc, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb,
                    const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
                    const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out,
                    const FusedArgs& fa) {
   if (layout == KRQ_W_TILED)
-    launch<MODE, KRQ_W_TILED, XK, NORM>(M, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, w_scale,
+    launch<MODE, KRQ_W_TILED, XK, NORM>(M, awc, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, w_scale,
                                          w_per_row, m, NO, K, kts, out, fa);
   else
-    launch<MODE, KRQ_W_ROWMAJOR, XK, NORM>(M, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, w_scale,
+    launch<MODE, KRQ_W_ROWMAJOR, XK, NORM>(M, awc, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, w_scale,
                                             w_per_row, m, NO, K, kts, out, fa);
 }
 
+struct FusedPlan {
+  int nw;       // waves that stream weights
+  int awc;      // chunks per lane of the activation wave (0: none, every wave runs the prologue)
+  size_t smem;  // dynamic LDS bytes
+};
+
+// One-row launches (M == 1, bf16 activations) get the activation wave of gemv_fp8_kernel.h when
+// its registers hold what it loads: the whole row (per-token scale) or the slice (static scale),
+// K <= 4096 with RMSNorm (the row's partials, 64 x kSsPerLane); KRQ_GEMV_AW=0 turns it off. The
+// two-matrix SwiGLU block keeps the shared prologue, as in the plain kernel, and so do grids of
+// fewer blocks than CUs (the one-pass residual GEMVs).
+int act_wave_chunks(int64_t M, int64_t K, int64_t ks, int mode, int x_kind, bool norm) {
+  static const bool aw_ok = [] {
+    const char* e = getenv("KRQ_GEMV_AW");
+    return !(e && atoi(e) == 0);
+  }();
+  if (!aw_ok || M != 1 || x_kind == KRQ_X_FP8 || mode == KRQ_OUT_SWIGLU) return 0;
+  if (norm && K > 512 * kAwSmall) return 0;
+  const int64_t span = x_kind == KRQ_X_BF16_DYN ? K : ks;
+  return span <= 512 * kAwSmall ? kAwSmall : span <= 512 * kAwLarge ? kAwLarge : 0;
+}
+
 // Waves and LDS bytes of a fused FP8 launch; false if the prologue's staging does not fit.
-bool plan(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind, bool norm, int* nw_out,
-          size_t* smem_out) {
+bool plan(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind, bool norm, FusedPlan* out) {
   if (M < 1 || M > 32 || split < 1 || K < 64 || K % split || (K / split) % 64) return false;
   if (norm && x_kind == KRQ_X_FP8) return false;
   if (x_kind == KRQ_X_BF16_DYN && M != 1) return false;
   const int64_t ks = K / split;
-  if (norm && x_kind == KRQ_X_BF16_STATIC && M * ks * 2 > kNormStageMax) return false;
-  const int kts = static_cast<int>(ks / 64);
   const int P = mode == KRQ_OUT_SWIGLU ? 2 : 1;
-  const int MT = M <= 16 ? 1 : 2;
   const int64_t NO = mode == KRQ_OUT_SWIGLU ? N / 2 : N;
-  int nw = plan_waves((kts + 1) / 2, P, M <= 4 ? 4 : 2, NO / 16 * split);
-  const int64_t xchunks = x_kind == KRQ_X_BF16_DYN ? (K + 7) / 8 : x_kind == KRQ_X_BF16_STATIC ? M * (ks / 8) : 0;
-  const int xc = x_kind == KRQ_X_BF16_DYN ? kXChunksDyn : kXChunks;
-  if (norm && x_kind == KRQ_X_BF16_DYN && K / 16 > 64 * kSsPerLane) return false;
-  auto short_of = [&](int w) {
-    return (int64_t)w * 64 * xc < xchunks ||
-           (norm && x_kind == KRQ_X_BF16_STATIC && (int64_t)w * 64 * kSsChunks * 4 < M * (K / 16));
-  };
-  while (short_of(nw) && nw < kMaxThreads / 64) ++nw;
-  if (short_of(nw)) return false;
+  const int awc = NO / 16 * split >= kCUs ? act_wave_chunks(M, K, ks, mode, x_kind, norm) : 0;
+  if (awc == 0 && norm && x_kind == KRQ_X_BF16_STATIC && M * ks * 2 > kNormStageMax) return false;
+  const int kts = static_cast<int>(ks / 64);
+  const int MT = M <= 16 ? 1 : 2;
+  int nw = plan_waves((kts + 1) / 2, P, M <= 4 ? 4 : 2, NO / 16 * split, awc > 0);
+  bool staged_ss = false;  // the sum-of-squares partials staged in LDS (RMSNorm of M rows)
+  if (awc == 0) {
+    const int64_t xchunks = x_kind == KRQ_X_BF16_DYN ? (K + 7) / 8 : x_kind == KRQ_X_BF16_STATIC ? M * (ks / 8) : 0;
+    const int xc = x_kind == KRQ_X_BF16_DYN ? kXChunksDyn : kXChunks;
+    if (norm && x_kind == KRQ_X_BF16_DYN && K / 16 > 64 * kSsPerLane) return false;
+    staged_ss = norm && x_kind == KRQ_X_BF16_STATIC;
+    auto short_of = [&](int w) {
+      return (int64_t)w * 64 * xc < xchunks || (staged_ss && (int64_t)w * 64 * kSsChunks * 4 < M * (K / 16));
+    };
+    while (short_of(nw) && nw < kMaxThreads / 64) ++nw;
+    if (short_of(nw)) return false;
+  } else {
+    nw = min(nw, kMaxThreads / 64 - 1);
+  }
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) + (x_kind == KRQ_X_FP8 ? 0 : (size_t)M * ks) +
-                      (norm && x_kind == KRQ_X_BF16_STATIC ? (size_t)M * (K / 16) * sizeof(float) : 0);
+                      (staged_ss ? (size_t)M * (K / 16) * sizeof(float) : 0);
   if (smem > kMaxSmem) return false;
-  *nw_out = nw;
-  *smem_out = smem;
+  *out = FusedPlan{nw, awc, smem};
   return true;
 }
 
@@ -114,9 +154,8 @@ bool plan(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind, bool
 
 extern "C" int64_t krq_gemv_fp8_fused_fits(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind,
                                            int norm) {
-  int nw = 0;
-  size_t smem = 0;
-  return plan(M, N, K, split, mode, x_kind, norm != 0, &nw, &smem) ? 1 : 0;
+  FusedPlan p;
+  return plan(M, N, K, split, mode, x_kind, norm != 0, &p) ? 1 : 0;
 }
 
 extern "C" int krq_gemv_fp8_fused(const void* x, int x_kind, const float* x_scale, const float* x_inv,
@@ -152,9 +191,8 @@ extern "C" int krq_gemv_fp8_fused(const void* x, int x_kind, const float* x_scal
   const int64_t NO = mode == KRQ_OUT_SWIGLU ? N / 2 : N;
   KRQ_REQUIRE(NO % 16 == 0 && (mode != KRQ_OUT_SWIGLU || N % 2 == 0) && NO / 16 <= 0x7fffffff,
               "gemv_fp8_fused: no tiling divides N=%lld", (long long)N);
-  int nw = 0;
-  size_t smem = 0;
-  KRQ_REQUIRE(plan(M, N, K, split, mode, x_kind, norm, &nw, &smem),
+  FusedPlan p;
+  KRQ_REQUIRE(plan(M, N, K, split, mode, x_kind, norm, &p),
               "gemv_fp8_fused: M=%lld x K/split=%lld does not fit the in-kernel staging; normalize and "
               "quantize rows first (krq_rmsnorm_quant_rows)", (long long)M, (long long)(K / split));
   const int kts = static_cast<int>(K / split / 64);
@@ -166,7 +204,7 @@ extern "C" int krq_gemv_fp8_fused(const void* x, int x_kind, const float* x_scal
   const int m = static_cast<int>(M);
   hipStream_t s = (hipStream_t)stream;
 #define KRQ_CASE(MODE, XK, NORM)                                                                          \
-  launch_layout<MODE, XK, NORM>(w_layout, m, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, w_scale, \
+  launch_layout<MODE, XK, NORM>(w_layout, m, p.awc, grid, p.nw, p.smem, s, xb, x_scale, x_inv, x_per_row, wb, w_scale, \
                                 w_per_row, m, NO, K, kts, out, fa)
   if (mode == kOutResidual) {
     if (x_kind == KRQ_X_FP8) KRQ_CASE(kOutResidual, KRQ_X_FP8, false);

@@ -20,13 +20,13 @@ int plan_waves(int nsteps, int P, int U, int64_t blocks, bool act_wave) {
   // enough, two waves, unless the grid has fewer blocks than the chip has CUs x 2 (the single-pass
   // O and down, 160 blocks: 5.07 / 8.74 us with 4 waves against 6.50 / 8.75 with 2 at M = 1),
   // where four keep more loads in flight. The two-matrix SwiGLU block takes two waves. Beside an
-  // activation wave (one-row kernel), three (four waves in all): down 7.68 -> 7.16 us and the FP8
-  // lm_head 64.7 -> 63.1 us at M = 1.
+  // activation wave (one-row kernel), three instead of two (four waves in all): down 7.68 -> 7.16
+  // us and the FP8 lm_head 64.7 -> 63.1 us at M = 1.
   const int w = (nsteps + U - 1) / U;
   if (P != 1) return 2;
   if (w <= 4) return w;
-  if (act_wave) return 3;
-  return blocks < 512 ? 4 : 2;
+  if (blocks < 512) return 4;
+  return act_wave ? 3 : 2;
 }
 }  // namespace krq
 
@@ -159,6 +159,9 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
     awc = K <= 512 * kAwSmall ? kAwSmall : K <= 512 * kAwLarge ? kAwLarge : 0;
   if (x_kind == KRQ_X_BF16_STATIC && aw_ok && M == 1)
     awc = ks <= 512 * kAwSmall ? kAwSmall : ks <= 512 * kAwLarge ? kAwLarge : 0;
+  // With fewer blocks than CUs each block's prologue is its CU's critical path, and spreading it
+  // over all waves is faster (the one-pass residual GEMVs, 160 blocks: O 6.21 against 6.65 us).
+  if (NO / 16 / pb * split < kCUs) awc = 0;
   int nw = plan_waves((kts + 1) / 2, P, U, NO / 16 / pb * split, awc > 0);
   // the other fused prologues hold at most kXChunks 16-byte chunks per thread
   int64_t xchunks = 0;

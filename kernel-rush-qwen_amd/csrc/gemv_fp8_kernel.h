@@ -35,6 +35,7 @@ constexpr int kSsPerLane = 4;
 constexpr int kMaxThreads = 512;
 // one-row activation wave: 16-byte chunks per lane (the whole row, K <= 64 * 8 * AWC)
 constexpr int kAwSmall = 8, kAwLarge = 20;
+constexpr int64_t kCUs = 256;  // compute units of the MI355X
 
 // The activation wave of the one-row kernels: one extra wave per block that quantizes the block's
 // K slice [k0, k0 + ks) of the bf16 row into LDS, while the other waves only issue their weight
@@ -42,29 +43,56 @@ constexpr int kAwSmall = 8, kAwLarge = 20;
 // stream, and it runs at raised issue priority; the weight waves wait for it at one barrier.
 //   KRQ_X_BF16_DYN: loads the whole row, takes its amax (ActScale arithmetic), quantizes the slice.
 //   KRQ_X_BF16_STATIC (M = 1): loads the slice and quantizes it with the given inverse scale.
-template <int XK, int AWC>
+// NORM: the loaded chunks are first normalized, h = bf16(bf16(x * rstd) * w_ln), with rstd from the
+// row's sum-of-squares partials in the canonical order (K <= 4096: T = K / 16 <= 64 * kSsPerLane).
+template <int XK, int AWC, bool NORM>
 KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restrict__ xsc,
                              const float* __restrict__ xinv, int64_t K, int64_t k0, int ks, int lane,
-                             uint8_t* xq, float* xs_l) {
+                             uint8_t* xq, float* xs_l, const FusedArgs& fa) {
+  constexpr int LC = NORM ? AWC : 1;
+  constexpr int SC = NORM ? kSsPerLane : 1;
   __builtin_amdgcn_s_setprio(3);
   // DYN: chunk i = lane + 64 c of the row holds elements 8i .. 8i + 7 (indices past the row repeat
   // its last chunk); STATIC: the same over the slice
   const int lo = static_cast<int>(k0 >> 3), n = ks >> 3;
   const int last = XK == KRQ_X_BF16_DYN ? static_cast<int>(K >> 3) - 1 : n - 1;
-  const uint8_t* xb = XK == KRQ_X_BF16_DYN ? x : x + 2 * k0;
-  uint4 v[AWC];
+  const int64_t e0 = XK == KRQ_X_BF16_DYN ? 0 : k0;  // first element of chunk 0
+  const int T = static_cast<int>(K >> 4);
+  const uint8_t* lnb = reinterpret_cast<const uint8_t*>(fa.ln);
+  uint4 v[AWC], lv[LC];
+  float sp[SC];
 #pragma unroll
-  for (int c = 0; c < AWC; ++c) v[c] = ld16(xb + 16 * min(lane + 64 * c, last));
+  for (int c = 0; c < AWC; ++c) {
+    const int64_t e = e0 + 8 * (int64_t)min(lane + 64 * c, last);
+    v[c] = ld16(x + 2 * e);
+    if (NORM) lv[c] = ld16(lnb + 2 * e);
+  }
+  if (NORM) {
+#pragma unroll
+    for (int c = 0; c < SC; ++c) sp[c] = fa.ss_in[min(lane + 64 * c, T - 1)];
+  }
   float inv = 0.0f;
   if (XK == KRQ_X_BF16_STATIC) {
     inv = xinv[0];
     if (lane == 0) xs_l[0] = xsc[0];
   }
   __builtin_amdgcn_sched_barrier(0);  // every row load in flight before the first wait
+  if (NORM) {
+    float a = 0.0f;
+#pragma unroll
+    for (int c = 0; c < SC; ++c)
+      if (lane + 64 * c < T) a += sp[c];
+    const float rstd = rstd_of(a, K, fa.eps);
+    // only chunks inside the row (slice): the clamped repeats are left raw and kept out of the amax
+#pragma unroll
+    for (int c = 0; c < AWC; ++c)
+      if (lane + 64 * c <= last) v[c] = norm8(v[c], lv[NORM ? c : 0], rstd);
+  }
   if (XK == KRQ_X_BF16_DYN) {
     u16x2 mb = {0, 0};
 #pragma unroll
-    for (int c = 0; c < AWC; ++c) mb = absmax8_bits(v[c], mb);
+    for (int c = 0; c < AWC; ++c)
+      if (!NORM || lane + 64 * c <= last) mb = absmax8_bits(v[c], mb);
     const float am = fmaxf(wave_max_nonneg(bits_max_to_f32(mb)), 1e-6f);
     inv = inv_from_amax(am);
     if (lane == 0) xs_l[0] = scale_from_amax(am);
@@ -98,7 +126,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
                 "paired row blocks: MFMA, no SwiGLU or residual epilogue");
   static_assert(!NORM || XK != KRQ_X_FP8, "the RMSNorm prologue takes bf16 activations");
   constexpr bool AW = AWC > 0;
-  static_assert(!AW || (XK != KRQ_X_FP8 && !NORM && MT == 1), "activation wave: one bf16 row, no RMSNorm");
+  static_assert(!AW || (XK != KRQ_X_FP8 && MT == 1), "activation wave: one bf16 row");
   constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : PB;  // weight row blocks streamed per step
   constexpr bool FUSED = XK != KRQ_X_FP8;
   constexpr int SC = XK == KRQ_X_BF16_DYN ? kSsPerLane : kSsChunks;
@@ -140,10 +168,10 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
       if (NORM) lv[c] = ld16(lnb + 2 * e);
     }
   }
-  if (NORM && XK == KRQ_X_BF16_DYN) {  // every wave reads the row's partials itself
+  if (NORM && XK == KRQ_X_BF16_DYN && !AW) {  // every wave reads the row's partials itself
 #pragma unroll
     for (int c = 0; c < SC; ++c) sp[c] = fa.ss_in[min(lane + 64 * c, T - 1)];
-  } else if (NORM) {
+  } else if (NORM && !AW) {
     const int nss = M * T / 4;  // 16-byte chunks of the partials
 #pragma unroll
     for (int c = 0; c < SC; ++c)
@@ -152,7 +180,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
 
   // (wave index read as a scalar: the compiler then knows the branch is uniform per wave)
   if (AW && __builtin_amdgcn_readfirstlane(wave) == nw) {
-    activation_wave<XK, AW ? AWC : 1>(x, xsc, xinv, K, k0, ks, lane, xq, xs_l);
+    activation_wave<XK, AW ? AWC : 1, NORM>(x, xsc, xinv, K, k0, ks, lane, xq, xs_l, fa);
     __syncthreads();  // the slice and its scale are in LDS
   } else {
   // scale of this thread's activation row, read now so its latency hides under the weight stream
@@ -191,7 +219,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- RMSNorm (NORM): row rstd from the partials, then normalize the loaded chunks ----
-  if (NORM && XK == KRQ_X_BF16_DYN) {
+  if (NORM && XK == KRQ_X_BF16_DYN && !AW) {
     float a = 0.0f;
 #pragma unroll
     for (int c = 0; c < SC; ++c)
@@ -202,7 +230,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
 #pragma unroll
     for (int c = 0; c < kXChunksDyn; ++c)
       if (8 * (int64_t)(threadIdx.x + c * blockDim.x) < K) xv[c] = norm8(xv[c], lv[c], rstd);
-  } else if (NORM) {
+  } else if (NORM && !AW) {
     float* sst = reinterpret_cast<float*>(xq + (size_t)M * ks);
     const int nss = M * T / 4;
 #pragma unroll
@@ -353,10 +381,10 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(KRQ_FP8_KERNEL_PARAMS)
 }
 
 // the fused kernel (fused_fp8.hip): RMSNorm prologue and / or residual epilogue
-template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, bool NORM>
+template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, bool NORM, int AWC>
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8_fused(KRQ_FP8_KERNEL_PARAMS, FusedArgs fa) {
-  gemv_fp8_body<MT, MODE, LAYOUT, XK, ALGO, U, 1, NORM, 0>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M, NO, K,
-                                                           kts, out, aux, fa);
+  gemv_fp8_body<MT, MODE, LAYOUT, XK, ALGO, U, 1, NORM, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M, NO,
+                                                             K, kts, out, aux, fa);
 }
 
 }  // namespace
