@@ -21,7 +21,8 @@ int plan_waves(int nsteps, int P, int U, int64_t blocks, bool act_wave) {
   // O and down, 160 blocks: 5.07 / 8.74 us with 4 waves against 6.50 / 8.75 with 2 at M = 1),
   // where four keep more loads in flight. The two-matrix SwiGLU block takes two waves. Beside an
   // activation wave (one-row kernel), three instead of two (four waves in all): down 7.68 -> 7.16
-  // us and the FP8 lm_head 64.7 -> 63.1 us at M = 1.
+  // us and the FP8 lm_head 64.7 -> 63.1 us at M = 1. With the deep rings (U of 8 or 10 beside the
+  // activation wave) the same rule gives one wave for up to U steps and two for up to 2U.
   const int w = (nsteps + U - 1) / U;
   if (P != 1) return 2;
   if (w <= 4) return w;
@@ -34,22 +35,35 @@ namespace {
 
 #define KRQ_GEMV_ARGS xb, x_scale, x_inv, x_per_row, wb, w_scale, w_per_row, m, NO, K, kts, out, aux
 
-// one bf16 row: MT 1, U 4, no pairing; awc = chunks per lane of the activation wave (0: none)
+// one bf16 row: MT 1, no pairing; awc = chunks per lane of the activation wave (0: none); u = step
+// slots per weight wave: 4, or (activation wave, tiled single-matrix matrix-core kernels) 8 or 10
 template <int MODE, int LAYOUT, int XK, int ALGO>
-void launch_row(int awc, dim3 grid, dim3 block, size_t smem, hipStream_t s, const uint8_t* xb,
+void launch_row(int awc, int u, dim3 grid, dim3 block, size_t smem, hipStream_t s, const uint8_t* xb,
                 const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
                 const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out,
                 void* aux) {
-  if (awc == kAwSmall)
-    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, 4, 1, kAwSmall>), grid, block, smem, s, KRQ_GEMV_ARGS);
-  else if (awc == kAwLarge)
-    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, 4, 1, kAwLarge>), grid, block, smem, s, KRQ_GEMV_ARGS);
-  else
+  constexpr bool deep = LAYOUT == KRQ_W_TILED && ALGO == 1 && MODE != KRQ_OUT_SWIGLU;
+#define KRQ_ROW_U(AWC)                                                                                       \
+  if (deep && u == kDeepU)                                                                                   \
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, deep ? kDeepU : 4, 1, AWC>), grid, block, smem, s, \
+                       KRQ_GEMV_ARGS);                                                                       \
+  else if (deep && u == kMidU)                                                                               \
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, deep ? kMidU : 4, 1, AWC>), grid, block, smem, s,  \
+                       KRQ_GEMV_ARGS);                                                                       \
+  else                                                                                                       \
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, 4, 1, AWC>), grid, block, smem, s, KRQ_GEMV_ARGS);
+  if (awc == kAwSmall) {
+    KRQ_ROW_U(kAwSmall)
+  } else if (awc == kAwLarge) {
+    KRQ_ROW_U(kAwLarge)
+  } else {
     hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, 4, 1, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
+  }
+#undef KRQ_ROW_U
 }
 
 template <int MODE, int LAYOUT, int XK>
-int launch(int algo, int pb, int awc, int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb,
+int launch(int algo, int pb, int awc, int u, int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb,
            const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
            const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out,
            void* aux) {
@@ -57,17 +71,17 @@ int launch(int algo, int pb, int awc, int M, dim3 grid, int nw, size_t smem, hip
   constexpr int PB2 = MODE == KRQ_OUT_SWIGLU ? 1 : 2;  // no paired variant of the SwiGLU kernel
   if constexpr (XK == KRQ_X_BF16_DYN) {  // (M == 1)
     if (algo == 2)
-      launch_row<MODE, LAYOUT, XK, 2>(awc, grid, block, smem, s, KRQ_GEMV_ARGS);
+      launch_row<MODE, LAYOUT, XK, 2>(awc, u, grid, block, smem, s, KRQ_GEMV_ARGS);
     else
-      launch_row<MODE, LAYOUT, XK, 1>(awc, grid, block, smem, s, KRQ_GEMV_ARGS);
+      launch_row<MODE, LAYOUT, XK, 1>(awc, u, grid, block, smem, s, KRQ_GEMV_ARGS);
     return 0;
   }
   if constexpr (XK == KRQ_X_BF16_STATIC) {
     if (awc > 0) {  // (M == 1)
       if (algo == 2)
-        launch_row<MODE, LAYOUT, XK, 2>(awc, grid, block, smem, s, KRQ_GEMV_ARGS);
+        launch_row<MODE, LAYOUT, XK, 2>(awc, u, grid, block, smem, s, KRQ_GEMV_ARGS);
       else
-        launch_row<MODE, LAYOUT, XK, 1>(awc, grid, block, smem, s, KRQ_GEMV_ARGS);
+        launch_row<MODE, LAYOUT, XK, 1>(awc, u, grid, block, smem, s, KRQ_GEMV_ARGS);
       return 0;
     }
   }
@@ -88,16 +102,16 @@ int launch(int algo, int pb, int awc, int M, dim3 grid, int nw, size_t smem, hip
 }
 
 template <int MODE, int LAYOUT>
-void launch_xk(int xk, int algo, int pb, int awc, int M, dim3 grid, int nw, size_t smem, hipStream_t s,
+void launch_xk(int xk, int algo, int pb, int awc, int u, int M, dim3 grid, int nw, size_t smem, hipStream_t s,
                const uint8_t* xb, const float* x_scale, const float* x_inv, int x_per_row,
                const uint8_t* wb, const float* w_scale, int w_per_row, int m, int64_t NO,
                int64_t K, int kts, void* out, void* aux) {
   if (xk == KRQ_X_FP8)
-    launch<MODE, LAYOUT, KRQ_X_FP8>(algo, pb, awc, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
+    launch<MODE, LAYOUT, KRQ_X_FP8>(algo, pb, awc, u, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
   else if (xk == KRQ_X_BF16_DYN)
-    launch<MODE, LAYOUT, KRQ_X_BF16_DYN>(algo, pb, awc, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
+    launch<MODE, LAYOUT, KRQ_X_BF16_DYN>(algo, pb, awc, u, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
   else
-    launch<MODE, LAYOUT, KRQ_X_BF16_STATIC>(algo, pb, awc, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
+    launch<MODE, LAYOUT, KRQ_X_BF16_STATIC>(algo, pb, awc, u, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
 }
 
 }  // namespace
@@ -162,7 +176,20 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   // With fewer blocks than CUs each block's prologue is its CU's critical path, and spreading it
   // over all waves is faster (the one-pass residual GEMVs, 160 blocks: O 6.21 against 6.65 us).
   if (NO / 16 / pb * split < kCUs) awc = 0;
-  int nw = plan_waves((kts + 1) / 2, P, U, NO / 16 / pb * split, awc > 0);
+  // Deep ring beside the activation wave (tiled single-matrix matrix-core kernels): each weight wave
+  // holds all of its steps in flight at once, one memory round trip and no masked slots. Measured at
+  // M = 1 (graph of 72 launches over 36 layers): QKV (10 steps, one wave of 10) 5.24 -> 4.84 us, O (8
+  // steps, one wave of 8) 4.38 -> 4.25, down (19 steps, two waves of 10) 7.51 -> 6.90; rings of
+  // 8 for 10 steps (two rounds) or 12 (masked slots) measured slower, and so did the SwiGLU block.
+  const int nsteps = (kts + 1) / 2;
+  int u = U;
+  static const bool deep_ok = [] {
+    const char* e = getenv("KRQ_GEMV_DEEP");
+    return !(e && atoi(e) == 0);
+  }();
+  if (deep_ok && awc > 0 && algo == 1 && mode != KRQ_OUT_SWIGLU && w_layout == KRQ_W_TILED)
+    u = nsteps <= kMidU ? kMidU : kDeepU;
+  int nw = plan_waves(nsteps, P, u, NO / 16 / pb * split, awc > 0);
   // the other fused prologues hold at most kXChunks 16-byte chunks per thread
   int64_t xchunks = 0;
   if (x_kind == KRQ_X_BF16_DYN && awc == 0) xchunks = (K + 7) / 8;
@@ -181,7 +208,7 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   const int m = static_cast<int>(M);
   hipStream_t s = (hipStream_t)stream;
 #define KRQ_FP8_CASE(MODE, LAYOUT)                                                                   \
-  launch_xk<MODE, LAYOUT>(x_kind, algo, pb, awc, m, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, \
+  launch_xk<MODE, LAYOUT>(x_kind, algo, pb, awc, u, m, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, \
                           w_scale, w_per_row, m, NO, K, kts, out, aux)
   if (w_layout == KRQ_W_TILED) {
     if (mode == KRQ_OUT_BF16) KRQ_FP8_CASE(KRQ_OUT_BF16, KRQ_W_TILED);
