@@ -308,9 +308,13 @@ def lm_bytes(M, kind):
 
 def dominant_key(M, mode, fused, layout):
     """The template name rocprofv3 reports for the GEMV kernel of these arguments
-    (k_gemv_fp8<MT, MODE, LAYOUT, XK, ALGO, U, PB, AWC>; the SwiGLU kernel is never paired and
-    has no activation wave), to look up its measured HBM traffic."""
+    (k_gemv_fp8<MT, MODE, LAYOUT, XK, ALGO, U, PB, AWC>; the SwiGLU kernel is never paired; at
+    M = 1 with bf16 input (K = 2560) it runs beside an activation wave of 8 chunks per lane, with
+    five step slots on the tiled layout), to look up its measured HBM traffic."""
     mt = 1 if M <= 16 else 2
+    if fused and M == 1:
+        u = 5 if layout == 1 else 4
+        return f"k_gemv_fp8<{mt}, {mode}, {layout}, 1, 1, {u}, 1, 8>"
     u = 4 if M <= 4 else 2
     return f"k_gemv_fp8<{mt}, {mode}, {layout}, {1 if fused else 0}, 1, {u}, 1, 0>"
 

@@ -36,19 +36,21 @@ namespace {
 #define KRQ_GEMV_ARGS xb, x_scale, x_inv, x_per_row, wb, w_scale, w_per_row, m, NO, K, kts, out, aux
 
 // one bf16 row: MT 1, no pairing; awc = chunks per lane of the activation wave (0: none); u = step
-// slots per weight wave: 4, or (activation wave, tiled single-matrix matrix-core kernels) 8 or 10
+// slots per weight wave: 4, or (activation wave, tiled matrix-core kernels) 8 or 10 for one matrix,
+// 5 for the two-matrix SwiGLU block
 template <int MODE, int LAYOUT, int XK, int ALGO>
 void launch_row(int awc, int u, dim3 grid, dim3 block, size_t smem, hipStream_t s, const uint8_t* xb,
                 const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
                 const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out,
                 void* aux) {
-  constexpr bool deep = LAYOUT == KRQ_W_TILED && ALGO == 1 && MODE != KRQ_OUT_SWIGLU;
+  constexpr bool deep = LAYOUT == KRQ_W_TILED && ALGO == 1 && MODE != kOutArgmax;
+  constexpr int DU = MODE == KRQ_OUT_SWIGLU ? kSwiU : kDeepU, MU = MODE == KRQ_OUT_SWIGLU ? kSwiU : kMidU;
 #define KRQ_ROW_U(AWC)                                                                                       \
-  if (deep && u == kDeepU)                                                                                   \
-    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, deep ? kDeepU : 4, 1, AWC>), grid, block, smem, s, \
+  if (deep && u == DU)                                                                                       \
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, deep ? DU : 4, 1, AWC>), grid, block, smem, s, \
                        KRQ_GEMV_ARGS);                                                                       \
-  else if (deep && u == kMidU)                                                                               \
-    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, deep ? kMidU : 4, 1, AWC>), grid, block, smem, s,  \
+  else if (deep && u == MU)                                                                                  \
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, deep ? MU : 4, 1, AWC>), grid, block, smem, s,  \
                        KRQ_GEMV_ARGS);                                                                       \
   else                                                                                                       \
     hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, 4, 1, AWC>), grid, block, smem, s, KRQ_GEMV_ARGS);
@@ -161,15 +163,15 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   const int U = (algo == 2 || M <= 4) ? 4 : 2;
   // one-row kind: an activation wave holding the whole row (K <= 10240; KRQ_GEMV_AW=0 turns it off),
   // else every wave takes part in the prologue. Measured at M = 1: QKV 5.92 -> 5.29 us, O 5.15 ->
-  // 4.41, down 7.91 -> 7.16, FP8 lm_head 64.9 -> 63.1; the SwiGLU GEMV, whose two-matrix block has
-  // a long main loop that hides the prologue, keeps the shared prologue (10.92 against 11.04 us).
+  // 4.41, down 7.91 -> 7.16, FP8 lm_head 64.9 -> 63.1; the SwiGLU GEMV 11.24 -> 10.86 with the
+  // five-slot ring below (with four slots the activation wave did not pay: 11.45).
   static const bool aw_ok = [] {
     const char* e = getenv("KRQ_GEMV_AW");
     return !(e && atoi(e) == 0);
   }();
   // With static scales (M == 1) the wave quantizes the slice alone.
   int awc = 0;
-  if (x_kind == KRQ_X_BF16_DYN && aw_ok && mode != KRQ_OUT_SWIGLU)
+  if (x_kind == KRQ_X_BF16_DYN && aw_ok)
     awc = K <= 512 * kAwSmall ? kAwSmall : K <= 512 * kAwLarge ? kAwLarge : 0;
   if (x_kind == KRQ_X_BF16_STATIC && aw_ok && M == 1)
     awc = ks <= 512 * kAwSmall ? kAwSmall : ks <= 512 * kAwLarge ? kAwLarge : 0;
@@ -180,15 +182,17 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   // holds all of its steps in flight at once, one memory round trip and no masked slots. Measured at
   // M = 1 (graph of 72 launches over 36 layers): QKV (10 steps, one wave of 10) 5.24 -> 4.84 us, O (8
   // steps, one wave of 8) 4.38 -> 4.25, down (19 steps, two waves of 10) 7.51 -> 6.90; rings of
-  // 8 for 10 steps (two rounds) or 12 (masked slots) measured slower, and so did the SwiGLU block.
+  // 8 for 10 steps (two rounds) or 12 (masked slots) measured slower. The two-matrix SwiGLU block
+  // (four loads a step) takes five slots with two weight waves (ten slots spill registers).
   const int nsteps = (kts + 1) / 2;
   int u = U;
   static const bool deep_ok = [] {
     const char* e = getenv("KRQ_GEMV_DEEP");
     return !(e && atoi(e) == 0);
   }();
-  if (deep_ok && awc > 0 && algo == 1 && mode != KRQ_OUT_SWIGLU && w_layout == KRQ_W_TILED)
-    u = nsteps <= kMidU ? kMidU : kDeepU;
+  // The lm_head (argmax epilogue, 9,496 blocks) keeps four slots: 63.1 against 64.4 us.
+  if (deep_ok && awc > 0 && algo == 1 && w_layout == KRQ_W_TILED && mode != kOutArgmax)
+    u = mode == KRQ_OUT_SWIGLU ? kSwiU : nsteps <= kMidU ? kMidU : kDeepU;
   int nw = plan_waves(nsteps, P, u, NO / 16 / pb * split, awc > 0);
   // the other fused prologues hold at most kXChunks 16-byte chunks per thread
   int64_t xchunks = 0;

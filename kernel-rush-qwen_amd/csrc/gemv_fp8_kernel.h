@@ -36,7 +36,7 @@ constexpr int kMaxThreads = 512;
 // one-row activation wave: 16-byte chunks per lane (the whole row, K <= 64 * 8 * AWC)
 constexpr int kAwSmall = 8, kAwLarge = 20;
 // step slots of the deep-ring one-row kernels (a weight wave issues all of its steps at once)
-constexpr int kMidU = 8, kDeepU = 10;
+constexpr int kMidU = 8, kDeepU = 10, kSwiU = 5;
 constexpr int64_t kCUs = 256;  // compute units of the MI355X
 
 // The activation wave of the one-row kernels: one extra wave per block that quantizes the block's
