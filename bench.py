@@ -215,30 +215,43 @@ def graph_time(torch, fn, reps, iters=5):
 
 def kernel_table(torch, fp8, L, layers, xs, M, reps):
     """Each kernel of the step alone, back-to-back launches cycling layers (hipEvents around a
-    graph replay). At M = 1 the GEMV quantizes its activations itself (one kernel per
-    projection); at larger M the per-token quantization kernel runs first and the GEMV reads
-    e4m3 activations."""
+    graph replay). Where the GEMV can scale its bf16 activations per token itself (M = 1, and
+    M <= 16 with K <= 4096) it is one kernel per projection, as in the step; otherwise (the
+    down projection at M > 1, M = 32) the per-token quantization kernel runs first and the GEMV
+    reads e4m3 activations. At M > 1 the e4m3 GEMV of the in-kernel projections is timed too
+    (name/e4m3), for the comparison."""
     rows = []
-    fused = M == 1
-    for name, N, K, split, mode in PROJ:
-        m = {"partial": L.OUT_PARTIAL, "swiglu": L.OUT_SWIGLU, "bf16": L.OUT_BF16}[mode]
-        x = xs[name]
-        if fused:
-            o = fp8.gemv_fp8_bf16_launch(x, layers[0][name], split, m)
-            fn = lambda i, name=name, x=x, split=split, m=m, o=o: fp8.gemv_fp8_bf16_launch(
-                x, layers[i % len(layers)][name], split, m, out=o)
-            xbytes = 2 * M * K
-        else:
-            x8, sc = fp8.quant_rows(x)
-            sc = sc.reshape(-1)
-            o = fp8.gemv_fp8_launch(x8, sc, layers[0][name], split, m)
-            fn = lambda i, name=name, x8=x8, sc=sc, split=split, m=m, o=o: fp8.gemv_fp8_launch(
-                x8, sc, layers[i % len(layers)][name], split, m, out=o)
-            xbytes = M * K
+    two_kernel = False
+
+    def add(name, N, K, split, mode, fn, xbytes):
         tmin, tmed = graph_time(torch, fn, reps)
         b = N * K + 4 * N + xbytes + 4 * M + out_bytes(M, N, split, mode)
         rows.append(dict(name=name, N=N, K=K, M=M, split=split, mode=mode, us_min=tmin, us_med=tmed,
                          bytes=b, gbs=b / tmin / 1e3, frac=b / (tmin * 1e-6) / HBM_PEAK))
+
+    def e4m3_fn(x, name, split, m):
+        x8, sc = fp8.quant_rows(x)
+        sc = sc.reshape(-1)
+        o = fp8.gemv_fp8_launch(x8, sc, layers[0][name], split, m)
+        return lambda i: fp8.gemv_fp8_launch(x8, sc, layers[i % len(layers)][name], split, m, out=o)
+
+    extra = []
+    for name, N, K, split, mode in PROJ:
+        m = {"partial": L.OUT_PARTIAL, "swiglu": L.OUT_SWIGLU, "bf16": L.OUT_BF16}[mode]
+        x = xs[name]
+        if fp8._fits_fused(x, split, None):
+            o = fp8.gemv_fp8_bf16_launch(x, layers[0][name], split, m)
+            fn = lambda i, name=name, x=x, split=split, m=m, o=o: fp8.gemv_fp8_bf16_launch(
+                x, layers[i % len(layers)][name], split, m, out=o)
+            add(name, N, K, split, mode, fn, 2 * M * K)
+            if M > 1:
+                extra.append((name + "/e4m3", N, K, split, mode, e4m3_fn(x, name, split, m), M * K))
+        else:
+            two_kernel = True
+            add(name, N, K, split, mode, e4m3_fn(x, name, split, m), M * K)
+    for e in extra:
+        add(*e)
+    fused = M == 1
     if fused:   # the vector-ALU kernel on the same operands, for the M = 1 design comparison
         for name, N, K, split, mode in PROJ:
             m = {"partial": L.OUT_PARTIAL, "swiglu": L.OUT_SWIGLU, "bf16": L.OUT_BF16}[mode]
@@ -250,7 +263,7 @@ def kernel_table(torch, fp8, L, layers, xs, M, reps):
             b = N * K + 4 * N + 2 * M * K + 4 * M + out_bytes(M, N, split, mode)
             rows.append(dict(name=name + "/valu", N=N, K=K, M=M, split=split, mode=mode, us_min=tmin,
                              us_med=tmed, bytes=b, gbs=b / tmin / 1e3, frac=b / (tmin * 1e-6) / HBM_PEAK))
-    if not fused:
+    if two_kernel:
         x = xs["down"]
         tq, tqm = graph_time(torch, lambda i: fp8.quant_rows(x), reps)
         qb = 3 * M * I + 4 * M
