@@ -56,11 +56,38 @@ __global__ __launch_bounds__(kRowThreads) void k_rmsnorm_quant_rows(const uint16
 
 #define KRQ_FUSED_FP8_ARGS xb, x_scale, x_inv, x_per_row, wb, w_scale, w_per_row, m, NO, K, kts, out, nullptr, fa
 
+// u: step slots of the one-row launches beside the activation wave on the tiled layout (deep rings,
+// plan()): 5 for the SwiGLU block, 8 or 10 otherwise; 0 for the default rings
 template <int MODE, int LAYOUT, int XK, bool NORM>
-void launch(int M, int awc, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb, const float* x_scale,
-            const float* x_inv, int x_per_row, const uint8_t* wb, const float* w_scale, int w_per_row, int m,
-            int64_t NO, int64_t K, int kts, void* out, const FusedArgs& fa) {
+void launch(int M, int awc, int u, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb,
+            const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb, const float* w_scale,
+            int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out, const FusedArgs& fa) {
   const dim3 block((nw + (awc > 0 ? 1 : 0)) * 64);
+  if constexpr (LAYOUT == KRQ_W_TILED) {
+    constexpr int DU = MODE == KRQ_OUT_SWIGLU ? kSwiU : kDeepU, MU = MODE == KRQ_OUT_SWIGLU ? kSwiU : kMidU;
+    if constexpr (XK != KRQ_X_FP8) {
+      if (u > 0 && awc == kAwSmall) {
+        if (u == MU)
+          hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, MU, NORM, kAwSmall>), grid, block, smem, s,
+                             KRQ_FUSED_FP8_ARGS);
+        else
+          hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, DU, NORM, kAwSmall>), grid, block, smem, s,
+                             KRQ_FUSED_FP8_ARGS);
+        return;
+      }
+      if constexpr (!NORM) {  // (with RMSNorm the wave takes rows of at most 4,096)
+        if (u > 0 && awc == kAwLarge) {
+          if (u == MU)
+            hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, MU, NORM, kAwLarge>), grid, block, smem, s,
+                               KRQ_FUSED_FP8_ARGS);
+          else
+            hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, DU, NORM, kAwLarge>), grid, block, smem, s,
+                               KRQ_FUSED_FP8_ARGS);
+          return;
+        }
+      }
+    }
+  }
   if constexpr (XK != KRQ_X_FP8) {
     if (awc == kAwSmall) {
       hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, 4, NORM, kAwSmall>), grid, block, smem, s,
@@ -82,35 +109,46 @@ void launch(int M, int awc, dim3 grid, int nw, size_t smem, hipStream_t s, const
 }
 
 template <int MODE, int XK, bool NORM>
-void launch_layout(int layout, int M, int awc, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb,
-                   const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
+void launch_layout(int layout, int M, int awc, int u, dim3 grid, int nw, size_t smem, hipStream_t s,
+                   const uint8_t* xb, const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
                    const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out,
                    const FusedArgs& fa) {
   if (layout == KRQ_W_TILED)
-    launch<MODE, KRQ_W_TILED, XK, NORM>(M, awc, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, w_scale,
+    launch<MODE, KRQ_W_TILED, XK, NORM>(M, awc, u, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, w_scale,
                                          w_per_row, m, NO, K, kts, out, fa);
-  else
-    launch<MODE, KRQ_W_ROWMAJOR, XK, NORM>(M, awc, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, w_scale,
-                                            w_per_row, m, NO, K, kts, out, fa);
+  else  // (the default rings with the planned waves: deep rings are tiled only)
+    launch<MODE, KRQ_W_ROWMAJOR, XK, NORM>(M, awc, 0, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb,
+                                            w_scale, w_per_row, m, NO, K, kts, out, fa);
 }
 
 struct FusedPlan {
   int nw;       // waves that stream weights
   int awc;      // chunks per lane of the activation wave (0: none, every wave runs the prologue)
+  int u;        // step slots of the deep ring (tiled layout), 0: the default ring
   size_t smem;  // dynamic LDS bytes
 };
+
+// Deep rings for the one-row launches on the tiled layout (KRQ_FUSED_DEEP=0 turns them off): as in
+// the plain kernels, each weight wave holds all of its steps in flight at once.
+bool deep_rings() {
+  static const bool on = [] {
+    const char* e = getenv("KRQ_FUSED_DEEP");
+    return !(e && atoi(e) == 0);
+  }();
+  return on;
+}
 
 // One-row launches (M == 1, bf16 activations) get the activation wave of gemv_fp8_kernel.h when
 // its registers hold what it loads: the whole row (per-token scale) or the slice (static scale),
 // K <= 4096 with RMSNorm (the row's partials, 64 x kSsPerLane); KRQ_GEMV_AW=0 turns it off. The
-// two-matrix SwiGLU block keeps the shared prologue, as in the plain kernel, and so do grids of
-// fewer blocks than CUs (the one-pass residual GEMVs).
+// two-matrix SwiGLU block takes it with the deep rings only, and grids of fewer blocks than CUs
+// (the one-pass residual GEMVs) keep the shared prologue.
 int act_wave_chunks(int64_t M, int64_t K, int64_t ks, int mode, int x_kind, bool norm) {
   static const bool aw_ok = [] {
     const char* e = getenv("KRQ_GEMV_AW");
     return !(e && atoi(e) == 0);
   }();
-  if (!aw_ok || M != 1 || x_kind == KRQ_X_FP8 || mode == KRQ_OUT_SWIGLU) return 0;
+  if (!aw_ok || M != 1 || x_kind == KRQ_X_FP8 || (mode == KRQ_OUT_SWIGLU && !deep_rings())) return 0;
   if (norm && K > 512 * kAwSmall) return 0;
   const int64_t span = x_kind == KRQ_X_BF16_DYN ? K : ks;
   return span <= 512 * kAwSmall ? kAwSmall : span <= 512 * kAwLarge ? kAwLarge : 0;
@@ -128,7 +166,18 @@ bool plan(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind, bool
   if (awc == 0 && norm && x_kind == KRQ_X_BF16_STATIC && M * ks * 2 > kNormStageMax) return false;
   const int kts = static_cast<int>(ks / 64);
   const int MT = M <= 16 ? 1 : 2;
-  int nw = plan_waves((kts + 1) / 2, P, M <= 4 ? 4 : 2, NO / 16 * split, awc > 0);
+  const int nsteps = (kts + 1) / 2;
+  int nw = plan_waves(nsteps, P, M <= 4 ? 4 : 2, NO / 16 * split, awc > 0);
+  // Deep rings beside the activation wave (tiled layout, M == 1): the plain kernels' rings, 8 or 10
+  // slots, 5 for the two-matrix SwiGLU block, which then takes the activation wave too. Measured in
+  // the fused FP8 layer at M = 1: gate_up + RMSNorm 11.60 -> 10.46 us, QKV + RMSNorm 6.80 -> 6.56.
+  // The one-pass residual GEMVs (fewer blocks than CUs, every wave in the prologue) measured slower
+  // with one round of 8- or 10-slot rings (O 6.21 -> 6.64, down 10.39 -> 12.12) and keep four slots.
+  int u = 0;
+  if (deep_rings() && M == 1 && x_kind != KRQ_X_FP8 && awc > 0) {
+    u = mode == KRQ_OUT_SWIGLU ? kSwiU : nsteps <= kMidU ? kMidU : kDeepU;
+    nw = plan_waves(nsteps, P, u, NO / 16 * split, true);
+  }
   bool staged_ss = false;  // the sum-of-squares partials staged in LDS (RMSNorm of M rows)
   if (awc == 0) {
     const int64_t xchunks = x_kind == KRQ_X_BF16_DYN ? (K + 7) / 8 : x_kind == KRQ_X_BF16_STATIC ? M * (ks / 8) : 0;
@@ -146,7 +195,7 @@ bool plan(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind, bool
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) + (x_kind == KRQ_X_FP8 ? 0 : (size_t)M * ks) +
                       (staged_ss ? (size_t)M * (K / 16) * sizeof(float) : 0);
   if (smem > kMaxSmem) return false;
-  *out = FusedPlan{nw, awc, smem};
+  *out = FusedPlan{nw, awc, u, smem};
   return true;
 }
 
@@ -204,7 +253,7 @@ extern "C" int krq_gemv_fp8_fused(const void* x, int x_kind, const float* x_scal
   const int m = static_cast<int>(M);
   hipStream_t s = (hipStream_t)stream;
 #define KRQ_CASE(MODE, XK, NORM)                                                                          \
-  launch_layout<MODE, XK, NORM>(w_layout, m, p.awc, grid, p.nw, p.smem, s, xb, x_scale, x_inv, x_per_row, wb, w_scale, \
+  launch_layout<MODE, XK, NORM>(w_layout, m, p.awc, p.u, grid, p.nw, p.smem, s, xb, x_scale, x_inv, x_per_row, wb, w_scale, \
                                 w_per_row, m, NO, K, kts, out, fa)
   if (mode == kOutResidual) {
     if (x_kind == KRQ_X_FP8) KRQ_CASE(kOutResidual, KRQ_X_FP8, false);
