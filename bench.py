@@ -215,13 +215,11 @@ def graph_time(torch, fn, reps, iters=5):
 
 def kernel_table(torch, fp8, L, layers, xs, M, reps):
     """Each kernel of the step alone, back-to-back launches cycling layers (hipEvents around a
-    graph replay). Where the GEMV can scale its bf16 activations per token itself (M = 1, and
-    M <= 16 with K <= 4096) it is one kernel per projection, as in the step; otherwise (the
-    down projection at M > 1, M = 32) the per-token quantization kernel runs first and the GEMV
-    reads e4m3 activations. At M > 1 the e4m3 GEMV of the in-kernel projections is timed too
-    (name/e4m3), for the comparison."""
+    graph replay), each projection the way the step runs it: at M = 1 the GEMV scales its bf16 row
+    per token itself (one kernel per projection); at M > 1 quant_rows_tiled runs first and the GEMV
+    reads the tiled e4m3 activations. For comparison: at M = 1 the vector-ALU kernel on the same
+    operands (name/valu), at M > 1 the GEMV on the same e4m3 rows row-major (name/rowx)."""
     rows = []
-    two_kernel = False
 
     def add(name, N, K, split, mode, fn, xbytes):
         tmin, tmed = graph_time(torch, fn, reps)
@@ -229,43 +227,37 @@ def kernel_table(torch, fp8, L, layers, xs, M, reps):
         rows.append(dict(name=name, N=N, K=K, M=M, split=split, mode=mode, us_min=tmin, us_med=tmed,
                          bytes=b, gbs=b / tmin / 1e3, frac=b / (tmin * 1e-6) / HBM_PEAK))
 
-    def e4m3_fn(x, name, split, m):
+    def bf16_fn(x, name, split, m, algo):
+        o = fp8.gemv_fp8_bf16_launch(x, layers[0][name], split, m, None, algo)
+        return lambda i: fp8.gemv_fp8_bf16_launch(x, layers[i % len(layers)][name], split, m, None, algo, out=o)
+
+    def tiled_fn(x, name, split, m):
+        x8, sc = fp8.quant_rows_tiled(x)
+        o = fp8.gemv_fp8_tiled_launch(x8, sc, layers[0][name], M, split, m)
+        return lambda i: fp8.gemv_fp8_tiled_launch(x8, sc, layers[i % len(layers)][name], M, split, m, out=o)
+
+    def rowx_fn(x, name, split, m):
         x8, sc = fp8.quant_rows(x)
         sc = sc.reshape(-1)
         o = fp8.gemv_fp8_launch(x8, sc, layers[0][name], split, m)
         return lambda i: fp8.gemv_fp8_launch(x8, sc, layers[i % len(layers)][name], split, m, out=o)
 
-    extra = []
+    modes = {"partial": L.OUT_PARTIAL, "swiglu": L.OUT_SWIGLU, "bf16": L.OUT_BF16}
     for name, N, K, split, mode in PROJ:
-        m = {"partial": L.OUT_PARTIAL, "swiglu": L.OUT_SWIGLU, "bf16": L.OUT_BF16}[mode]
-        x = xs[name]
-        if fp8._fits_fused(x, split, None):
-            o = fp8.gemv_fp8_bf16_launch(x, layers[0][name], split, m)
-            fn = lambda i, name=name, x=x, split=split, m=m, o=o: fp8.gemv_fp8_bf16_launch(
-                x, layers[i % len(layers)][name], split, m, out=o)
-            add(name, N, K, split, mode, fn, 2 * M * K)
-            if M > 1:
-                extra.append((name + "/e4m3", N, K, split, mode, e4m3_fn(x, name, split, m), M * K))
+        x, m = xs[name], modes[mode]
+        if M == 1:
+            add(name, N, K, split, mode, bf16_fn(x, name, split, m, L.ALGO_AUTO), 2 * M * K)
         else:
-            two_kernel = True
-            add(name, N, K, split, mode, e4m3_fn(x, name, split, m), M * K)
-    for e in extra:
-        add(*e)
-    fused = M == 1
-    if fused:   # the vector-ALU kernel on the same operands, for the M = 1 design comparison
-        for name, N, K, split, mode in PROJ:
-            m = {"partial": L.OUT_PARTIAL, "swiglu": L.OUT_SWIGLU, "bf16": L.OUT_BF16}[mode]
-            x = xs[name]
-            o = fp8.gemv_fp8_bf16_launch(x, layers[0][name], split, m, None, L.ALGO_VALU)
-            fn = lambda i, name=name, x=x, split=split, m=m, o=o: fp8.gemv_fp8_bf16_launch(
-                x, layers[i % len(layers)][name], split, m, None, L.ALGO_VALU, out=o)
-            tmin, tmed = graph_time(torch, fn, reps)
-            b = N * K + 4 * N + 2 * M * K + 4 * M + out_bytes(M, N, split, mode)
-            rows.append(dict(name=name + "/valu", N=N, K=K, M=M, split=split, mode=mode, us_min=tmin,
-                             us_med=tmed, bytes=b, gbs=b / tmin / 1e3, frac=b / (tmin * 1e-6) / HBM_PEAK))
-    if two_kernel:
+            add(name, N, K, split, mode, tiled_fn(x, name, split, m), M * K)
+    for name, N, K, split, mode in PROJ:
+        x, m = xs[name], modes[mode]
+        if M == 1:
+            add(name + "/valu", N, K, split, mode, bf16_fn(x, name, split, m, L.ALGO_VALU), 2 * M * K)
+        else:
+            add(name + "/rowx", N, K, split, mode, rowx_fn(x, name, split, m), M * K)
+    if M > 1:
         x = xs["down"]
-        tq, tqm = graph_time(torch, lambda i: fp8.quant_rows(x), reps)
+        tq, tqm = graph_time(torch, lambda i: fp8.quant_rows_tiled(x), reps)
         qb = 3 * M * I + 4 * M
         rows.append(dict(name="quant_rows", N=0, K=I, M=M, split=1, mode="-", us_min=tq, us_med=tqm,
                          bytes=qb, gbs=qb / tq / 1e3, frac=qb / (tq * 1e-6) / HBM_PEAK))
@@ -323,13 +315,14 @@ def dominant_key(M, mode, fused, layout):
     """The template name rocprofv3 reports for the GEMV kernel of these arguments
     (k_gemv_fp8<MT, MODE, LAYOUT, XK, ALGO, U, PB, AWC>; the SwiGLU kernel is never paired; at
     M = 1 with bf16 input (K = 2560) it runs beside an activation wave of 8 chunks per lane, with
-    five step slots on the tiled layout), to look up its measured HBM traffic."""
+    five step slots on the tiled layout; at M > 1 it reads tiled e4m3 activations, XK 3), to look
+    up its measured HBM traffic."""
     mt = 1 if M <= 16 else 2
     if fused and M == 1:
         u = 5 if layout == 1 else 4
         return f"k_gemv_fp8<{mt}, {mode}, {layout}, 1, 1, {u}, 1, 8>"
     u = 4 if M <= 4 else 2
-    return f"k_gemv_fp8<{mt}, {mode}, {layout}, {1 if fused else 0}, 1, {u}, 1, 0>"
+    return f"k_gemv_fp8<{mt}, {mode}, {layout}, {3 if M > 1 else 0}, 1, {u}, 1, 0>"
 
 
 def measured_traffic(cfg, key):

@@ -47,6 +47,8 @@ extern "C" {
 #define KRQ_X_FP8 0          /* x is e4m3 [M,K]; x_scale holds its scale (per row or tensor) */
 #define KRQ_X_BF16_DYN 1     /* x is bf16 [1,K]; the per-token scale is computed in the kernel */
 #define KRQ_X_BF16_STATIC 2  /* x is bf16 [M,K]; quantized with x_inv, scaled by x_scale */
+#define KRQ_X_FP8_TILED 3    /* x is e4m3 in the tiled activation layout of krq_quant_rows_tiled,
+                                with its scale */
 
 /* lm-head weight kinds */
 #define KRQ_LM_BF16 0
@@ -98,6 +100,16 @@ int krq_cast_fp8(const void* x_bf16, int64_t M, int64_t K, const float* inv, int
  * the cast above. xs[m] = scale of row m (amax[m]/448 as above).
  */
 int krq_quant_rows(const void* x_bf16, int64_t M, int64_t K, void* x8, float* xs, void* stream);
+
+/*
+ * krq_quant_rows with the e4m3 rows written in the tiled activation layout the FP8 GEMV reads
+ * as KRQ_X_FP8_TILED (no reference counterpart: the same bytes as quant_rows, permuted, for the
+ * gemv_fp8 / gemv_swiglu_fp8 calls of experiments/modal_fp8.py:67-69 at M > 1): rows padded to
+ * MP = 16 * ceil(M / 16) (pad rows zero), split into 16-row x 64-byte tiles in the order
+ * [MP / 16][K / 64]; inside a tile, lane l = 16 g + r holds row r's bytes 16 g .. 16 g + 15.
+ * x8_tiled holds MP * K bytes; K % 64 == 0. xs as krq_quant_rows (M values).
+ */
+int krq_quant_rows_tiled(const void* x_bf16, int64_t M, int64_t K, void* x8_tiled, float* xs, void* stream);
 
 /*
  * FP8 skinny GEMM/GEMV, M <= 32: replaces linear_fp8 -> torch._scaled_mm (reference

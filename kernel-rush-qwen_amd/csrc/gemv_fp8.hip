@@ -88,7 +88,8 @@ int launch(int algo, int pb, int awc, int u, int M, dim3 grid, int nw, size_t sm
     }
   }
   if (algo == 2) {
-    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 2, 4, 1, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
+    if constexpr (XK != KRQ_X_FP8_TILED)  // (rejected by the caller)
+      hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 2, 4, 1, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
   } else if (M <= 4) {
     hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, 4, 1, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
   } else if (M <= 16 && pb == 2) {
@@ -110,6 +111,8 @@ void launch_xk(int xk, int algo, int pb, int awc, int u, int M, dim3 grid, int n
                int64_t K, int kts, void* out, void* aux) {
   if (xk == KRQ_X_FP8)
     launch<MODE, LAYOUT, KRQ_X_FP8>(algo, pb, awc, u, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
+  else if (xk == KRQ_X_FP8_TILED)
+    launch<MODE, LAYOUT, KRQ_X_FP8_TILED>(algo, pb, awc, u, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
   else if (xk == KRQ_X_BF16_DYN)
     launch<MODE, LAYOUT, KRQ_X_BF16_DYN>(algo, pb, awc, u, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
   else
@@ -125,7 +128,7 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   KRQ_REQUIRE(x && w8 && w_scale && (out || mode == kOutArgmax) && (aux || mode != kOutArgmax),
               "gemv_fp8: null pointer");
   KRQ_REQUIRE(aligned16(x) && aligned16(w8), "gemv_fp8: x and w8 must be 16-byte aligned");
-  KRQ_REQUIRE(x_kind >= KRQ_X_FP8 && x_kind <= KRQ_X_BF16_STATIC, "gemv_fp8: bad x_kind %d", x_kind);
+  KRQ_REQUIRE(x_kind >= KRQ_X_FP8 && x_kind <= KRQ_X_FP8_TILED, "gemv_fp8: bad x_kind %d", x_kind);
   KRQ_REQUIRE(x_kind == KRQ_X_BF16_DYN || x_scale, "gemv_fp8: x_scale is required");
   KRQ_REQUIRE(x_kind != KRQ_X_BF16_STATIC || x_inv, "gemv_fp8: x_inv is required");
   KRQ_REQUIRE(M >= 1 && M <= 32, "gemv_fp8: M=%lld outside 1..32", (long long)M);
@@ -138,6 +141,7 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   KRQ_REQUIRE(mode >= KRQ_OUT_BF16 && mode <= kOutArgmax, "gemv_fp8: bad mode %d", mode);
   KRQ_REQUIRE(algo >= 0 && algo <= 2, "gemv_fp8: bad algo %d", algo);
   KRQ_REQUIRE(algo != 2 || M == 1, "gemv_fp8: the vector-ALU kernel takes M == 1 only");
+  KRQ_REQUIRE(algo != 2 || x_kind != KRQ_X_FP8_TILED, "gemv_fp8: tiled activations take the matrix-core kernel");
   KRQ_REQUIRE(x_kind != KRQ_X_BF16_DYN || M == 1, "gemv_fp8: in-kernel per-token scaling takes M == 1");
   KRQ_REQUIRE(mode == KRQ_OUT_PARTIAL || split == 1, "gemv_fp8: split %d needs the partials output", split);
   KRQ_REQUIRE(mode != kOutArgmax || N <= 0x7fffffff, "gemv_fp8: N=%lld too large for int indices", (long long)N);
@@ -205,7 +209,7 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
               (long long)(xchunks * 8));
   if (awc > 0) nw = min(nw, kMaxThreads / 64 - 1);
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) +
-                      (x_kind == KRQ_X_FP8 ? 0 : (size_t)M * ks);
+                      (x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED ? 0 : (size_t)M * ks);
   const dim3 grid(static_cast<unsigned>(NO / 16 / pb), static_cast<unsigned>(split));
   const uint8_t* xb = (const uint8_t*)x;
   const uint8_t* wb = (const uint8_t*)w8;

@@ -5,6 +5,9 @@
 // Activation kinds (template XK):
 //   KRQ_X_FP8          x is e4m3 [M, K] with its scale; matrix-core A operands are loaded from
 //                      global memory by the lanes whose row m < M.
+//   KRQ_X_FP8_TILED    the same e4m3 rows in the tiled activation layout (krq_quant_rows_tiled:
+//                      16-row x 64-byte tiles, lane 16 g + r holding row r's bytes 16 g .. 16 g + 15),
+//                      so each A operand load is one contiguous KiB, like the weights'.
 //   KRQ_X_BF16_DYN     x is bf16 [1, K]; the block computes the per-token scale itself
 //                      (amax over all of K, ActScale arithmetic), quantizes its K slice into LDS.
 //   KRQ_X_BF16_STATIC  x is bf16 [M, K] with a given inverse scale (SharedScale / ActScale
@@ -126,11 +129,13 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   __shared__ uint32_t last_s;
   static_assert(PB == 1 || (MODE != KRQ_OUT_SWIGLU && MODE != kOutResidual && ALGO != 2),
                 "paired row blocks: MFMA, no SwiGLU or residual epilogue");
-  static_assert(!NORM || XK != KRQ_X_FP8, "the RMSNorm prologue takes bf16 activations");
+  static_assert(!NORM || (XK != KRQ_X_FP8 && XK != KRQ_X_FP8_TILED), "the RMSNorm prologue takes bf16 activations");
   constexpr bool AW = AWC > 0;
-  static_assert(!AW || (XK != KRQ_X_FP8 && MT == 1), "activation wave: one bf16 row");
+  static_assert(!AW || (XK != KRQ_X_FP8 && XK != KRQ_X_FP8_TILED && MT == 1), "activation wave: one bf16 row");
+  static_assert(XK != KRQ_X_FP8_TILED || ALGO != 2, "tiled activations: matrix-core kernels");
   constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : PB;  // weight row blocks streamed per step
-  constexpr bool FUSED = XK != KRQ_X_FP8;
+  constexpr bool XT = XK == KRQ_X_FP8_TILED;
+  constexpr bool FUSED = XK != KRQ_X_FP8 && !XT;  // bf16 activations quantized into LDS
   constexpr int SC = XK == KRQ_X_BF16_DYN ? kSsPerLane : kSsChunks;
   // nw = the waves that stream weights (all but the activation wave)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x >> 6) - (AW ? 1 : 0);
@@ -209,10 +214,15 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
     if (!FUSED) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const int m = ALGO == 2 ? 0 : min(mt * 16 + r, M - 1);
-        const uint8_t* xr = x + (int64_t)m * K + g * 16;
-        xl[u][mt] = ld16(xr + t0 * 64);
-        xh[u][mt] = ld16(xr + t1 * 64);
+        if (XT) {  // tile (mt, t) of the activations: this lane's 16 bytes of it
+          xl[u][mt] = ld16(x + (((int64_t)mt * (K >> 6) + t0) * 64 + lane) * 16);
+          xh[u][mt] = ld16(x + (((int64_t)mt * (K >> 6) + t1) * 64 + lane) * 16);
+        } else {
+          const int m = ALGO == 2 ? 0 : min(mt * 16 + r, M - 1);
+          const uint8_t* xr = x + (int64_t)m * K + g * 16;
+          xl[u][mt] = ld16(xr + t0 * 64);
+          xh[u][mt] = ld16(xr + t1 * 64);
+        }
       }
     }
   };
@@ -254,7 +264,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   }
 
   // ---- fused activation prologue, part 2: scale, quantize the slice into LDS ----
-  if (XK == KRQ_X_FP8) {
+  if (XK == KRQ_X_FP8 || XT) {
     xs_l[threadIdx.x & 31] = xs_reg;
   } else if (XK == KRQ_X_BF16_DYN) {
     if constexpr (!AW) {  // (with the activation wave, the slice is already in LDS after the barrier below)

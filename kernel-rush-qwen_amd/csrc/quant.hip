@@ -223,11 +223,22 @@ __global__ __launch_bounds__(kQT) void k_weight_rows_vec(const uint16_t* __restr
   }
 }
 
-// per-row activation scale, and with x8 the per-token cast (quant_rows)
-__global__ __launch_bounds__(kQT) void k_act_rows_vec(const uint16_t* __restrict__ x, int64_t K,
+// per-row activation scale, and with x8 the per-token cast (quant_rows); TILED: x8 in the tiled
+// activation layout (tiled_offset, the weights' tiling), one block per row of the M rows padded to
+// a multiple of 16, the pad rows written as zeros
+template <bool TILED>
+__global__ __launch_bounds__(kQT) void k_act_rows_vec(const uint16_t* __restrict__ x, int64_t M, int64_t K,
                                                       float headroom, float* amax, float* inv,
                                                       float* scale, uint8_t* __restrict__ x8) {
   const int64_t r = blockIdx.x;
+  if (TILED && r >= M) {
+#pragma unroll
+    for (int c = 0; c < kVecChunks; ++c) {
+      const int64_t e = 8 * (int64_t)(threadIdx.x + c * kQT);
+      if (e < K) *reinterpret_cast<uint2*>(x8 + tiled_offset(r, e, K)) = make_uint2(0u, 0u);
+    }
+    return;
+  }
   const uint8_t* row = reinterpret_cast<const uint8_t*>(x + r * K);
   uint4 v[kVecChunks];
   float m = 0.0f;
@@ -249,7 +260,7 @@ __global__ __launch_bounds__(kQT) void k_act_rows_vec(const uint16_t* __restrict
 #pragma unroll
     for (int c = 0; c < kVecChunks; ++c) {
       const int64_t e = 8 * (int64_t)(threadIdx.x + c * kQT);
-      if (e < K) *reinterpret_cast<uint2*>(x8 + r * K + e) = quant8(v[c], iv);
+      if (e < K) *reinterpret_cast<uint2*>(x8 + (TILED ? tiled_offset(r, e, K) : r * K + e)) = quant8(v[c], iv);
     }
   }
 }
@@ -332,8 +343,12 @@ extern "C" int krq_act_scale(const void* x_bf16, int64_t M, int64_t K, int per_r
   hipStream_t s = (hipStream_t)stream;
   if (per_row) {
     KRQ_REQUIRE(M <= 0x7fffffff, "act_scale: M=%lld too large", (long long)M);
-    hipLaunchKernelGGL(vec_ok(x_bf16, K, K) ? k_act_rows_vec : k_act_rows, dim3(static_cast<unsigned>(M)),
-                       dim3(kQT), 0, s, (const uint16_t*)x_bf16, K, headroom, amax, inv, scale, nullptr);
+    if (vec_ok(x_bf16, K, K))
+      hipLaunchKernelGGL(k_act_rows_vec<false>, dim3(static_cast<unsigned>(M)), dim3(kQT), 0, s,
+                         (const uint16_t*)x_bf16, M, K, headroom, amax, inv, scale, nullptr);
+    else
+      hipLaunchKernelGGL(k_act_rows, dim3(static_cast<unsigned>(M)), dim3(kQT), 0, s, (const uint16_t*)x_bf16, K,
+                         headroom, amax, inv, scale, nullptr);
   } else {
     KRQ_REQUIRE(ws != nullptr, "act_scale: per-tensor scale needs a workspace");
     const int g = grid_for(M * K, kQT * 16, kActPartials);
@@ -364,10 +379,26 @@ extern "C" int krq_quant_rows(const void* x_bf16, int64_t M, int64_t K, void* x8
   KRQ_REQUIRE(x_bf16 && x8 && xs, "quant_rows: null pointer");
   KRQ_REQUIRE(M > 0 && K > 0 && M <= 0x7fffffff, "quant_rows: bad shape M=%lld K=%lld",
               (long long)M, (long long)K);
-  hipLaunchKernelGGL(vec_ok(x_bf16, K, K) && aligned16(x8) ? k_act_rows_vec : k_act_rows,
-                     dim3(static_cast<unsigned>(M)), dim3(kQT), 0, (hipStream_t)stream,
-                     (const uint16_t*)x_bf16, K, 1.0f, nullptr, nullptr, xs, (uint8_t*)x8);
+  if (vec_ok(x_bf16, K, K) && aligned16(x8))
+    hipLaunchKernelGGL(k_act_rows_vec<false>, dim3(static_cast<unsigned>(M)), dim3(kQT), 0, (hipStream_t)stream,
+                       (const uint16_t*)x_bf16, M, K, 1.0f, nullptr, nullptr, xs, (uint8_t*)x8);
+  else
+    hipLaunchKernelGGL(k_act_rows, dim3(static_cast<unsigned>(M)), dim3(kQT), 0, (hipStream_t)stream,
+                       (const uint16_t*)x_bf16, K, 1.0f, nullptr, nullptr, xs, (uint8_t*)x8);
   return krq_check_launch("quant_rows");
+}
+
+extern "C" int krq_quant_rows_tiled(const void* x_bf16, int64_t M, int64_t K, void* x8_tiled, float* xs,
+                                    void* stream) {
+  KRQ_REQUIRE(x_bf16 && x8_tiled && xs, "quant_rows_tiled: null pointer");
+  KRQ_REQUIRE(M > 0 && M <= 0x7fffffe0 && K > 0 && K % 64 == 0,
+              "quant_rows_tiled: bad shape M=%lld K=%lld (K a multiple of 64)", (long long)M, (long long)K);
+  KRQ_REQUIRE(vec_ok(x_bf16, K, K) && aligned16(x8_tiled),
+              "quant_rows_tiled: x and x8_tiled must be 16-byte aligned and K at most %lld", (long long)kVecMaxK);
+  const int64_t mp = (M + 15) / 16 * 16;  // rows padded to whole 16-row tiles
+  hipLaunchKernelGGL(k_act_rows_vec<true>, dim3(static_cast<unsigned>(mp)), dim3(kQT), 0, (hipStream_t)stream,
+                     (const uint16_t*)x_bf16, M, K, 1.0f, nullptr, nullptr, xs, (uint8_t*)x8_tiled);
+  return krq_check_launch("quant_rows_tiled");
 }
 
 extern "C" int krq_pack_fp8(const void* w8_rowmajor, int64_t N, int64_t K, void* w8_tiled,

@@ -18,7 +18,7 @@ OUT_BF16, OUT_PARTIAL, OUT_SWIGLU, OUT_RESIDUAL = 0, 1, 2, 4
 W_ROWMAJOR, W_TILED = 0, 1
 LM_BF16, LM_FP8 = 0, 1
 ALGO_AUTO, ALGO_MFMA, ALGO_VALU = 0, 1, 2
-X_FP8, X_BF16_DYN, X_BF16_STATIC = 0, 1, 2
+X_FP8, X_BF16_DYN, X_BF16_STATIC, X_FP8_TILED = 0, 1, 2, 3
 
 _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
 
@@ -30,6 +30,7 @@ EXPORTS = {
     "krq_act_scale_ws_floats": (_i64, [_i64, _i64]),
     "krq_cast_fp8": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _vp]),
     "krq_quant_rows": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    "krq_quant_rows_tiled": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "krq_gemv_fp8": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64,
                             _i32, _i32, _i32, _vp, _vp]),
     "krq_gemv_bf16": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp]),

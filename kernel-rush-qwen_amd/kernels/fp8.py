@@ -12,6 +12,7 @@ torch's float8_e4m3fn cast gives):
   quantize         the same per output row (scale [N])
   ActScale         amax = max(max|x|, 1e-6) * headroom; inv = 448 / amax; scale = amax / 448
   quant_rows       ActScale per row, then x8 = e4m3(clamp(x * inv[m], +-448)); xs = scale [M, 1]
+                   (quant_rows_tiled: the same bytes in the tiled activation layout)
   gemv_fp8 et al.  y = (sum_k x8 w8) * x_scale * w_scale with fp32 accumulation
 Quantized weights carry, beside the reference's row-major [N, K] bytes, a copy in the GEMV
 kernels' tiled layout (FP8Weight.tiled).
@@ -128,6 +129,20 @@ def quant_rows(x):
     return x8, xs
 
 
+def quant_rows_tiled(x):
+    """quant_rows with the e4m3 rows in the tiled activation layout the FP8 GEMV reads as
+    X_FP8_TILED: the M rows padded with zero rows to MP = 16 * ceil(M / 16), in 16-row x 64-byte
+    tiles (the tiling of FP8Weight.tiled), so each matrix-core operand load is one contiguous KiB.
+    Returns (x8t uint8 [MP * K], xs fp32 [M, 1]); the bytes are quant_rows' bytes, permuted."""
+    x2 = _rows(x)
+    M, K = x2.shape
+    mp = (M + 15) // 16 * 16
+    x8t = torch.empty((mp * K,), device=x2.device, dtype=torch.uint8)
+    xs = torch.empty((M, 1), device=x2.device, dtype=torch.float32)
+    L.call("krq_quant_rows_tiled", L.ptr(x2), M, K, L.ptr(x8t), L.ptr(xs), L.stream(x2))
+    return x8t, xs
+
+
 def _cast_hip(x, a):
     x2 = _rows(x)
     M, K = x2.shape
@@ -223,6 +238,19 @@ def gemv_fp8_launch(x8, xs, q, split=1, mode=L.OUT_BF16, algo=L.ALGO_AUTO, out=N
     return _gemv(x8, L.X_FP8, xs.reshape(-1), None, M, q, split, mode, algo, out)
 
 
+def gemv_fp8_tiled_launch(x8t, xs, q, M, split=1, mode=L.OUT_BF16, out=None):
+    """One launch of the FP8 GEMV (matrix-core kernel) on M rows of e4m3 activations in the tiled
+    layout of quant_rows_tiled (x8t: 16 * ceil(M / 16) * K bytes) with their scales xs (1 or M
+    values). Returns out as gemv_fp8_launch."""
+    K = q[0].shape[1]
+    mp = (M + 15) // 16 * 16
+    if x8t.dtype != torch.uint8 or x8t.numel() != mp * K or not x8t.is_contiguous():
+        raise ValueError(f"x8t must be a contiguous uint8 tensor of {mp * K} bytes (quant_rows_tiled)")
+    if xs.dtype != torch.float32 or xs.numel() not in (1, M):
+        raise ValueError("xs must be fp32 with 1 or M values")
+    return _gemv(x8t, L.X_FP8_TILED, xs.reshape(-1), None, M, q, split, mode, L.ALGO_MFMA, out)
+
+
 def gemv_fp8_bf16_launch(x, q, split=1, mode=L.OUT_BF16, a=None, algo=L.ALGO_AUTO, out=None):
     """One launch of the FP8 GEMV kernel on bf16 activations quantized inside the kernel:
     per token (M == 1, a is None) or with the inverse scale of an ActScale / SharedScale a."""
@@ -256,6 +284,14 @@ def _activation_fp8(x, a, xs):
     return x8, s.reshape(-1)
 
 
+def _tiled_rows(x, a, xs, algo):
+    """bf16 rows scaled per token at 1 < M <= 32 go through quant_rows_tiled and the GEMV on tiled
+    activations (the same operands as quant_rows + the row-major e4m3 GEMV, contiguous loads)."""
+    M, K = x.shape
+    return (xs is None and a is None and x.dtype == torch.bfloat16 and 1 < M <= DECODE_MAX_ROWS
+            and K % 64 == 0 and algo != L.ALGO_VALU)
+
+
 def _chunked(x8, xs, fn):
     M = x8.shape[0]
     if M <= DECODE_MAX_ROWS:
@@ -278,6 +314,9 @@ def gemv_fp8(x, q, split=1, a=None, xs=None, algo=L.ALGO_AUTO):
     mode = L.OUT_BF16 if split == 1 else L.OUT_PARTIAL
     if xs is None and _fits_fused(x, split, a):
         return gemv_fp8_bf16_launch(x, q, split, mode, a, algo)
+    if _tiled_rows(x, a, xs, algo):
+        x8t, s = quant_rows_tiled(x)
+        return gemv_fp8_tiled_launch(x8t, s, q, M, split, mode)
     x8, s = _activation_fp8(x, a, xs)
     return _chunked(x8, s, lambda xc, sc: gemv_fp8_launch(xc, sc, q, split, mode, algo))
 
@@ -288,6 +327,9 @@ def gemv_swiglu_fp8(x, q, a=None, xs=None, algo=L.ALGO_AUTO):
     reference's experiments/modal_fp8.py:67."""
     if xs is None and _fits_fused(x, 1, a):
         return gemv_fp8_bf16_launch(x, q, 1, L.OUT_SWIGLU, a, algo)
+    if _tiled_rows(x, a, xs, algo):
+        x8t, s = quant_rows_tiled(x)
+        return gemv_fp8_tiled_launch(x8t, s, q, x.shape[0], 1, L.OUT_SWIGLU)
     x8, s = _activation_fp8(x, a, xs)
     return _chunked(x8, s, lambda xc, sc: gemv_fp8_launch(xc, sc, q, 1, L.OUT_SWIGLU, algo))
 

@@ -56,6 +56,11 @@ def test_invalid_arguments_fail_before_any_launch():
     # split > 1 without the partials output
     rc = lib.krq_gemv_bf16(p, p, 0, 1, 64, 256, 2, 0, p, _null())
     assert rc == L.KRQ_EINVAL
+    # tiled activations take the matrix-core kernel; their quantizer needs K % 64 == 0
+    rc = lib.krq_gemv_fp8(p, L.X_FP8_TILED, p, None, 0, p, 1, p, 1, 1, 64, 256, 1, 0, 2, p, _null())
+    assert rc == L.KRQ_EINVAL and b"tiled activations" in lib.krq_last_error()
+    rc = lib.krq_quant_rows_tiled(p, 16, 100, p, p, _null())
+    assert rc == L.KRQ_EINVAL and b"K=100" in lib.krq_last_error()
     # null pointers
     rc = lib.krq_quant_fp8_rows(None, 16, 64, 64, p, None, p, _null())
     assert rc == L.KRQ_EINVAL

@@ -483,6 +483,54 @@ def test_dynamic_quant_rounds_overshoot_to_448(dev, algo):
             assert torch.equal(fused, fp8.gemv_fp8_launch(x8, xs, q, split, mode, algo)), split
 
 
+@pytest.mark.parametrize("M", [1, 2, 5, 16, 17, 32])
+@pytest.mark.parametrize("K", [64, 2560, 9728])
+def test_quant_rows_tiled(dev, M, K):
+    """quant_rows_tiled writes quant_rows' bytes in the tiled activation layout: the oracle's rows,
+    padded with zero rows to a multiple of 16, through the weights' tiling (O.tile), bit for bit;
+    the scales equal quant_rows'."""
+    x = act(M, K, 300 + M + K)
+    x8t, xs = fp8.quant_rows_tiled(x.to(dev))
+    r8, rs = O.quant_rows(u16(x))
+    mp = (M + 15) // 16 * 16
+    pad = np.zeros((mp, K), dtype=np.uint8)
+    pad[:M] = r8
+    assert np.array_equal(x8t.cpu().numpy(), O.tile(pad).reshape(-1))
+    assert np.array_equal(xs.cpu().numpy().reshape(-1), rs.reshape(-1))
+
+
+TILED_SHAPES = {"qkv": (QKV, (1, 2)), "o": (O_PROJ, (4,)), "down": (DOWN, (4,)), "small": ((64, 384), (1, 2))}
+
+
+@pytest.mark.parametrize("name", list(TILED_SHAPES))
+@pytest.mark.parametrize("M", [2, 5, 16, 17, 32])
+def test_gemv_on_tiled_activations(dev, name, M):
+    """The FP8 GEMV reading tiled activations (quant_rows_tiled) equals the GEMV reading the same
+    e4m3 rows row-major (quant_rows) bit for bit: the same operands through the same launch plan;
+    gemv_fp8 takes this path for bf16 rows at 1 < M <= 32, and it meets the parity bar."""
+    (N, K), splits = TILED_SHAPES[name]
+    w, x = _fp8_case(N, K, M, 80 + SEEDS[name])
+    q = fp8.quantize(w.to(dev))
+    xd = x.to(dev)
+    x8, xs = fp8.quant_rows(xd)
+    x8t, xst = fp8.quant_rows_tiled(xd)
+    r8, rs = O.quantize(u16(w))
+    x8r, xsr = O.quant_rows(u16(x))
+    _, yref = O.fp8_matmul(x8r, xsr, r8, rs)
+    for split in splits:
+        mode = L.OUT_BF16 if split == 1 else L.OUT_PARTIAL
+        t = fp8.gemv_fp8_tiled_launch(x8t, xst, q, M, split, mode)
+        r = fp8.gemv_fp8_launch(x8, xs, q, split, mode)
+        assert torch.equal(t, r), (name, M, split)
+        y = fp8.gemv_fp8(xd, q, split)
+        assert torch.equal(y, t), (name, M, split)
+        f = t.float().cpu().numpy() if split == 1 else _sum_partials(t)
+        assert rel_err(f, yref) <= TOL, (name, M, split)
+    qs = fp8.quantize(weight(2 * 1024, K, 81).to(dev))
+    sw = fp8.gemv_swiglu_fp8(xd, qs)
+    assert torch.equal(sw, fp8.gemv_fp8_launch(x8, xs, qs, 1, L.OUT_SWIGLU)), (name, M)
+
+
 @pytest.mark.parametrize("M", [1, 4, 16])
 def test_fused_static_quant_matches_cast_path(dev, M):
     N, K = O_PROJ
