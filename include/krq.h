@@ -240,6 +240,10 @@ int64_t krq_gemv_fp8_fused_fits(int64_t M, int64_t N, int64_t K, int split, int 
  * krq_quant_rows applied to krq_rmsnorm_rows' output (K <= 16384). */
 int krq_rmsnorm_quant_rows(const void* x, const float* ss_in, const void* ln, float eps, int64_t M,
                            int64_t K, void* x8, float* x_scale, void* stream);
+/* The same with x8 in the tiled activation layout of krq_quant_rows_tiled (16 * ceil(M / 16) rows,
+ * pad rows zero; K % 64 == 0), read by the GEMVs as KRQ_X_FP8_TILED. */
+int krq_rmsnorm_quant_rows_tiled(const void* x, const float* ss_in, const void* ln, float eps, int64_t M,
+                                 int64_t K, void* x8_tiled, float* x_scale, void* stream);
 
 /*
  * FP8 prefill GEMM (M > 32): out bf16 [M, N] = bf16((x8 . w8^T) * x_scale[m or 0] * w_scale[n or 0]),

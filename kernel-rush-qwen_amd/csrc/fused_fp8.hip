@@ -23,16 +23,26 @@ constexpr size_t kMaxSmem = 60 * 1024;
 constexpr int64_t kNormStageMax = 24 * 1024;
 
 // RMSNorm + per-token e4m3 quantization of whole rows (one block per row): x8 = e4m3(h * inv),
-// xs = amax(h) / 448 with the ActScale arithmetic of quant_rows (amax floored at 1e-6).
-template <int C>
+// xs = amax(h) / 448 with the ActScale arithmetic of quant_rows (amax floored at 1e-6). TILED: x8
+// in the tiled activation layout (tiled_offset), one block per row of the M rows padded to a
+// multiple of 16, the pad rows zero.
+template <int C, bool TILED>
 __global__ __launch_bounds__(kRowThreads) void k_rmsnorm_quant_rows(const uint16_t* __restrict__ x,
                                                                     const float* __restrict__ ss_in,
                                                                     const uint16_t* __restrict__ ln, float eps,
-                                                                    int64_t K, uint8_t* __restrict__ x8,
+                                                                    int64_t M, int64_t K, uint8_t* __restrict__ x8,
                                                                     float* __restrict__ xs) {
   __shared__ float sst[kRowThreads * C / 2];
   __shared__ float rstd_sh;
   const int m = blockIdx.x;
+  if (TILED && m >= M) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int64_t e = 8 * (int64_t)(threadIdx.x + c * kRowThreads);
+      if (e < K) *reinterpret_cast<uint2*>(x8 + tiled_offset(m, e, K)) = make_uint2(0u, 0u);
+    }
+    return;
+  }
   uint4 v[C], lv[C];
   const float rstd = row_prologue<C>(x, ss_in, ln, eps, K, m, sst, &rstd_sh, v, lv);
   float am = 0.0f;
@@ -50,7 +60,7 @@ __global__ __launch_bounds__(kRowThreads) void k_rmsnorm_quant_rows(const uint16
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const int64_t e = 8 * (int64_t)(threadIdx.x + c * kRowThreads);
-    if (e < K) *reinterpret_cast<uint2*>(x8 + m * K + e) = quant8(v[c], iv);
+    if (e < K) *reinterpret_cast<uint2*>(x8 + (TILED ? tiled_offset(m, e, K) : m * K + e)) = quant8(v[c], iv);
   }
 }
 
@@ -65,7 +75,7 @@ void launch(int M, int awc, int u, dim3 grid, int nw, size_t smem, hipStream_t s
   const dim3 block((nw + (awc > 0 ? 1 : 0)) * 64);
   if constexpr (LAYOUT == KRQ_W_TILED) {
     constexpr int DU = MODE == KRQ_OUT_SWIGLU ? kSwiU : kDeepU, MU = MODE == KRQ_OUT_SWIGLU ? kSwiU : kMidU;
-    if constexpr (XK != KRQ_X_FP8) {
+    if constexpr (XK == KRQ_X_BF16_DYN || XK == KRQ_X_BF16_STATIC) {
       if (u > 0 && awc == kAwSmall) {
         if (u == MU)
           hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, MU, NORM, kAwSmall>), grid, block, smem, s,
@@ -88,7 +98,7 @@ void launch(int M, int awc, int u, dim3 grid, int nw, size_t smem, hipStream_t s
       }
     }
   }
-  if constexpr (XK != KRQ_X_FP8) {
+  if constexpr (XK == KRQ_X_BF16_DYN || XK == KRQ_X_BF16_STATIC) {
     if (awc == kAwSmall) {
       hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, 4, NORM, kAwSmall>), grid, block, smem, s,
                          KRQ_FUSED_FP8_ARGS);
@@ -148,7 +158,8 @@ int act_wave_chunks(int64_t M, int64_t K, int64_t ks, int mode, int x_kind, bool
     const char* e = getenv("KRQ_GEMV_AW");
     return !(e && atoi(e) == 0);
   }();
-  if (!aw_ok || M != 1 || x_kind == KRQ_X_FP8 || (mode == KRQ_OUT_SWIGLU && !deep_rings())) return 0;
+  if (!aw_ok || M != 1 || x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED || (mode == KRQ_OUT_SWIGLU && !deep_rings()))
+    return 0;
   if (norm && K > 512 * kAwSmall) return 0;
   const int64_t span = x_kind == KRQ_X_BF16_DYN ? K : ks;
   return span <= 512 * kAwSmall ? kAwSmall : span <= 512 * kAwLarge ? kAwLarge : 0;
@@ -157,7 +168,7 @@ int act_wave_chunks(int64_t M, int64_t K, int64_t ks, int mode, int x_kind, bool
 // Waves and LDS bytes of a fused FP8 launch; false if the prologue's staging does not fit.
 bool plan(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind, bool norm, FusedPlan* out) {
   if (M < 1 || M > 32 || split < 1 || K < 64 || K % split || (K / split) % 64) return false;
-  if (norm && x_kind == KRQ_X_FP8) return false;
+  if (norm && (x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED)) return false;
   if (x_kind == KRQ_X_BF16_DYN && M != 1) return false;
   const int64_t ks = K / split;
   const int P = mode == KRQ_OUT_SWIGLU ? 2 : 1;
@@ -192,7 +203,8 @@ bool plan(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind, bool
   } else {
     nw = min(nw, kMaxThreads / 64 - 1);
   }
-  const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) + (x_kind == KRQ_X_FP8 ? 0 : (size_t)M * ks) +
+  const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) +
+                      (x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED ? 0 : (size_t)M * ks) +
                       (staged_ss ? (size_t)M * (K / 16) * sizeof(float) : 0);
   if (smem > kMaxSmem) return false;
   *out = FusedPlan{nw, awc, u, smem};
@@ -214,7 +226,7 @@ extern "C" int krq_gemv_fp8_fused(const void* x, int x_kind, const float* x_scal
                                   void* res_out, float* ss_out, uint32_t* cnt, void* out, void* stream) {
   KRQ_REQUIRE(x && w8 && w_scale, "gemv_fp8_fused: null pointer");
   KRQ_REQUIRE(aligned16(x) && aligned16(w8), "gemv_fp8_fused: x and w8 must be 16-byte aligned");
-  KRQ_REQUIRE(x_kind >= KRQ_X_FP8 && x_kind <= KRQ_X_BF16_STATIC, "gemv_fp8_fused: bad x_kind %d", x_kind);
+  KRQ_REQUIRE(x_kind >= KRQ_X_FP8 && x_kind <= KRQ_X_FP8_TILED, "gemv_fp8_fused: bad x_kind %d", x_kind);
   KRQ_REQUIRE(x_kind == KRQ_X_BF16_DYN || x_scale, "gemv_fp8_fused: x_scale is required");
   KRQ_REQUIRE(x_kind != KRQ_X_BF16_STATIC || x_inv, "gemv_fp8_fused: x_inv is required");
   KRQ_REQUIRE(M >= 1 && M <= 32, "gemv_fp8_fused: M=%lld outside 1..32", (long long)M);
@@ -231,7 +243,7 @@ extern "C" int krq_gemv_fp8_fused(const void* x, int x_kind, const float* x_scal
   KRQ_REQUIRE(norm || mode == kOutResidual,
               "gemv_fp8_fused: neither RMSNorm (ln) nor the residual epilogue; call krq_gemv_fp8");
   KRQ_REQUIRE(!(norm && mode == kOutResidual), "gemv_fp8_fused: RMSNorm and the residual epilogue in one call");
-  KRQ_REQUIRE(!norm || (ss_in && aligned16(ln) && aligned16(ss_in) && x_kind != KRQ_X_FP8),
+  KRQ_REQUIRE(!norm || (ss_in && aligned16(ln) && aligned16(ss_in) && x_kind != KRQ_X_FP8 && x_kind != KRQ_X_FP8_TILED),
               "gemv_fp8_fused: RMSNorm needs bf16 activations, ss_in and aligned ln / ss_in");
   KRQ_REQUIRE(mode != kOutResidual || (res_in && res_out && ss_out && (split == 1 || (cnt && out))),
               "gemv_fp8_fused: the residual epilogue needs res_in, res_out, ss_out and, for split > 1, "
@@ -257,6 +269,7 @@ extern "C" int krq_gemv_fp8_fused(const void* x, int x_kind, const float* x_scal
                                 w_per_row, m, NO, K, kts, out, fa)
   if (mode == kOutResidual) {
     if (x_kind == KRQ_X_FP8) KRQ_CASE(kOutResidual, KRQ_X_FP8, false);
+    else if (x_kind == KRQ_X_FP8_TILED) KRQ_CASE(kOutResidual, KRQ_X_FP8_TILED, false);
     else if (x_kind == KRQ_X_BF16_DYN) KRQ_CASE(kOutResidual, KRQ_X_BF16_DYN, false);
     else KRQ_CASE(kOutResidual, KRQ_X_BF16_STATIC, false);
   } else if (x_kind == KRQ_X_BF16_DYN) {
@@ -279,8 +292,23 @@ extern "C" int krq_rmsnorm_quant_rows(const void* x, const float* ss_in, const v
   KRQ_REQUIRE(M >= 1 && M <= 0x7fffffff && K > 0 && K % 16 == 0 && K <= kRowMaxK,
               "rmsnorm_quant_rows: bad shape M=%lld K=%lld (K a multiple of 16, at most %d)", (long long)M,
               (long long)K, kRowMaxK);
-  hipLaunchKernelGGL(K <= kRowSmallK ? k_rmsnorm_quant_rows<2> : k_rmsnorm_quant_rows<kRowChunks>,
+  hipLaunchKernelGGL((K <= kRowSmallK ? k_rmsnorm_quant_rows<2, false> : k_rmsnorm_quant_rows<kRowChunks, false>),
                      dim3(static_cast<unsigned>(M)), dim3(kRowThreads), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, ss_in, (const uint16_t*)ln, eps, K, (uint8_t*)x8, x_scale);
+                     (const uint16_t*)x, ss_in, (const uint16_t*)ln, eps, M, K, (uint8_t*)x8, x_scale);
   return krq_check_launch("rmsnorm_quant_rows");
+}
+
+extern "C" int krq_rmsnorm_quant_rows_tiled(const void* x, const float* ss_in, const void* ln, float eps, int64_t M,
+                                      int64_t K, void* x8, float* x_scale, void* stream) {
+  KRQ_REQUIRE(x && ss_in && ln && x8 && x_scale, "rmsnorm_quant_rows_tiled: null pointer");
+  KRQ_REQUIRE(aligned16(x) && aligned16(ln) && aligned16(x8), "rmsnorm_quant_rows_tiled: x, ln and x8 must be 16-byte aligned");
+  KRQ_REQUIRE(M >= 1 && M <= 0x7fffffff && K > 0 && K % 16 == 0 && K <= kRowMaxK,
+              "rmsnorm_quant_rows_tiled: bad shape M=%lld K=%lld (K a multiple of 16, at most %d)", (long long)M,
+              (long long)K, kRowMaxK);
+  KRQ_REQUIRE(K % 64 == 0, "rmsnorm_quant_rows_tiled: K=%lld must be a multiple of 64", (long long)K);
+  const int64_t mp = (M + 15) / 16 * 16;  // rows padded to whole 16-row tiles
+  hipLaunchKernelGGL((K <= kRowSmallK ? k_rmsnorm_quant_rows<2, true> : k_rmsnorm_quant_rows<kRowChunks, true>),
+                     dim3(static_cast<unsigned>(mp)), dim3(kRowThreads), 0, (hipStream_t)stream,
+                     (const uint16_t*)x, ss_in, (const uint16_t*)ln, eps, M, K, (uint8_t*)x8, x_scale);
+  return krq_check_launch("rmsnorm_quant_rows_tiled");
 }

@@ -48,6 +48,7 @@ EXPORTS = {
                                   _i32, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "krq_gemv_fp8_fused_fits": (_i64, [_i64, _i64, _i64, _i32, _i32, _i32, _i32]),
     "krq_rmsnorm_quant_rows": (_i32, [_vp, _vp, _vp, _f32, _i64, _i64, _vp, _vp, _vp]),
+    "krq_rmsnorm_quant_rows_tiled": (_i32, [_vp, _vp, _vp, _f32, _i64, _i64, _vp, _vp, _vp]),
     "krq_gemm_fp8": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64, _vp, _vp]),
     "krq_pack_fp8": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "krq_unpack_fp8": (_i32, [_vp, _i64, _i64, _vp, _vp]),

@@ -135,7 +135,15 @@ def _launch_fp8(x, q, split, mode, norm, ep, eps, a, out):
     kind = L.X_BF16_STATIC if a is not None else L.X_BF16_DYN
     if not fits(M, N, K, split, mode, kind, 1 if norm is not None else 0):
         # stage outside: normalize (and quantize) the rows first, then e4m3 activations
+        # (per-token scales: the rows in the tiled activation layout, read as one KiB per operand)
+        tiled = a is None and K % 64 == 0
         if norm is not None:
+            if tiled:
+                x8 = torch.empty(((M + 15) // 16 * 16 * K,), device=x.device, dtype=torch.uint8)
+                xs = torch.empty((M,), device=x.device, dtype=torch.float32)
+                L.call("krq_rmsnorm_quant_rows_tiled", L.ptr(x), L.ptr(ss), L.ptr(ln), float(eps), M, K,
+                       L.ptr(x8), L.ptr(xs), L.stream(x))
+                return _fp8.gemv_fp8_tiled_launch(x8, xs, q, M, split, mode, out)
             if a is None:
                 x8 = torch.empty((M, K), device=x.device, dtype=torch.float8_e4m3fn)
                 xs = torch.empty((M,), device=x.device, dtype=torch.float32)
@@ -144,8 +152,12 @@ def _launch_fp8(x, q, split, mode, norm, ep, eps, a, out):
             else:
                 x8, xs = _fp8._cast(_rmsnorm(x, ln, ss, eps), a), a.scale.reshape(1)
             return _fp8.gemv_fp8_launch(x8, xs, q, split, mode, L.ALGO_MFMA, out)
-        x8, xs = _fp8._activation_fp8(x, a, None)
-        kind, xin, x_scale, x_inv = L.X_FP8, x8, xs, None
+        if tiled:
+            x8, xs = _fp8.quant_rows_tiled(x)
+            kind, xin, x_scale, x_inv = L.X_FP8_TILED, x8, xs.reshape(-1), None
+        else:
+            x8, xs = _fp8._activation_fp8(x, a, None)
+            kind, xin, x_scale, x_inv = L.X_FP8, x8, xs, None
     elif a is not None:
         xin, x_scale, x_inv = x, a.scale.reshape(1), a.inv.reshape(1)
     else:

@@ -264,6 +264,28 @@ def test_rmsnorm_quant_rows_is_quant_rows_of_rmsnorm(dev, M, K):
     assert np.mean(got != want) < 0.05
 
 
+@pytest.mark.parametrize("M,K", [(1, H), (3, H), (17, H), (2, I), (5, 16384)])
+def test_rmsnorm_quant_rows_tiled(dev, M, K):
+    """krq_rmsnorm_quant_rows_tiled writes krq_rmsnorm_quant_rows' bytes in the tiled activation
+    layout: the rows, padded with zero rows to a multiple of 16, through the weights' tiling
+    (O.tile), bit for bit, with the same scales."""
+    from kernels import _lib as L
+    x, ln, ss, _ = _norm_inputs(M, K, 90 + M)
+    xd, lnd, ssd = x.to(dev), ln.to(dev), torch.from_numpy(ss).to(dev)
+    x8 = torch.empty((M, K), device=dev, dtype=torch.float8_e4m3fn)
+    xs = torch.empty((M,), device=dev, dtype=torch.float32)
+    L.call("krq_rmsnorm_quant_rows", L.ptr(xd), L.ptr(ssd), L.ptr(lnd), EPS, M, K, L.ptr(x8), L.ptr(xs), L.stream(xd))
+    mp = (M + 15) // 16 * 16
+    x8t = torch.empty((mp * K,), device=dev, dtype=torch.uint8)
+    xst = torch.empty((M,), device=dev, dtype=torch.float32)
+    L.call("krq_rmsnorm_quant_rows_tiled", L.ptr(xd), L.ptr(ssd), L.ptr(lnd), EPS, M, K, L.ptr(x8t), L.ptr(xst),
+           L.stream(xd))
+    pad = np.zeros((mp, K), dtype=np.uint8)
+    pad[:M] = x8.view(torch.uint8).cpu().numpy()
+    assert np.array_equal(x8t.cpu().numpy(), O.tile(pad).reshape(-1))
+    assert torch.equal(xst, xs)
+
+
 @pytest.mark.parametrize("M,N,split,swiglu", [(1, NQKV, 2, False), (4, NQKV, 2, False), (4, 2 * I, 1, True),
                                               (16, NQKV, 2, False), (32, 2 * I, 1, True)])
 def test_fp8_rmsnorm_prologue_static_scale(dev, M, N, split, swiglu):
