@@ -53,6 +53,7 @@ extern "C" {
 /* lm-head weight kinds */
 #define KRQ_LM_BF16 0
 #define KRQ_LM_FP8 1
+#define KRQ_LM_FP8_TILED_H 2  /* FP8 weights, h e4m3 in the tiled activation layout */
 
 /*
  * Per-output-channel weight quantizer. Replaces the weight-packing step of engine loading
@@ -155,6 +156,9 @@ int krq_gemv_bf16(const void* x, const void* w, int w_layout, int64_t M, int64_t
  * w_kind KRQ_LM_FP8:  w e4m3 [V,K] in w_layout with per-row w_scale[V]; h e4m3 [M,K] with
  *                     per-token h_scale[M], or (h_scale NULL, M == 1) h bf16 [1,K] scaled per
  *                     token inside the kernel; logits as krq_gemv_fp8 KRQ_OUT_BF16.
+ * w_kind KRQ_LM_FP8_TILED_H: as KRQ_LM_FP8 with h e4m3 in the tiled activation layout of
+ *                     krq_quant_rows_tiled and its h_scale[M] (no reference counterpart: the same
+ *                     operands, contiguous loads).
  * logits: optional bf16 [M,V] output (NULL to skip). ws: scratch of at least
  * krq_lmhead_ws_bytes(M, V) bytes (overwritten; calls that overlap must not share it).
  */

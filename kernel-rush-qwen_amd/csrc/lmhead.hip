@@ -59,7 +59,9 @@ extern "C" int krq_lmhead_argmax(const void* h, const float* h_scale, const void
                                  void* stream) {
   KRQ_REQUIRE(h && w && ws && idx_out, "lmhead_argmax: null pointer");
   KRQ_REQUIRE(M >= 1 && M <= 32, "lmhead_argmax: M=%lld outside 1..32", (long long)M);
-  KRQ_REQUIRE(w_kind == KRQ_LM_BF16 || w_kind == KRQ_LM_FP8, "lmhead_argmax: bad weight kind %d", w_kind);
+  KRQ_REQUIRE(w_kind == KRQ_LM_BF16 || w_kind == KRQ_LM_FP8 || w_kind == KRQ_LM_FP8_TILED_H,
+              "lmhead_argmax: bad weight kind %d", w_kind);
+  KRQ_REQUIRE(w_kind != KRQ_LM_FP8_TILED_H || h_scale, "lmhead_argmax: tiled e4m3 h needs h_scale");
   KRQ_REQUIRE(w_layout == KRQ_W_ROWMAJOR || w_layout == KRQ_W_TILED, "lmhead_argmax: bad layout %d", w_layout);
   KRQ_REQUIRE(w_kind == KRQ_LM_BF16 || w_scale, "lmhead_argmax: FP8 weights need w_scale");
   KRQ_REQUIRE(w_kind == KRQ_LM_BF16 || h_scale || M == 1,
@@ -72,8 +74,8 @@ extern "C" int krq_lmhead_argmax(const void* h, const float* h_scale, const void
   if (w_kind == KRQ_LM_BF16)
     rc = gemv_bf16_run(h, w, w_layout, M, V, K, 1, kOutArgmax, logits, ws, stream);
   else if (h_scale)
-    rc = gemv_fp8_run(h, KRQ_X_FP8, h_scale, nullptr, M > 1, w, w_layout, w_scale, 1, M, V, K, 1,
-                      kOutArgmax, 0, logits, ws, stream);
+    rc = gemv_fp8_run(h, w_kind == KRQ_LM_FP8_TILED_H ? KRQ_X_FP8_TILED : KRQ_X_FP8, h_scale, nullptr, M > 1, w,
+                      w_layout, w_scale, 1, M, V, K, 1, kOutArgmax, 0, logits, ws, stream);
   else
     rc = gemv_fp8_run(h, KRQ_X_BF16_DYN, nullptr, nullptr, 0, w, w_layout, w_scale, 1, M, V, K, 1,
                       kOutArgmax, 0, logits, ws, stream);

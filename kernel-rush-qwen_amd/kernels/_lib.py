@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkrq.so")
 KRQ_OK, KRQ_EINVAL, KRQ_EHIP = 0, -1, -2
 OUT_BF16, OUT_PARTIAL, OUT_SWIGLU, OUT_RESIDUAL = 0, 1, 2, 4
 W_ROWMAJOR, W_TILED = 0, 1
-LM_BF16, LM_FP8 = 0, 1
+LM_BF16, LM_FP8, LM_FP8_TILED_H = 0, 1, 2
 ALGO_AUTO, ALGO_MFMA, ALGO_VALU = 0, 1, 2
 X_FP8, X_BF16_DYN, X_BF16_STATIC, X_FP8_TILED = 0, 1, 2, 3
 

@@ -3,8 +3,8 @@
 Reference semantics: logits = gemv(h, lm_head, 1) (bf16) then torch.argmax(logits, -1)
 (engine/engine.py:1021-1022), i.e. the lowest index among the largest bf16-rounded logits; the
 reference's fused form keeps the same rule (engine/kernels/mega.py:412-436). The FP8 variant
-scales activations per token (inside the GEMV at M == 1, else fp8.quant_rows) and uses
-per-channel weights (fp8.quantize).
+scales activations per token (inside the GEMV at M == 1, else fp8.quant_rows_tiled, the rows in
+the tiled activation layout) and uses per-channel weights (fp8.quantize).
 """
 
 import torch
@@ -14,10 +14,11 @@ from . import fp8 as _fp8
 from . import gemv as _gemv
 
 
-def lm_head_argmax(h, w, return_logits=False):
+def lm_head_argmax(h, w, return_logits=False, h_layout="tiled"):
     """h [M, K] bf16 (M <= 32); w the tied embedding, bf16 [V, K], or an FP8Weight from
     fp8.quantize (per-channel scales). Returns int64 [M] token ids, or (ids, bf16 logits [M, V])
-    with return_logits=True."""
+    with return_logits=True. h_layout ("tiled" or "rowmajor"): how the FP8 head's quantized rows
+    are laid out at M > 1 (the same operands either way; tiled loads are contiguous)."""
     L.require_device(h)
     M, K = h.shape
     if isinstance(w, tuple):
@@ -28,6 +29,9 @@ def lm_head_argmax(h, w, return_logits=False):
             raise ValueError("the FP8 lm head needs per-channel scales (fp8.quantize)")
         if M == 1:   # per-token scale computed inside the GEMV
             hin, hsc, wk = _fp8._rows(h), None, L.LM_FP8
+        elif K % 64 == 0 and h_layout == "tiled":  # e4m3 rows in the tiled activation layout
+            h8, hs = _fp8.quant_rows_tiled(h)
+            hin, hsc, wk = h8, hs.reshape(-1), L.LM_FP8_TILED_H
         else:
             h8, hs = _fp8.quant_rows(h)
             hin, hsc, wk = h8, hs.reshape(-1), L.LM_FP8

@@ -375,6 +375,9 @@ def test_lmhead_fp8_argmax(dev, M):
     ref_idx = O.argmax_lowest(O.round_bf16(ref.astype(np.float32)))
     assert rel_err(lg, ref) <= TOL
     assert np.array_equal(idx, ref_idx)
+    if M > 1:  # tiled e4m3 rows (the default) and row-major ones: the same logits, bit for bit
+        idx_r, logits_r = lmhead.lm_head_argmax(h.to(dev), q, return_logits=True, h_layout="rowmajor")
+        assert torch.equal(logits_r, logits) and np.array_equal(idx_r.cpu().numpy(), idx)
 
 
 def test_lmhead_ties_lowest_index(dev):
