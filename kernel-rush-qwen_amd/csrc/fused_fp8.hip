@@ -22,46 +22,93 @@ constexpr size_t kMaxSmem = 60 * 1024;
 // largest bf16 x slice (bytes) a block normalizes in its prologue (as in fused_gemv.hip)
 constexpr int64_t kNormStageMax = 24 * 1024;
 
-// RMSNorm + per-token e4m3 quantization of whole rows (one block per row): x8 = e4m3(h * inv),
-// xs = amax(h) / 448 with the ActScale arithmetic of quant_rows (amax floored at 1e-6). TILED: x8
-// in the tiled activation layout (tiled_offset), one block per row of the M rows padded to a
-// multiple of 16, the pad rows zero.
-template <int C, bool TILED>
-__global__ __launch_bounds__(kRowThreads) void k_rmsnorm_quant_rows(const uint16_t* __restrict__ x,
-                                                                    const float* __restrict__ ss_in,
-                                                                    const uint16_t* __restrict__ ln, float eps,
-                                                                    int64_t M, int64_t K, uint8_t* __restrict__ x8,
-                                                                    float* __restrict__ xs) {
-  __shared__ float sst[kRowThreads * C / 2];
-  __shared__ float rstd_sh;
-  const int m = blockIdx.x;
+// RMSNorm + per-token e4m3 quantization of whole rows (one block of NT threads per row, K % 16 == 0,
+// K <= kRowMaxK): x8 = e4m3(h * inv), xs = amax(h) / 448 with the ActScale arithmetic of quant_rows
+// (amax floored at 1e-6), h = RMSNorm(x) * ln as every normalizing kernel computes it. Each wave
+// sums the row's sum-of-squares partials itself in the canonical order (lane l takes t = l, l + 64,
+// ..., SC per lane) instead of staging them in LDS, each thread holds 16-value pieces (two 16-byte
+// loads of x and of ln, one 16-byte store), and the amax is DPP wave maxima and one barrier.
+// Measured on MI355X (fused FP8 layer, M = 16, against 256 threads of 8-value chunks with the
+// partials staged in LDS and four barriers): gate_up + RMSNorm 15.01 -> 14.90 us, QKV + RMSNorm
+// 9.29 -> 9.09 us. TILED: x8 in the tiled activation layout (tiled_offset), one block per row of
+// the M rows padded to a multiple of 16, the pad rows zero.
+constexpr int kNqThreads = 512;
+template <int NT, int SC, bool TILED>
+__global__ __launch_bounds__(NT) void k_rmsnorm_quant_rows(const uint16_t* __restrict__ x,
+                                                           const float* __restrict__ ss_in,
+                                                           const uint16_t* __restrict__ ln, float eps,
+                                                           int64_t M, int64_t K, uint8_t* __restrict__ x8,
+                                                           float* __restrict__ xs) {
+  constexpr int C = kRowMaxK / 16 / NT;
+  __shared__ float red[NT / 64];
+  const int64_t m = blockIdx.x;
   if (TILED && m >= M) {
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-      const int64_t e = 8 * (int64_t)(threadIdx.x + c * kRowThreads);
-      if (e < K) *reinterpret_cast<uint2*>(x8 + tiled_offset(m, e, K)) = make_uint2(0u, 0u);
+      const int64_t e = 16 * (int64_t)(threadIdx.x + c * NT);
+      if (e < K) *reinterpret_cast<uint4*>(x8 + tiled_offset(m, e, K)) = zero4();
     }
     return;
   }
-  uint4 v[C], lv[C];
-  const float rstd = row_prologue<C>(x, ss_in, ln, eps, K, m, sst, &rstd_sh, v, lv);
+  const int lane = threadIdx.x & 63;
+  const int T = (int)(K >> 4);
+  const uint8_t* xr = reinterpret_cast<const uint8_t*>(x + m * K);
+  const uint8_t* lr = reinterpret_cast<const uint8_t*>(ln);
+  // every load unconditional, at a clamped address (pieces past K repeat the last piece)
+  uint4 v[C][2], lv[C][2];
+  float sp[SC];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int64_t e = min(16 * (int64_t)(threadIdx.x + c * NT), K - 16);
+    v[c][0] = ld16(xr + 2 * e);
+    v[c][1] = ld16(xr + 2 * e + 16);
+    lv[c][0] = ld16(lr + 2 * e);
+    lv[c][1] = ld16(lr + 2 * e + 16);
+  }
+#pragma unroll
+  for (int j = 0; j < SC; ++j) sp[j] = ss_in[m * T + min(lane + 64 * j, T - 1)];
+  float a = 0.0f;
+#pragma unroll
+  for (int j = 0; j < SC; ++j)
+    if (lane + 64 * j < T) a += sp[j];
+  const float rstd = rstd_of(a, K, eps);
   float am = 0.0f;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
-    if (8 * (int64_t)(threadIdx.x + c * kRowThreads) < K) {
-      v[c] = norm8(v[c], lv[c], rstd);
-      am = absmax8(v[c], am);
-    }
+    v[c][0] = norm8(v[c][0], lv[c][0], rstd);
+    v[c][1] = norm8(v[c][1], lv[c][1], rstd);
+    if (16 * (int64_t)(threadIdx.x + c * NT) < K) am = absmax8(v[c][1], absmax8(v[c][0], am));
   }
-  am = block_max<kRowThreads>(am);
-  const float a = fmaxf(am, 1e-6f);
-  const float iv = inv_from_amax(a);
-  if (threadIdx.x == 0) xs[m] = scale_from_amax(a);
+  am = wave_max_nonneg(am);
+  if (lane == 0) red[threadIdx.x >> 6] = am;
+  __syncthreads();
+  float b = red[0];
+#pragma unroll
+  for (int i = 1; i < NT / 64; ++i) b = fmaxf(b, red[i]);
+  b = fmaxf(b, 1e-6f);
+  const float iv = inv_from_amax(b);
+  if (threadIdx.x == 0) xs[m] = scale_from_amax(b);
 #pragma unroll
   for (int c = 0; c < C; ++c) {
-    const int64_t e = 8 * (int64_t)(threadIdx.x + c * kRowThreads);
-    if (e < K) *reinterpret_cast<uint2*>(x8 + (TILED ? tiled_offset(m, e, K) : m * K + e)) = quant8(v[c], iv);
+    const int64_t e = 16 * (int64_t)(threadIdx.x + c * NT);
+    if (e < K) {
+      const uint2 lo = quant8(v[c][0], iv), hi = quant8(v[c][1], iv);
+      *reinterpret_cast<uint4*>(x8 + (TILED ? tiled_offset(m, e, K) : m * K + e)) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    }
   }
+}
+
+template <bool TILED>
+void launch_rmsnorm_quant(int64_t rows, const void* x, const float* ss_in, const void* ln, float eps, int64_t M,
+                          int64_t K, void* x8, float* x_scale, hipStream_t s) {
+  // SC partials per lane: T = K / 16 <= 64 * SC
+  const dim3 g(static_cast<unsigned>(rows)), b(kNqThreads);
+  if (K <= 4096)
+    hipLaunchKernelGGL((k_rmsnorm_quant_rows<kNqThreads, 4, TILED>), g, b, 0, s, (const uint16_t*)x, ss_in,
+                       (const uint16_t*)ln, eps, M, K, (uint8_t*)x8, x_scale);
+  else
+    hipLaunchKernelGGL((k_rmsnorm_quant_rows<kNqThreads, kRowMaxK / 16 / 64, TILED>), g, b, 0, s,
+                       (const uint16_t*)x, ss_in, (const uint16_t*)ln, eps, M, K, (uint8_t*)x8, x_scale);
 }
 
 #define KRQ_FUSED_FP8_ARGS xb, x_scale, x_inv, x_per_row, wb, w_scale, w_per_row, m, NO, K, kts, out, nullptr, fa
@@ -292,9 +339,7 @@ extern "C" int krq_rmsnorm_quant_rows(const void* x, const float* ss_in, const v
   KRQ_REQUIRE(M >= 1 && M <= 0x7fffffff && K > 0 && K % 16 == 0 && K <= kRowMaxK,
               "rmsnorm_quant_rows: bad shape M=%lld K=%lld (K a multiple of 16, at most %d)", (long long)M,
               (long long)K, kRowMaxK);
-  hipLaunchKernelGGL((K <= kRowSmallK ? k_rmsnorm_quant_rows<2, false> : k_rmsnorm_quant_rows<kRowChunks, false>),
-                     dim3(static_cast<unsigned>(M)), dim3(kRowThreads), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, ss_in, (const uint16_t*)ln, eps, M, K, (uint8_t*)x8, x_scale);
+  launch_rmsnorm_quant<false>(M, x, ss_in, ln, eps, M, K, x8, x_scale, (hipStream_t)stream);
   return krq_check_launch("rmsnorm_quant_rows");
 }
 
@@ -307,8 +352,6 @@ extern "C" int krq_rmsnorm_quant_rows_tiled(const void* x, const float* ss_in, c
               (long long)K, kRowMaxK);
   KRQ_REQUIRE(K % 64 == 0, "rmsnorm_quant_rows_tiled: K=%lld must be a multiple of 64", (long long)K);
   const int64_t mp = (M + 15) / 16 * 16;  // rows padded to whole 16-row tiles
-  hipLaunchKernelGGL((K <= kRowSmallK ? k_rmsnorm_quant_rows<2, true> : k_rmsnorm_quant_rows<kRowChunks, true>),
-                     dim3(static_cast<unsigned>(mp)), dim3(kRowThreads), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, ss_in, (const uint16_t*)ln, eps, M, K, (uint8_t*)x8, x_scale);
+  launch_rmsnorm_quant<true>(mp, x, ss_in, ln, eps, M, K, x8, x_scale, (hipStream_t)stream);
   return krq_check_launch("rmsnorm_quant_rows_tiled");
 }
