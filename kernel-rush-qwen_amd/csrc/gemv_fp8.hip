@@ -23,9 +23,13 @@ int plan_waves(int nsteps, int P, int U, int64_t blocks, bool act_wave) {
   // activation wave (one-row kernel), three instead of two (four waves in all): down 7.68 -> 7.16
   // us and the FP8 lm_head 64.7 -> 63.1 us at M = 1. With the deep rings (U of 8 or 10 beside the
   // activation wave) the same rule gives one wave for up to U steps and two for up to 2U.
+  // Multi-row blocks (two-slot rings) on a grid smaller than the chip (the one-pass residual GEMVs,
+  // 160 blocks) take up to eight waves: O + residual 8.49 -> 7.99 us, down + residual 13.32 ->
+  // 12.29 at M = 16 (at M = 1 four waves stay faster: 6.20 against 7.10 us for O).
   const int w = (nsteps + U - 1) / U;
   if (P != 1) return 2;
   if (w <= 4) return w;
+  if (U == 2 && blocks < kCUs) return min(w, 8);
   if (blocks < 512) return 4;
   return act_wave ? 3 : 2;
 }
