@@ -102,7 +102,10 @@ def test_act_scale_and_cast(dev):
     assert z.amax.item() == np.float32(1e-6)
 
 
-@pytest.mark.parametrize("M,K", [(1, 2560), (16, 9728), (32, 4096), (3, 64)])
+# 512-thread kernel (K % 16 == 0, up to its 16,384 maximum), 8-value chunk kernel (K % 16 == 8),
+# scalar kernel (K % 8 != 0, and rows longer than the vector kernels hold)
+@pytest.mark.parametrize("M,K", [(1, 2560), (16, 9728), (32, 4096), (3, 64), (2, 16384), (2, 200), (3, 100),
+                                 (1, 20000)])
 def test_quant_rows(dev, M, K):
     x = act(M, K, 7 + M)
     x[0, 0] = 0.0
