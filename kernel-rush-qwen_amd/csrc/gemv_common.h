@@ -45,8 +45,13 @@ struct Best {
   int i;
 };
 
-// larger value wins; among equal values the lower index (torch.argmax keeps the first maximum)
-KRQ_DEV bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+// larger value wins; among equal values the lower index (torch.argmax keeps the first maximum);
+// NaN is larger than every number, as in torch.argmax and numpy.argmax
+KRQ_DEV bool better(float v, int i, float bv, int bi) {
+  const bool n = v != v, bn = bv != bv;
+  if (n || bn) return n && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
 
 KRQ_DEV Best shfl_best(Best b, int o) {
   Best r;

@@ -15,35 +15,82 @@ using namespace krq;
 namespace {
 
 constexpr int kFoldThreads = 1024;
+constexpr int kFoldPer = 10;  // candidates per thread per batch (V = 151,936: one batch)
 
+// The candidate (v, i) as one unsigned 64-bit key whose order is better()'s: the high word maps v
+// to an order-preserving integer (NaN above everything, -0 as +0), the low word is ~i (the lower
+// index wins a tie).
+KRQ_DEV uint64_t fold_key(Best b) {
+  uint32_t hi;
+  if (b.v != b.v) {
+    hi = 0xffffffffu;
+  } else {
+    const uint32_t u = b.v == 0.0f ? 0u : __float_as_uint(b.v);
+    hi = (u >> 31) ? ~u : (u | 0x80000000u);
+  }
+  return (static_cast<uint64_t>(hi) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(b.i));
+}
+
+template <int CTRL>
+KRQ_DEV uint64_t dpp_max_u64(uint64_t k) {
+  const uint32_t hi = static_cast<uint32_t>(k >> 32), lo = static_cast<uint32_t>(k);
+  const uint32_t oh = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(hi), CTRL, 0xf, 0xf, false));
+  const uint32_t ol = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(lo), CTRL, 0xf, 0xf, false));
+  const uint64_t o = (static_cast<uint64_t>(oh) << 32) | ol;
+  return o > k ? o : k;
+}
+
+// max of the key over each row of 16 lanes (every lane of the row ends with it)
+KRQ_DEV uint64_t row16_max_u64(uint64_t k) {
+  k = dpp_max_u64<0xB1>(k);   // quad_perm(1,0,3,2): lane ^ 1
+  k = dpp_max_u64<0x4E>(k);   // quad_perm(2,3,0,1): lane ^ 2
+  k = dpp_max_u64<0x141>(k);  // row_half_mirror: the other quad of each 8
+  return dpp_max_u64<0x140>(k);  // row_mirror: the other half of each 16
+}
+
+KRQ_DEV uint64_t readlane_u64(uint64_t k, int l) {
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(k >> 32), l);
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(k), l);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// One block per token row: every candidate load of a batch is issued before the first is used
+// (one memory round trip), the keys are reduced with DPP steps inside each wave and across the
+// block's 16 waves by wave 0.
 __global__ __launch_bounds__(kFoldThreads) void k_argmax_fold(const Best* __restrict__ cand, int64_t nrb,
                                                               int M, int64_t* __restrict__ idx_out) {
-  __shared__ Best wb[kFoldThreads / 64];
-  const int m = blockIdx.x;
-  Best b{-INFINITY, 0x7fffffff};
-  // four independent loads in flight per thread per round
-  for (int64_t rb0 = threadIdx.x; rb0 < nrb; rb0 += 4 * kFoldThreads) {
-    Best c[4];
+  __shared__ uint64_t wk[kFoldThreads / 64];
+  const int m = blockIdx.x, lane = threadIdx.x & 63;
+  uint64_t best = 0;  // below every candidate's key
+  for (int64_t base = 0; base < nrb; base += (int64_t)kFoldPer * kFoldThreads) {
+    Best c[kFoldPer];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t rb = rb0 + (int64_t)q * kFoldThreads;
-      c[q] = rb < nrb ? cand[rb * M + m] : Best{-INFINITY, 0x7fffffff};
+    for (int q = 0; q < kFoldPer; ++q) {
+      const int64_t rb = min(base + threadIdx.x + (int64_t)q * kFoldThreads, nrb - 1);  // clamped, valid
+      c[q] = cand[rb * M + m];
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (better(c[q].v, c[q].i, b.v, b.i)) b = c[q];
+    for (int q = 0; q < kFoldPer; ++q) {
+      const uint64_t k = fold_key(c[q]);
+      if (base + threadIdx.x + (int64_t)q * kFoldThreads < nrb && k > best) best = k;
+    }
   }
+  best = row16_max_u64(best);
+  uint64_t w = readlane_u64(best, 0);
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const Best c = shfl_best(b, o);
-    if (better(c.v, c.i, b.v, b.i)) b = c;
+  for (int l = 16; l < 64; l += 16) {
+    const uint64_t o = readlane_u64(best, l);
+    w = o > w ? o : w;
   }
-  if ((threadIdx.x & 63) == 0) wb[threadIdx.x >> 6] = b;
+  if (lane == 0) wk[threadIdx.x >> 6] = w;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < kFoldThreads / 64; ++w)
-      if (better(wb[w].v, wb[w].i, b.v, b.i)) b = wb[w];
-    idx_out[m] = b.i == 0x7fffffff ? 0 : b.i;
+  if (threadIdx.x < 64) {
+    uint64_t k = wk[lane & (kFoldThreads / 64 - 1)];  // 16 waves: lanes 0..15 of each row
+    k = row16_max_u64(k);
+    if (threadIdx.x == 0) {
+      const uint32_t i = ~static_cast<uint32_t>(k);
+      idx_out[m] = i >= 0x7fffffffu ? 0 : static_cast<int64_t>(i);
+    }
   }
 }
 

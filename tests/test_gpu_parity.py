@@ -393,6 +393,25 @@ def test_lmhead_ties_lowest_index(dev):
     assert idx.tolist() == [17, 17]
 
 
+def test_lmhead_nan_is_max(dev):
+    """torch.argmax (engine.py:1021-1022) and the oracle's numpy argmax take NaN as the maximum and
+    return its first index: a NaN logit row wins over every number; all-NaN logits give index 0."""
+    V, K = 4096, 256
+    E = weight(V, K, 21)
+    for j in (3000, 123):                 # two NaN logit rows
+        E[j, :] = float("nan")
+    h = act(2, K, 22)
+    idx = lmhead.lm_head_argmax(h.to(dev), E.to(dev)).cpu().numpy()
+    ref = O.argmax_lowest(h.float().numpy() @ E.float().numpy().T)
+    assert ref.tolist() == [123, 123] and idx.tolist() == [123, 123]
+    hn = h.clone()
+    hn[1, 7] = float("nan")               # row 1: every logit NaN
+    q = fp8.quantize(weight(V, K, 23).to(dev))
+    idx8 = lmhead.lm_head_argmax(hn.to(dev), q).cpu().numpy()
+    assert idx8[1] == 0
+    assert idx8[0] == lmhead.lm_head_argmax(h.to(dev), q).cpu().numpy()[0]  # row 0 untouched
+
+
 # ---------------------------------------------------------------------------------------------
 # graph replay and determinism
 # ---------------------------------------------------------------------------------------------
