@@ -50,7 +50,9 @@ constexpr int64_t kCUs = 256;  // compute units of the MI355X
 //   KRQ_X_BF16_STATIC (M = 1): loads the slice and quantizes it with the given inverse scale.
 // NORM: the loaded chunks are first normalized, h = bf16(bf16(x * rstd) * w_ln), with rstd from the
 // row's sum-of-squares partials in the canonical order (K <= 4096: T = K / 16 <= 64 * kSsPerLane).
-template <int XK, int AWC, bool NORM>
+// ORDER: the wave meets the weight waves at a bare s_barrier (no fence, no wait) once all of its
+// loads are issued, and the weight waves issue their ring only after it; see gemv_fp8_body.
+template <int XK, int AWC, bool NORM, bool ORDER>
 KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restrict__ xsc,
                              const float* __restrict__ xinv, int64_t K, int64_t k0, int ks, int lane,
                              uint8_t* xq, float* xs_l, const FusedArgs& fa) {
@@ -82,6 +84,7 @@ KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restr
     if (lane == 0) xs_l[0] = xsc[0];
   }
   __builtin_amdgcn_sched_barrier(0);  // every row load in flight before the first wait
+  if constexpr (ORDER) __builtin_amdgcn_s_barrier();
   if (NORM) {
     float a = 0.0f;
 #pragma unroll
@@ -137,6 +140,13 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   constexpr bool XT = XK == KRQ_X_FP8_TILED;
   constexpr bool FUSED = XK != KRQ_X_FP8 && !XT;  // bf16 activations quantized into LDS
   constexpr int SC = XK == KRQ_X_BF16_DYN ? kSsPerLane : kSsChunks;
+  // Load order of the RMSNorm activation wave beside a single-matrix ring: the CU returns loads in
+  // issue order, so the wave's row, RMSNorm-weight and partials loads, issued while the weight wave
+  // issues its ring, land only after most of it. Making the weight waves issue after the activation wave's loads
+  // (one bare barrier) took the M = 1 QKV + RMSNorm launch from 6.58 to 5.22 us; the plain one-row
+  // kernels (row loads only: QKV 4.71 -> 5.01 us) and the two-round SwiGLU block (gate_up +
+  // RMSNorm 10.5 -> 10.75 us) measured slower with it, so they keep issuing at once.
+  constexpr bool ORDER = AWC > 0 && NORM && MODE != KRQ_OUT_SWIGLU;
   // nw = the waves that stream weights (all but the activation wave)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x >> 6) - (AW ? 1 : 0);
   const int r = lane & 15, g = lane >> 4;
@@ -187,7 +197,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
 
   // (wave index read as a scalar: the compiler then knows the branch is uniform per wave)
   if (AW && __builtin_amdgcn_readfirstlane(wave) == nw) {
-    activation_wave<XK, AW ? AWC : 1, NORM>(x, xsc, xinv, K, k0, ks, lane, xq, xs_l, fa);
+    activation_wave<XK, AW ? AWC : 1, NORM, ORDER>(x, xsc, xinv, K, k0, ks, lane, xq, xs_l, fa);
     __syncthreads();  // the slice and its scale are in LDS
   } else {
   // scale of this thread's activation row, read now so its latency hides under the weight stream
@@ -197,6 +207,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   const float xs_reg = XK != KRQ_X_BF16_DYN && !AW ? xsc[x_per_row ? xrow : 0] : 1.0f;
 
   // ---- weight (and, for e4m3 activations, A operand) loads: a ring of U step slots ----
+  if constexpr (ORDER) __builtin_amdgcn_s_barrier();  // the activation wave's loads are issued
   uint4 wl[U], wh[U], ul[U], uh[U], xl[U][MT], xh[U][MT];
   // A slot past this wave's last step reloads that step (an address already in flight or cached,
   // so no extra HBM traffic) and is masked where consumed. Rows m >= M read row M - 1: their
