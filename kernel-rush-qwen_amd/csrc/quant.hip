@@ -259,9 +259,9 @@ __global__ __launch_bounds__(kQT) void k_act_rows_vec(const uint16_t* __restrict
 // 16-byte store), the row amax as DPP wave maxima and one barrier, 512 threads. Measured on MI355X
 // (graph of 72 launches, M = 16; K = 2,560 / 4,096 / 9,728): 2.47 / 2.54 / 3.11 us against 2.87 /
 // 2.90 / 3.64 for k_act_rows_vec (256 threads, 8-value pieces, shuffle reductions, two barriers);
-// 256 and 1,024 threads measured slower. TILED: x8 in the tiled
-// activation layout (tiled_offset, the weights' tiling), one block per row of the M rows padded to a
-// multiple of 16, the pad rows written as zeros.
+// 256 and 1,024 threads measured slower. TILED: x8 in the tiled activation layout (tiled_offset,
+// the weights' tiling), one block per row of the M rows padded to a multiple of 16, the pad rows
+// written as zeros.
 constexpr int kRowNT = 512;
 template <int NT, bool TILED>
 __global__ __launch_bounds__(NT) void k_act_rows_fast(const uint16_t* __restrict__ x, int64_t M, int64_t K,
