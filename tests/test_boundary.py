@@ -61,6 +61,13 @@ def test_invalid_arguments_fail_before_any_launch():
     assert rc == L.KRQ_EINVAL and b"tiled activations" in lib.krq_last_error()
     rc = lib.krq_quant_rows_tiled(p, 16, 100, p, p, _null())
     assert rc == L.KRQ_EINVAL and b"K=100" in lib.krq_last_error()
+    rc = lib.krq_quant_rows_tiled(p, 16, 16384 + 64, p, p, _null())
+    assert rc == L.KRQ_EINVAL and b"K at most 16384" in lib.krq_last_error()
+    rc = lib.krq_rmsnorm_quant_rows_tiled(p, p, p, 1e-6, 2, 2576, p, p, _null())
+    assert rc == L.KRQ_EINVAL and b"multiple of 64" in lib.krq_last_error()
+    # the tiled e4m3 lm_head rows need their per-row scales
+    rc = lib.krq_lmhead_argmax(p, None, p, L.LM_FP8_TILED_H, 1, p, 16, 1024, 256, None, p, 1 << 20, p, _null())
+    assert rc == L.KRQ_EINVAL and b"h_scale" in lib.krq_last_error()
     # null pointers
     rc = lib.krq_quant_fp8_rows(None, 16, 64, 64, p, None, p, _null())
     assert rc == L.KRQ_EINVAL
