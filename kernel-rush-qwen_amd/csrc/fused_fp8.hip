@@ -12,8 +12,6 @@
 // The kernel template is gemv_fp8_kernel.h's; the fused variants always use the matrix cores.
 #include "gemv_fp8_kernel.h"
 
-#include <stdlib.h>
-
 using namespace krq;
 
 namespace {
@@ -40,7 +38,7 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_quant_rows(const uint16_t* __res
                                                            int64_t M, int64_t K, uint8_t* __restrict__ x8,
                                                            float* __restrict__ xs) {
   constexpr int C = kRowMaxK / 16 / NT;
-  __shared__ float red[NT / 64];
+  __shared__ uint32_t red[NT / 64];
   const int64_t m = blockIdx.x;
   if (TILED && m >= M) {
 #pragma unroll
@@ -72,20 +70,19 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_quant_rows(const uint16_t* __res
   for (int j = 0; j < SC; ++j)
     if (lane + 64 * j < T) a += sp[j];
   const float rstd = rstd_of(a, K, eps);
-  float am = 0.0f;
+  uint32_t am = 0;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     v[c][0] = norm8(v[c][0], lv[c][0], rstd);
     v[c][1] = norm8(v[c][1], lv[c][1], rstd);
     if (16 * (int64_t)(threadIdx.x + c * NT) < K) am = absmax8(v[c][1], absmax8(v[c][0], am));
   }
-  am = wave_max_nonneg(am);
+  am = wave_max_u32_dpp(am);
   if (lane == 0) red[threadIdx.x >> 6] = am;
   __syncthreads();
-  float b = red[0];
 #pragma unroll
-  for (int i = 1; i < NT / 64; ++i) b = fmaxf(b, red[i]);
-  b = fmaxf(b, 1e-6f);
+  for (int i = 0; i < NT / 64; ++i) am = umax32(am, red[i]);
+  const float b = clamp_min_nan(as_f32(am), 1e-6f);
   const float iv = inv_from_amax(b);
   if (threadIdx.x == 0) xs[m] = scale_from_amax(b);
 #pragma unroll
@@ -185,28 +182,12 @@ struct FusedPlan {
   size_t smem;  // dynamic LDS bytes
 };
 
-// Deep rings for the one-row launches on the tiled layout (KRQ_FUSED_DEEP=0 turns them off): as in
-// the plain kernels, each weight wave holds all of its steps in flight at once.
-bool deep_rings() {
-  static const bool on = [] {
-    const char* e = getenv("KRQ_FUSED_DEEP");
-    return !(e && atoi(e) == 0);
-  }();
-  return on;
-}
-
 // One-row launches (M == 1, bf16 activations) get the activation wave of gemv_fp8_kernel.h when
 // its registers hold what it loads: the whole row (per-token scale) or the slice (static scale),
-// K <= 4096 with RMSNorm (the row's partials, 64 x kSsPerLane); KRQ_GEMV_AW=0 turns it off. The
-// two-matrix SwiGLU block takes it with the deep rings only, and grids of fewer blocks than CUs
+// K <= 4096 with RMSNorm (the row's partials, 64 x kSsPerLane). Grids of fewer blocks than CUs
 // (the one-pass residual GEMVs) keep the shared prologue.
 int act_wave_chunks(int64_t M, int64_t K, int64_t ks, int mode, int x_kind, bool norm) {
-  static const bool aw_ok = [] {
-    const char* e = getenv("KRQ_GEMV_AW");
-    return !(e && atoi(e) == 0);
-  }();
-  if (!aw_ok || M != 1 || x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED || (mode == KRQ_OUT_SWIGLU && !deep_rings()))
-    return 0;
+  if (M != 1 || x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED) return 0;
   if (norm && K > 512 * kAwSmall) return 0;
   const int64_t span = x_kind == KRQ_X_BF16_DYN ? K : ks;
   return span <= 512 * kAwSmall ? kAwSmall : span <= 512 * kAwLarge ? kAwLarge : 0;
@@ -232,7 +213,7 @@ bool plan(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind, bool
   // The one-pass residual GEMVs (fewer blocks than CUs, every wave in the prologue) measured slower
   // with one round of 8- or 10-slot rings (O 6.21 -> 6.64, down 10.39 -> 12.12) and keep four slots.
   int u = 0;
-  if (deep_rings() && M == 1 && x_kind != KRQ_X_FP8 && awc > 0) {
+  if (M == 1 && x_kind != KRQ_X_FP8 && awc > 0) {
     u = mode == KRQ_OUT_SWIGLU ? kSwiU : nsteps <= kMidU ? kMidU : kDeepU;
     nw = plan_waves(nsteps, P, u, NO / 16 * split, true);
   }

@@ -167,12 +167,8 @@ int krq::gemv_bf16_run(const void* x, const void* w, int w_layout, int64_t M, in
               "gemv_bf16: no tiling divides N=%lld (output columns must be a multiple of 16)", (long long)N);
   KRQ_REQUIRE(NO / 16 <= 0x7fffffff && split <= 65535, "gemv_bf16: grid too large");
   const int kts = static_cast<int>(K / split / 32);
-  static const bool pair_ok = [] {
-    const char* e = getenv("KRQ_GEMV_PAIR");
-    return !(e && atoi(e) == 0);
-  }();
   // paired only where halving the blocks still leaves thousands (the lm_head), as in gemv_fp8.hip
-  const int pb = (pair_ok && mode != KRQ_OUT_SWIGLU && M > 4 && (NO / 16) % 2 == 0 &&
+  const int pb = (mode != KRQ_OUT_SWIGLU && M > 4 && (NO / 16) % 2 == 0 &&
                   (NO / 16) * split >= 4096) ? 2 : 1;
   const int P = mode == KRQ_OUT_SWIGLU ? 2 : pb;
   const int MT = M <= 16 ? 1 : 2;

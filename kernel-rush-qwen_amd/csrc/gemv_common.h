@@ -145,9 +145,10 @@ KRQ_DEV uint2 quant8_own_amax(uint4 v, float s) {
   return r;
 }
 
-// |x| max of 8 bf16 on their bits: |x| orders as its bit pattern (sign cleared), so a packed
-// 16-bit integer max per 32-bit word suffices; m holds two running maxima. Integer work only, which
-// also keeps the compiler from holding fp32 copies of the row for the quantization that follows.
+// |x| max of 8 bf16 on their bits: |x| orders as its bit pattern (sign cleared), with NaN above
+// every number (mag_bits), so a packed 16-bit integer max per 32-bit word suffices; m holds two
+// running maxima. Integer work only, which also keeps the compiler from holding fp32 copies of the
+// row for the quantization that follows.
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 KRQ_DEV u16x2 absmax8_bits(uint4 v, u16x2 m) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -155,7 +156,13 @@ KRQ_DEV u16x2 absmax8_bits(uint4 v, u16x2 m) {
   for (int q = 0; q < 4; ++q) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[q] & 0x7fff7fffu));
   return m;
 }
-KRQ_DEV float bits_max_to_f32(u16x2 m) { return as_f32(static_cast<uint32_t>(m.x > m.y ? m.x : m.y) << 16); }
+// the two running maxima as one fp32 magnitude bit pattern (mag_bits of the larger)
+KRQ_DEV uint32_t bits_max_to_u32(u16x2 m) { return static_cast<uint32_t>(m.x > m.y ? m.x : m.y) << 16; }
+
+// running |x| max (fp32 magnitude bits, NaN-keeping) of 8 bf16
+KRQ_DEV uint32_t absmax8(uint4 v, uint32_t m) {
+  return umax32(m, bits_max_to_u32(absmax8_bits(v, u16x2{0, 0})));
+}
 
 // 8 bf16 times a given inverse scale -> 8 e4m3 bytes, with the reference's clamp to +-448 (the
 // products can exceed it); NaN stays a NaN code (its sign does not reach the products)
@@ -170,16 +177,6 @@ KRQ_DEV uint2 quant8_clamped(uint4 v, float s) {
   r.y = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(as_f32(v.w << 16) * s),
                                                               clamp448(as_f32(v.w & 0xffff0000u) * s), p, true));
   return r;
-}
-
-KRQ_DEV float absmax8(uint4 v, float m) {
-  const uint32_t a[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    m = fmaxf(m, fabsf(as_f32(a[q] << 16)));
-    m = fmaxf(m, fabsf(as_f32(a[q] & 0xffff0000u)));
-  }
-  return m;
 }
 
 // vector-ALU dot products (M == 1 kernels)

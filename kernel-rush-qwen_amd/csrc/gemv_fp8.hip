@@ -3,17 +3,10 @@
 // epilogue conventions: gemv_common.h.
 #include "gemv_fp8_kernel.h"
 
-#include <stdlib.h>
-
 using namespace krq;
 
 namespace krq {
 int plan_waves(int nsteps, int P, int U, int64_t blocks, bool act_wave) {
-  static const int env = [] {
-    const char* s = getenv("KRQ_GEMV_WAVES");
-    return s ? atoi(s) : 0;
-  }();
-  if (env >= 1 && env <= 8) return env;
   if (nsteps < 2) return 1;
   // measured on MI355X at the Qwen3-4B shapes: a single-matrix block takes just enough waves for
   // all of its steps to be in flight at once (one memory round trip), up to 4; when that is not
@@ -156,32 +149,24 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   if (algo == 0) algo = 1;
   const int kts = static_cast<int>(K / split / 64);
   const int ks = kts * 64;
-  // paired row blocks for the multi-row matrix-core kernels (KRQ_GEMV_PAIR=0 turns them off)
-  static const bool pair_ok = [] {
-    const char* e = getenv("KRQ_GEMV_PAIR");
-    return !(e && atoi(e) == 0);
-  }();
-  // Measured: pairing halves the blocks, which costs the Qwen3-4B projections (640-768 blocks)
-  // more than the saved activation reads gain; the lm_head (9,496 blocks) gains 10-15%.
-  const int pb = (pair_ok && mode != KRQ_OUT_SWIGLU && algo != 2 && M > 4 && (NO / 16) % 2 == 0 &&
+  // Paired row blocks for the multi-row matrix-core kernels. Measured: pairing halves the blocks,
+  // which costs the Qwen3-4B projections (640-768 blocks) more than the saved activation reads
+  // gain; the lm_head (9,496 blocks) gains 10-15%.
+  const int pb = (mode != KRQ_OUT_SWIGLU && algo != 2 && M > 4 && (NO / 16) % 2 == 0 &&
                   (NO / 16) * split >= 4096) ? 2 : 1;
   const int P = mode == KRQ_OUT_SWIGLU ? 2 : pb;
   const int MT = (algo == 2 || M <= 16) ? 1 : 2;
   // step slots per wave of the variant launch() picks
   const int U = (algo == 2 || M <= 4) ? 4 : 2;
-  // one-row kind: an activation wave holding the whole row (K <= 10240; KRQ_GEMV_AW=0 turns it off),
-  // else every wave takes part in the prologue. Measured at M = 1: QKV 5.92 -> 5.29 us, O 5.15 ->
+  // one-row kind: an activation wave holding the whole row (K <= 10240), else every wave takes part
+  // in the prologue. Measured at M = 1: QKV 5.92 -> 5.29 us, O 5.15 ->
   // 4.41, down 7.91 -> 7.16, FP8 lm_head 64.9 -> 63.1; the SwiGLU GEMV 11.24 -> 10.86 with the
   // five-slot ring below (with four slots the activation wave did not pay: 11.45).
-  static const bool aw_ok = [] {
-    const char* e = getenv("KRQ_GEMV_AW");
-    return !(e && atoi(e) == 0);
-  }();
   // With static scales (M == 1) the wave quantizes the slice alone.
   int awc = 0;
-  if (x_kind == KRQ_X_BF16_DYN && aw_ok)
+  if (x_kind == KRQ_X_BF16_DYN)
     awc = K <= 512 * kAwSmall ? kAwSmall : K <= 512 * kAwLarge ? kAwLarge : 0;
-  if (x_kind == KRQ_X_BF16_STATIC && aw_ok && M == 1)
+  if (x_kind == KRQ_X_BF16_STATIC && M == 1)
     awc = ks <= 512 * kAwSmall ? kAwSmall : ks <= 512 * kAwLarge ? kAwLarge : 0;
   // With fewer blocks than CUs each block's prologue is its CU's critical path, and spreading it
   // over all waves is faster (the one-pass residual GEMVs, 160 blocks: O 6.21 against 6.65 us).
@@ -194,12 +179,8 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   // (four loads a step) takes five slots with two weight waves (ten slots spill registers).
   const int nsteps = (kts + 1) / 2;
   int u = U;
-  static const bool deep_ok = [] {
-    const char* e = getenv("KRQ_GEMV_DEEP");
-    return !(e && atoi(e) == 0);
-  }();
   // The lm_head (argmax epilogue, 9,496 blocks) keeps four slots: 63.1 against 64.4 us.
-  if (deep_ok && awc > 0 && algo == 1 && w_layout == KRQ_W_TILED && mode != kOutArgmax)
+  if (awc > 0 && algo == 1 && w_layout == KRQ_W_TILED && mode != kOutArgmax)
     u = mode == KRQ_OUT_SWIGLU ? kSwiU : nsteps <= kMidU ? kMidU : kDeepU;
   int nw = plan_waves(nsteps, P, u, NO / 16 / pb * split, awc > 0);
   // the other fused prologues hold at most kXChunks 16-byte chunks per thread

@@ -101,7 +101,7 @@ KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restr
 #pragma unroll
     for (int c = 0; c < AWC; ++c)
       if (!NORM || lane + 64 * c <= last) mb = absmax8_bits(v[c], mb);
-    const float am = fmaxf(wave_max_nonneg(bits_max_to_f32(mb)), 1e-6f);
+    const float am = clamp_min_nan(as_f32(wave_max_u32_dpp(bits_max_to_u32(mb))), 1e-6f);
     inv = inv_from_amax(am);
     if (lane == 0) xs_l[0] = scale_from_amax(am);
   }
@@ -128,7 +128,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   // nw*P*MT*256 partial sums | e4m3 activation slice [M][ks] | (NORM) sum-of-squares [M][K/16]
   extern __shared__ float red[];
   __shared__ float xs_l[32], rstd_s[32];
-  __shared__ float amax_w[kMaxThreads / 64];
+  __shared__ uint32_t amax_w[kMaxThreads / 64];
   __shared__ uint32_t last_s;
   static_assert(PB == 1 || (MODE != KRQ_OUT_SWIGLU && MODE != kOutResidual && ALGO != 2),
                 "paired row blocks: MFMA, no SwiGLU or residual epilogue");
@@ -279,16 +279,16 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
     xs_l[threadIdx.x & 31] = xs_reg;
   } else if (XK == KRQ_X_BF16_DYN) {
     if constexpr (!AW) {  // (with the activation wave, the slice is already in LDS after the barrier below)
-      float am = 0.0f;
+      uint32_t am = 0;
 #pragma unroll
       for (int c = 0; c < kXChunksDyn; ++c)
         if (!NORM || 8 * (int64_t)(threadIdx.x + c * blockDim.x) < K) am = absmax8(xv[c], am);
-      am = wave_max(am);
+      am = wave_max_u32(am);
       if (lane == 0) amax_w[wave] = am;
       __syncthreads();
-      float a = amax_w[0];
-      for (int w = 1; w < nw; ++w) a = fmaxf(a, amax_w[w]);
-      a = fmaxf(a, 1e-6f);
+      uint32_t ab = amax_w[0];
+      for (int w = 1; w < nw; ++w) ab = umax32(ab, amax_w[w]);
+      const float a = clamp_min_nan(as_f32(ab), 1e-6f);
       const float inv = inv_from_amax(a);
       if (threadIdx.x == 0) xs_l[0] = scale_from_amax(a);
 #pragma unroll

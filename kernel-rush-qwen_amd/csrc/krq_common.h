@@ -101,32 +101,46 @@ KRQ_HD int64_t tiled_offset(int64_t n, int64_t k, int64_t K) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Wave / block reductions
+// Magnitude maxima that keep NaN. The reference takes every amax with torch reductions that
+// propagate NaN (w.abs().max(), torch.aminmax + torch.maximum, amax(1)) and floors it with
+// clamp_min, which keeps NaN too; a NaN element therefore makes its row's (or tensor's) scale NaN
+// and every quantized byte of it a NaN code. fmaxf drops NaN, so the kernels compare magnitudes as
+// fp32 bit patterns with the sign cleared instead: for numbers these order like the values
+// (+0 < denormals < normals < +inf), and every NaN pattern lies above +inf, so an unsigned integer
+// max returns NaN as soon as one element is NaN. The folded bits are read back with as_f32.
 // ---------------------------------------------------------------------------------------------
-KRQ_DEV float wave_max(float v) {
+KRQ_HD uint32_t mag_bits(float f) { return as_u32(f) & 0x7fffffffu; }
+
+// max(a, lo) that keeps a NaN a, as torch's clamp_min does (fmaxf(NaN, lo) would give lo)
+KRQ_HD float clamp_min_nan(float a, float lo) { return a != a ? a : fmaxf(a, lo); }
+
+KRQ_DEV uint32_t umax32(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// max over the wave; every lane gets it
+KRQ_DEV uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  for (int o = 32; o > 0; o >>= 1) v = umax32(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), o, kWave)));
   return v;
 }
 
 template <int CTRL>
-KRQ_DEV float dpp_max(float a) {
-  return fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), CTRL, 0xf, 0xf, false)));
+KRQ_DEV uint32_t dpp_max_u32(uint32_t a) {
+  return umax32(a, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(a), CTRL, 0xf, 0xf, false)));
 }
 
-// max over the wave of non-negative values, returned wave-uniform: DPP steps inside each row of 16
-// lanes (quad swaps, then the half-row and row mirrors), then the four row results read as
-// scalars; a few VALU cycles per step instead of an LDS-crossbar round trip per shuffle
-KRQ_DEV float wave_max_nonneg(float v) {
-  v = dpp_max<0xB1>(v);   // quad_perm(1,0,3,2): lane ^ 1
-  v = dpp_max<0x4E>(v);   // quad_perm(2,3,0,1): lane ^ 2
-  v = dpp_max<0x141>(v);  // row_half_mirror: the other quad of each 8
-  v = dpp_max<0x140>(v);  // row_mirror: the other half of each 16
-  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+// max over the wave, returned wave-uniform: DPP steps inside each row of 16 lanes (quad swaps, then
+// the half-row and row mirrors), then the four row results read as scalars; a few VALU cycles per
+// step instead of an LDS-crossbar round trip per shuffle
+KRQ_DEV uint32_t wave_max_u32_dpp(uint32_t v) {
+  v = dpp_max_u32<0xB1>(v);   // quad_perm(1,0,3,2): lane ^ 1
+  v = dpp_max_u32<0x4E>(v);   // quad_perm(2,3,0,1): lane ^ 2
+  v = dpp_max_u32<0x141>(v);  // row_half_mirror: the other quad of each 8
+  v = dpp_max_u32<0x140>(v);  // row_mirror: the other half of each 16
+  const uint32_t r0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 0));
+  const uint32_t r1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 16));
+  const uint32_t r2 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 32));
+  const uint32_t r3 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 48));
+  return umax32(umax32(r0, r1), umax32(r2, r3));
 }
 
 KRQ_DEV float wave_sum(float v) {
@@ -137,15 +151,15 @@ KRQ_DEV float wave_sum(float v) {
 
 // max over a block of NT threads (NT a multiple of 64, at most 1024); every thread gets it.
 template <int NT>
-KRQ_DEV float block_max(float v) {
-  __shared__ float red[NT / kWave];
-  v = wave_max(v);
+KRQ_DEV uint32_t block_max_u32(uint32_t v) {
+  __shared__ uint32_t red[NT / kWave];
+  v = wave_max_u32(v);
   const int w = threadIdx.x / kWave;
   if ((threadIdx.x & (kWave - 1)) == 0) red[w] = v;
   __syncthreads();
-  float r = red[0];
+  uint32_t r = red[0];
 #pragma unroll
-  for (int i = 1; i < NT / kWave; ++i) r = fmaxf(r, red[i]);
+  for (int i = 1; i < NT / kWave; ++i) r = umax32(r, red[i]);
   __syncthreads();
   return r;
 }

@@ -60,14 +60,14 @@ __global__ __launch_bounds__(kQT) void k_weight_rows(const uint16_t* __restrict_
   if (MODE == 2) {
     s = scale[0];
   } else {
-    float m = 0.0f;
-    for (int64_t k = threadIdx.x; k < K; k += kQT) m = fmaxf(m, fabsf(bf16_to_f32(row[k])));
-    m = block_max<kQT>(m);
+    uint32_t mb = 0;
+    for (int64_t k = threadIdx.x; k < K; k += kQT) mb = umax32(mb, mag_bits(bf16_to_f32(row[k])));
+    const float m = as_f32(block_max_u32<kQT>(mb));
     if (MODE == 1) {
       if (threadIdx.x == 0) row_amax[n] = m;
       return;
     }
-    s = scale_from_amax(fmaxf(m, 1e-12f));
+    s = scale_from_amax(clamp_min_nan(m, 1e-12f));
     if (threadIdx.x == 0) scale[n] = s;
   }
   for (int64_t k = threadIdx.x; k < K; k += kQT) {
@@ -80,10 +80,10 @@ __global__ __launch_bounds__(kQT) void k_weight_rows(const uint16_t* __restrict_
 // per-tensor pass 2: one block folds the N row maxima into scale0
 __global__ __launch_bounds__(1024) void k_fold_scale(const float* __restrict__ row_amax, int64_t N,
                                                      float* __restrict__ scale0) {
-  float m = 0.0f;
-  for (int64_t i = threadIdx.x; i < N; i += 1024) m = fmaxf(m, row_amax[i]);
-  m = block_max<1024>(m);
-  if (threadIdx.x == 0) scale0[0] = scale_from_amax(fmaxf(m, 1e-12f));
+  uint32_t mb = 0;
+  for (int64_t i = threadIdx.x; i < N; i += 1024) mb = umax32(mb, mag_bits(row_amax[i]));
+  const float m = as_f32(block_max_u32<1024>(mb));
+  if (threadIdx.x == 0) scale0[0] = scale_from_amax(clamp_min_nan(m, 1e-12f));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -91,7 +91,7 @@ __global__ __launch_bounds__(1024) void k_fold_scale(const float* __restrict__ r
 //   amax = max(max|x|, 1e-6) * headroom; inv = fp32(1/amax) * 448; scale = amax * fp32(1/448)
 // ---------------------------------------------------------------------------------------------
 KRQ_DEV void act_finish(float m, float headroom, float* amax, float* inv, float* scale, int64_t i) {
-  const float a = fmaxf(m, 1e-6f) * headroom;
+  const float a = clamp_min_nan(m, 1e-6f) * headroom;
   amax[i] = a;
   inv[i] = inv_from_amax(a);
   scale[i] = scale_from_amax(a);
@@ -100,21 +100,21 @@ KRQ_DEV void act_finish(float m, float headroom, float* amax, float* inv, float*
 // per tensor pass 1: block-strided partial maxima into ws[blockIdx.x]
 __global__ __launch_bounds__(kQT) void k_absmax_partial(const uint16_t* __restrict__ x, int64_t n,
                                                         float* __restrict__ ws) {
-  float m = 0.0f;
+  uint32_t mb = 0;
   for (int64_t i = blockIdx.x * (int64_t)kQT + threadIdx.x; i < n; i += (int64_t)gridDim.x * kQT)
-    m = fmaxf(m, fabsf(bf16_to_f32(x[i])));
-  m = block_max<kQT>(m);
-  if (threadIdx.x == 0) ws[blockIdx.x] = m;
+    mb = umax32(mb, mag_bits(bf16_to_f32(x[i])));
+  mb = block_max_u32<kQT>(mb);
+  if (threadIdx.x == 0) ws[blockIdx.x] = as_f32(mb);
 }
 
 // per tensor pass 2
 __global__ __launch_bounds__(1024) void k_act_fold(const float* __restrict__ ws, int g,
                                                    float headroom, float* amax, float* inv,
                                                    float* scale) {
-  float m = 0.0f;
-  for (int i = threadIdx.x; i < g; i += 1024) m = fmaxf(m, ws[i]);
-  m = block_max<1024>(m);
-  if (threadIdx.x == 0) act_finish(m, headroom, amax, inv, scale, 0);
+  uint32_t mb = 0;
+  for (int i = threadIdx.x; i < g; i += 1024) mb = umax32(mb, mag_bits(ws[i]));
+  mb = block_max_u32<1024>(mb);
+  if (threadIdx.x == 0) act_finish(as_f32(mb), headroom, amax, inv, scale, 0);
 }
 
 // per row: one block per row m; with x8 != nullptr the row is also cast (quant_rows)
@@ -123,10 +123,9 @@ __global__ __launch_bounds__(kQT) void k_act_rows(const uint16_t* __restrict__ x
                                                   float* scale, uint8_t* __restrict__ x8) {
   const int64_t r = blockIdx.x;
   const uint16_t* row = x + r * K;
-  float m = 0.0f;
-  for (int64_t k = threadIdx.x; k < K; k += kQT) m = fmaxf(m, fabsf(bf16_to_f32(row[k])));
-  m = block_max<kQT>(m);
-  const float a = fmaxf(m, 1e-6f) * headroom;
+  uint32_t mb = 0;
+  for (int64_t k = threadIdx.x; k < K; k += kQT) mb = umax32(mb, mag_bits(bf16_to_f32(row[k])));
+  const float a = clamp_min_nan(as_f32(block_max_u32<kQT>(mb)), 1e-6f) * headroom;
   const float iv = inv_from_amax(a);
   if (threadIdx.x == 0) {
     if (amax) amax[r] = a;
@@ -194,23 +193,23 @@ __global__ __launch_bounds__(kQT) void k_weight_rows_vec(const uint16_t* __restr
   const int64_t n = blockIdx.x;
   const uint8_t* row = reinterpret_cast<const uint8_t*>(w + n * ldw);
   uint4 v[kVecChunks];
-  float m = 0.0f;
+  uint32_t mb = 0;
 #pragma unroll
   for (int c = 0; c < kVecChunks; ++c) {
     const int64_t e = 8 * (int64_t)(threadIdx.x + c * kQT);
     v[c] = e < K ? ld16nt(row + 2 * e) : zero4();
-    m = absmax8(v[c], m);
+    mb = absmax8(v[c], mb);
   }
   float s;
   if (MODE == 2) {
     s = scale[0];
   } else {
-    m = block_max<kQT>(m);
+    const float m = as_f32(block_max_u32<kQT>(mb));
     if (MODE == 1) {
       if (threadIdx.x == 0) row_amax[n] = m;
       return;
     }
-    s = scale_from_amax(fmaxf(m, 1e-12f));
+    s = scale_from_amax(clamp_min_nan(m, 1e-12f));
     if (threadIdx.x == 0) scale[n] = s;
   }
 #pragma unroll
@@ -231,15 +230,14 @@ __global__ __launch_bounds__(kQT) void k_act_rows_vec(const uint16_t* __restrict
   const int64_t r = blockIdx.x;
   const uint8_t* row = reinterpret_cast<const uint8_t*>(x + r * K);
   uint4 v[kVecChunks];
-  float m = 0.0f;
+  uint32_t mb = 0;
 #pragma unroll
   for (int c = 0; c < kVecChunks; ++c) {
     const int64_t e = 8 * (int64_t)(threadIdx.x + c * kQT);
     v[c] = e < K ? ld16(row + 2 * e) : zero4();
-    m = absmax8(v[c], m);
+    mb = absmax8(v[c], mb);
   }
-  m = block_max<kQT>(m);
-  const float a = fmaxf(m, 1e-6f) * headroom;
+  const float a = clamp_min_nan(as_f32(block_max_u32<kQT>(mb)), 1e-6f) * headroom;
   const float iv = inv_from_amax(a);
   if (threadIdx.x == 0) {
     if (amax) amax[r] = a;
@@ -267,7 +265,7 @@ template <int NT, bool TILED>
 __global__ __launch_bounds__(NT) void k_act_rows_fast(const uint16_t* __restrict__ x, int64_t M, int64_t K,
                                                       float* __restrict__ scale, uint8_t* __restrict__ x8) {
   constexpr int C = static_cast<int>(kVecMaxK / 16 / NT);
-  __shared__ float red[NT / 64];
+  __shared__ uint32_t red[NT / 64];
   const int64_t r = blockIdx.x;
   if (TILED && r >= M) {
 #pragma unroll
@@ -279,22 +277,21 @@ __global__ __launch_bounds__(NT) void k_act_rows_fast(const uint16_t* __restrict
   }
   const uint8_t* row = reinterpret_cast<const uint8_t*>(x + r * K);
   uint4 v[C][2];
-  float m = 0.0f;
+  uint32_t mb = 0;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const int64_t e = 16 * (int64_t)(threadIdx.x + c * NT);
     const bool in = e < K;
     v[c][0] = in ? ld16(row + 2 * e) : zero4();
     v[c][1] = in ? ld16(row + 2 * e + 16) : zero4();
-    m = absmax8(v[c][1], absmax8(v[c][0], m));
+    mb = absmax8(v[c][1], absmax8(v[c][0], mb));
   }
-  m = wave_max_nonneg(m);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  mb = wave_max_u32_dpp(mb);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mb;
   __syncthreads();
-  float a = red[0];
 #pragma unroll
-  for (int i = 1; i < NT / 64; ++i) a = fmaxf(a, red[i]);
-  a = fmaxf(a, 1e-6f);
+  for (int i = 0; i < NT / 64; ++i) mb = umax32(mb, red[i]);
+  const float a = clamp_min_nan(as_f32(mb), 1e-6f);
   const float iv = inv_from_amax(a);
   if (threadIdx.x == 0) scale[r] = scale_from_amax(a);
 #pragma unroll
