@@ -19,8 +19,11 @@
 // write through to memory and their loads read memory from every XCD; a producer waits for its
 // stores to complete before it publishes. No cache writeback or invalidate is needed. The last
 // block out (counted per group, then over groups) zeroes the control words again, so graph
-// replays need no host reset. A wait is bounded: past kSpinLimit polls the block sets the error
-// word and goes on, so the kernel ends even if the device could not hold all G blocks.
+// replays need no host reset. A wait is bounded: past max_polls polls (kSpinLimit by default) the
+// block sets the error word and goes on with NaN activation scales, so the kernel ends even if the
+// device could not hold all G blocks, and every partial that block writes is NaN: a launch whose
+// co-residency assumption failed cannot pass as data. (act is complete either way: phase 1 never
+// waits.)
 #include "gemv_common.h"
 
 #include <stdlib.h>
@@ -44,9 +47,11 @@ __global__ __launch_bounds__(NW * 64, 2) void k_mlp_fp8(
     const uint8_t* __restrict__ x, const float* __restrict__ xsc, const uint8_t* __restrict__ wgu,
     const float* __restrict__ gsc, int g_per_row, const uint8_t* __restrict__ wd,
     const float* __restrict__ dsc, int d_per_row, int M, int H, int I, int S, uint16_t* act,
-    uint32_t* ctl, float* __restrict__ out) {
+    uint32_t* ctl, float* __restrict__ out, uint32_t max_polls) {
   extern __shared__ __align__(16) uint8_t lds[];  // red | xq1 (M == 1: H bytes) | xq2 (M*ks2)
-  __shared__ float xs1[32], xs2[32], inv2[32], amax_w[NW];
+  __shared__ float xs1[32], xs2[32], inv2[32];
+  __shared__ uint32_t amax_w[NW];
+  __shared__ uint32_t p1_bad;  // this block's phase-1 wait timed out
   __shared__ uint16_t act_s[32 * 16];
   constexpr int NT = NW * 64, NV = MT * 256;
   const int n1 = I >> 4, n2 = (H >> 4) * S;
@@ -57,7 +62,7 @@ __global__ __launch_bounds__(NW * 64, 2) void k_mlp_fp8(
   uint8_t* xq1 = lds + NW * 2 * NV * sizeof(float);
   uint8_t* xq2 = xq1 + (XK == KRQ_X_BF16_DYN ? H : 0);
   bool have_x = false, p1_seen = false;
-  float amax_loc = 0.0f;  // threads m < M: running amax of act row m over this block's items
+  uint32_t amax_loc = 0;  // threads m < M: running amax (mag_bits) of act row m over this block's items
 
   for (int t = blockIdx.x; t < n1; t += G) {
     // Lane coordinates are re-derived opaquely in every item: otherwise the compiler hoists the
@@ -110,16 +115,16 @@ __global__ __launch_bounds__(NW * 64, 2) void k_mlp_fp8(
       __builtin_amdgcn_sched_barrier(0);
       if (!have_x) {
         if (XK == KRQ_X_BF16_DYN) {
-          float am = 0.0f;
+          uint32_t am = 0;
 #pragma unroll
           for (int c = 0; c < kXC; ++c) am = absmax8(xv[c], am);
-          am = wave_max(am);
+          am = wave_max_u32(am);
           if (lane == 0) amax_w[wave] = am;
           __syncthreads();
-          float a = amax_w[0];
+          uint32_t ab = amax_w[0];
 #pragma unroll
-          for (int w = 1; w < NW; ++w) a = fmaxf(a, amax_w[w]);
-          a = fmaxf(a, 1e-6f);
+          for (int w = 1; w < NW; ++w) ab = umax32(ab, amax_w[w]);
+          const float a = clamp_min_nan(as_f32(ab), 1e-6f);
           const float inv = inv_from_amax(a);
           if (threadIdx.x == 0) xs1[0] = scale_from_amax(a);
 #pragma unroll
@@ -192,13 +197,13 @@ __global__ __launch_bounds__(NW * 64, 2) void k_mlp_fp8(
       }
       if (threadIdx.x < (unsigned)M) {
 #pragma unroll
-        for (int c = 0; c < 16; ++c) amax_loc = fmaxf(amax_loc, fabsf(bf16_to_f32(act_s[threadIdx.x * 16 + c])));
+        for (int c = 0; c < 16; ++c) amax_loc = umax32(amax_loc, mag_bits(bf16_to_f32(act_s[threadIdx.x * 16 + c])));
       }
       __syncthreads();  // red and act_s are rewritten by the next item
     }
   }
   // publish this block's phase 1 (every block counts, with or without items)
-  if (threadIdx.x < (unsigned)M) cmax(&ctl[grp * kGroupWords + kAmax + threadIdx.x], as_u32(amax_loc));
+  if (threadIdx.x < (unsigned)M) cmax(&ctl[grp * kGroupWords + kAmax + threadIdx.x], amax_loc);
   stores_done();
   __syncthreads();
   if (threadIdx.x == 0) cadd(&ctl[grp * kGroupWords + kDone], 1u);
@@ -230,26 +235,28 @@ __global__ __launch_bounds__(NW * 64, 2) void k_mlp_fp8(
       __builtin_amdgcn_sched_barrier(0);
       if (!p1_seen) {
         if (threadIdx.x == 0) {
-          uint32_t polls = 0;
+          uint32_t polls = 0, bad = 0;
           for (;;) {
             uint32_t done = 0;
 #pragma unroll
             for (int q = 0; q < kGroups; ++q) done += cload(&ctl[q * kGroupWords + kDone]);
             if (done >= (uint32_t)G) break;
-            if (++polls > kSpinLimit) {
+            if (++polls > max_polls) {
               cstore(&ctl[kErr], 1u);
+              bad = 1;
               break;
             }
             __builtin_amdgcn_s_sleep(2);
           }
+          p1_bad = bad;
         }
         __syncthreads();
         // per-token scales of act (final once phase 1 is done), kept for this block's later items
         if (threadIdx.x < (unsigned)M) {
-          float a = 0.0f;
+          uint32_t ab = 0;
 #pragma unroll
-          for (int q = 0; q < kGroups; ++q) a = fmaxf(a, as_f32(cload(&ctl[q * kGroupWords + kAmax + threadIdx.x])));
-          a = fmaxf(a, 1e-6f);
+          for (int q = 0; q < kGroups; ++q) ab = umax32(ab, cload(&ctl[q * kGroupWords + kAmax + threadIdx.x]));
+          const float a = p1_bad ? __builtin_nanf("") : clamp_min_nan(as_f32(ab), 1e-6f);
           xs2[threadIdx.x] = scale_from_amax(a);
           inv2[threadIdx.x] = inv_from_amax(a);
         }
@@ -347,15 +354,11 @@ constexpr int kNW = 4;  // waves per block
 // phase 2 holds a whole item (19 steps over 4 waves), so its loads are all issued before the wait
 constexpr int kU2 = 5;
 
-// Blocks of one launch: `programs` (or KRQ_MLP_BLOCKS, or one per CU), clamped to the blocks the
-// device holds at once for this kernel and shared-memory size - a phase-2 block waits on every
-// block's phase 1, so all of them must be resident - and to the larger phase's item count.
+// Blocks of one launch: `programs` (or one per CU), clamped to the blocks the device holds at once
+// for this kernel and shared-memory size - a phase-2 block waits on every block's phase 1, so all
+// of them must be resident - and to the larger phase's item count.
 template <typename Kernel>
 int grid_blocks(Kernel kernel, size_t smem, int programs, int items, int* G) {
-  static const int env = [] {
-    const char* s = getenv("KRQ_MLP_BLOCKS");
-    return s ? atoi(s) : 0;
-  }();
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -364,7 +367,7 @@ int grid_blocks(Kernel kernel, size_t smem, int programs, int items, int* G) {
     krq_set_error("mlp_fp8: occupancy query failed");
     return KRQ_EHIP;
   }
-  int g = programs > 0 ? programs : (env > 0 ? env : cus);
+  int g = programs > 0 ? programs : cus;
   g = g < cus * per_cu ? g : cus * per_cu;
   *G = g < items ? g : items;
   return KRQ_OK;
@@ -374,11 +377,11 @@ int grid_blocks(Kernel kernel, size_t smem, int programs, int items, int* G) {
 
 extern "C" int64_t krq_mlp_ctl_words(void) { return kCtlWords; }
 
-extern "C" int krq_mlp_fp8(const void* x, int x_kind, const float* x_scale, const void* w_gu,
-                           int w_layout, const float* gu_scale, int gu_per_row, const void* w_down,
-                           const float* down_scale, int down_per_row, int64_t M, int64_t H, int64_t I,
-                           int split, void* act, uint32_t* ctl, int programs, void* out,
-                           void* stream) {
+extern "C" int krq_mlp_fp8_bounded(const void* x, int x_kind, const float* x_scale, const void* w_gu,
+                                   int w_layout, const float* gu_scale, int gu_per_row, const void* w_down,
+                                   const float* down_scale, int down_per_row, int64_t M, int64_t H,
+                                   int64_t I, int split, void* act, uint32_t* ctl, int programs,
+                                   uint32_t max_polls, void* out, void* stream) {
   KRQ_REQUIRE(x && w_gu && w_down && gu_scale && down_scale && act && ctl && out, "mlp_fp8: null pointer");
   KRQ_REQUIRE(aligned16(x) && aligned16(w_gu) && aligned16(w_down) && aligned16(act),
               "mlp_fp8: x, weights and act must be 16-byte aligned");
@@ -405,7 +408,7 @@ extern "C" int krq_mlp_fp8(const void* x, int x_kind, const float* x_scale, cons
   const uint8_t* db = (const uint8_t*)w_down;
   const int m = (int)M, h = (int)H, ii = (int)I;
 #define KRQ_MLP_ARGS xb, x_scale, gb, gu_scale, gu_per_row, db, down_scale, down_per_row, m, h, ii, split, \
-                     (uint16_t*)act, ctl, (float*)out
+                     (uint16_t*)act, ctl, (float*)out, max_polls
 #define KRQ_MLP_LAUNCH(MTV, XKV, LAY)                                                           \
   do {                                                                                          \
     auto kern = k_mlp_fp8<MTV, XKV, LAY, kNW, MTV == 1 ? 4 : 3, kU2>;                           \
@@ -427,4 +430,13 @@ extern "C" int krq_mlp_fp8(const void* x, int x_kind, const float* x_scale, cons
 #undef KRQ_MLP_LAUNCH
 #undef KRQ_MLP_ARGS
   return krq_check_launch("mlp_fp8");
+}
+
+extern "C" int krq_mlp_fp8(const void* x, int x_kind, const float* x_scale, const void* w_gu,
+                           int w_layout, const float* gu_scale, int gu_per_row, const void* w_down,
+                           const float* down_scale, int down_per_row, int64_t M, int64_t H, int64_t I,
+                           int split, void* act, uint32_t* ctl, int programs, void* out,
+                           void* stream) {
+  return krq_mlp_fp8_bounded(x, x_kind, x_scale, w_gu, w_layout, gu_scale, gu_per_row, w_down, down_scale,
+                             down_per_row, M, H, I, split, act, ctl, programs, kSpinLimit, out, stream);
 }

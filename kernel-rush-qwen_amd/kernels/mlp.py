@@ -1,5 +1,5 @@
 """Persistent fused decode MLP: act = SwiGLU(h @ [gate; up]^T), then the fp32 split-K partials of
-the down projection, in one launch of the HIP kernel k_mlp_fp8 (libkrq.so, krq_mlp_fp8).
+the down projection.
 
 Drop-in for the reference's engine/kernels/mlp.py: PersistentMLP(M, H, I, device, programs,
 split=4, bn=16, bn2=16, chunk=512) and __call__(h, w_gu, w_down) -> fp32 [split, M, H], summed
@@ -8,14 +8,16 @@ FP8Weight tuples of fp8.quantize (per-channel e4m3) and activations are scaled p
 linear_fp8 / quant_rows do: at M == 1 the kernel scales h itself, at larger M fp8.quant_rows runs
 first; the SwiGLU activations are re-quantized per token inside the kernel once all of them exist.
 
-`programs` is the number of blocks, as in the reference; the library clamps it to the blocks the
-device holds at once (so spin-waits cannot deadlock), and `programs=None` takes one per CU. The
-control words are zeroed here once and left zeroed by every launch.
-
-BF16 weights (the reference engine's default, engine/engine.py:911-915) return the same contract
-through the two GEMV launches of kernels.gemv (SwiGLU, then the split-K down partials): on MI355X
-the one-launch form measured slower than the pair for FP8 weights (the cross-XCD handoff between
-the phases costs more than the launch boundary), so the BF16 path is the pair.
+Two forms give the same contract. By default both phases are separate GEMV launches
+(fp8.gemv_swiglu_fp8 then fp8.gemv_fp8 for FP8 weights, kernels.gemv for BF16 weights): on MI355X
+that pair measured faster than one persistent launch (17.2 against 31 us at M = 1, 26.7 against
+55 us at M = 16 for FP8 weights), because the cross-XCD handoff between the phases costs more than
+a launch boundary. one_launch=True runs both phases in one launch of the HIP kernel k_mlp_fp8
+(libkrq.so, krq_mlp_fp8; FP8 weights only): `programs` is then the number of blocks, as in the
+reference; the library clamps it to the blocks the device holds at once (so spin-waits cannot
+deadlock), and `programs=None` takes one per CU. Its control words are zeroed here once and left
+zeroed by every launch; a block whose phase-1 wait gives up writes NaN partials, and failed()
+reports it.
 """
 
 import torch
@@ -28,7 +30,8 @@ from . import gemv as _gemv
 class PersistentMLP:
     """Workspace for one M. Call with (h [M, H] bf16, w_gu [2I, H], w_down [H, I]) as FP8Weight."""
 
-    def __init__(self, M, H, I, device, programs=None, split=4, bn=16, bn2=16, chunk=512):
+    def __init__(self, M, H, I, device, programs=None, split=4, bn=16, bn2=16, chunk=512,
+                 one_launch=False):
         # the reference's shape contract (engine/kernels/mlp.py:100-103)
         assert I % chunk == 0 and chunk % bn == 0 and I % split == 0
         assert (I // split) % 64 == 0 and H % bn2 == 0
@@ -38,6 +41,7 @@ class PersistentMLP:
             raise ValueError(f"PersistentMLP: M={M} outside 1..32")
         self.M, self.H, self.I, self.G = M, H, I, programs
         self.split, self.bn, self.bn2, self.chunk = split, bn, bn2, chunk
+        self.one_launch = one_launch
         self.ctl = torch.zeros((int(L.lib().krq_mlp_ctl_words()),), device=device, dtype=torch.int32)
         self.act = None   # bf16 [M, I] SwiGLU activations of the last call
 
@@ -53,7 +57,9 @@ class PersistentMLP:
         self.act = act
         return _gemv.gemv(act, w_down, self.split)
 
-    def __call__(self, h, w_gu, w_down):
+    def __call__(self, h, w_gu, w_down, max_polls=None):
+        """max_polls (one-launch form): bound on the phase-1 wait's polls (default: about a
+        second's worth); a small value forces the timeout path, for tests."""
         if isinstance(w_gu, torch.Tensor) and isinstance(w_down, torch.Tensor):
             if w_gu.dtype != torch.bfloat16 or w_down.dtype != torch.bfloat16:
                 raise ValueError("PersistentMLP: weights are FP8Weight tuples or bf16 tensors")
@@ -76,6 +82,10 @@ class PersistentMLP:
         M = h2.shape[0]
         if M != self.M:
             raise ValueError(f"PersistentMLP built for M={self.M}, called with M={M}")
+        if not self.one_launch:
+            act = _fp8.gemv_swiglu_fp8(h2, w_gu)
+            self.act = act
+            return _fp8.gemv_fp8(act, w_down, S)
         if M == 1:
             xin, kind, xs = h2, L.X_BF16_DYN, None
         else:
@@ -83,12 +93,18 @@ class PersistentMLP:
             kind, xs = L.X_FP8, xs.reshape(-1)
         act = torch.empty((M, I), device=h.device, dtype=torch.bfloat16)
         out = torch.empty((S, M, H), device=h.device, dtype=torch.float32)
-        L.call("krq_mlp_fp8", L.ptr(xin), kind, L.ptr(xs), L.ptr(gu), lay_gu, L.ptr(gs), g_pr,
-               L.ptr(dn), L.ptr(ds), d_pr, M, H, I, S, L.ptr(act), L.ptr(self.ctl),
-               int(self.G or 0), L.ptr(out), L.stream(h))
+        if max_polls is None:
+            L.call("krq_mlp_fp8", L.ptr(xin), kind, L.ptr(xs), L.ptr(gu), lay_gu, L.ptr(gs), g_pr,
+                   L.ptr(dn), L.ptr(ds), d_pr, M, H, I, S, L.ptr(act), L.ptr(self.ctl),
+                   int(self.G or 0), L.ptr(out), L.stream(h))
+        else:
+            L.call("krq_mlp_fp8_bounded", L.ptr(xin), kind, L.ptr(xs), L.ptr(gu), lay_gu, L.ptr(gs), g_pr,
+                   L.ptr(dn), L.ptr(ds), d_pr, M, H, I, S, L.ptr(act), L.ptr(self.ctl),
+                   int(self.G or 0), int(max_polls), L.ptr(out), L.stream(h))
         self.act = act
         return out
 
     def failed(self):
-        """True if a launch flagged a phase-1 wait that timed out (synchronizes the device)."""
+        """True if a one-launch call flagged a phase-1 wait that timed out (its partials are NaN);
+        synchronizes the device."""
         return bool(self.ctl[-1].item())

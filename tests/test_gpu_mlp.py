@@ -1,5 +1,5 @@
-"""Fused decode MLP (kernels.mlp.PersistentMLP over krq_mlp_fp8) against the CPU oracle and the
-two-launch path (gemv_swiglu_fp8 then the per-token-scaled down GEMV). Outputs are fp32 split-K
+"""Fused decode MLP (kernels.mlp.PersistentMLP(one_launch=True) over krq_mlp_fp8) against the CPU
+oracle and the two-launch path (gemv_swiglu_fp8 then the per-token-scaled down GEMV). Outputs are fp32 split-K
 partials [S, M, H]; the bar is max|y - ref| <= 1e-2 * max|ref| per split and summed."""
 
 import numpy as np
@@ -64,7 +64,7 @@ def case(M, h_, i_, seed):
 def test_mlp_fp8_vs_oracle(dev, M, S):
     wgu, wd, x = case(M, H, I, 40 + M)
     qgu, qd = fp8.quantize(wgu.to(dev)), fp8.quantize(wd.to(dev))
-    pm = PersistentMLP(M, H, I, dev, split=S)
+    pm = PersistentMLP(M, H, I, dev, split=S, one_launch=True)
     out = pm(x.to(dev), qgu, qd)
     assert out.shape == (S, M, H) and out.dtype == torch.float32
     act_ref, parts = O.mlp_fp8(u16(x), u8(qgu[0]), qgu[1].cpu().numpy(), u8(qd[0]),
@@ -97,7 +97,7 @@ def test_mlp_fp8_matches_two_launch_path(dev, M):
     wgu, wd, x = case(M, H, I, 50 + M)
     qgu, qd = fp8.quantize(wgu.to(dev)), fp8.quantize(wd.to(dev))
     xd = x.to(dev)
-    pm = PersistentMLP(M, H, I, dev)
+    pm = PersistentMLP(M, H, I, dev, one_launch=True)
     out = pm(xd, qgu, qd)
     a = fp8.gemv_swiglu_fp8(xd, qgu)
     sep = fp8.gemv_fp8(a, qd, 4)
@@ -115,8 +115,8 @@ def test_mlp_any_block_count_same_result(dev, programs):
     wgu, wd, x = case(M, h_, i_, 60)
     qgu, qd = fp8.quantize(wgu.to(dev)), fp8.quantize(wd.to(dev))
     xd = x.to(dev)
-    ref = PersistentMLP(M, h_, i_, dev)(xd, qgu, qd)
-    pm = PersistentMLP(M, h_, i_, dev, programs=programs)
+    ref = PersistentMLP(M, h_, i_, dev, one_launch=True)(xd, qgu, qd)
+    pm = PersistentMLP(M, h_, i_, dev, programs=programs, one_launch=True)
     out = pm(xd, qgu, qd)
     assert torch.equal(out, ref)
     assert not pm.failed() and int(pm.ctl.abs().sum()) == 0
@@ -128,7 +128,7 @@ def test_mlp_rowmajor_equals_tiled(dev):
     qgu, qd = fp8.quantize(wgu.to(dev)), fp8.quantize(wd.to(dev))
     rgu, rd = fp8.FP8Weight(qgu[0], qgu[1], None), fp8.FP8Weight(qd[0], qd[1], None)
     xd = x.to(dev)
-    pm = PersistentMLP(M, H, I, dev)
+    pm = PersistentMLP(M, H, I, dev, one_launch=True)
     a = pm(xd, qgu, qd)
     b = pm(xd, rgu, rd)
     assert torch.equal(a, b)
@@ -139,7 +139,7 @@ def test_mlp_counters_reset_across_calls_and_graph_replays(dev):
     wgu, wd, x = case(M, H, I, 80)
     qgu, qd = fp8.quantize(wgu.to(dev)), fp8.quantize(wd.to(dev))
     xd = x.to(dev)
-    pm = PersistentMLP(M, H, I, dev)
+    pm = PersistentMLP(M, H, I, dev, one_launch=True)
     first = pm(xd, qgu, qd).clone()
     for _ in range(3):
         assert torch.equal(pm(xd, qgu, qd), first)
@@ -185,3 +185,34 @@ def test_mlp_bf16_weights(dev, M):
     assert rel_err(y.cpu().numpy(), ref) <= TOL
     # the same kernels as the two GEMV calls
     assert torch.equal(out, G.gemv(G.gemv_swiglu(h.to(dev), wgu.to(dev)), wd.to(dev), 4))
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_mlp_default_is_the_two_launch_pair(dev, M):
+    """PersistentMLP's default form for FP8 weights is the two GEMV launches: bit-identical to
+    calling them directly."""
+    wgu, wd, x = case(M, H, I, 90 + M)
+    qgu, qd = fp8.quantize(wgu.to(dev)), fp8.quantize(wd.to(dev))
+    xd = x.to(dev)
+    out = PersistentMLP(M, H, I, dev)(xd, qgu, qd)
+    assert torch.equal(out, fp8.gemv_fp8(fp8.gemv_swiglu_fp8(xd, qgu), qd, 4))
+
+
+def test_mlp_wait_timeout_poisons_partials(dev):
+    """A phase-1 wait that gives up (forced from the host with a bound of 0 polls) sets the error
+    word and makes that block's partials NaN; every other partial equals the good launch's. The
+    kernel still ends (every wait is bounded) and the next launch is good again."""
+    M, h_, i_ = 16, 512, 1024
+    wgu, wd, x = case(M, h_, i_, 61)
+    qgu, qd = fp8.quantize(wgu.to(dev)), fp8.quantize(wd.to(dev))
+    xd = x.to(dev)
+    good = PersistentMLP(M, h_, i_, dev, one_launch=True)(xd, qgu, qd)
+    pm = PersistentMLP(M, h_, i_, dev, one_launch=True)
+    out = pm(xd, qgu, qd, max_polls=0)
+    torch.cuda.synchronize()
+    nan = torch.isnan(out)
+    print(f"timed-out partials: {int(nan.sum())} of {out.numel()}, flagged {pm.failed()}")
+    assert torch.equal(out[~nan], good[~nan])
+    assert pm.failed() == bool(nan.any())
+    pm.ctl.zero_()
+    assert torch.equal(pm(xd, qgu, qd), good) and not pm.failed()
