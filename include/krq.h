@@ -153,18 +153,21 @@ int krq_gemv_bf16(const void* x, const void* w, int w_layout, int64_t M, int64_t
  * then a per-row fold).
  * w_kind KRQ_LM_BF16: h bf16 [M,K], w bf16 [V,K] in w_layout (row-major, or tiled as for
  *                     krq_gemv_bf16); h_scale / w_scale unused.
- * w_kind KRQ_LM_FP8:  w e4m3 [V,K] in w_layout with per-row w_scale[V]; h e4m3 [M,K] with
- *                     per-token h_scale[M], or (h_scale NULL, M == 1) h bf16 [1,K] scaled per
- *                     token inside the kernel; logits as krq_gemv_fp8 KRQ_OUT_BF16.
+ * w_kind KRQ_LM_FP8:  w e4m3 [V,K] in w_layout with w_scale[V] (w_per_row = 1, per channel) or
+ *                     w_scale[1] (w_per_row = 0, per tensor: the engine's quantize_weight lm8,
+ *                     engine.py:504-505); h e4m3 [M,K] with h_scale[M] (h_per_row = 1, per token)
+ *                     or h_scale[1] (h_per_row = 0, one scale: linear_fp8's ActScale or a
+ *                     SharedScale, engine.py:989), or (h_scale NULL, M == 1) h bf16 [1,K] scaled
+ *                     per token inside the kernel; logits as krq_gemv_fp8 KRQ_OUT_BF16.
  * w_kind KRQ_LM_FP8_TILED_H: as KRQ_LM_FP8 with h e4m3 in the tiled activation layout of
- *                     krq_quant_rows_tiled and its h_scale[M] (no reference counterpart: the same
+ *                     krq_quant_rows_tiled and its h_scale (no reference counterpart: the same
  *                     operands, contiguous loads).
  * logits: optional bf16 [M,V] output (NULL to skip). ws: scratch of at least
  * krq_lmhead_ws_bytes(M, V) bytes (overwritten; calls that overlap must not share it).
  */
-int krq_lmhead_argmax(const void* h, const float* h_scale, const void* w, int w_kind, int w_layout,
-                      const float* w_scale, int64_t M, int64_t V, int64_t K, void* logits,
-                      void* ws, int64_t ws_bytes, int64_t* idx_out, void* stream);
+int krq_lmhead_argmax(const void* h, const float* h_scale, int h_per_row, const void* w, int w_kind,
+                      int w_layout, const float* w_scale, int w_per_row, int64_t M, int64_t V, int64_t K,
+                      void* logits, void* ws, int64_t ws_bytes, int64_t* idx_out, void* stream);
 int64_t krq_lmhead_ws_bytes(int64_t M, int64_t V);
 
 /*
@@ -178,8 +181,9 @@ int64_t krq_lmhead_ws_bytes(int64_t M, int64_t V);
  * (KRQ_X_BF16_DYN, M == 1). Both weights in w_layout with per-row (or per-tensor) scales.
  * act: bf16 [M,I] workspace (also an output: the SwiGLU activations).
  * ctl: krq_mlp_ctl_words() uint32 words, zero before the first call; the kernel leaves them zero
- *      again, except the last word, which it sets to 1 if a block waited too long for phase 1
- *      (then the output is not valid). Calls sharing ctl must not overlap.
+ *      again, except the last word, which it sets to 1 if a block waited too long for phase 1.
+ *      Such a block writes NaN to every partial it owns, so an incomplete result never passes
+ *      as data. Calls sharing ctl must not overlap.
  * programs: number of blocks (0 = one per CU); clamped to what the device holds at once.
  * Needs H % 64 == 0, I % 16 == 0, (I/split) % 64 == 0 and M*I/split within the kernel's staging
  * limit (raise split for large M).
@@ -188,6 +192,12 @@ int krq_mlp_fp8(const void* x, int x_kind, const float* x_scale, const void* w_g
                 const float* gu_scale, int gu_per_row, const void* w_down, const float* down_scale,
                 int down_per_row, int64_t M, int64_t H, int64_t I, int split, void* act,
                 uint32_t* ctl, int programs, void* out, void* stream);
+/* krq_mlp_fp8 with the phase-1 wait bounded at max_polls polls instead of about a second's worth
+ * (no counterpart in the reference: lets a test force the timeout path from the host). */
+int krq_mlp_fp8_bounded(const void* x, int x_kind, const float* x_scale, const void* w_gu, int w_layout,
+                        const float* gu_scale, int gu_per_row, const void* w_down, const float* down_scale,
+                        int down_per_row, int64_t M, int64_t H, int64_t I, int split, void* act,
+                        uint32_t* ctl, int programs, uint32_t max_polls, void* out, void* stream);
 int64_t krq_mlp_ctl_words(void);
 
 /*

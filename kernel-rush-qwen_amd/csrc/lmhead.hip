@@ -100,10 +100,10 @@ extern "C" int64_t krq_lmhead_ws_bytes(int64_t M, int64_t V) {
   return (V / 16) * M * (int64_t)sizeof(Best);
 }
 
-extern "C" int krq_lmhead_argmax(const void* h, const float* h_scale, const void* w, int w_kind,
-                                 int w_layout, const float* w_scale, int64_t M, int64_t V, int64_t K,
-                                 void* logits, void* ws, int64_t ws_bytes, int64_t* idx_out,
-                                 void* stream) {
+extern "C" int krq_lmhead_argmax(const void* h, const float* h_scale, int h_per_row, const void* w,
+                                 int w_kind, int w_layout, const float* w_scale, int w_per_row, int64_t M,
+                                 int64_t V, int64_t K, void* logits, void* ws, int64_t ws_bytes,
+                                 int64_t* idx_out, void* stream) {
   KRQ_REQUIRE(h && w && ws && idx_out, "lmhead_argmax: null pointer");
   KRQ_REQUIRE(M >= 1 && M <= 32, "lmhead_argmax: M=%lld outside 1..32", (long long)M);
   KRQ_REQUIRE(w_kind == KRQ_LM_BF16 || w_kind == KRQ_LM_FP8 || w_kind == KRQ_LM_FP8_TILED_H,
@@ -121,10 +121,11 @@ extern "C" int krq_lmhead_argmax(const void* h, const float* h_scale, const void
   if (w_kind == KRQ_LM_BF16)
     rc = gemv_bf16_run(h, w, w_layout, M, V, K, 1, kOutArgmax, logits, ws, stream);
   else if (h_scale)
-    rc = gemv_fp8_run(h, w_kind == KRQ_LM_FP8_TILED_H ? KRQ_X_FP8_TILED : KRQ_X_FP8, h_scale, nullptr, M > 1, w,
-                      w_layout, w_scale, 1, M, V, K, 1, kOutArgmax, 0, logits, ws, stream);
+    rc = gemv_fp8_run(h, w_kind == KRQ_LM_FP8_TILED_H ? KRQ_X_FP8_TILED : KRQ_X_FP8, h_scale, nullptr,
+                      h_per_row != 0 && M > 1, w, w_layout, w_scale, w_per_row != 0, M, V, K, 1, kOutArgmax, 0,
+                      logits, ws, stream);
   else
-    rc = gemv_fp8_run(h, KRQ_X_BF16_DYN, nullptr, nullptr, 0, w, w_layout, w_scale, 1, M, V, K, 1,
+    rc = gemv_fp8_run(h, KRQ_X_BF16_DYN, nullptr, nullptr, 0, w, w_layout, w_scale, w_per_row != 0, M, V, K, 1,
                       kOutArgmax, 0, logits, ws, stream);
   if (rc != KRQ_OK) return rc;
   hipLaunchKernelGGL(k_argmax_fold, dim3(static_cast<unsigned>(M)), dim3(kFoldThreads), 0,

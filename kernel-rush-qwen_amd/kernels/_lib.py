@@ -34,11 +34,13 @@ EXPORTS = {
     "krq_gemv_fp8": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64,
                             _i32, _i32, _i32, _vp, _vp]),
     "krq_gemv_bf16": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp]),
-    "krq_lmhead_argmax": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp, _i64, _i64, _i64, _vp, _vp, _i64,
-                                 _vp, _vp]),
+    "krq_lmhead_argmax": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _i64, _i64, _i64, _vp, _vp,
+                                 _i64, _vp, _vp]),
     "krq_lmhead_ws_bytes": (_i64, [_i64, _i64]),
     "krq_mlp_fp8": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64,
                            _i32, _vp, _vp, _i32, _vp, _vp]),
+    "krq_mlp_fp8_bounded": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _i32, _i64, _i64,
+                                   _i64, _i32, _vp, _vp, _i32, ctypes.c_uint32, _vp, _vp]),
     "krq_mlp_ctl_words": (_i64, []),
     "krq_gemv_bf16_fused": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _f32, _vp,
                                    _vp, _vp, _vp, _vp, _vp]),

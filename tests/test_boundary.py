@@ -66,13 +66,14 @@ def test_invalid_arguments_fail_before_any_launch():
     rc = lib.krq_rmsnorm_quant_rows_tiled(p, p, p, 1e-6, 2, 2576, p, p, _null())
     assert rc == L.KRQ_EINVAL and b"multiple of 64" in lib.krq_last_error()
     # the tiled e4m3 lm_head rows need their per-row scales
-    rc = lib.krq_lmhead_argmax(p, None, p, L.LM_FP8_TILED_H, 1, p, 16, 1024, 256, None, p, 1 << 20, p, _null())
+    rc = lib.krq_lmhead_argmax(p, None, 1, p, L.LM_FP8_TILED_H, 1, p, 1, 16, 1024, 256, None, p, 1 << 20, p,
+                               _null())
     assert rc == L.KRQ_EINVAL and b"h_scale" in lib.krq_last_error()
     # null pointers
     rc = lib.krq_quant_fp8_rows(None, 16, 64, 64, p, None, p, _null())
     assert rc == L.KRQ_EINVAL
     # workspace too small
-    rc = lib.krq_lmhead_argmax(p, None, p, 0, 0, None, 1, 1024, 256, None, p, 8, p, _null())
+    rc = lib.krq_lmhead_argmax(p, None, 0, p, 0, 0, None, 0, 1, 1024, 256, None, p, 8, p, _null())
     assert rc == L.KRQ_EINVAL and b"workspace" in lib.krq_last_error()
     with pytest.raises(ValueError):
         L.call("krq_pack_fp8", p, 17, 64, p, _null())

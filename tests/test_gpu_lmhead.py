@@ -1,0 +1,196 @@
+"""LM head + greedy argmax at the real vocabulary (V = 151,936, K = 2,560), over
+eight hidden-state seeds per M, for the BF16 tied head (engine.py:1021-1022), the per-channel FP8
+head, and the engine's per-tensor FP8 head (lm8 = quantize_weight(lm_head), engine.py:504-505,
+called as linear_fp8(h, lm8) then torch.argmax, engine.py:989, :1022) both through linear_fp8 and
+through the fused lm_head_argmax.
+
+The reference index is the oracle's: argmax (lowest index of the maximum) of the bf16-rounded
+exact logits. A kernel accumulating K exact products in fp32, in any order, and applying two fp32
+scale multiplies is within E = K * 2^-24 * S + 2^-22 * |y| of the exact logit y (S = the scaled
+sum of |products|). Every logit that can reach the top after that error, C = {j : y_j >=
+y_1 - 2E - ulp(y_1)}, decides the kernel's argmax: if C is the top logit alone, no other logit
+can reach its bf16 value; otherwise, if each of them lies farther than E from a bf16 rounding
+midpoint, the kernel's bf16 logits of C equal the oracle's. Either way the index is identical,
+which the test then asserts. A row where some candidate sits within E of a midpoint is
+reported as inside the bound (its fp64 top-2 margin is printed) and must still pick a logit
+within the bound of the maximum.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from kernels import fp8, lmhead
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+V, K = 151936, 2560
+SEEDS = range(8)
+TOL = 1e-2
+
+
+def u16(t):
+    return t.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def u8(t):
+    return t.cpu().contiguous().view(torch.uint8).numpy()
+
+
+def rel_err(y, ref):
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.abs(y - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def hidden(M, seed):
+    g = torch.Generator().manual_seed(100 + M + 1000 * seed)
+    return torch.randn(M, K, generator=g).to(torch.bfloat16)
+
+
+def _bf16_ulp(v):
+    e = np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+def check_rows(idx, y, S, what):
+    """idx: the kernel's int64 [M]; y: exact logits float64 [M, V]; S: scaled sums of |products|
+    [M, V]. Asserts the identical index on every row the fp32 bound decides; returns the number of
+    rows inside the bound."""
+    ref = O.argmax_lowest(O.round_bf16(y.astype(np.float32)))
+    inside = 0
+    for m in range(y.shape[0]):
+        ym, sm = y[m], S[m]
+        E = K * 2.0 ** -24 * sm + 2.0 ** -22 * np.abs(ym)
+        top2 = np.partition(ym, -2)[-2:]
+        y1, margin = top2[1], top2[1] - top2[0]
+        ulp = _bf16_ulp(y1)
+        cand = np.nonzero(ym >= y1 - 2 * E.max() - ulp)[0]
+        a = np.abs(ym[cand]).astype(np.float64)    # bf16 rounding is symmetric in the sign
+        u = _bf16_ulp(a)
+        lo = np.floor(a / u) * u                    # bf16 grid point at or below a
+        u_dn = _bf16_ulp(lo * (1 - 2.0 ** -10))     # spacing just below lo (u / 2 at a power of two)
+        dist = np.minimum(np.abs(a - (lo + u / 2)), np.abs(a - (lo - u_dn / 2)))
+        # one candidate: no other logit can reach its bf16 value, however it rounds
+        stable = cand.size == 1 or bool(np.all(dist > E[cand]))
+        if stable:
+            assert idx[m] == ref[m], f"{what} row {m}: {idx[m]} vs oracle {ref[m]} (margin {margin:.3e})"
+        else:
+            inside += 1
+            print(f"  {what} row {m}: inside the fp32 bound (top-2 margin {margin:.3e}, "
+                  f"{cand.size} candidates, E {E[cand].max():.2e}); kernel {idx[m]}, oracle {ref[m]}")
+            assert ym[idx[m]] >= y1 - 2 * E.max() - ulp
+    return inside
+
+
+@pytest.fixture(scope="module")
+def head(dev):
+    """The tied embedding (seed 7) and its exact float64 forms, built once for the module."""
+    E = (torch.randn(V, K, generator=torch.Generator().manual_seed(7)) * 0.02).to(torch.bfloat16)
+    Ed = E.to(dev)
+    Ef = O.bf16_to_f32(u16(E)).astype(np.float64)
+    q_pc = fp8.quantize(Ed)
+    q_pt = fp8.quantize_weight(Ed)
+    w_pc = O.e4m3_decode(u8(q_pc[0])).astype(np.float64)
+    w_pt = O.e4m3_decode(u8(q_pt[0])).astype(np.float64)
+    r8, rs = O.quantize(u16(E))
+    assert np.array_equal(u8(q_pc[0]), r8) and np.array_equal(q_pc[1].cpu().numpy(), rs)
+    t8, ts = O.quantize_weight(u16(E))
+    assert np.array_equal(u8(q_pt[0]), t8) and q_pt[1].item() == ts
+    return dict(E=E, Ed=Ed, Ef=Ef, q_pc=q_pc, q_pt=q_pt, w_pc=w_pc, w_pt=w_pt,
+                Ef_abs=np.abs(Ef), w_pc_abs=np.abs(w_pc), w_pt_abs=np.abs(w_pt),
+                s_pc=q_pc[1].cpu().numpy().astype(np.float64), s_pt=float(q_pt[1].item()))
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_lmhead_bf16_argmax_seeds(dev, head, M):
+    inside = 0
+    for seed in SEEDS:
+        h = hidden(M, seed)
+        hf = O.bf16_to_f32(u16(h)).astype(np.float64)
+        y = hf @ head["Ef"].T
+        S = np.abs(hf) @ head["Ef_abs"].T
+        idx, logits = lmhead.lm_head_argmax(h.to(dev), head["Ed"], return_logits=True)
+        idx = idx.cpu().numpy()
+        lg = logits.float().cpu().numpy()
+        assert np.array_equal(idx, O.argmax_lowest(lg)), "kernel idx disagrees with its own logits"
+        assert rel_err(lg, y) <= TOL
+        inside += check_rows(idx, y, S, f"bf16 M={M} seed {seed}")
+    print(f"bf16 M={M}: {inside} of {M * len(SEEDS)} rows inside the fp32 bound")
+    assert inside <= M * len(SEEDS) // 2
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_lmhead_fp8_per_channel_argmax_seeds(dev, head, M):
+    q = head["q_pc"]
+    inside = 0
+    for seed in SEEDS:
+        h = hidden(M, seed)
+        hd = h.to(dev)
+        h8, hs = fp8.quant_rows(hd)
+        r8, rs = O.quant_rows(u16(h))
+        assert np.array_equal(u8(h8), r8) and np.array_equal(hs.cpu().numpy().reshape(-1), rs)
+        xf = O.e4m3_decode(r8).astype(np.float64)
+        scale = rs.astype(np.float64)[:, None] * head["s_pc"][None, :]
+        y = (xf @ head["w_pc"].T) * scale
+        S = (np.abs(xf) @ head["w_pc_abs"].T) * scale
+        idx, logits = lmhead.lm_head_argmax(hd, q, return_logits=True)
+        idx = idx.cpu().numpy()
+        lg = logits.float().cpu().numpy()
+        assert np.array_equal(idx, O.argmax_lowest(lg))
+        assert rel_err(lg, y) <= TOL
+        inside += check_rows(idx, y, S, f"fp8/channel M={M} seed {seed}")
+        if M > 1 and seed == 0:  # tiled e4m3 rows (the default) and row-major ones: the same logits
+            idx_r, logits_r = lmhead.lm_head_argmax(hd, q, return_logits=True, h_layout="rowmajor")
+            assert torch.equal(logits_r, logits) and np.array_equal(idx_r.cpu().numpy(), idx)
+    print(f"fp8 per-channel M={M}: {inside} of {M * len(SEEDS)} rows inside the fp32 bound")
+    assert inside <= M * len(SEEDS) // 2
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_lmhead_fp8_per_tensor_engine_path(dev, head, M):
+    """The engine's FP8 lm head: linear_fp8(h, quantize_weight(E)) + torch.argmax, and the fused
+    lm_head_argmax on the same per-tensor weights (one ActScale over h, as linear_fp8 takes),
+    both against the oracle of the same semantics (ActScale per tensor, cast, exact product)."""
+    q = head["q_pt"]
+    inside = 0
+    for seed in SEEDS:
+        h = hidden(M, seed)
+        hd = h.to(dev)
+        amax, inv, scale = O.act_scale(u16(h))
+        xf = O.e4m3_decode(O.cast(u16(h), inv)).astype(np.float64)
+        sc = float(scale) * head["s_pt"]
+        y = (xf @ head["w_pt"].T) * sc
+        S = (np.abs(xf) @ head["w_pt_abs"].T) * sc
+        lin = fp8.linear_fp8(hd, q)
+        idx_lin = torch.argmax(lin, -1).cpu().numpy()
+        assert rel_err(lin.float().cpu().numpy(), y) <= TOL
+        idx, logits = lmhead.lm_head_argmax(hd, q, return_logits=True)
+        idx = idx.cpu().numpy()
+        lg = logits.float().cpu().numpy()
+        assert np.array_equal(idx, O.argmax_lowest(lg))
+        assert rel_err(lg, y) <= TOL
+        n1 = check_rows(idx, y, S, f"fp8/tensor fused M={M} seed {seed}")
+        n2 = check_rows(idx_lin, y, S, f"fp8/tensor linear_fp8 M={M} seed {seed}")
+        inside += max(n1, n2)
+    print(f"fp8 per-tensor M={M}: {inside} of {M * len(SEEDS)} rows inside the fp32 bound")
+    assert inside <= M * len(SEEDS) // 2
+
+
+def test_lmhead_fp8_static_scale(dev, head):
+    """lm_head_argmax with a SharedScale (the engine's static decode scale, engine.py:977-989):
+    the cast of linear_fp8(h, lm8, a), the same logits bit for bit where the launch shapes agree
+    (M = 16: one e4m3 operand, one scale), and the oracle's argmax on decided rows."""
+    M = 16
+    q = head["q_pt"]
+    h = hidden(M, 11)
+    hd = h.to(dev)
+    a = fp8.SharedScale(torch.tensor([448.0 / 6.0], device=dev), torch.tensor(6.0 / 448.0, device=dev))
+    idx, logits = lmhead.lm_head_argmax(hd, q, return_logits=True, a=a)
+    xf = O.e4m3_decode(O.cast(u16(h), np.float32(448.0 / 6.0))).astype(np.float64)
+    sc = float(np.float32(6.0 / 448.0)) * head["s_pt"]
+    y = (xf @ head["w_pt"].T) * sc
+    S = (np.abs(xf) @ head["w_pt_abs"].T) * sc
+    assert rel_err(logits.float().cpu().numpy(), y) <= TOL
+    check_rows(idx.cpu().numpy(), y, S, "fp8/tensor static M=16")
