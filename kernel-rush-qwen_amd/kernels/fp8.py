@@ -205,6 +205,7 @@ def _weight_operand(q):
 
 
 FUSED_MAX_ELEMS = 8 * 64 * 64  # activation slice the GEMV can quantize in its prologue (static scale)
+TILED_ROWS_MAX_K = 16384  # longest row krq_quant_rows_tiled takes (its vector kernel's register tile)
 FUSED_MAX_ELEMS_DYN = 8 * 64 * 32  # row the GEMV can scale per token itself (M == 1)
 
 
@@ -286,10 +287,11 @@ def _activation_fp8(x, a, xs):
 
 def _tiled_rows(x, a, xs, algo):
     """bf16 rows scaled per token at 1 < M <= 32 go through quant_rows_tiled and the GEMV on tiled
-    activations (the same operands as quant_rows + the row-major e4m3 GEMV, contiguous loads)."""
+    activations (the same operands as quant_rows + the row-major e4m3 GEMV, contiguous loads);
+    rows longer than quant_rows_tiled takes use quant_rows and the row-major e4m3 GEMV."""
     M, K = x.shape
     return (xs is None and a is None and x.dtype == torch.bfloat16 and 1 < M <= DECODE_MAX_ROWS
-            and K % 64 == 0 and algo != L.ALGO_VALU)
+            and K % 64 == 0 and K <= TILED_ROWS_MAX_K and algo != L.ALGO_VALU)
 
 
 def _chunked(x8, xs, fn):
