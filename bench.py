@@ -1,28 +1,32 @@
 """Benchmark of the FP8 decode-matmul path on one MI355X.
 
-Default workload ("C2"): one Qwen3-4B decoder layer's projections at
-M = 1 - QKV [6144x2560], O [2560x4096], gate_up [19456x2560] (SwiGLU epilogue), down
-[2560x9728] - with per-channel FP8 e4m3 weights and per-token dynamic FP8 activation scales.
-One step = the four projections of one layer with the reference engine's output contract
-(engine/engine.py:69, :1005): QKV split 2, O split 4, down split 4 (fp32 split-K partials),
-gate_up bf16 SwiGLU. At M = 1 each projection is one GEMV launch that quantizes its activations
-itself; at larger M the per-token quantization kernel runs first. Successive steps use the next
-of 36 layers of distinct weights (3.6 GB) so the 256 MB MALL cannot serve repeats, as the
-reference's tuner cycles layers (engine/engine.py:845-847, :887-891). The K timed steps are one
-hipGraph replay.
+BASELINE.json's metric is quoted at M = 1 and M = 16 (configs[1] "C2" and configs[2] "C3"), so
+the default workload (--config decode) measures both in one invocation. A C2 / C3 layer step is
+one Qwen3-4B decoder layer's projections - QKV [6144x2560], O [2560x4096], gate_up [19456x2560]
+(SwiGLU epilogue), down [2560x9728] - with per-channel FP8 e4m3 weights and per-token dynamic FP8
+activation scales, under the reference engine's output contract (engine/engine.py:69, :1005):
+QKV split 2, O split 4, down split 4 (fp32 split-K partials), gate_up bf16 SwiGLU. At M = 1 each
+projection is one GEMV launch that quantizes its activations itself; at M = 16 the per-token
+quantization kernel (quant_rows_tiled) runs before each GEMV. Successive steps use the next of 36
+layers of distinct weights (3.6 GB) so the 256 MB MALL cannot serve repeats, as the reference's
+tuner cycles layers (engine/engine.py:845-847, :887-891).
 
-value = algorithmic bytes of the K steps / their time, in GB/s. Bytes per projection call:
-N*K (w8) + 4N (w scale) + 2MK (bf16 x) + 4M (x scale) + output (2MN bf16, 4SMN partials,
-2MI SwiGLU).
+Headline: one step = a C2 layer step followed by a C3 layer step (another layer's weights). K
+steps are captured into one hipGraph, the graph is replayed R >= 5 times and each replay is timed
+with hipEvents between synchronizations: value = algorithmic bytes of the K steps / the median
+replay's time (the best replay is reported beside it). Each M is also timed alone the same way
+(per_m in the JSON line), with its per-projection table (graph of back-to-back launches cycling
+the 36 layers; min and median of 5 replays) and the roofline of its dominant kernel, the gate_up
+GEMV, whose HBM traffic comes from the committed rocprofv3 counter summaries
+(profiles/traffic_c2.json, traffic_c3.json). Bytes per projection call: N*K (w8) + 4N (w scale)
++ 2MK (bf16 x) + 4M (x scale) + output (2MN bf16, 4SMN partials, 2MI SwiGLU).
 
-Also printed (stderr): per-kernel table from graph-replayed back-to-back launches (hipEvents),
-and the roofline of the dominant kernel (the gate_up GEMV; its HBM traffic from the committed
-rocprofv3 counter summary). --config c3 runs M = 16, --config c3m32 M = 32, --config c4 the
-lm_head + argmax (--lm bf16|fp8, --m 1|16), --config c5 the full decode step (36 layers + lm_head).
---config layer runs the fused FP8 decoder layer (kernels.fused_gemv: O with the residual epilogue,
-gate_up with the RMSNorm prologue, down with the residual epilogue, the next QKV with the RMSNorm
-prologue, chained as engine/engine.py:953-961 chains them; --m rows), --config prefill the FP8
-prefill GEMM against the library GEMM (--m rows, default 1024).
+Other configs: c2 / c3 / c3m32 (one M alone: 1 / 16 / 32), c4 the lm_head + argmax (--lm
+bf16|fp8, --m 1|16), c5 the full decode step (36 layers + lm_head, one graph), layer the fused
+FP8 decoder layer (kernels.fused_gemv: O with the residual epilogue, gate_up with the RMSNorm
+prologue, down with the residual epilogue, the next QKV with the RMSNorm prologue, chained as
+engine/engine.py:953-961 chains them; --m rows), prefill the FP8 prefill GEMM against the library
+GEMM (--m rows, default 1024).
 """
 
 import argparse
@@ -225,7 +229,7 @@ def kernel_table(torch, fp8, L, layers, xs, M, reps):
         tmin, tmed = graph_time(torch, fn, reps)
         b = N * K + 4 * N + xbytes + 4 * M + out_bytes(M, N, split, mode)
         rows.append(dict(name=name, N=N, K=K, M=M, split=split, mode=mode, us_min=tmin, us_med=tmed,
-                         bytes=b, gbs=b / tmin / 1e3, frac=b / (tmin * 1e-6) / HBM_PEAK))
+                         bytes=b, gbs=b / tmed / 1e3, frac=b / (tmed * 1e-6) / HBM_PEAK))
 
     def bf16_fn(x, name, split, m, algo):
         o = fp8.gemv_fp8_bf16_launch(x, layers[0][name], split, m, None, algo)
@@ -255,34 +259,37 @@ def kernel_table(torch, fp8, L, layers, xs, M, reps):
             add(name + "/valu", N, K, split, mode, bf16_fn(x, name, split, m, L.ALGO_VALU), 2 * M * K)
         else:
             add(name + "/rowx", N, K, split, mode, rowx_fn(x, name, split, m), M * K)
-    if M > 1:
-        x = xs["down"]
-        tq, tqm = graph_time(torch, lambda i: fp8.quant_rows_tiled(x), reps)
-        qb = 3 * M * I + 4 * M
-        rows.append(dict(name="quant_rows", N=0, K=I, M=M, split=1, mode="-", us_min=tq, us_med=tqm,
-                         bytes=qb, gbs=qb / tq / 1e3, frac=qb / (tq * 1e-6) / HBM_PEAK))
+    if M > 1:  # the per-token quantizer launch in front of each GEMV, per activation width
+        for name, K in (("quant/qkv,gu", H), ("quant/o", NQD), ("quant/down", I)):
+            x = xs["down"] if K == I else xs["o"] if K == NQD else xs["qkv"]
+            tq, tqm = graph_time(torch, lambda i: fp8.quant_rows_tiled(x), reps)
+            qb = 2 * M * K + 16 * ((M + 15) // 16) * K + 4 * M
+            rows.append(dict(name=name, N=0, K=K, M=M, split=1, mode="-", us_min=tq, us_med=tqm,
+                             bytes=qb, gbs=qb / tqm / 1e3, frac=qb / (tqm * 1e-6) / HBM_PEAK))
     return rows
 
 
-def cpu_baseline(torch, M, budget_s):
+def cpu_baseline(torch, Ms, budget_s):
     """The reference's CPU path ("torch dequant+matmul", dequant inside the timed region) on
-    this host, over the four projections of one layer; bounded to about budget_s seconds."""
+    this host, over the four projections of one layer at each M in Ms (the headline's halves);
+    bounded to about budget_s seconds in all."""
     from oracle import oracle as O
     torch.set_num_threads(os.cpu_count() or 1)
     total_b, total_t, reps_done = 0, 0.0, 0
     g = torch.Generator().manual_seed(0)
     cases = []
-    for name, N, K, split, mode in PROJ:
-        w8 = (torch.randn(N, K, generator=g) * 200).clamp(-448, 448).to(torch.float8_e4m3fn)
-        ws = torch.rand(N, generator=g) * 1e-4
-        x8 = (torch.randn(M, K, generator=g) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
-        xs = torch.rand(M, 1, generator=g) * 1e-2
-        cases.append((name, N, K, split, mode, w8, ws, x8, xs))
+    for M in Ms:
+        for name, N, K, split, mode in PROJ:
+            w8 = (torch.randn(N, K, generator=g) * 200).clamp(-448, 448).to(torch.float8_e4m3fn)
+            ws = torch.rand(N, generator=g) * 1e-4
+            x8 = (torch.randn(M, K, generator=g) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
+            xs = torch.rand(M, 1, generator=g) * 1e-2
+            cases.append((M, name, N, K, w8, ws, x8, xs))
     for c in cases:
-        O.torch_dequant_matmul(c[7], c[8], c[5], c[6])   # warm-up
+        O.torch_dequant_matmul(c[6], c[7], c[4], c[5])   # warm-up
     t_start = time.perf_counter()
     while True:
-        for name, N, K, split, mode, w8, ws, x8, xs in cases:
+        for M, name, N, K, w8, ws, x8, xs in cases:
             t0 = time.perf_counter()
             O.torch_dequant_matmul(x8, xs, w8, ws)
             total_t += time.perf_counter() - t0
@@ -298,9 +305,10 @@ def cpu_baseline(torch, M, budget_s):
                 break
     except OSError:
         pass
-    return {"value": total_b / total_t / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
+    ms = "+".join(str(m) for m in Ms)
+    return {"value": round(total_b / total_t / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"{reps_done} passes over the 4 projections of one layer at M={M} "
+            "sample": f"{reps_done} passes over the 4 projections of one layer at M={ms} "
                       f"(torch CPU dequant+matmul, bf16 out), {total_t:.1f} s of CPU time; "
                       f"host {model or platform.processor()}, os.cpu_count()={os.cpu_count()}"}
 
@@ -334,9 +342,10 @@ def measured_traffic(cfg, key):
         return None
 
 
-def timed_graph(torch, step, steps, warmup):
-    """W untimed eager steps, then K steps captured into one graph and replayed once untimed and
-    once timed between synchronizations. Returns ms for the K steps."""
+def timed_graph(torch, step, steps, warmup, replays):
+    """W untimed eager steps, then K steps captured into one graph, replayed once untimed and then
+    `replays` times, each replay timed with hipEvents between synchronizations.
+    Returns the sorted list of replay times in ms (each for K steps)."""
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
@@ -351,24 +360,59 @@ def timed_graph(torch, step, steps, warmup):
             step(i)
     g.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    g.replay()
-    e1.record()
-    e1.synchronize()
-    torch.cuda.synchronize()
+    ts = []
+    for _ in range(replays):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        g.replay()
+        e1.record()
+        e1.synchronize()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
     del g
-    return e0.elapsed_time(e1)
+    return sorted(ts)
+
+
+def median(ts):
+    return ts[len(ts) // 2]
 
 
 def print_rows(rows, reps):
     log(f"[bench] per-kernel (graph of {reps} back-to-back launches, cycling {LAYERS} layers):")
-    log(f"  {'kernel':<12} {'N':>6} {'K':>5} {'M':>3} {'S':>2} {'us(min)':>8} {'us(med)':>8} "
+    log(f"  {'kernel':<14} {'N':>6} {'K':>5} {'M':>3} {'S':>2} {'us(min)':>8} {'us(med)':>8} "
         f"{'bytes':>11} {'GB/s':>7} {'%peak':>6}")
     for r in rows:
-        log(f"  {r['name']:<12} {r['N']:>6} {r['K']:>5} {r['M']:>3} {r['split']:>2} {r['us_min']:>8.2f} "
+        log(f"  {r['name']:<14} {r['N']:>6} {r['K']:>5} {r['M']:>3} {r['split']:>2} {r['us_min']:>8.2f} "
             f"{r['us_med']:>8.2f} {r['bytes']:>11} {r['gbs']:>7.0f} {100 * r['frac']:>5.1f}%")
+
+
+def roofline_of(rows, M, L, layout, cfg):
+    """Roofline of the step's dominant kernel (the GEMV with the largest median time) from the
+    kernel table: algorithmic bytes per launch / its median launch time (hipEvents)."""
+    dom = max((r for r in rows if r["name"] in ("qkv", "o", "gate_up", "down")), key=lambda r: r["us_med"])
+    mode = {"partial": L.OUT_PARTIAL, "swiglu": L.OUT_SWIGLU, "bf16": L.OUT_BF16}[dom["mode"]]
+    key = dominant_key(M, mode, M == 1, L.W_TILED if layout == "tiled" else L.W_ROWMAJOR)
+    a = dom["bytes"] / dom["us_med"] / 1e3
+    return {"bound": "hbm", "achieved": round(a, 1), "peak": 8000.0, "unit": "GB/s",
+            "frac": round(a / 8000.0, 4), "traffic": measured_traffic(cfg, key),
+            "kernel": f"gemv_fp8 {dom['name']} [{dom['N']}x{dom['K']}] M={M} ({key})",
+            "bytes_per_launch": dom["bytes"], "us_per_launch": round(dom["us_med"], 3),
+            "us_per_launch_min": round(dom["us_min"], 3)}
+
+
+def per_m_summary(M, ts, steps, step_bytes, rows, roof):
+    t_med, t_min = median(ts), ts[0]
+    proj = {r["name"]: {"us_med": round(r["us_med"], 3), "us_min": round(r["us_min"], 3), "bytes": r["bytes"],
+                        "gbs": round(r["bytes"] / r["us_med"] / 1e3, 1),
+                        "pct_of_hbm_peak": round(100 * r["bytes"] / (r["us_med"] * 1e-6) / HBM_PEAK, 2)}
+            for r in rows if "/" not in r["name"]}
+    value = step_bytes * steps / (t_med * 1e-3) / 1e9
+    return {"M": M, "steps": steps, "replays": len(ts), "ms_per_step": round(t_med / steps, 5),
+            "ms_per_step_min": round(t_min / steps, 5), "bytes_per_step": step_bytes,
+            "value": round(value, 1), "value_best": round(step_bytes * steps / (t_min * 1e-3) / 1e9, 1),
+            "unit": "GB/s", "pct_of_hbm_peak": round(100 * value / 8000.0, 2), "kernels": proj,
+            "roofline": roof}
 
 
 def main():
@@ -376,7 +420,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c3m32", "c4", "c5", "layer", "prefill"])
+    ap.add_argument("--replays", type=int, default=7, help="timed replays of the step graph (>= 5)")
+    ap.add_argument("--config", default="decode",
+                    choices=["decode", "c2", "c3", "c3m32", "c4", "c5", "layer", "prefill"])
     ap.add_argument("--m", type=int, default=None, help="rows for --config c4 / c5 / layer (default 1) "
                     "and prefill (default 1024)")
     ap.add_argument("--lm", default="bf16", choices=["bf16", "fp8"], help="lm head weights (c4)")
@@ -385,6 +431,7 @@ def main():
     ap.add_argument("--reps", type=int, default=72, help="launches per graph in the kernel table")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-table", action="store_true", help="skip the per-kernel tables (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 256 MiB device copy (known bytes) to scale HBM counters")
     args = ap.parse_args()
@@ -392,6 +439,8 @@ def main():
         print("bench.py: this build measures one GPU only (the path runs on one GPU; sharding across "
               "GPUs is a design note, not an implementation); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.replays < 1:
+        sys.exit("bench.py: --replays must be at least 1")
 
     import torch
     from kernels import _lib as L
@@ -401,18 +450,18 @@ def main():
     cfg = args.config
     if cfg == "prefill":
         return prefill(torch, fp8, dev_rows=args.m or 1024)
-    M = {"c2": 1, "c3": 16, "c3m32": 32}.get(cfg, args.m or 1)
-    steps = args.steps or {"c4": 20, "c5": 5}.get(cfg, 360)
+    Ms = {"decode": [1, 16], "c2": [1], "c3": [16], "c3m32": [32]}.get(cfg, [args.m or 1])
+    steps = args.steps or {"c4": 20, "c5": 5, "decode": 180}.get(cfg, 360)
     warmup = args.warmup if args.warmup is not None else {"c4": 2, "c5": 1}.get(cfg, 36)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     t0 = time.time()
-    layers, xs, E, q8 = None, None, None, None
+    layers, xs, E, q8 = None, {}, None, None
     if cfg != "c4":
         layers = make_layers(torch, fp8, dev, LAYERS)
         if args.layout == "rowmajor":
             layers = [{k: fp8.FP8Weight(q[0], q[1], None) for k, q in Lw.items()} for Lw in layers]
-        xs = make_inputs(torch, dev, M)
+        xs = {M: make_inputs(torch, dev, M) for M in Ms}
     if cfg in ("c4", "c5"):
         g = torch.Generator(device=dev).manual_seed(7)
         E = (torch.randn(V, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
@@ -423,42 +472,76 @@ def main():
             if args.layout == "rowmajor":
                 q8 = fp8.FP8Weight(q8[0], q8[1], None)
             E = None
-        hg = torch.Generator().manual_seed(100 + M)
-        h = torch.randn(M, H, generator=hg).to(torch.bfloat16).to(dev)
+        hg = torch.Generator().manual_seed(100 + Ms[0])
+        h = torch.randn(Ms[0], H, generator=hg).to(torch.bfloat16).to(dev)
     torch.cuda.synchronize()
-    log(f"[bench] {cfg}: weights ready in {time.time() - t0:.1f} s; M={M}")
+    log(f"[bench] {cfg}: weights ready in {time.time() - t0:.1f} s; M={Ms}")
 
-    layer_bytes = sum(proj_bytes(M, N, K, split, mode) for _, N, K, split, mode in PROJ)
+    def layer_bytes(M):
+        return sum(proj_bytes(M, N, K, split, mode) for _, N, K, split, mode in PROJ)
 
-    def layer_step(i):
-        Lw = layers[i % LAYERS]
-        for name, N, K, split, mode in PROJ:
-            run_proj(fp8, Lw, name, xs[name], split, mode)
+    def layer_step(M, offset=0):
+        def step(i):
+            Lw = layers[(i + offset) % LAYERS]
+            for name, N, K, split, mode in PROJ:
+                run_proj(fp8, Lw, name, xs[M][name], split, mode)
+        return step
 
-    if cfg in ("c2", "c3", "c3m32"):
-        step, step_bytes = layer_step, layer_bytes
-        work = (f"{cfg.upper()}: one Qwen3-4B decoder layer's QKV/O/gate_up/down FP8 projections "
-                f"at M={M}, per-token dynamic scales, per-channel weights, cycling {LAYERS} layers")
+    per_m = {}
+    roofline = None
+    if cfg in ("decode", "c2", "c3", "c3m32"):
+        # the M = 16 half reads layers 18 apart from the M = 1 half of the same step
+        parts = [(M, layer_step(M, 18 * j)) for j, M in enumerate(Ms)]
+
+        def step(i):
+            for _, fn in parts:
+                fn(i)
+        step_bytes = sum(layer_bytes(M) for M in Ms)
+        ms_list = "+".join(str(M) for M in Ms)
+        work = (f"{'C2+C3' if cfg == 'decode' else cfg.upper()}: one Qwen3-4B decoder layer's QKV/O/gate_up/down "
+                f"FP8 projections at M={ms_list} (per step, each M on its own layer), per-token dynamic scales, "
+                f"per-channel weights, cycling {LAYERS} layers")
     elif cfg == "layer":
-        step, step_bytes, fused_stages = fused_layer(torch, dev, layers, xs, M)
+        M = Ms[0]
+        step, step_bytes, fused_stages = fused_layer(torch, dev, layers, xs[M], M)
         work = (f"fused FP8 decoder layer at M={M}: O + residual, gate_up with RMSNorm, down + residual, "
                 f"next QKV with RMSNorm (kernels.fused_gemv), per-token scales, cycling {LAYERS} layers")
     elif cfg == "c4":
         w_lm = E if E is not None else q8
         step = lambda i: lmhead.lm_head_argmax(h, w_lm)
-        step_bytes = lm_bytes(M, args.lm)
-        work = (f"C4: tied lm_head [{V}x{H}] {args.lm.upper()} GEMV fused with greedy argmax at M={M}")
+        step_bytes = lm_bytes(Ms[0], args.lm)
+        work = (f"C4: tied lm_head [{V}x{H}] {args.lm.upper()} GEMV fused with greedy argmax at M={Ms[0]}")
     else:
+        c5_layer = layer_step(Ms[0])
+
         def step(i):
             for li in range(LAYERS):
-                layer_step(li)
+                c5_layer(li)
             lmhead.lm_head_argmax(h, E)
-        step_bytes = LAYERS * layer_bytes + lm_bytes(M, "bf16")
-        work = (f"C5: full decode-step weight stream at M={M}: {LAYERS} layers x FP8 QKV/O/gate_up/down "
+        step_bytes = LAYERS * layer_bytes(Ms[0]) + lm_bytes(Ms[0], "bf16")
+        work = (f"C5: full decode-step weight stream at M={Ms[0]}: {LAYERS} layers x FP8 QKV/O/gate_up/down "
                 f"+ BF16 lm_head with argmax, one hipGraph")
 
-    ms = timed_graph(torch, step, steps, warmup)
-    value = step_bytes * steps / (ms * 1e-3) / 1e9
+    ts = timed_graph(torch, step, steps, warmup, args.replays)
+    t_med, t_min = median(ts), ts[0]
+    value = step_bytes * steps / (t_med * 1e-3) / 1e9
+    log(f"[bench] {cfg}: {args.replays} replays of {steps} steps: median {t_med / steps * 1e3:.2f} us/step, "
+        f"best {t_min / steps * 1e3:.2f} us/step, {value:.0f} GB/s ({100 * value / 8000:.1f}% of 8 TB/s)")
+
+    if cfg in ("decode", "c2", "c3", "c3m32"):
+        for M, fn in parts:
+            tsm = timed_graph(torch, fn, steps, 0, args.replays) if len(parts) > 1 else ts
+            rows = [] if args.no_table else kernel_table(torch, fp8, L, layers, xs[M], M, args.reps)
+            if rows:
+                print_rows(rows, args.reps)
+            tcfg = {1: "c2", 16: "c3", 32: "c3m32"}[M]
+            roof = roofline_of(rows, M, L, args.layout, tcfg) if rows else None
+            per_m[str(M)] = per_m_summary(M, tsm, steps, layer_bytes(M), rows, roof)
+            pm = per_m[str(M)]
+            log(f"[bench] M={M} alone: median {pm['ms_per_step'] * 1e3:.2f} us/step (best "
+                f"{pm['ms_per_step_min'] * 1e3:.2f}), {pm['value']:.0f} GB/s, {pm['pct_of_hbm_peak']:.1f}% of 8 TB/s")
+        roofs = [pm["roofline"] for pm in per_m.values() if pm["roofline"]]
+        roofline = max(roofs, key=lambda r: r["us_per_launch"]) if roofs else None
 
     if args.calibrate_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
@@ -477,43 +560,39 @@ def main():
         log(f"[bench] fused layer stages (graph of {args.reps} back-to-back launches, cycling {LAYERS} layers):")
         for r in rows:
             log(f"  {r['name']:<14} {r['us_min']:8.2f} us (median {r['us_med']:.2f})  {r['bytes']:>10} B  "
-                f"{r['bytes'] / r['us_min'] / 1e3:7.0f} GB/s")
-        dom = max(rows, key=lambda r: r["bytes"])
-        key = None
-        kern = f"fused {dom['name']} M={M}"
-        dom_bytes, dom_us = dom["bytes"], dom["us_min"]
-    elif cfg in ("c2", "c3", "c3m32"):
-        rows = kernel_table(torch, fp8, L, layers, xs, M, args.reps)
-        print_rows(rows, args.reps)
-        dom = max(rows[:4], key=lambda r: r["bytes"])
-        key = dominant_key(M, L.OUT_SWIGLU, M == 1, L.W_TILED if args.layout == "tiled" else L.W_ROWMAJOR)
-        kern = f"gemv_fp8 {dom['name']} [{dom['N']}x{dom['K']}] M={M} ({key})"
-        dom_bytes, dom_us = dom["bytes"], dom["us_min"]
-    else:
+                f"{r['bytes'] / r['us_med'] / 1e3:7.0f} GB/s")
+        dom = max(rows, key=lambda r: r["us_med"])
+        a = dom["bytes"] / dom["us_med"] / 1e3
+        roofline = {"bound": "hbm", "achieved": round(a, 1), "peak": 8000.0, "unit": "GB/s",
+                    "frac": round(a / 8000.0, 4), "traffic": None, "kernel": f"fused {dom['name']} M={Ms[0]}",
+                    "bytes_per_launch": dom["bytes"], "us_per_launch": round(dom["us_med"], 3)}
+    elif cfg in ("c4", "c5"):
         w_lm = E if E is not None else q8
         tmin, tmed = graph_time(torch, lambda i: lmhead.lm_head_argmax(h, w_lm), 8 if cfg == "c4" else 4)
         kind = "bf16" if E is not None else "fp8"
-        dom_bytes, dom_us = lm_bytes(M, kind), tmin
-        key = None
-        kern = f"lmhead_argmax {kind} [{V}x{H}] M={M}"
-        log(f"[bench] lm_head {kind} M={M}: {tmin:.2f} us (median {tmed:.2f}), "
-            f"{dom_bytes / tmin / 1e3:.0f} GB/s, {100 * dom_bytes / (tmin * 1e-6) / HBM_PEAK:.1f}% of 8 TB/s")
-    roofline = {"bound": "hbm", "achieved": round(dom_bytes / dom_us / 1e3, 1), "peak": 8000.0,
-                "unit": "GB/s", "frac": round(dom_bytes / (dom_us * 1e-6) / HBM_PEAK, 4),
-                "traffic": measured_traffic(cfg, key) if key else None,
-                "kernel": kern, "bytes_per_launch": dom_bytes, "us_per_launch": round(dom_us, 3)}
+        b = lm_bytes(Ms[0], kind)
+        a = b / tmed / 1e3
+        roofline = {"bound": "hbm", "achieved": round(a, 1), "peak": 8000.0, "unit": "GB/s",
+                    "frac": round(a / 8000.0, 4), "traffic": None,
+                    "kernel": f"lmhead_argmax {kind} [{V}x{H}] M={Ms[0]}", "bytes_per_launch": b,
+                    "us_per_launch": round(tmed, 3), "us_per_launch_min": round(tmin, 3)}
+        log(f"[bench] lm_head {kind} M={Ms[0]}: {tmed:.2f} us (min {tmin:.2f}), {a:.0f} GB/s, "
+            f"{100 * a / 8000:.1f}% of 8 TB/s")
 
     cpu = None
-    if not args.no_cpu and cfg in ("c2", "c3", "c3m32"):
-        cpu = cpu_baseline(torch, M, args.cpu_seconds)
+    if not args.no_cpu and cfg in ("decode", "c2", "c3", "c3m32"):
+        cpu = cpu_baseline(torch, Ms, args.cpu_seconds)
 
     print(json.dumps({
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
-        "steps": steps, "warmup": warmup, "ms_per_step": round(ms / steps, 5),
+        "steps": steps, "warmup": warmup, "ms_per_step": round(t_med / steps, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8_e4m3",
         "data": "synthetic (seeded N(0,0.02) weights generated on device, N(0,1) activations)",
-        "config": {"workload": work, "M": M, "bytes_per_step": step_bytes, "layout": args.layout,
-                   "pct_of_hbm_peak": round(100 * value / 8000.0, 2)},
+        "config": {"workload": work, "M": Ms if len(Ms) > 1 else Ms[0], "bytes_per_step": step_bytes,
+                   "layout": args.layout, "pct_of_hbm_peak": round(100 * value / 8000.0, 2),
+                   "replays": args.replays, "ms_per_step_min": round(t_min / steps, 5),
+                   "value_best": round(step_bytes * steps / (t_min * 1e-3) / 1e9, 1)},
+        "per_m": per_m or None,
         "roofline": roofline, "cpu_baseline": cpu}), flush=True)
 
 
