@@ -14,8 +14,8 @@ int plan_waves(int nsteps, int P, int U, int64_t blocks, bool act_wave) {
   // O and down, 160 blocks: 5.07 / 8.74 us with 4 waves against 6.50 / 8.75 with 2 at M = 1),
   // where four keep more loads in flight. The two-matrix SwiGLU block takes two waves. Beside an
   // activation wave (one-row kernel), three instead of two (four waves in all): down 7.68 -> 7.16
-  // us and the FP8 lm_head 64.7 -> 63.1 us at M = 1. With the deep rings (U of 8 or 10 beside the
-  // activation wave) the same rule gives one wave for up to U steps and two for up to 2U.
+  // us and the FP8 lm_head 64.7 -> 63.1 us at M = 1. With the deep rings (U of 8, 10 or 20 beside
+  // the activation wave) the same rule gives one wave for up to U steps and two for up to 2U.
   // Multi-row blocks (two-slot rings) on a grid smaller than the chip (the one-pass residual GEMVs,
   // 160 blocks) take up to eight waves: O + residual 8.49 -> 7.99 us, down + residual 13.32 ->
   // 12.29 at M = 16 (at M = 1 four waves stay faster: 6.20 against 7.10 us for O).
@@ -26,32 +26,61 @@ int plan_waves(int nsteps, int P, int U, int64_t blocks, bool act_wave) {
   if (blocks < 512) return 4;
   return act_wave ? 3 : 2;
 }
+
+// Ring of the multi-row matrix-core blocks (1 < M <= 16, one row block per workgroup): every step
+// of the block in flight at once. Up to 10 steps of one matrix: one weight wave of 8 or 10 slots,
+// which also writes its outputs straight from its accumulators; otherwise waves of 5 slots, at most
+// four. Measured at M = 16 on tiled e4m3 rows (graph of 72 launches over 36 layers), against the
+// earlier two-slot rings: QKV (10 steps) 5.55 -> 4.85 us, gate_up (20 steps, two matrices)
+// 11.28 -> 11.17, down (19 steps) 7.56 -> 7.44, O (8 steps) 4.51 -> 4.53.
+void rows_ring(int nsteps, int P, int* u, int* nw) {
+  if (P == 1 && nsteps <= 8) {
+    *u = 8;
+    *nw = 1;
+  } else if (P == 1 && nsteps <= 10) {
+    *u = 10;
+    *nw = 1;
+  } else {
+    *u = 5;
+    *nw = min((nsteps + 4) / 5, 4);
+  }
+}
 }  // namespace krq
 
 namespace {
 
 #define KRQ_GEMV_ARGS xb, x_scale, x_inv, x_per_row, wb, w_scale, w_per_row, m, NO, K, kts, out, aux
 
+// one-row activation wave: 16-byte chunks per lane holding the whole row (K <= 512 AWC), the
+// smallest that fits, so no lane loads a clamped repeat of the row's last chunk
+constexpr int kAwRow = 5;  // K <= 2560
+
 // one bf16 row: MT 1, no pairing; awc = chunks per lane of the activation wave (0: none); u = step
-// slots per weight wave: 4, or (activation wave, tiled matrix-core kernels) 8 or 10 for one matrix,
-// 5 for the two-matrix SwiGLU block
+// slots per weight wave: 4, or (activation wave, tiled matrix-core kernels) 8, 10 or 20 for one
+// matrix, 5 for the two-matrix SwiGLU block
 template <int MODE, int LAYOUT, int XK, int ALGO>
 void launch_row(int awc, int u, dim3 grid, dim3 block, size_t smem, hipStream_t s, const uint8_t* xb,
                 const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
                 const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out,
                 void* aux) {
   constexpr bool deep = LAYOUT == KRQ_W_TILED && ALGO == 1 && MODE != kOutArgmax;
-  constexpr int DU = MODE == KRQ_OUT_SWIGLU ? kSwiU : kDeepU, MU = MODE == KRQ_OUT_SWIGLU ? kSwiU : kMidU;
-#define KRQ_ROW_U(AWC)                                                                                       \
-  if (deep && u == DU)                                                                                       \
-    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, deep ? DU : 4, 1, AWC>), grid, block, smem, s, \
-                       KRQ_GEMV_ARGS);                                                                       \
-  else if (deep && u == MU)                                                                                  \
-    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, deep ? MU : 4, 1, AWC>), grid, block, smem, s,  \
-                       KRQ_GEMV_ARGS);                                                                       \
-  else                                                                                                       \
+  constexpr bool one = MODE != KRQ_OUT_SWIGLU;
+  constexpr int U20 = deep && one ? kBigU : 4, U10 = deep && one ? kDeepU : 4, U8 = deep && one ? kMidU : 4;
+  constexpr int U5 = deep && !one ? kSwiU : 4;
+#define KRQ_ROW_U(AWC)                                                                                         \
+  if (deep && one && u == kBigU)                                                                               \
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, U20, 1, AWC>), grid, block, smem, s, KRQ_GEMV_ARGS); \
+  else if (deep && one && u == kDeepU)                                                                         \
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, U10, 1, AWC>), grid, block, smem, s, KRQ_GEMV_ARGS); \
+  else if (deep && one && u == kMidU)                                                                          \
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, U8, 1, AWC>), grid, block, smem, s, KRQ_GEMV_ARGS); \
+  else if (deep && !one && u == kSwiU)                                                                         \
+    hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, U5, 1, AWC>), grid, block, smem, s, KRQ_GEMV_ARGS); \
+  else                                                                                                         \
     hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, ALGO, 4, 1, AWC>), grid, block, smem, s, KRQ_GEMV_ARGS);
-  if (awc == kAwSmall) {
+  if (awc == kAwRow) {
+    KRQ_ROW_U(kAwRow)
+  } else if (awc == kAwSmall) {
     KRQ_ROW_U(kAwSmall)
   } else if (awc == kAwLarge) {
     KRQ_ROW_U(kAwLarge)
@@ -61,13 +90,36 @@ void launch_row(int awc, int u, dim3 grid, dim3 block, size_t smem, hipStream_t 
 #undef KRQ_ROW_U
 }
 
+// 1 < M <= 16 on e4m3 rows (tiled or row-major), one row block per workgroup, rows_ring's slots
 template <int MODE, int LAYOUT, int XK>
-int launch(int algo, int pb, int awc, int u, int M, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* xb,
-           const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
-           const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out,
-           void* aux) {
-  const dim3 block((nw + (awc > 0 ? 1 : 0)) * 64);
+void launch_rows(int u, dim3 grid, dim3 block, size_t smem, hipStream_t s, const uint8_t* xb,
+                 const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
+                 const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out,
+                 void* aux) {
+  constexpr bool one = MODE != KRQ_OUT_SWIGLU;
+  if constexpr (XK == KRQ_X_FP8 || XK == KRQ_X_FP8_TILED) {
+    if (one && u == 10)
+      hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, one ? 10 : 5, 1, 0>), grid, block, smem, s,
+                         KRQ_GEMV_ARGS);
+    else if (one && u == 8)
+      hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, one ? 8 : 5, 1, 0>), grid, block, smem, s,
+                         KRQ_GEMV_ARGS);
+    else
+      hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, 5, 1, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
+  }
+}
+
+template <int MODE, int LAYOUT, int XK>
+int launch(int algo, int pb, int awc, int u, bool rows, int M, dim3 grid, int nthreads, size_t smem,
+           hipStream_t s, const uint8_t* xb, const float* x_scale, const float* x_inv, int x_per_row,
+           const uint8_t* wb, const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts,
+           void* out, void* aux) {
+  const dim3 block(nthreads);
   constexpr int PB2 = MODE == KRQ_OUT_SWIGLU ? 1 : 2;  // no paired variant of the SwiGLU kernel
+  if (rows) {
+    launch_rows<MODE, LAYOUT, XK>(u, grid, block, smem, s, KRQ_GEMV_ARGS);
+    return 0;
+  }
   if constexpr (XK == KRQ_X_BF16_DYN) {  // (M == 1)
     if (algo == 2)
       launch_row<MODE, LAYOUT, XK, 2>(awc, u, grid, block, smem, s, KRQ_GEMV_ARGS);
@@ -102,18 +154,20 @@ int launch(int algo, int pb, int awc, int u, int M, dim3 grid, int nw, size_t sm
 }
 
 template <int MODE, int LAYOUT>
-void launch_xk(int xk, int algo, int pb, int awc, int u, int M, dim3 grid, int nw, size_t smem, hipStream_t s,
-               const uint8_t* xb, const float* x_scale, const float* x_inv, int x_per_row,
-               const uint8_t* wb, const float* w_scale, int w_per_row, int m, int64_t NO,
-               int64_t K, int kts, void* out, void* aux) {
+void launch_xk(int xk, int algo, int pb, int awc, int u, bool rows, int M, dim3 grid, int nthreads, size_t smem,
+               hipStream_t s, const uint8_t* xb, const float* x_scale, const float* x_inv, int x_per_row,
+               const uint8_t* wb, const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts,
+               void* out, void* aux) {
+#define KRQ_XK_ARGS algo, pb, awc, u, rows, M, grid, nthreads, smem, s, KRQ_GEMV_ARGS
   if (xk == KRQ_X_FP8)
-    launch<MODE, LAYOUT, KRQ_X_FP8>(algo, pb, awc, u, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
+    launch<MODE, LAYOUT, KRQ_X_FP8>(KRQ_XK_ARGS);
   else if (xk == KRQ_X_FP8_TILED)
-    launch<MODE, LAYOUT, KRQ_X_FP8_TILED>(algo, pb, awc, u, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
+    launch<MODE, LAYOUT, KRQ_X_FP8_TILED>(KRQ_XK_ARGS);
   else if (xk == KRQ_X_BF16_DYN)
-    launch<MODE, LAYOUT, KRQ_X_BF16_DYN>(algo, pb, awc, u, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
+    launch<MODE, LAYOUT, KRQ_X_BF16_DYN>(KRQ_XK_ARGS);
   else
-    launch<MODE, LAYOUT, KRQ_X_BF16_STATIC>(algo, pb, awc, u, M, grid, nw, smem, s, KRQ_GEMV_ARGS);
+    launch<MODE, LAYOUT, KRQ_X_BF16_STATIC>(KRQ_XK_ARGS);
+#undef KRQ_XK_ARGS
 }
 
 }  // namespace
@@ -139,6 +193,9 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   KRQ_REQUIRE(algo >= 0 && algo <= 2, "gemv_fp8: bad algo %d", algo);
   KRQ_REQUIRE(algo != 2 || M == 1, "gemv_fp8: the vector-ALU kernel takes M == 1 only");
   KRQ_REQUIRE(algo != 2 || x_kind != KRQ_X_FP8_TILED, "gemv_fp8: tiled activations take the matrix-core kernel");
+  // In-kernel per-token scaling takes one row. (Scaling M > 1 rows per token inside the GEMV means
+  // every workgroup reads the whole bf16 rows for their amax: at M = 16 the QKV / O / gate_up steps
+  // measured ~14 us each that way against 4.8 + 2.5 us for quant_rows_tiled and the GEMV.)
   KRQ_REQUIRE(x_kind != KRQ_X_BF16_DYN || M == 1, "gemv_fp8: in-kernel per-token scaling takes M == 1");
   KRQ_REQUIRE(mode == KRQ_OUT_PARTIAL || split == 1, "gemv_fp8: split %d needs the partials output", split);
   KRQ_REQUIRE(mode != kOutArgmax || N <= 0x7fffffff, "gemv_fp8: N=%lld too large for int indices", (long long)N);
@@ -149,6 +206,7 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   if (algo == 0) algo = 1;
   const int kts = static_cast<int>(K / split / 64);
   const int ks = kts * 64;
+  const int nsteps = (kts + 1) / 2;
   // Paired row blocks for the multi-row matrix-core kernels. Measured: pairing halves the blocks,
   // which costs the Qwen3-4B projections (640-768 blocks) more than the saved activation reads
   // gain; the lm_head (9,496 blocks) gains 10-15%.
@@ -156,53 +214,66 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
                   (NO / 16) * split >= 4096) ? 2 : 1;
   const int P = mode == KRQ_OUT_SWIGLU ? 2 : pb;
   const int MT = (algo == 2 || M <= 16) ? 1 : 2;
-  // step slots per wave of the variant launch() picks
-  const int U = (algo == 2 || M <= 4) ? 4 : 2;
-  // one-row kind: an activation wave holding the whole row (K <= 10240), else every wave takes part
-  // in the prologue. Measured at M = 1: QKV 5.92 -> 5.29 us, O 5.15 ->
-  // 4.41, down 7.91 -> 7.16, FP8 lm_head 64.9 -> 63.1; the SwiGLU GEMV 11.24 -> 10.86 with the
-  // five-slot ring below (with four slots the activation wave did not pay: 11.45).
-  // With static scales (M == 1) the wave quantizes the slice alone.
-  int awc = 0;
-  if (x_kind == KRQ_X_BF16_DYN)
-    awc = K <= 512 * kAwSmall ? kAwSmall : K <= 512 * kAwLarge ? kAwLarge : 0;
-  if (x_kind == KRQ_X_BF16_STATIC && M == 1)
-    awc = ks <= 512 * kAwSmall ? kAwSmall : ks <= 512 * kAwLarge ? kAwLarge : 0;
-  // With fewer blocks than CUs each block's prologue is its CU's critical path, and spreading it
-  // over all waves is faster (the one-pass residual GEMVs, 160 blocks: O 6.21 against 6.65 us).
-  if (NO / 16 / pb * split < kCUs) awc = 0;
-  // Deep ring beside the activation wave (tiled single-matrix matrix-core kernels): each weight wave
-  // holds all of its steps in flight at once, one memory round trip and no masked slots. Measured at
-  // M = 1 (graph of 72 launches over 36 layers): QKV (10 steps, one wave of 10) 5.24 -> 4.84 us, O (8
-  // steps, one wave of 8) 4.38 -> 4.25, down (19 steps, two waves of 10) 7.51 -> 6.90; rings of
-  // 8 for 10 steps (two rounds) or 12 (masked slots) measured slower. The two-matrix SwiGLU block
-  // (four loads a step) takes five slots with two weight waves (ten slots spill registers).
-  const int nsteps = (kts + 1) / 2;
-  int u = U;
-  // The lm_head (argmax epilogue, 9,496 blocks) keeps four slots: 63.1 against 64.4 us.
-  if (awc > 0 && algo == 1 && w_layout == KRQ_W_TILED && mode != kOutArgmax)
-    u = mode == KRQ_OUT_SWIGLU ? kSwiU : nsteps <= kMidU ? kMidU : kDeepU;
-  int nw = plan_waves(nsteps, P, u, NO / 16 / pb * split, awc > 0);
-  // the other fused prologues hold at most kXChunks 16-byte chunks per thread
-  int64_t xchunks = 0;
-  if (x_kind == KRQ_X_BF16_DYN && awc == 0) xchunks = (K + 7) / 8;
-  if (x_kind == KRQ_X_BF16_STATIC && awc == 0) xchunks = M * (ks / 8);
-  const int xc = x_kind == KRQ_X_BF16_DYN ? kXChunksDyn : kXChunks;
-  while ((int64_t)nw * 64 * xc < xchunks && nw < kMaxThreads / 64) ++nw;
-  KRQ_REQUIRE((int64_t)nw * 64 * xc >= xchunks,
-              "gemv_fp8: activation slice of %lld elements too large for in-kernel quantization",
-              (long long)(xchunks * 8));
-  if (awc > 0) nw = min(nw, kMaxThreads / 64 - 1);
-  const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) +
-                      (x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED ? 0 : (size_t)M * ks);
+  const int64_t blocks = NO / 16 / pb * split;
+  // Multi-row blocks on e4m3 rows (1 < M <= 16, one row block per workgroup, matrix cores) take
+  // rows_ring.
+  const bool rows = M > 1 && M <= 16 && pb == 1 && algo == 1 && (x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED);
+  int awc = 0, u = 0, nw = 0, na = 0;
+  if (rows) {
+    rows_ring(nsteps, P, &u, &nw);
+  } else {
+    // one-row kind: an activation wave holding the whole row (K <= 10240), else every wave takes
+    // part in the prologue. Measured at M = 1: QKV 5.92 -> 5.29 us, O 5.15 -> 4.41, down 7.91 ->
+    // 7.16, FP8 lm_head 64.9 -> 63.1; the SwiGLU GEMV 11.24 -> 10.86 with the five-slot ring below
+    // (with four slots the activation wave did not pay: 11.45). With static scales (M == 1) the
+    // wave quantizes the slice alone.
+    auto pick = [](int64_t span) {
+      return span <= 512 * kAwRow ? kAwRow : span <= 512 * kAwSmall ? kAwSmall : span <= 512 * kAwLarge ? kAwLarge : 0;
+    };
+    if (x_kind == KRQ_X_BF16_DYN) awc = pick(K);
+    if (x_kind == KRQ_X_BF16_STATIC && M == 1) awc = pick(ks);
+    // With fewer blocks than CUs each block's prologue is its CU's critical path, and spreading it
+    // over all waves is faster (the one-pass residual GEMVs, 160 blocks: O 6.21 against 6.65 us).
+    if (blocks < kCUs) awc = 0;
+    na = awc > 0 ? 1 : 0;
+    // Deep ring beside the activation wave (tiled single-matrix matrix-core kernels): each weight
+    // wave holds all of its steps in flight at once, one memory round trip and no masked slots.
+    // Measured at M = 1 (graph of 72 launches over 36 layers): QKV (10 steps, one wave of 10)
+    // 5.24 -> 4.84 us, O (8 steps, one wave of 8) 4.38 -> 4.25, down (19 steps) two waves of 10
+    // 7.51 -> 6.90, then one wave of 20 (which also writes its outputs straight from its
+    // accumulators) 6.68 -> 6.33; rings of 8 for 10 steps (two rounds) or 12 (masked slots) measured
+    // slower. The two-matrix SwiGLU block (four loads a step) takes five slots with two weight
+    // waves (ten slots, given the registers by launch bounds of its three waves, measured slower:
+    // 10.51 -> 11.00 us). The lm_head (argmax epilogue, 9,496 blocks) keeps four slots: 63.1
+    // against 64.4 us.
+    u = (algo == 2 || M <= 4) ? 4 : 2;
+    if (awc > 0 && algo == 1 && w_layout == KRQ_W_TILED && mode != kOutArgmax)
+      u = mode == KRQ_OUT_SWIGLU ? kSwiU : nsteps <= kMidU ? kMidU : nsteps <= kDeepU ? kDeepU
+                                                               : nsteps <= kBigU ? kBigU : kDeepU;
+    nw = plan_waves(nsteps, P, u, blocks, awc > 0);
+    // the other fused prologues hold at most kXChunks 16-byte chunks per thread
+    int64_t xchunks = 0;
+    if (x_kind == KRQ_X_BF16_DYN && awc == 0) xchunks = (K + 7) / 8;
+    if (x_kind == KRQ_X_BF16_STATIC && awc == 0) xchunks = M * (ks / 8);
+    const int xc = x_kind == KRQ_X_BF16_DYN ? kXChunksDyn : kXChunks;
+    while ((int64_t)nw * 64 * xc < xchunks && nw < kMaxThreads / 64) ++nw;
+    KRQ_REQUIRE((int64_t)nw * 64 * xc >= xchunks,
+                "gemv_fp8: activation slice of %lld elements too large for in-kernel quantization",
+                (long long)(xchunks * 8));
+    if (awc > 0) nw = min(nw, kMaxThreads / 64 - 1);
+  }
+  // LDS: the weight waves' partial sums, then the bf16 kinds' quantized slice [M][ks]
+  const size_t slice = x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED ? 0 : (size_t)M * ks;
+  const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) + slice;
   const dim3 grid(static_cast<unsigned>(NO / 16 / pb), static_cast<unsigned>(split));
+  const int nthreads = (nw + na) * 64;
   const uint8_t* xb = (const uint8_t*)x;
   const uint8_t* wb = (const uint8_t*)w8;
   const int m = static_cast<int>(M);
   hipStream_t s = (hipStream_t)stream;
-#define KRQ_FP8_CASE(MODE, LAYOUT)                                                                   \
-  launch_xk<MODE, LAYOUT>(x_kind, algo, pb, awc, u, m, grid, nw, smem, s, xb, x_scale, x_inv, x_per_row, wb, \
-                          w_scale, w_per_row, m, NO, K, kts, out, aux)
+#define KRQ_FP8_CASE(MODE, LAYOUT)                                                                          \
+  launch_xk<MODE, LAYOUT>(x_kind, algo, pb, awc, u, rows, m, grid, nthreads, smem, s, xb, x_scale, x_inv, \
+                          x_per_row, wb, w_scale, w_per_row, m, NO, K, kts, out, aux)
   if (w_layout == KRQ_W_TILED) {
     if (mode == KRQ_OUT_BF16) KRQ_FP8_CASE(KRQ_OUT_BF16, KRQ_W_TILED);
     else if (mode == KRQ_OUT_PARTIAL) KRQ_FP8_CASE(KRQ_OUT_PARTIAL, KRQ_W_TILED);

@@ -39,7 +39,7 @@ constexpr int kMaxThreads = 512;
 // one-row activation wave: 16-byte chunks per lane (the whole row, K <= 64 * 8 * AWC)
 constexpr int kAwSmall = 8, kAwLarge = 20;
 // step slots of the deep-ring one-row kernels (a weight wave issues all of its steps at once)
-constexpr int kMidU = 8, kDeepU = 10, kSwiU = 5;
+constexpr int kMidU = 8, kDeepU = 10, kSwiU = 5, kBigU = 20;
 constexpr int64_t kCUs = 256;  // compute units of the MI355X
 
 // The activation wave of the one-row kernels: one extra wave per block that quantizes the block's
@@ -195,10 +195,14 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
       sv[c] = ld16(reinterpret_cast<const uint8_t*>(fa.ss_in) + 16 * min((int)threadIdx.x + c * (int)blockDim.x, nss - 1));
   }
 
+  // a block whose only weight wave writes its outputs from registers (no cross-wave sum)
+  constexpr bool DIRECT_OK = MT == 1 && PB == 1 && (MODE == KRQ_OUT_BF16 || MODE == KRQ_OUT_PARTIAL);
+  const bool direct = DIRECT_OK && nw == 1;
   // (wave index read as a scalar: the compiler then knows the branch is uniform per wave)
   if (AW && __builtin_amdgcn_readfirstlane(wave) == nw) {
     activation_wave<XK, AW ? AWC : 1, NORM, ORDER>(x, xsc, xinv, K, k0, ks, lane, xq, xs_l, fa);
     __syncthreads();  // the slice and its scale are in LDS
+    if (direct) return;
   } else {
   // scale of this thread's activation row, read now so its latency hides under the weight stream
   // (every thread loads and stores it, threads t and t + 32 the same value, so the load is not
@@ -378,6 +382,25 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
     au += __shfl_xor(au, 32, kWave);
     acc[0] = v4f{g == 0 ? a : 0.f, 0.f, 0.f, 0.f};
     accu[0] = v4f{g == 0 ? au : 0.f, 0.f, 0.f, 0.f};
+  }
+  if (direct) {
+    // lane l, element i holds output row 4 (l / 16) + i, column 16 rb + l % 16 (xs_l is in LDS:
+    // written by this wave, or by the activation wave before the barrier above)
+    if constexpr (DIRECT_OK) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = 4 * g + i;
+        if (m < M) {
+          const int64_t n = rb * 16 + r;
+          const float y = acc[0][i] * xs_l[m] * cs.g;
+          if (MODE == KRQ_OUT_BF16)
+            reinterpret_cast<uint16_t*>(out)[(int64_t)m * NO + n] = f32_to_bf16(y);
+          else
+            reinterpret_cast<float*>(out)[((int64_t)sidx * M + m) * NO + n] = y;
+        }
+      }
+    }
+    return;
   }
   stash<MT, P>(red, wave, lane, acc, accu);
   }  // weight waves
