@@ -171,6 +171,23 @@ int krq_lmhead_argmax(const void* h, const float* h_scale, int h_per_row, const 
 int64_t krq_lmhead_ws_bytes(int64_t M, int64_t V);
 
 /*
+ * krq_lmhead_argmax without the workspace argument: the call allocates nothing. No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Arguments and results are those
+ * of krq_lmhead_argmax. The argmax candidates go to a scratch array of KRQ_LMHEAD_SCRATCH_BYTES
+ * that the library holds on each GPU it runs on until the process ends; a call whose
+ * krq_lmhead_ws_bytes(M, V) exceeds it is refused with KRQ_EINVAL (4 MiB: every M <= 32 at the
+ * Qwen3 vocabulary of 151,936). stream must belong to the current device. The first call on a
+ * device resolves the array's address there (hipGetSymbolAddress; no allocation): a caller that
+ * captures the call into a graph makes one call on that device beforehand. Every call on one GPU
+ * shares its array, so calls that overlap on one GPU (two streams, two threads) race.
+ */
+#define KRQ_LMHEAD_SCRATCH_BYTES 4194304
+int krq_lmhead_argmax_noalloc(const void* h, const float* h_scale, int h_per_row, const void* w, int w_kind,
+                              int w_layout, const float* w_scale, int w_per_row, int64_t M, int64_t V,
+                              int64_t K, void* logits, int64_t* idx_out, void* stream);
+
+/*
  * Fused decode MLP, one launch: replaces PersistentMLP (reference engine/kernels/mlp.py:22-118,
  * called at engine/engine.py:911-915 and :1015) for FP8 weights, M <= 32.
  *   act[m,i]   = SwiGLU as krq_gemv_fp8 KRQ_OUT_SWIGLU of x with w_gu (e4m3 [2I,H] = [gate; up])

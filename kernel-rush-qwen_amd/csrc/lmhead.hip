@@ -8,6 +8,9 @@
 // so graph replays need no reset and the result does not depend on block scheduling.
 // Reference semantics: logits = bf16(h . E^T), torch.argmax (first maximum) - engine/engine.py:
 // 1021-1022; fused form engine/kernels/mega.py:396-441.
+#include <atomic>
+#include <mutex>
+
 #include "gemv_common.h"
 
 using namespace krq;
@@ -100,11 +103,12 @@ extern "C" int64_t krq_lmhead_ws_bytes(int64_t M, int64_t V) {
   return (V / 16) * M * (int64_t)sizeof(Best);
 }
 
-extern "C" int krq_lmhead_argmax(const void* h, const float* h_scale, int h_per_row, const void* w,
-                                 int w_kind, int w_layout, const float* w_scale, int w_per_row, int64_t M,
-                                 int64_t V, int64_t K, void* logits, void* ws, int64_t ws_bytes,
-                                 int64_t* idx_out, void* stream) {
-  KRQ_REQUIRE(h && w && ws && idx_out, "lmhead_argmax: null pointer");
+namespace {
+
+// Argument checks of both entry points (all but the workspace).
+int lmhead_check(const void* h, const float* h_scale, const void* w, int w_kind, int w_layout,
+                 const float* w_scale, int64_t M, int64_t V, const int64_t* idx_out) {
+  KRQ_REQUIRE(h && w && idx_out, "lmhead_argmax: null pointer");
   KRQ_REQUIRE(M >= 1 && M <= 32, "lmhead_argmax: M=%lld outside 1..32", (long long)M);
   KRQ_REQUIRE(w_kind == KRQ_LM_BF16 || w_kind == KRQ_LM_FP8 || w_kind == KRQ_LM_FP8_TILED_H,
               "lmhead_argmax: bad weight kind %d", w_kind);
@@ -115,8 +119,14 @@ extern "C" int krq_lmhead_argmax(const void* h, const float* h_scale, int h_per_
               "lmhead_argmax: bf16 activations with FP8 weights are scaled in the kernel for M == 1 only");
   KRQ_REQUIRE(V > 0 && V % 16 == 0 && V <= 0x7fffffff, "lmhead_argmax: V=%lld must be a positive multiple of 16",
               (long long)V);
-  KRQ_REQUIRE(ws_bytes >= krq_lmhead_ws_bytes(M, V), "lmhead_argmax: workspace of %lld bytes < %lld",
-              (long long)ws_bytes, (long long)krq_lmhead_ws_bytes(M, V));
+  return KRQ_OK;
+}
+
+// The two launches into the candidate buffer ws (krq_lmhead_ws_bytes(M, V) bytes, all of which the
+// GEMV writes before the fold reads them: nothing needs clearing between calls).
+int lmhead_launch(const void* h, const float* h_scale, int h_per_row, const void* w, int w_kind, int w_layout,
+                  const float* w_scale, int w_per_row, int64_t M, int64_t V, int64_t K, void* logits, void* ws,
+                  int64_t* idx_out, void* stream) {
   int rc;
   if (w_kind == KRQ_LM_BF16)
     rc = gemv_bf16_run(h, w, w_layout, M, V, K, 1, kOutArgmax, logits, ws, stream);
@@ -132,4 +142,90 @@ extern "C" int krq_lmhead_argmax(const void* h, const float* h_scale, int h_per_
                      (hipStream_t)stream, reinterpret_cast<const Best*>(ws), V / 16, static_cast<int>(M),
                      idx_out);
   return krq_check_launch("lmhead_argmax");
+}
+
+}  // namespace
+
+extern "C" int krq_lmhead_argmax(const void* h, const float* h_scale, int h_per_row, const void* w,
+                                 int w_kind, int w_layout, const float* w_scale, int w_per_row, int64_t M,
+                                 int64_t V, int64_t K, void* logits, void* ws, int64_t ws_bytes,
+                                 int64_t* idx_out, void* stream) {
+  const int rc = lmhead_check(h, h_scale, w, w_kind, w_layout, w_scale, M, V, idx_out);
+  if (rc != KRQ_OK) return rc;
+  KRQ_REQUIRE(ws, "lmhead_argmax: null pointer");
+  KRQ_REQUIRE(ws_bytes >= krq_lmhead_ws_bytes(M, V), "lmhead_argmax: workspace of %lld bytes < %lld",
+              (long long)ws_bytes, (long long)krq_lmhead_ws_bytes(M, V));
+  return lmhead_launch(h, h_scale, h_per_row, w, w_kind, w_layout, w_scale, w_per_row, M, V, K, logits, ws,
+                       idx_out, stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Allocation-free variant: the candidates live in `scratch`, which the code object carries, so the
+// call allocates nothing. Each GPU holds its own copy (at its own address) from the library's first
+// use on it until the process ends. In host code `scratch` names a host-side stand-in: kernels get
+// the address hipGetSymbolAddress returns for the current device, never the array's name.
+// ---------------------------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[KRQ_LMHEAD_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch[kMaxDevices];  // device address of `scratch` per device; null until resolved
+std::mutex g_scratch_mu;
+
+// The address of this device's `scratch`, resolved on the first call on the device (with it
+// current) and kept.
+int scratch_address(int dev, void** out) {
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) {
+        krq_set_error("lmhead_argmax_noalloc: hipGetSymbolAddress on device %d: %s", dev,
+                      e != hipSuccess ? hipGetErrorString(e) : "null address");
+        return KRQ_EHIP;
+      }
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return KRQ_OK;
+}
+
+}  // namespace
+
+extern "C" int krq_lmhead_argmax_noalloc(const void* h, const float* h_scale, int h_per_row, const void* w,
+                                         int w_kind, int w_layout, const float* w_scale, int w_per_row,
+                                         int64_t M, int64_t V, int64_t K, void* logits, int64_t* idx_out,
+                                         void* stream) {
+  int rc = lmhead_check(h, h_scale, w, w_kind, w_layout, w_scale, M, V, idx_out);
+  if (rc != KRQ_OK) return rc;
+  KRQ_REQUIRE(krq_lmhead_ws_bytes(M, V) <= KRQ_LMHEAD_SCRATCH_BYTES,
+              "lmhead_argmax_noalloc: M=%lld, V=%lld need %lld bytes of candidates, above the scratch "
+              "maximum of %d (use krq_lmhead_argmax with a workspace)",
+              (long long)M, (long long)V, (long long)krq_lmhead_ws_bytes(M, V), KRQ_LMHEAD_SCRATCH_BYTES);
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    krq_set_error("lmhead_argmax_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return KRQ_EHIP;
+  }
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+    if (e != hipSuccess) {
+      krq_set_error("lmhead_argmax_noalloc: hipStreamGetDevice: %s", hipGetErrorString(e));
+      return KRQ_EHIP;
+    }
+    KRQ_REQUIRE(sdev == dev, "lmhead_argmax_noalloc: stream on device %d while device %d is current", (int)sdev,
+                dev);
+  }
+  KRQ_REQUIRE(dev >= 0 && dev < kMaxDevices, "lmhead_argmax_noalloc: device %d beyond %d", dev, kMaxDevices);
+  void* ws = nullptr;
+  rc = scratch_address(dev, &ws);
+  if (rc != KRQ_OK) return rc;
+  return lmhead_launch(h, h_scale, h_per_row, w, w_kind, w_layout, w_scale, w_per_row, M, V, K, logits, ws,
+                       idx_out, stream);
 }

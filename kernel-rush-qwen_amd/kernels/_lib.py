@@ -19,6 +19,7 @@ W_ROWMAJOR, W_TILED = 0, 1
 LM_BF16, LM_FP8, LM_FP8_TILED_H = 0, 1, 2
 ALGO_AUTO, ALGO_MFMA, ALGO_VALU = 0, 1, 2
 X_FP8, X_BF16_DYN, X_BF16_STATIC, X_FP8_TILED = 0, 1, 2, 3
+LMHEAD_SCRATCH_BYTES = 4194304  # KRQ_LMHEAD_SCRATCH_BYTES
 
 _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
 
@@ -37,6 +38,8 @@ EXPORTS = {
     "krq_lmhead_argmax": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _i64, _i64, _i64, _vp, _vp,
                                  _i64, _vp, _vp]),
     "krq_lmhead_ws_bytes": (_i64, [_i64, _i64]),
+    "krq_lmhead_argmax_noalloc": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _i64, _i64, _i64, _vp,
+                                         _vp, _vp]),
     "krq_mlp_fp8": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64,
                            _i32, _vp, _vp, _i32, _vp, _vp]),
     "krq_mlp_fp8_bounded": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _i32, _i64, _i64,

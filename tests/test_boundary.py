@@ -69,6 +69,13 @@ def test_invalid_arguments_fail_before_any_launch():
     rc = lib.krq_lmhead_argmax(p, None, 1, p, L.LM_FP8_TILED_H, 1, p, 1, 16, 1024, 256, None, p, 1 << 20, p,
                                _null())
     assert rc == L.KRQ_EINVAL and b"h_scale" in lib.krq_last_error()
+    # the allocation-free lm_head: its argument checks, then its scratch limit, before any HIP call
+    rc = lib.krq_lmhead_argmax_noalloc(p, None, 1, p, L.LM_FP8_TILED_H, 1, p, 1, 16, 1024, 256, None, p,
+                                       _null())
+    assert rc == L.KRQ_EINVAL and b"h_scale" in lib.krq_last_error()
+    assert lib.krq_lmhead_ws_bytes(32, 262144) == L.LMHEAD_SCRATCH_BYTES
+    rc = lib.krq_lmhead_argmax_noalloc(p, p, 1, p, L.LM_FP8, 1, p, 1, 32, 262144 + 16, 2560, None, p, _null())
+    assert rc == L.KRQ_EINVAL and b"scratch maximum of 4194304" in lib.krq_last_error()
     # null pointers
     rc = lib.krq_quant_fp8_rows(None, 16, 64, 64, p, None, p, _null())
     assert rc == L.KRQ_EINVAL
