@@ -319,27 +319,16 @@ def lm_bytes(M, kind):
     return V * H + 4 * V + 2 * M * H + 4 * M + 8 * M
 
 
-def dominant_key(M, mode, fused, layout):
-    """The template name rocprofv3 reports for the GEMV kernel of these arguments
-    (k_gemv_fp8<MT, MODE, LAYOUT, XK, ALGO, U, PB, AWC>; the SwiGLU kernel is never paired; at
-    M = 1 with bf16 input (K = 2560) it runs beside an activation wave of 8 chunks per lane, with
-    five step slots on the tiled layout; at M > 1 it reads tiled e4m3 activations, XK 3), to look
-    up its measured HBM traffic."""
-    mt = 1 if M <= 16 else 2
-    if fused and M == 1:
-        u = 5 if layout == 1 else 4
-        return f"k_gemv_fp8<{mt}, {mode}, {layout}, 1, 1, {u}, 1, 8>"
-    u = 4 if M <= 4 else 2
-    return f"k_gemv_fp8<{mt}, {mode}, {layout}, {3 if M > 1 else 0}, 1, {u}, 1, 0>"
-
-
-def measured_traffic(cfg, key):
+def measured_traffic(cfg, name):
+    """(HBM bytes per launch, kernel template) of projection `name` from the committed counter
+    summary profiles/traffic_<cfg>.json (FETCH_SIZE + WRITE_SIZE, scaled by a known-size copy),
+    or (None, None) when there is none."""
     path = os.path.join(ROOT, "profiles", f"traffic_{cfg}.json")
     try:
-        k = json.load(open(path))["kernels"][key]
-        return int(round(k["read_bytes_median"] + k["write_bytes_median"]))
+        k = json.load(open(path))["projections"][name]
+        return int(round(k["read_bytes_median"] + k["write_bytes_median"])), k["kernel"]
     except (OSError, KeyError, ValueError):
-        return None
+        return None, None
 
 
 def timed_graph(torch, step, steps, warmup, replays):
@@ -391,12 +380,11 @@ def roofline_of(rows, M, L, layout, cfg):
     """Roofline of the step's dominant kernel (the GEMV with the largest median time) from the
     kernel table: algorithmic bytes per launch / its median launch time (hipEvents)."""
     dom = max((r for r in rows if r["name"] in ("qkv", "o", "gate_up", "down")), key=lambda r: r["us_med"])
-    mode = {"partial": L.OUT_PARTIAL, "swiglu": L.OUT_SWIGLU, "bf16": L.OUT_BF16}[dom["mode"]]
-    key = dominant_key(M, mode, M == 1, L.W_TILED if layout == "tiled" else L.W_ROWMAJOR)
+    traffic, kernel = measured_traffic(cfg, dom["name"]) if layout == "tiled" else (None, None)
     a = dom["bytes"] / dom["us_med"] / 1e3
     return {"bound": "hbm", "achieved": round(a, 1), "peak": 8000.0, "unit": "GB/s",
-            "frac": round(a / 8000.0, 4), "traffic": measured_traffic(cfg, key),
-            "kernel": f"gemv_fp8 {dom['name']} [{dom['N']}x{dom['K']}] M={M} ({key})",
+            "frac": round(a / 8000.0, 4), "traffic": traffic,
+            "kernel": f"gemv_fp8 {dom['name']} [{dom['N']}x{dom['K']}] M={M}" + (f" ({kernel})" if kernel else ""),
             "bytes_per_launch": dom["bytes"], "us_per_launch": round(dom["us_med"], 3),
             "us_per_launch_min": round(dom["us_min"], 3)}
 

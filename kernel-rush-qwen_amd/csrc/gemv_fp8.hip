@@ -170,6 +170,11 @@ void launch_xk(int xk, int algo, int pb, int awc, int u, bool rows, int M, dim3 
 #undef KRQ_XK_ARGS
 }
 
+// Activation-wave chunks per lane holding `span` bf16 elements (0: too long for one wave).
+int aw_chunks(int64_t span) {
+  return span <= 512 * kAwRow ? kAwRow : span <= 512 * kAwSmall ? kAwSmall : span <= 512 * kAwLarge ? kAwLarge : 0;
+}
+
 }  // namespace
 
 int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const float* x_inv,
@@ -207,6 +212,10 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   const int kts = static_cast<int>(K / split / 64);
   const int ks = kts * 64;
   const int nsteps = (kts + 1) / 2;
+  const uint8_t* xb = (const uint8_t*)x;
+  const uint8_t* wb = (const uint8_t*)w8;
+  const int m = static_cast<int>(M);
+  hipStream_t s = (hipStream_t)stream;
   // Paired row blocks for the multi-row matrix-core kernels. Measured: pairing halves the blocks,
   // which costs the Qwen3-4B projections (640-768 blocks) more than the saved activation reads
   // gain; the lm_head (9,496 blocks) gains 10-15%.
@@ -227,11 +236,8 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
     // 7.16, FP8 lm_head 64.9 -> 63.1; the SwiGLU GEMV 11.24 -> 10.86 with the five-slot ring below
     // (with four slots the activation wave did not pay: 11.45). With static scales (M == 1) the
     // wave quantizes the slice alone.
-    auto pick = [](int64_t span) {
-      return span <= 512 * kAwRow ? kAwRow : span <= 512 * kAwSmall ? kAwSmall : span <= 512 * kAwLarge ? kAwLarge : 0;
-    };
-    if (x_kind == KRQ_X_BF16_DYN) awc = pick(K);
-    if (x_kind == KRQ_X_BF16_STATIC && M == 1) awc = pick(ks);
+    if (x_kind == KRQ_X_BF16_DYN) awc = aw_chunks(K);
+    if (x_kind == KRQ_X_BF16_STATIC && M == 1) awc = aw_chunks(ks);
     // With fewer blocks than CUs each block's prologue is its CU's critical path, and spreading it
     // over all waves is faster (the one-pass residual GEMVs, 160 blocks: O 6.21 against 6.65 us).
     if (blocks < kCUs) awc = 0;
@@ -267,10 +273,6 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) + slice;
   const dim3 grid(static_cast<unsigned>(NO / 16 / pb), static_cast<unsigned>(split));
   const int nthreads = (nw + na) * 64;
-  const uint8_t* xb = (const uint8_t*)x;
-  const uint8_t* wb = (const uint8_t*)w8;
-  const int m = static_cast<int>(M);
-  hipStream_t s = (hipStream_t)stream;
 #define KRQ_FP8_CASE(MODE, LAYOUT)                                                                          \
   launch_xk<MODE, LAYOUT>(x_kind, algo, pb, awc, u, rows, m, grid, nthreads, smem, s, xb, x_scale, x_inv, \
                           x_per_row, wb, w_scale, w_per_row, m, NO, K, kts, out, aux)
@@ -297,3 +299,20 @@ extern "C" int krq_gemv_fp8(const void* x, int x_kind, const float* x_scale, con
   return gemv_fp8_run(x, x_kind, x_scale, x_inv, x_per_row, w8, w_layout, w_scale, w_per_row, M, N,
                       K, split, mode, algo, out, nullptr, stream);
 }
+
+#ifdef KRQ_TIMELINE
+// Timeline build only: copy the stamps of this file's GEMV kernels (8 slots per block, block
+// index blockIdx.y * gridDim.x + blockIdx.x) to host memory; the stamp clock's rate in kHz.
+extern "C" int krq_timeline_read(void* dst, int64_t bytes) {
+  if (bytes < 0 || bytes > (int64_t)sizeof(krq_timeline)) return KRQ_EINVAL;
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(krq_timeline), (size_t)bytes, 0, hipMemcpyDeviceToHost) == hipSuccess
+             ? KRQ_OK
+             : KRQ_EHIP;
+}
+extern "C" int krq_timeline_clock_khz(void) {
+  int dev = 0, khz = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess) return 0;
+  return khz;
+}
+#endif

@@ -22,6 +22,26 @@
 
 #include "gemv_common.h"
 
+#ifdef KRQ_TIMELINE
+// Timeline build only (compiled out of the shipped library): per block of the last launch that
+// ran, wall-clock stamps (100 MHz) at entry, activation slice ready, main loop done and outputs
+// issued (slots 0-3), and the compute unit it ran on (slot 4, __smid: XCD, shader engine, CU),
+// read back with krq_timeline_read. One copy per translation unit.
+static __device__ unsigned long long krq_timeline[8 * 65536];
+#define KRQ_STAMP(i, who)                                                                          \
+  do {                                                                                             \
+    const unsigned long long b_ = 8ull * (blockIdx.y * gridDim.x + blockIdx.x);                    \
+    if ((who) && b_ < 8ull * 65536) {                                                              \
+      krq_timeline[b_ + (i)] = wall_clock64();                                                     \
+      if ((i) == 0) krq_timeline[b_ + 4] = __smid();                                               \
+    }                                                                                              \
+  } while (0)
+#else
+#define KRQ_STAMP(i, who) \
+  do {                    \
+  } while (0)
+#endif
+
 namespace {
 using namespace krq;
 
@@ -159,6 +179,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   const int T = (int)(K >> 4);    // sum-of-squares partials per row
   uint8_t* xq = reinterpret_cast<uint8_t*>(red + nw * P * MT * 256);
   const int jcount = wave < nsteps ? (nsteps - wave + nw - 1) / nw : 0;
+  KRQ_STAMP(0, threadIdx.x == 0);
   const ColScales cs = load_col_scales<MODE, PB>(wsc, w_per_row, NO, rb);
 
   // ---- fused activation prologue, part 1: activation loads ahead of the weight stream ----
@@ -201,6 +222,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   // (wave index read as a scalar: the compiler then knows the branch is uniform per wave)
   if (AW && __builtin_amdgcn_readfirstlane(wave) == nw) {
     activation_wave<XK, AW ? AWC : 1, NORM, ORDER>(x, xsc, xinv, K, k0, ks, lane, xq, xs_l, fa);
+    KRQ_STAMP(1, lane == 0);
     __syncthreads();  // the slice and its scale are in LDS
     if (direct) return;
   } else {
@@ -313,6 +335,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
     xs_l[threadIdx.x & 31] = xs_reg;
   }
   if (FUSED) __syncthreads();
+  if constexpr (!AW) KRQ_STAMP(1, threadIdx.x == 0);
 
   // ---- main loop: consume slot u (step cc), then refill it with step cc + U ----
   v4f acc[MT], accu[MT];
@@ -383,6 +406,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
     acc[0] = v4f{g == 0 ? a : 0.f, 0.f, 0.f, 0.f};
     accu[0] = v4f{g == 0 ? au : 0.f, 0.f, 0.f, 0.f};
   }
+  KRQ_STAMP(2, threadIdx.x == 0);
   if (direct) {
     // lane l, element i holds output row 4 (l / 16) + i, column 16 rb + l % 16 (xs_l is in LDS:
     // written by this wave, or by the activation wave before the barrier above)
@@ -400,6 +424,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
         }
       }
     }
+    KRQ_STAMP(3, threadIdx.x == 0);
     return;
   }
   stash<MT, P>(red, wave, lane, acc, accu);
@@ -412,6 +437,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
     epilogue<MT, MODE, P>(red, 0, nw, M, NO, rb, sidx, xs_l, cs, out, aux);
     if (PB == 2) epilogue<MT, MODE, P>(red, 1, nw, M, NO, rbu, sidx, xs_l, ColScales{cs.u, 1.0f}, out, aux);
   }
+  KRQ_STAMP(3, threadIdx.x == 0);
 }
 
 #define KRQ_FP8_KERNEL_PARAMS                                                                             \

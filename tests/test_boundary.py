@@ -27,6 +27,8 @@ def test_library_exports_every_header_symbol():
     for name in declared:
         assert hasattr(lib, name)
     assert lib.krq_version().decode().startswith("krq")
+    # the per-block stamps exist only in the timeline build (build_lib.py --timeline)
+    assert not hasattr(lib, "krq_timeline_read")
 
 
 def test_workspace_sizes_are_host_only():
