@@ -136,8 +136,8 @@ int krq_gemv_fp8(const void* x, int x_kind, const float* x_scale, const float* x
                  void* out, void* stream);
 
 /*
- * BF16 skinny GEMM/GEMV, M <= 32: gemv / gemv_m1 / gemv_swiglu / gemv_m1_swiglu / gemv_rows
- * (reference engine/kernels/gemv.py:43-348).
+ * BF16 skinny GEMM/GEMV, M <= 32: gemv / gemv_m1 / gemv_swiglu / gemv_m1_swiglu
+ * (reference engine/kernels/gemv.py:43-266).
  *   acc = x[M,K] . w[N,K]^T in fp32; modes as krq_gemv_fp8.
  * w_layout KRQ_W_ROWMAJOR: bf16 [N,K]; KRQ_W_TILED: the tiled layout above applied to the [N, 2K]
  * byte matrix (made by krq_pack_fp8(w, N, 2K, w_tiled)).
@@ -145,6 +145,17 @@ int krq_gemv_fp8(const void* x, int x_kind, const float* x_scale, const float* x
  */
 int krq_gemv_bf16(const void* x, const void* w, int w_layout, int64_t M, int64_t N, int64_t K,
                   int split, int mode, void* out, void* stream);
+
+/*
+ * Persistent BF16 GEMV: gemv_rows(x, w, programs, swiglu) (reference engine/kernels/gemv.py:334-348,
+ * kernel :276-331; the engine's rows1 / rows2 candidates, engine.py:147-148). Exactly `programs`
+ * workgroups; workgroup p owns output rows [p N / programs, (p + 1) N / programs) over the full K.
+ *   out[M, N] = bf16(x[M,K] . w[N,K]^T), or with swiglu != 0 (w = [gate; up], [2N, K]) the
+ *   SwiGLU of gemv_swiglu; w row-major bf16. The result does not depend on `programs`.
+ * Needs 1 <= M <= 32, K % 32 == 0, programs >= 1.
+ */
+int krq_gemv_bf16_rows(const void* x, const void* w, int64_t M, int64_t N, int64_t K, int programs,
+                       int swiglu, void* out, void* stream);
 
 /*
  * LM head + greedy argmax: logits = bf16(h . E^T) and idx[m] = lowest index of the maximum bf16

@@ -6,6 +6,8 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
+
 using namespace krq;
 
 namespace {
@@ -118,6 +120,110 @@ __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x
   if (PB == 2) epilogue<MT, MODE, P>(red, 1, nw, M, NO, rbu, sidx, ones, ColScales{1.0f, 1.0f}, out, aux);
 }
 
+// Persistent row partition (the reference's gemv_rows, engine/kernels/gemv.py:270-348): exactly
+// G = gridDim.x workgroups; workgroup p owns output rows [p N / G, (p + 1) N / G) over the full K
+// and walks them in 16-row chunks, chunk c to wave c mod nw. A chunk streams its rows' whole K
+// through a ring of U step slots on the BF16 matrix cores (row-major weights: a chunk may start
+// on any row) and writes the rows it owns straight from its accumulators; lanes of rows past the
+// workgroup's range reload its last row and store nothing. One wave sums each output row, in one
+// order, so the result does not depend on G. P = 2 (SwiGLU): gate rows n, up rows N + n of the
+// [2N, K] matrix, bf16(bf16(silu(bf16 g)) * bf16 u) as gemv.py:125-130.
+template <int MT, int P, int U>
+__global__ __launch_bounds__(512) void k_gemv_bf16_rows(const uint8_t* __restrict__ x,
+                                                       const uint8_t* __restrict__ w, int M, int64_t N,
+                                                       int64_t K, void* __restrict__ out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t G = gridDim.x, pid = blockIdx.x;
+  const int64_t r0 = pid * N / G, r1 = (pid + 1) * N / G;
+  const int64_t rowb = 2 * K;
+  const int kts = static_cast<int>(K >> 5);  // 64-byte (32-element) tiles of a row
+  const int nsteps = (kts + 1) >> 1;
+  const int64_t nchunks = (r1 - r0 + 15) >> 4;
+  const uint8_t* xr[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) xr[mt] = x + (int64_t)min(mt * 16 + r, M - 1) * rowb + g * 16;
+  for (int64_t c = wave; c < nchunks; c += nw) {
+    const int64_t n0 = r0 + 16 * c, nrow = min(n0 + r, r1 - 1);
+    const uint8_t* wg = w + nrow * rowb + g * 16;
+    const uint8_t* wu = w + (N + nrow) * rowb + g * 16;  // (P == 2)
+    v4f acc[MT], accu[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+      accu[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
+    uint4 wl[U], wh[U], ul[U], uh[U], xl[U][MT], xh[U][MT];
+    // every slot load is issued (a slot past the last step reloads it and is masked where consumed)
+    auto load_slot = [&](int u, int cc) {
+      const int j = min(cc, nsteps - 1);
+      const int64_t t0 = 2 * j, t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
+      wl[u] = ld16nt(wg + t0 * 64);
+      wh[u] = ld16nt(wg + t1 * 64);
+      if (P == 2) {
+        ul[u] = ld16nt(wu + t0 * 64);
+        uh[u] = ld16nt(wu + t1 * 64);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        xl[u][mt] = ld16(xr[mt] + t0 * 64);
+        xh[u][mt] = ld16(xr[mt] + t1 * 64);
+      }
+    };
+    auto consume_slot = [&](int u, int cc) {
+      const int j = min(cc, nsteps - 1);
+      const bool ok = cc < nsteps, hi = ok && (2 * j + 1 < kts);
+      const uint4 bl = sel4(ok, wl[u]), bh = sel4(hi, wh[u]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xl[u][mt]), as_v8bf(bl), acc[mt], 0, 0, 0);
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xh[u][mt]), as_v8bf(bh), acc[mt], 0, 0, 0);
+      }
+      if (P == 2) {
+        const uint4 cl = sel4(ok, ul[u]), ch = sel4(hi, uh[u]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xl[u][mt]), as_v8bf(cl), accu[mt], 0, 0, 0);
+          accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xh[u][mt]), as_v8bf(ch), accu[mt], 0, 0, 0);
+        }
+      }
+    };
+#pragma unroll
+    for (int u = 0; u < U; ++u) load_slot(u, u);
+    __builtin_amdgcn_sched_barrier(0);
+    int base = 0;
+    for (; base + U < nsteps; base += U) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        consume_slot(u, base + u);
+        load_slot(u, base + u + U);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) consume_slot(u, base + u);
+    // lane (g, r), element i of tile mt: output row m = 16 mt + 4 g + i, column n0 + r
+    const int64_t n = n0 + r;
+    if (n < r1) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = mt * 16 + 4 * g + i;
+          if (m >= M) continue;
+          uint16_t y;
+          if (P == 2) {
+            const float gg = round_bf16(acc[mt][i]), uu = round_bf16(accu[mt][i]);
+            const float sl = round_bf16(gg / (1.0f + expf(-gg)));
+            y = f32_to_bf16(sl * uu);
+          } else {
+            y = f32_to_bf16(acc[mt][i]);
+          }
+          reinterpret_cast<uint16_t*>(out)[(int64_t)m * N + n] = y;
+        }
+    }
+  }
+}
+
 template <int MODE, int LAYOUT>
 void launch(int M, int pb, dim3 grid, int nw, size_t smem, hipStream_t s, const uint8_t* x,
             const uint8_t* w, int m, int64_t NO, int64_t K, int kts, void* out, void* aux) {
@@ -190,4 +296,36 @@ extern "C" int krq_gemv_bf16(const void* x, const void* w, int w_layout, int64_t
                              int split, int mode, void* out, void* stream) {
   KRQ_REQUIRE(mode >= KRQ_OUT_BF16 && mode <= KRQ_OUT_SWIGLU, "gemv_bf16: bad mode %d", mode);
   return gemv_bf16_run(x, w, w_layout, M, N, K, split, mode, out, nullptr, stream);
+}
+
+extern "C" int krq_gemv_bf16_rows(const void* x, const void* w, int64_t M, int64_t N, int64_t K, int programs,
+                                  int swiglu, void* out, void* stream) {
+  KRQ_REQUIRE(x && w && out, "gemv_rows: null pointer");
+  KRQ_REQUIRE(aligned16(x) && aligned16(w), "gemv_rows: x and w must be 16-byte aligned");
+  KRQ_REQUIRE(M >= 1 && M <= 32, "gemv_rows: M=%lld outside 1..32", (long long)M);
+  KRQ_REQUIRE(N > 0 && K > 0 && K % 32 == 0,
+              "gemv_rows: bad shape N=%lld K=%lld (K must be a positive multiple of 32)", (long long)N,
+              (long long)K);
+  KRQ_REQUIRE(programs >= 1, "gemv_rows: programs=%d must be at least 1", programs);
+  KRQ_REQUIRE(N <= 0x3fffffffffffll / programs, "gemv_rows: N=%lld too large", (long long)N);
+  // waves: the most 16-row chunks any workgroup owns (at most 8; more chunks loop)
+  const int64_t maxrows = (N + programs - 1) / programs;
+  const int nw = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(8, (maxrows + 15) / 16)));
+  const dim3 grid(static_cast<unsigned>(programs)), block(nw * 64);
+  const uint8_t* xb = (const uint8_t*)x;
+  const uint8_t* wb = (const uint8_t*)w;
+  const int m = static_cast<int>(M);
+  hipStream_t s = (hipStream_t)stream;
+  if (swiglu) {
+    if (M <= 16)
+      hipLaunchKernelGGL((k_gemv_bf16_rows<1, 2, 4>), grid, block, 0, s, xb, wb, m, N, K, out);
+    else
+      hipLaunchKernelGGL((k_gemv_bf16_rows<2, 2, 4>), grid, block, 0, s, xb, wb, m, N, K, out);
+  } else {
+    if (M <= 16)
+      hipLaunchKernelGGL((k_gemv_bf16_rows<1, 1, 4>), grid, block, 0, s, xb, wb, m, N, K, out);
+    else
+      hipLaunchKernelGGL((k_gemv_bf16_rows<2, 1, 4>), grid, block, 0, s, xb, wb, m, N, K, out);
+  }
+  return krq_check_launch("gemv_rows");
 }

@@ -35,6 +35,7 @@ EXPORTS = {
     "krq_gemv_fp8": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64,
                             _i32, _i32, _i32, _vp, _vp]),
     "krq_gemv_bf16": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp]),
+    "krq_gemv_bf16_rows": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _vp]),
     "krq_lmhead_argmax": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _i64, _i64, _i64, _vp, _vp,
                                  _i64, _vp, _vp]),
     "krq_lmhead_ws_bytes": (_i64, [_i64, _i64]),

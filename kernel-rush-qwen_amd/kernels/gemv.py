@@ -110,11 +110,35 @@ def gemv_m1_swiglu(x, w_gu):
 
 
 def gemv_rows(x, w, programs, swiglu=False, bn=16, bk=256, num_warps=4):
-    """Persistent-GEMV entry point of the reference (gemv.py:334-348): bf16 [M, N] out
-    (N = I and SwiGLU applied if swiglu, with w = [gate; up]). The launch shape of the HIP
-    kernel is chosen from the matrix shape, so programs / bn / bk / num_warps are accepted
-    for signature compatibility and do not change the result."""
-    return _launch(x, w, 1, L.OUT_SWIGLU if swiglu else L.OUT_BF16)
+    """Persistent GEMV over `programs` programs (reference gemv.py:334-348); bf16 [M, N] out
+    (N = I and SwiGLU applied if swiglu, with w = [gate; up]). Workgroup p of exactly `programs`
+    owns output rows [p N / programs, (p + 1) N / programs) over the full K, in 16-row chunks
+    (the reference's bn default). bn, bk and num_warps are the Triton kernel's tile sizes and warp
+    count; the HIP kernel sizes its waves from the rows a workgroup owns, so they are accepted for
+    the signature and change nothing. Every output row is summed by one wave in one order: the
+    result is the same for every `programs`. Reads the row-major bf16 w (not a packed copy)."""
+    L.require_device(x, w)
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise ValueError("gemv_rows expects bf16 x and w")
+    x = x.contiguous()
+    w = w if w.is_contiguous() else w.contiguous()
+    M, K = x.shape
+    if w.dim() != 2 or w.shape[1] != K:
+        raise ValueError(f"x [{M}, {K}] and w {tuple(w.shape)} do not match")
+    if swiglu and w.shape[0] % 2:
+        raise ValueError("gemv_rows(swiglu=True) expects w = [gate; up] with an even row count")
+    N = w.shape[0] // 2 if swiglu else w.shape[0]
+    programs = int(programs)
+
+    def one(xc):
+        out = torch.empty((xc.shape[0], N), device=x.device, dtype=torch.bfloat16)
+        L.call("krq_gemv_bf16_rows", L.ptr(xc), L.ptr(w), xc.shape[0], N, K, programs, int(bool(swiglu)),
+               L.ptr(out), L.stream(x))
+        return out
+
+    if M <= MAX_ROWS:
+        return one(x)
+    return torch.cat([one(x[m0:m0 + MAX_ROWS]) for m0 in range(0, M, MAX_ROWS)], dim=0)
 
 
 def gemv_tma(x, w, split=1):

@@ -58,6 +58,11 @@ def test_invalid_arguments_fail_before_any_launch():
     # split > 1 without the partials output
     rc = lib.krq_gemv_bf16(p, p, 0, 1, 64, 256, 2, 0, p, _null())
     assert rc == L.KRQ_EINVAL
+    # persistent BF16 GEMV: at least one program, whole 32-element K tiles
+    rc = lib.krq_gemv_bf16_rows(p, p, 1, 64, 256, 0, 0, p, _null())
+    assert rc == L.KRQ_EINVAL and b"programs=0" in lib.krq_last_error()
+    rc = lib.krq_gemv_bf16_rows(p, p, 1, 64, 200, 4, 0, p, _null())
+    assert rc == L.KRQ_EINVAL and b"multiple of 32" in lib.krq_last_error()
     # tiled activations take the matrix-core kernel; their quantizer needs K % 64 == 0
     rc = lib.krq_gemv_fp8(p, L.X_FP8_TILED, p, None, 0, p, 1, p, 1, 1, 64, 256, 1, 0, 2, p, _null())
     assert rc == L.KRQ_EINVAL and b"tiled activations" in lib.krq_last_error()

@@ -354,6 +354,32 @@ def test_gemv_swiglu_bf16_gate_up_shape(dev, M):
         assert torch.equal(gemv_m1_swiglu(x.to(dev), w.to(dev)), y)
 
 
+@pytest.mark.parametrize("M", [1, 5, 16, 32])
+@pytest.mark.parametrize("N,K,swiglu", [(6144, 2560, False), (100, 320, False), (2 * 1000, 2560, True)])
+def test_gemv_rows_programs(dev, M, N, K, swiglu):
+    """gemv_rows (reference gemv.py:270-348): workgroup p of exactly `programs` owns output rows
+    [p N / programs, (p + 1) N / programs). Against the oracle at every programs count, including
+    ranges that do not start on a 16-row boundary, more programs than rows and N not a multiple of
+    16; and bit-identical across programs counts (one wave sums each row in one order)."""
+    w, x = weight(N, K, 41 + M), act(M, K, 42 + M)
+    full = O.bf16_matmul(u16(x), u16(w))
+    if swiglu:
+        I = N // 2
+        ref = O.bf16_to_f32(O.swiglu(full[:, :I].astype(np.float32), full[:, I:].astype(np.float32)))
+    else:
+        ref = full
+    wd, xd = w.to(dev), x.to(dev)
+    first = None
+    for programs in (1, 7, 132, 256, 264, 512, N + 3):
+        y = gemv_rows(xd, wd, programs, swiglu=swiglu)
+        assert y.shape == ref.shape and y.dtype == torch.bfloat16
+        assert rel_err(y.float().cpu().numpy(), ref) <= TOL, programs
+        if first is None:
+            first = y
+        else:
+            assert torch.equal(y, first), programs
+
+
 def silu_mul_input(M, K, seed):
     """The down projection's input of BASELINE C2/C3: bf16(bf16(silu(g)) * u) of g, u ~ N(0, 1)
     bf16 pairs, rounded as engine/kernels/ops.py:171-172 rounds it (bench.py's make_inputs)."""
