@@ -98,6 +98,42 @@ def fused_layer(torch, dev, layers, xs, M):
     return step, b_o + b_gu + b_dn + b_qkv, stages
 
 
+def static_mlp(torch, fp8, dev, M):
+    """The engine's static-scale FP8 decode MLP (engine/engine.py:977-981, both sites FP8):
+    delta = linear_fp8(silu_mul(linear_fp8(h, gu8, a_gu)), down8, a_down), with per-tensor
+    weights (quantize_weight, as the engine packs gu8 / down8) and SharedScale slots filled from
+    the first layer's amax x 2 (the engine's FP8_DECODE_HEADROOM). Returns (the fused step:
+    mlp.mlp_fp8_static, two launches; the same on the unfused launches: the SwiGLU GEMV to bf16 act,
+    then linear_fp8's cast and down GEMV; algorithmic bytes per step)."""
+    from kernels.mlp import mlp_fp8_static
+    g = torch.Generator(device=dev)
+    layers = []
+    for li in range(LAYERS):
+        g.manual_seed(5000 + li)
+        gu = (torch.randn(2 * I, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        dn = (torch.randn(H, I, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        layers.append((fp8.quantize_weight(gu), fp8.quantize_weight(dn)))
+        del gu, dn
+    h = torch.randn(M, H, generator=torch.Generator().manual_seed(5100 + M)).to(torch.bfloat16).to(dev)
+
+    def shared(t):
+        a = fp8.ActScale(t, headroom=2.0)
+        return fp8.SharedScale(a.inv.clone(), a.scale.clone())
+    a_gu = shared(h)
+    a_dn = shared(fp8.gemv_swiglu_fp8(h, layers[0][0], a=a_gu))
+
+    def fused(i):
+        gu8, dn8 = layers[i % LAYERS]
+        mlp_fp8_static(h, gu8, dn8, a_gu, a_dn)
+
+    def unfused(i):
+        gu8, dn8 = layers[i % LAYERS]
+        fp8.linear_fp8(fp8.gemv_swiglu_fp8(h, gu8, a=a_gu), dn8, a_dn)
+
+    nbytes = 2 * I * H + 4 + 2 * M * H + H * I + 4 + 2 * M * H
+    return fused, unfused, nbytes
+
+
 def prefill(torch, fp8, dev_rows):
     """FP8 prefill GEMM at the four Qwen3-4B projections, M = dev_rows: krq_gemm_fp8 on e4m3
     activations against torch._scaled_mm (hipBLASLt) on the same operands, and the reference's
@@ -410,7 +446,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--replays", type=int, default=7, help="timed replays of the step graph (>= 5)")
     ap.add_argument("--config", default="decode",
-                    choices=["decode", "c2", "c3", "c3m32", "c4", "c5", "layer", "prefill"])
+                    choices=["decode", "c2", "c3", "c3m32", "c4", "c5", "layer", "mlp_static", "prefill"])
     ap.add_argument("--m", type=int, default=None, help="rows for --config c4 / c5 / layer (default 1) "
                     "and prefill (default 1024)")
     ap.add_argument("--lm", default="bf16", choices=["bf16", "fp8"], help="lm head weights (c4)")
@@ -445,7 +481,7 @@ def main():
     torch.cuda.set_device(dev)
     t0 = time.time()
     layers, xs, E, q8 = None, {}, None, None
-    if cfg != "c4":
+    if cfg not in ("c4", "mlp_static"):
         layers = make_layers(torch, fp8, dev, LAYERS)
         if args.layout == "rowmajor":
             layers = [{k: fp8.FP8Weight(q[0], q[1], None) for k, q in Lw.items()} for Lw in layers]
@@ -494,6 +530,10 @@ def main():
         step, step_bytes, fused_stages = fused_layer(torch, dev, layers, xs[M], M)
         work = (f"fused FP8 decoder layer at M={M}: O + residual, gate_up with RMSNorm, down + residual, "
                 f"next QKV with RMSNorm (kernels.fused_gemv), per-token scales, cycling {LAYERS} layers")
+    elif cfg == "mlp_static":
+        step, unfused_step, step_bytes = static_mlp(torch, fp8, dev, Ms[0])
+        work = (f"static-scale FP8 decode MLP at M={Ms[0]} (engine.py:977-981: gate_up with SiLU*up and the "
+                f"down input's cast in one launch, then down), per-tensor weights, cycling {LAYERS} layers")
     elif cfg == "c4":
         w_lm = E if E is not None else q8
         step = lambda i: lmhead.lm_head_argmax(h, w_lm)
@@ -540,6 +580,17 @@ def main():
         log("[bench] calibration copy: 268435456 bytes read, 268435456 bytes written")
         del src, dst
 
+    if cfg == "mlp_static":
+        tmin_u, tmed_u = graph_time(torch, unfused_step, args.reps)
+        tmin_f, tmed_f = graph_time(torch, step, args.reps)
+        log(f"[bench] static-scale MLP M={Ms[0]} (graph of {args.reps}, cycling {LAYERS} layers): fused (SwiGLU GEMV "
+            f"casting the down input, down GEMV) {tmed_f:.2f} us (min {tmin_f:.2f}); unfused (SwiGLU GEMV to bf16, "
+            f"linear_fp8) {tmed_u:.2f} us (min {tmin_u:.2f})")
+        a = step_bytes / tmed_f / 1e3
+        roofline = {"bound": "hbm", "achieved": round(a, 1), "peak": 8000.0, "unit": "GB/s",
+                    "frac": round(a / 8000.0, 4), "traffic": None, "kernel": f"static-scale FP8 MLP M={Ms[0]}",
+                    "bytes_per_launch": step_bytes, "us_per_launch": round(tmed_f, 3),
+                    "unfused_us": round(tmed_u, 3)}
     if cfg == "layer":
         rows = []
         for name, fn, nbytes in fused_stages:

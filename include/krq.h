@@ -136,6 +136,23 @@ int krq_gemv_fp8(const void* x, int x_kind, const float* x_scale, const float* x
                  void* out, void* stream);
 
 /*
+ * The FP8 SwiGLU GEMV with the next projection's input cast in its epilogue: the engine's
+ * static-scale decode MLP (reference engine/engine.py:977-981) computes
+ * act = silu_mul(linear_fp8(h, gu8, a_gu)) (ops.py:164-172) and then linear_fp8(act, down8, a_down),
+ * whose first step is _cast(act, a_down) (fp8.py:38-56, :104). Here, in one launch:
+ *   act[m,i]    = krq_gemv_fp8's KRQ_OUT_SWIGLU output (bf16), never stored;
+ *   x8_tiled    = e4m3(clamp(float(act) * out_inv[0], +-448)) in the tiled activation layout of
+ *                 krq_quant_rows_tiled (rows padded to 16 * ceil(M / 16), pad rows 0): the bytes of
+ *                 krq_cast_fp8(act, out_inv) permuted into that layout.
+ * The down projection then reads x8_tiled as KRQ_X_FP8_TILED with a_down's scale. Arguments as
+ * krq_gemv_fp8 (M <= 32, split 1); N = 2I with I % 64 == 0; out_inv: device fp32 [1].
+ */
+int krq_gemv_swiglu_fp8_cast(const void* x, int x_kind, const float* x_scale, const float* x_inv,
+                             int x_per_row, const void* w8, int w_layout, const float* w_scale, int w_per_row,
+                             int64_t M, int64_t N, int64_t K, const float* out_inv, void* x8_tiled,
+                             void* stream);
+
+/*
  * BF16 skinny GEMM/GEMV, M <= 32: gemv / gemv_m1 / gemv_swiglu / gemv_m1_swiglu
  * (reference engine/kernels/gemv.py:43-266).
  *   acc = x[M,K] . w[N,K]^T in fp32; modes as krq_gemv_fp8.

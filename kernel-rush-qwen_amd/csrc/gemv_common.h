@@ -233,11 +233,15 @@ KRQ_DEV ColScales load_col_scales(const float* __restrict__ wsc, int w_per_row, 
 }
 
 // P accumulator sets per wave in red; this call reads set p0 (and p0 + 1 for SwiGLU) and writes
-// row block rb.
+// row block rb. SwiGLU with aux = a device float `inv`: out receives the next projection's input,
+// e4m3(clamp(act * inv, +-448)) of the bf16 act, in the tiled activation layout (rows padded to
+// 16 MT, pad rows 0; NO % 64 == 0) instead of bf16 act.
 template <int MT, int MODE, int P>
 KRQ_DEV void epilogue(const float* red, int p0, int nw, int M, int64_t NO, int64_t rb, int split_idx,
                       const float* xs, ColScales cs, void* __restrict__ out, void* __restrict__ aux) {
   constexpr int NV = MT * 256;
+  const bool cast = MODE == KRQ_OUT_SWIGLU && aux != nullptr;
+  const float cinv = cast ? *static_cast<const float*>(aux) : 0.0f;
   for (int v = threadIdx.x; v < NV; v += blockDim.x) {
     const int mt = v >> 8, i = (v >> 6) & 3, ln = v & 63;
     const int m = mt * 16 + 4 * (ln >> 4) + i;
@@ -263,6 +267,19 @@ KRQ_DEV void epilogue(const float* red, int p0, int nw, int M, int64_t NO, int64
         if (better(c.v, c.i, b.v, b.i)) b = c;
       }
       if (valid && (ln & 15) == 0) reinterpret_cast<Best*>(aux)[rb * M + m] = b;
+      continue;
+    }
+    if (MODE == KRQ_OUT_SWIGLU && cast) {
+      uint8_t q = 0;  // pad rows m >= M
+      if (valid) {
+        const float gg = round_bf16(a * x * cs.g);
+        const float uu = round_bf16(au * x * cs.u);
+        const float sl = round_bf16(gg / (1.0f + expf(-gg)));
+        q = clamp_to_e4m3(round_bf16(sl * uu) * cinv);
+      }
+      // tile (m / 16, n / 64); lane 16 ((n % 64) / 16) + m % 16 holds bytes n % 16 of row m
+      const int64_t tile = (int64_t)(m >> 4) * (NO >> 6) + (n >> 6);
+      reinterpret_cast<uint8_t*>(out)[tile * 1024 + 16 * (16 * ((n & 63) >> 4) + (m & 15)) + (n & 15)] = q;
       continue;
     }
     if (!valid) continue;

@@ -300,6 +300,17 @@ extern "C" int krq_gemv_fp8(const void* x, int x_kind, const float* x_scale, con
                       K, split, mode, algo, out, nullptr, stream);
 }
 
+extern "C" int krq_gemv_swiglu_fp8_cast(const void* x, int x_kind, const float* x_scale, const float* x_inv,
+                                        int x_per_row, const void* w8, int w_layout, const float* w_scale,
+                                        int w_per_row, int64_t M, int64_t N, int64_t K, const float* out_inv,
+                                        void* x8_tiled, void* stream) {
+  KRQ_REQUIRE(out_inv && x8_tiled, "gemv_swiglu_fp8_cast: null pointer");
+  KRQ_REQUIRE(N > 0 && N % 128 == 0,
+              "gemv_swiglu_fp8_cast: N=%lld: the activation width N/2 must be a multiple of 64", (long long)N);
+  return gemv_fp8_run(x, x_kind, x_scale, x_inv, x_per_row, w8, w_layout, w_scale, w_per_row, M, N, K, 1,
+                      KRQ_OUT_SWIGLU, 0, x8_tiled, const_cast<float*>(out_inv), stream);
+}
+
 #ifdef KRQ_TIMELINE
 // Timeline build only: copy the stamps of this file's GEMV kernels (8 slots per block, block
 // index blockIdx.y * gridDim.x + blockIdx.x) to host memory; the stamp clock's rate in kHz.

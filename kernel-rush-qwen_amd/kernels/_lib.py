@@ -34,6 +34,8 @@ EXPORTS = {
     "krq_quant_rows_tiled": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "krq_gemv_fp8": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64,
                             _i32, _i32, _i32, _vp, _vp]),
+    "krq_gemv_swiglu_fp8_cast": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64,
+                                        _vp, _vp, _vp]),
     "krq_gemv_bf16": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp]),
     "krq_gemv_bf16_rows": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _vp]),
     "krq_lmhead_argmax": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _i64, _i64, _i64, _vp, _vp,

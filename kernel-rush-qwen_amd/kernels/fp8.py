@@ -336,6 +336,39 @@ def gemv_swiglu_fp8(x, q, a=None, xs=None, algo=L.ALGO_AUTO):
     return _chunked(x8, s, lambda xc, sc: gemv_fp8_launch(xc, sc, q, 1, L.OUT_SWIGLU, algo))
 
 
+def swiglu_cast_fp8(x, q, out_a, a=None, xs=None):
+    """gemv_swiglu_fp8(x, q, a, xs) cast for the next projection in the same launch
+    (krq_gemv_swiglu_fp8_cast): the SwiGLU epilogue writes e4m3(clamp(act * out_a.inv, +-448)) of
+    its bf16 act in the tiled activation layout of quant_rows_tiled, i.e. the bytes of
+    _cast(act, out_a) permuted, with no bf16 act stored and no cast launch. out_a is the next
+    projection's ActScale / SharedScale (device inv and scale), as the engine's static-scale decode
+    MLP passes it to linear_fp8 (engine/engine.py:977-981). M <= 32. Returns (x8_tiled uint8
+    [16 ceil(M / 16) * I], scale fp32 [1]) for gemv_fp8_tiled_launch."""
+    w, layout, ws, (N, K) = _weight_operand(q)
+    M = x.shape[0]
+    if M > DECODE_MAX_ROWS or x.shape[1] != K:
+        raise ValueError(f"swiglu_cast_fp8: x {tuple(x.shape)} against w [{N}, {K}] (M <= {DECODE_MAX_ROWS})")
+    if N % 128:
+        raise ValueError(f"swiglu_cast_fp8: the activation width {N // 2} must be a multiple of 64")
+    if xs is None and _fits_fused(x, 1, a):
+        xin = _rows(x)
+        kind, x_scale, x_inv = (L.X_BF16_DYN, None, None) if a is None else \
+            (L.X_BF16_STATIC, a.scale.reshape(1), a.inv.reshape(1))
+    elif _tiled_rows(x, a, xs, L.ALGO_AUTO):
+        xin, x_scale = quant_rows_tiled(x)
+        kind, x_inv = L.X_FP8_TILED, None
+    else:
+        xin, x_scale = _activation_fp8(x, a, xs)
+        kind, x_inv = L.X_FP8, None
+    L.require_device(xin, x_scale, x_inv, out_a.inv)
+    xpr = 1 if (x_scale is not None and x_scale.numel() == M and M > 1) else 0
+    MP = 16 * ((M + 15) // 16)
+    x8t = torch.empty((MP * (N // 2),), device=x.device, dtype=torch.uint8)
+    L.call("krq_gemv_swiglu_fp8_cast", L.ptr(xin), kind, L.ptr(x_scale), L.ptr(x_inv), xpr, L.ptr(w), layout,
+           L.ptr(ws), 1 if ws.numel() > 1 else 0, M, N, K, L.ptr(out_a.inv.reshape(1)), L.ptr(x8t), L.stream(x))
+    return x8t, out_a.scale.reshape(1)
+
+
 def gemm_fp8(x, q, a=None, xs=None):
     """Prefill FP8 GEMM (krq_gemm_fp8): bf16 [M, N] = bf16(x8 . w8^T * x_scale[m] * w_scale[n]),
     the product torch._scaled_mm gives linear_fp8 (engine/kernels/fp8.py:105-106).

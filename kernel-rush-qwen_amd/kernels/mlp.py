@@ -108,3 +108,17 @@ class PersistentMLP:
         """True if a one-launch call flagged a phase-1 wait that timed out (its partials are NaN);
         synchronizes the device."""
         return bool(self.ctl[-1].item())
+
+
+def mlp_fp8_static(h, gu8, down8, a_gu, a_down, split=1):
+    """The engine's static-scale FP8 decode MLP (engine/engine.py:977-981 with both sites in FP8):
+    linear_fp8(silu_mul(linear_fp8(h, gu8, a_gu)), down8, a_down), in two launches: the SwiGLU
+    GEMV with the down input's cast in its epilogue (fp8.swiglu_cast_fp8), then the down GEMV on
+    those tiled e4m3 rows. h bf16 [M, H] (M <= 32); gu8 / down8 from quantize_weight or quantize
+    (gu8 = [gate; up]); a_gu / a_down the sites' SharedScale (or ActScale). split == 1: bf16
+    [M, H]; split > 1: fp32 partials [split, M, H]. The SwiGLU sums come from the two-matrix
+    kernel rather than linear_fp8's [M, 2I] GEMV plus silu_mul, so the result equals the engine's
+    within the GEMM tolerance; the cast of act is bit-identical."""
+    x8t, sc = _fp8.swiglu_cast_fp8(h, gu8, a_down, a=a_gu)
+    return _fp8.gemv_fp8_tiled_launch(x8t, sc, down8, h.shape[0], split,
+                                      L.OUT_BF16 if split == 1 else L.OUT_PARTIAL)

@@ -216,3 +216,43 @@ def test_mlp_wait_timeout_poisons_partials(dev):
     assert pm.failed() == bool(nan.any())
     pm.ctl.zero_()
     assert torch.equal(pm(xd, qgu, qd), good) and not pm.failed()
+
+
+def _shared(t, headroom):
+    """A SharedScale slot pair filled the engine's way: the tensor's amax times a headroom
+    (engine.py:666-668 takes the prefill amax x FP8_DECODE_HEADROOM)."""
+    a = fp8.ActScale(t, headroom=headroom)
+    return fp8.SharedScale(a.inv.clone(), a.scale.clone())
+
+
+@pytest.mark.parametrize("M", [1, 4, 16, 32])
+@pytest.mark.parametrize("sites", ["static", "per_token", "per_channel"])
+def test_swiglu_cast_is_the_cast_of_act(dev, M, sites):
+    """fp8.swiglu_cast_fp8 writes, bit for bit, the tiled permutation (pad rows zero) of
+    _cast(act, a_down), where act is gemv_swiglu_fp8's bf16 output on the same operands: the down
+    input of the engine's static-scale decode MLP (engine.py:977-981) without the bf16 act or a
+    cast launch. With a_down's headroom below 1 some of act clamps to +-448. Then
+    mlp.mlp_fp8_static equals the down GEMV on those rows and the exact oracle of that product."""
+    from kernels.mlp import mlp_fp8_static
+    wgu, wd, x = case(M, H, I, 900 + M)
+    wq = fp8.quantize if sites == "per_channel" else fp8.quantize_weight
+    q_gu, q_d = wq(wgu.to(dev)), wq(wd.to(dev))
+    xd = x.to(dev)
+    a_gu = None if sites == "per_token" else _shared(xd, 2.0)
+    act = fp8.gemv_swiglu_fp8(xd, q_gu, a=a_gu)
+    for headroom in (2.0, 0.25):
+        a_d = _shared(act, headroom)
+        x8t, sc = fp8.swiglu_cast_fp8(xd, q_gu, a_d, a=a_gu)
+        ref8 = u8(fp8._cast(act, a_d))
+        MP = 16 * ((M + 15) // 16)
+        padded = np.zeros((MP, I), dtype=np.uint8)
+        padded[:M] = ref8
+        assert np.array_equal(u8(x8t), O.tile(padded)), headroom
+        assert np.array_equal(ref8, O.cast(u16(act), np.float32(a_d.inv.item())))
+        for split in (1, 4):
+            y = mlp_fp8_static(xd, q_gu, q_d, a_gu, a_d, split)
+            mode = L.OUT_BF16 if split == 1 else L.OUT_PARTIAL
+            assert torch.equal(y, fp8.gemv_fp8_tiled_launch(x8t, sc, q_d, M, split, mode))
+            yf = y.float().cpu().numpy() if split == 1 else y.double().sum(0).cpu().numpy()
+            _, yref = O.fp8_matmul(ref8, np.float32(sc.item()), u8(q_d[0]), q_d[1].cpu().numpy())
+            assert rel_err(yf, yref) <= TOL, (headroom, split)
