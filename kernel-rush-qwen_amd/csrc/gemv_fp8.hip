@@ -51,9 +51,6 @@ namespace {
 
 #define KRQ_GEMV_ARGS xb, x_scale, x_inv, x_per_row, wb, w_scale, w_per_row, m, NO, K, kts, out, aux
 
-// one-row activation wave: 16-byte chunks per lane holding the whole row (K <= 512 AWC), the
-// smallest that fits, so no lane loads a clamped repeat of the row's last chunk
-constexpr int kAwRow = 5;  // K <= 2560
 
 // one bf16 row: MT 1, no pairing; awc = chunks per lane of the activation wave (0: none); u = step
 // slots per weight wave: 4, or (activation wave, tiled matrix-core kernels) 8, 10 or 20 for one

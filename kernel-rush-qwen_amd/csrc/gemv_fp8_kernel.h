@@ -58,6 +58,8 @@ constexpr int kSsPerLane = 4;
 constexpr int kMaxThreads = 512;
 // one-row activation wave: 16-byte chunks per lane (the whole row, K <= 64 * 8 * AWC)
 constexpr int kAwSmall = 8, kAwLarge = 20;
+// the smallest one-row wave (K <= 2560), so no lane of a short row loads a clamped repeat of its last chunk
+constexpr int kAwRow = 5;
 // step slots of the deep-ring one-row kernels (a weight wave issues all of its steps at once)
 constexpr int kMidU = 8, kDeepU = 10, kSwiU = 5, kBigU = 20;
 constexpr int64_t kCUs = 256;  // compute units of the MI355X
