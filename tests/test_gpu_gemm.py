@@ -32,7 +32,11 @@ def bf(shape, seed, scale=1.0):
 
 @pytest.mark.parametrize("M,N,K,per_row", [(33, 128, 128, True), (128, 256, 256, False), (300, 384, 640, True),
                                            (257, 6144, 2560, True), (256, 2560, 9728, False),
-                                           (600, 512, 384, True), (1024, 2560, 9728, False), (777, 6144, 2560, True)])
+                                           (600, 512, 384, True), (1024, 2560, 9728, False), (777, 6144, 2560, True),
+                                           # 256 x 256 ring tiles (>= 128 of them): ragged M, a tile count
+                                           # that is not a multiple of the 8 XCDs, several tiles per CU
+                                           (2000, 4096, 2560, True), (2100, 4352, 256, True),
+                                           (4096, 8192, 384, False)])
 def test_gemm_fp8_matches_oracle(dev, M, N, K, per_row):
     w = bf((N, K), 1, 0.02).to(dev)
     q = F.quantize(w) if per_row else F.quantize_weight(w)
