@@ -13,6 +13,8 @@
 // Activations arrive as e4m3 (KRQ_X_FP8, with their scale) or as bf16 with an inverse scale
 // (KRQ_X_BF16_STATIC: ActScale / SharedScale): the block then quantizes its A tile on the way
 // into LDS, e4m3(clamp(x * inv)), the reference's cast fused into the GEMM.
+#include <type_traits>
+
 #include "gemv_common.h"
 
 using namespace krq;
@@ -144,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_fp8(const uint8_t* __restrict
 // Per stage s: wait for this wave's loads of stage s + 1, barrier (every wave's loads of s + 1
 // have landed and every wave is done with stage s - 1's buffer), issue the loads of stage
 // s + ST - 1 into that buffer, read stage s + 1's fragments into the other register set, and
-// multiply stage s. Loads past the last stage re-read the last stage (in bounds, never multiplied).
+// multiply stage s. Past the last stage the loads go to a sink (one cached KB, same count).
 namespace ring {
 
 constexpr int BK = 64, kThreads = 256;
@@ -164,8 +166,14 @@ KRQ_DEV void dma16(const uint8_t* g, uint32_t l) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(l), "v"(g) : "memory", "m0");
 }
 
+// global_load_lds_dword: 4 bytes per lane from g into LDS at l + 4 * lane (same waits as dma16)
+KRQ_DEV void dma4(const float* g, uint32_t l) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(l), "v"(g) : "memory", "m0");
+}
+
 template <int N>
 KRQ_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
@@ -176,46 +184,82 @@ KRQ_DEV void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <int BM, int BN, int ST>
+template <int BM, int BN>
 __global__ __launch_bounds__(kThreads, 1) void k_gemm_ring(const uint8_t* __restrict__ a, const float* __restrict__ asc,
                                                            int a_per_row, const uint8_t* __restrict__ b,
                                                            const float* __restrict__ bsc, int b_per_row, int M, int N,
                                                            int K, int tiles_m, int tiles, uint16_t* __restrict__ out) {
+  constexpr int ST = 4;                        // ring buffers
   constexpr int kStageBytes = (BM + BN) * BK;  // A rows, then B rows
   __shared__ __align__(1024) uint8_t ring[ST * kStageBytes];
-  constexpr int FI = BM / 64, FJ = BN / 64;  // 32-row fragments of a wave's quarter
-  constexpr int QA = BM / 64, QB = BN / 64;  // 1 KB loads per wave per stage
+  __shared__ __align__(1024) float scl[2][BM + BN];  // per tile (alternating): row scales, then column scales
+  __shared__ __align__(1024) uint8_t sink[1024];     // where the loads of stages past the last one land
+  constexpr int FI = BM / 64, FJ = BN / 64;          // 32-row fragments of a wave's quarter
+  constexpr int QA = BM / 64, QB = BN / 64;          // 1 KB loads per wave per stage
   constexpr int kVm = QA + QB;
-  constexpr int NF = FI + FJ;                // fragments per stage, two 16-byte reads each
-  static_assert(2 * NF <= FI * FJ, "one fragment read per product");
-  static_assert(ST >= 3 && (ST - 2) * kVm < 64, "ring depth");
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-
-  // tiles in M-fastest order, each XCD (blocks b, b + 8, ...) given a contiguous run of them
-  const int per = tiles >> 3;
-  const int bid = blockIdx.x;
-  const int t = bid < per * 8 ? (bid & 7) * per + (bid >> 3) : bid;
-  const int m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * BN;
+  constexpr int NF = FI + FJ;                 // fragments per stage, two 16-byte reads each
+  constexpr int kScl = (BM + BN) / 64 / 4;    // 256-byte scale loads per wave per tile
+  constexpr int RB = BN;                      // bytes per row of a wave's output quarter (BN/2 bf16)
+  constexpr int CPR = RB / 16;                // 16-byte chunks per such row
+  constexpr int kStores = FI * 32 * CPR / 64;  // 16-byte stores per lane per tile
+  static_assert(2 * NF <= FI * FJ && 2 * kVm <= FI * FJ, "one fragment read and one load per product");
+  static_assert((BM + BN) % 256 == 0, "scale loads");
+  static_assert(2 * kVm + kStores + kVm < 64, "vmcnt range");
+  static_assert(4 * 32 * RB <= kStageBytes, "output staging fits one ring buffer");
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = gridDim.x, bid = blockIdx.x;
   const int wm = (wave & 1) * (BM / 2), wn = (wave >> 1) * (BN / 2);
   const int nk = K / BK;
 
+  // This block's k-th tile: tiles in M-fastest order; in each round of G tiles the blocks of one
+  // XCD (b, b + 8, ...) take a contiguous run of them.
+  auto tile_of = [&](int k) {
+    const int base = k * G;
+    if (base + bid >= tiles) return -1;
+    if ((G & 7) == 0 && tiles - base >= G) return base + (bid & 7) * (G >> 3) + (bid >> 3);
+    return base + bid;
+  };
+
   // load q of this wave covers rows 16 (wave + 4 q) .. + 15 of A (q < QA) or of B; lane -> row
   // + lane / 4, position lane % 4
+  int m0 = 0, n0 = 0;
   const uint8_t* gsrc[kVm];
+  auto set_tile = [&](int p) {
+    m0 = (p % tiles_m) * BM;
+    n0 = (p / tiles_m) * BN;
 #pragma unroll
-  for (int q = 0; q < QA; ++q) {
-    const int row = 16 * (wave + 4 * q) + (lane >> 2);
-    gsrc[q] = a + (int64_t)min(m0 + row, M - 1) * K + 16 * ((lane & 3) ^ ((row >> 2) & 3));
-  }
+    for (int q = 0; q < QA; ++q) {
+      const int row = 16 * (wave + 4 * q) + (lane >> 2);
+      gsrc[q] = a + (int64_t)min(m0 + row, M - 1) * K + 16 * ((lane & 3) ^ ((row >> 2) & 3));
+    }
 #pragma unroll
-  for (int q = 0; q < QB; ++q) {
-    const int row = 16 * (wave + 4 * q) + (lane >> 2);
-    gsrc[QA + q] = b + (int64_t)(n0 + row) * K + 16 * ((lane & 3) ^ ((row >> 2) & 3));
-  }
-  const uint32_t lbase = lds_addr(ring) + 1024 * wave;
-  auto dma = [&](int q, int s, int buf) {
-    const int64_t k0 = (int64_t)min(s, nk - 1) * BK;
-    dma16(gsrc[q] + k0, lbase + buf * kStageBytes + (q < QA ? 4096 * q : BM * BK + 4096 * (q - QA)));
+    for (int q = 0; q < QB; ++q) {
+      const int row = 16 * (wave + 4 * q) + (lane >> 2);
+      gsrc[QA + q] = b + (int64_t)(n0 + row) * K + 16 * ((lane & 3) ^ ((row >> 2) & 3));
+    }
+  };
+  const uint32_t lbase = lds_addr(ring) + 1024 * wave, lsink = lds_addr(sink);
+  const uint32_t lscl = lds_addr(reinterpret_cast<const uint8_t*>(&scl[0][0]));
+  // a stage's load q, or past the last stage the same count of loads of one cached KB of B into the
+  // sink, chosen without a branch so that every stage issues the same loads and waits alike
+  auto ring_load = [&](int q, int s, int buf) {
+    const bool real = s < nk;
+    dma16(real ? gsrc[q] + (int64_t)s * BK : b + 16 * lane,
+          real ? lbase + buf * kStageBytes + (q < QA ? 4096 * q : BM * BK + 4096 * (q - QA)) : lsink);
+  };
+  // the tile's scales (kScl loads of 64 per wave; a per-tensor scale is loaded by every lane), then
+  // its stages 0 .. 2 into buffers 0 .. 2
+  auto tile_loads = [&](int sb) {
+#pragma unroll
+    for (int k = 0; k < kScl; ++k) {
+      const int e = (4 * k + wave) * 64 + lane;
+      dma4(e < BM ? asc + (a_per_row ? min(m0 + e, M - 1) : 0) : bsc + (b_per_row ? n0 + e - BM : 0),
+           lscl + 4 * (sb * (BM + BN) + (4 * k + wave) * 64));
+    }
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+      for (int q = 0; q < kVm; ++q) ring_load(q, p, p);
   };
 
   // fragment f (A for f < FI, else B) of a stage: row (lane & 31) of its 32-row block, logical
@@ -228,97 +272,135 @@ __global__ __launch_bounds__(kThreads, 1) void k_gemm_ring(const uint8_t* __rest
     fh[set][f][h] = *reinterpret_cast<const uint4*>(p + off[h]);
   };
   v16f acc[FI][FJ];
-#pragma unroll
-  for (int i = 0; i < FI; ++i)
-#pragma unroll
-    for (int j = 0; j < FJ; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  // one stage: loads of stage s + ST - 1 into buffer buf_load (the one stage s - 1 used), then the
-  // products of stage s from register set `set`, each followed by one read of stage s + 1's
-  // fragments (buffer buf_next) into the other set
-  auto stage = [&](int set, int s, int buf_next, int buf_load) {
-    wait_vm<(ST - 3) * kVm>();
-    lds_barrier();
-#pragma unroll
-    for (int q = 0; q < kVm; ++q) dma(q, s + ST - 1, buf_load);
+  // One stage: the products of stage s from register set `set`, each followed by one read of stage
+  // s + 1's fragments (buffer bn = (s + 1) % 4) into the other set. An odd stage s also loads stages
+  // s + 3 and s + 4, one load after each product: they are adjacent 64-byte halves of the same
+  // 128-byte lines (the second half is then served by the vector cache), and their buffers are the
+  // ones stages s - 1 and s used. The last stage (odd) reads and loads nothing.
+  auto body = [&](auto set_c, auto loads_c, auto reads_c, int s, int bn) __attribute__((always_inline)) {
+    constexpr int set = decltype(set_c)::value;
+    constexpr bool LOADS = decltype(loads_c)::value, READS = decltype(reads_c)::value;
 #pragma unroll
     for (int u = 0; u < FI * FJ; ++u) {
       const int i = u / FJ, j = u % FJ;
       acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
           pack_v8i(fh[set][FI + j][0], fh[set][FI + j][1]), pack_v8i(fh[set][i][0], fh[set][i][1]), acc[i][j], 0, 0,
           0, 0, 0, 0);
-      if (u < 2 * NF) read(set ^ 1, u >> 1, u & 1, buf_next);
+      if (LOADS && u < 2 * kVm) ring_load(u % kVm, u < kVm ? s + 3 : s + 4, (bn + (u < kVm ? 2 : 3)) & 3);
+      if (READS && u < 2 * NF) read(set ^ 1, u >> 1, u & 1, bn);
     }
+    if (READS) {
 #pragma unroll
-    for (int u = 0; u < FI * FJ; ++u) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (u < 2 * NF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      for (int u = 0; u < FI * FJ; ++u) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (u < 2 * NF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    }
+  };
+  using yes = std::true_type;
+  using no = std::false_type;
+  using set0 = std::integral_constant<int, 0>;
+  using set1 = std::integral_constant<int, 1>;
+
+  // Epilogue. acc[i][j] element e of lane l is the output at row m = wm + 32 i + l % 32 and column
+  // n = wn + 32 j + 8 (e / 4) + 4 (l / 32) + e % 4 (B is the first product operand): a lane holds
+  // four adjacent columns of a row. Ring buffer 3 is idle here (the next tile's loads fill buffers
+  // 0 .. 2), so each wave stages 32 rows of its quarter at a time in its own 8 KB of it (rows of
+  // BN bytes, 16-byte chunk c of row r at c ^ (r % 16)), 8 bytes per lane, then reads them back
+  // along rows and stores 16 bytes per lane: each store writes four whole row segments. The stores
+  // drain while the block's next tile runs. Rounding to bf16 is the hardware convert (nearest
+  // even, as f32_to_bf16 for every non-NaN value).
+  auto epilogue = [&](int cm0, int cn0, const float* sc) {
+    uint8_t* tq = ring + (ST - 1) * kStageBytes + wave * 32 * RB;
+#pragma unroll
+    for (int i = 0; i < FI; ++i) {
+      const int r = lane & 31;
+      const float sav = sc[wm + 32 * i + r];
+#pragma unroll
+      for (int j = 0; j < FJ; ++j)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int n = wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
+          const float4 sb4 = *reinterpret_cast<const float4*>(sc + BM + n);
+          const uint32_t lo = pack_bf16x2(acc[i][j][4 * g4 + 0] * sav * sb4.x, acc[i][j][4 * g4 + 1] * sav * sb4.y);
+          const uint32_t hi = pack_bf16x2(acc[i][j][4 * g4 + 2] * sav * sb4.z, acc[i][j][4 * g4 + 3] * sav * sb4.w);
+          const int c = 4 * j + g4;  // 16-byte chunk of the quarter's row
+          *reinterpret_cast<uint2*>(tq + r * RB + 16 * (c ^ (r & (CPR - 1))) + 8 * (lane >> 5)) = make_uint2(lo, hi);
+        }
+#pragma unroll
+      for (int it = 0; it < 32 * CPR / 64; ++it) {
+        const int rr = it * (64 / CPR) + lane / CPR, c = lane % CPR;
+        const uint4 v = *reinterpret_cast<const uint4*>(tq + rr * RB + 16 * (c ^ (rr & (CPR - 1))));
+        const int m = cm0 + wm + 32 * i + rr;
+        if (m < M) *reinterpret_cast<uint4*>(out + (int64_t)m * N + cn0 + wn + 8 * c) = v;
+      }
     }
   };
 
+  int p = tile_of(0);
+  if (p < 0) return;
+  set_tile(p);
+  tile_loads(0);
+  for (int k = 0;; ++k) {
+    // Stage 3 goes into buffer 3 once every wave is done with the previous epilogue's staging.
+    // In flight, oldest first: the scales and stages 0 .. 2, the previous tile's kStores stores
+    // (k > 0), stage 3.
+    lds_barrier();
 #pragma unroll
-  for (int p = 0; p < ST - 1; ++p)
+    for (int q = 0; q < kVm; ++q) ring_load(q, 3, 3);
+    if (k == 0) wait_vm<3 * kVm>();
+    else wait_vm<3 * kVm + kStores>();
+    lds_barrier();
 #pragma unroll
-    for (int q = 0; q < kVm; ++q) dma(q, p, p);
-  wait_vm<(ST - 2) * kVm>();
-  lds_barrier();
+    for (int f = 0; f < NF; ++f) {
+      read(0, f, 0, 0);
+      read(0, f, 1, 0);
+    }
 #pragma unroll
-  for (int f = 0; f < NF; ++f) {
-    read(0, f, 0, 0);
-    read(0, f, 1, 0);
+    for (int i = 0; i < FI; ++i)
+#pragma unroll
+      for (int j = 0; j < FJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    const int cm0 = m0, cn0 = n0;
+    const int next = tile_of(k + 1);
+    // stage 0 (needs stage 1) and stage 1 (needs stage 2, loads stages 4 and 5)
+    if (k == 0) wait_vm<2 * kVm>();
+    else wait_vm<2 * kVm + kStores>();
+    lds_barrier();
+    body(set0{}, no{}, yes{}, 0, 1);
+    if (k == 0) wait_vm<kVm>();
+    else wait_vm<kVm + kStores>();
+    lds_barrier();
+    body(set1{}, yes{}, yes{}, 1, 2);
+    // stages 2 .. nk - 2: an even stage waits for the next one with the following two in flight,
+    // an odd stage with one
+    int bn = 3;
+    for (int s = 2; s < nk - 2; s += 2) {
+      wait_vm<2 * kVm>();
+      lds_barrier();
+      body(set0{}, no{}, yes{}, s, bn);
+      bn = (bn + 1) & 3;
+      wait_vm<kVm>();
+      lds_barrier();
+      body(set1{}, yes{}, yes{}, s + 1, bn);
+      bn = (bn + 1) & 3;
+    }
+    wait_vm<2 * kVm>();
+    lds_barrier();
+    body(set0{}, no{}, yes{}, nk - 2, bn);
+    // last stage: once every wave is past this barrier the ring is free; the next tile starts loading
+    lds_barrier();
+    if (next >= 0) {
+      set_tile(next);
+      tile_loads((k + 1) & 1);
+    }
+    body(set1{}, no{}, no{}, nk - 1, 0);
+    epilogue(cm0, cn0, scl[k & 1]);
+    if (next < 0) break;
   }
-  // two stages per trip (K is a multiple of 128 bytes); buffer of stage s is s % ST
-  int bnext = 1, bload = ST - 1;
-  for (int s = 0; s < nk; s += 2) {
-    stage(0, s, bnext, bload);
-    bnext = bnext + 1 == ST ? 0 : bnext + 1;
-    bload = bload + 1 == ST ? 0 : bload + 1;
-    stage(1, s + 1, bnext, bload);
-    bnext = bnext + 1 == ST ? 0 : bnext + 1;
-    bload = bload + 1 == ST ? 0 : bload + 1;
-  }
-
-  // Epilogue. acc[i][j] element e of lane l is the output at row m = wm + 32 i + l % 32 and column
-  // n = wn + 32 j + 8 (e / 4) + 4 (l / 32) + e % 4 (B is the first product operand), so a lane holds
-  // four adjacent columns of a row. Each wave writes its (BM/2) x (BN/2) bf16 quarter into the idle
-  // ring (rows of BN bytes, 16-byte chunk c of row r at c ^ (r % (BN / 16))) 8 bytes at a time, then
-  // reads it back along rows and stores 16 bytes per lane, BN/2 * 2 bytes of a row per 16 lanes.
-  static_assert(FI * FJ * 32 * 32 * 2 * 4 <= ST * kStageBytes, "output tile fits the ring");
-  wait_vm<0>();
-  lds_barrier();
-  constexpr int RB = BN;        // bytes per row of a wave's quarter (BN/2 bf16)
-  constexpr int CPR = RB / 16;  // 16-byte chunks per row
-  uint8_t* tq = ring + wave * (BM / 2) * RB;
-#pragma unroll
-  for (int i = 0; i < FI; ++i) {
-    const int r = 32 * i + (lane & 31);
-    const float sav = asc[a_per_row ? min(m0 + wm + r, M - 1) : 0];
-#pragma unroll
-    for (int j = 0; j < FJ; ++j)
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int n = wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
-        const float* sbp = bsc + (b_per_row ? n0 + n : 0);
-        const int d = b_per_row ? 1 : 0;
-        const float4 sb4 = make_float4(sbp[0], sbp[d], sbp[2 * d], sbp[3 * d]);
-        const uint32_t lo = f32_to_bf16(acc[i][j][4 * g4 + 0] * sav * sb4.x) |
-                            ((uint32_t)f32_to_bf16(acc[i][j][4 * g4 + 1] * sav * sb4.y) << 16);
-        const uint32_t hi = f32_to_bf16(acc[i][j][4 * g4 + 2] * sav * sb4.z) |
-                            ((uint32_t)f32_to_bf16(acc[i][j][4 * g4 + 3] * sav * sb4.w) << 16);
-        const int c = (32 * j + 8 * g4) >> 3;  // 16-byte chunk of the quarter's row
-        *reinterpret_cast<uint2*>(tq + r * RB + 16 * (c ^ (r & (CPR - 1))) + 8 * (lane >> 5)) = make_uint2(lo, hi);
-      }
-  }
-  // the quarter's rows back, 64 lanes = 64 / CPR rows per instruction
-#pragma unroll
-  for (int it = 0; it < (BM / 2) * CPR / 64; ++it) {
-    const int r = it * (64 / CPR) + lane / CPR, c = lane % CPR;
-    const uint4 v = *reinterpret_cast<const uint4*>(tq + r * RB + 16 * (c ^ (r & (CPR - 1))));
-    const int m = m0 + wm + r;
-    if (m < M) *reinterpret_cast<uint4*>(out + (int64_t)m * N + n0 + wn + 8 * c) = v;
-  }
+  wait_vm<0>();  // no load into LDS outlives the block
 }
 
 }  // namespace ring
@@ -346,8 +428,14 @@ extern "C" int krq_gemm_fp8(const void* x, int x_kind, const float* x_scale, con
   // projections); on fewer tiles most compute units would idle, and the 128 x 128 kernel is faster.
   const int rtm = static_cast<int>((M + 255) / 256);
   const int64_t rtiles = (int64_t)rtm * (N / 256);
-  if (x_kind == KRQ_X_FP8 && N % 256 == 0 && K % 128 == 0 && aligned16(out) && rtiles >= 128) {
-    hipLaunchKernelGGL((ring::k_gemm_ring<256, 256, 5>), dim3(static_cast<unsigned>(rtiles)), dim3(ring::kThreads), 0, s,
+  if (x_kind == KRQ_X_FP8 && N % 256 == 0 && K % 128 == 0 && K >= 256 && aligned16(out) && rtiles >= 128) {
+    // persistent: one block per compute unit, each looping over its tiles
+    int dev = 0, cus = 0;
+    KRQ_REQUIRE(hipGetDevice(&dev) == hipSuccess &&
+                    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0,
+                "gemm_fp8: device query failed");
+    const int64_t blocks_r = rtiles < cus ? rtiles : cus;
+    hipLaunchKernelGGL((ring::k_gemm_ring<256, 256>), dim3(static_cast<unsigned>(blocks_r)), dim3(ring::kThreads), 0, s,
                        (const uint8_t*)x, x_scale, x_per_row, (const uint8_t*)w8, w_scale, w_per_row, (int)M, (int)N,
                        (int)K, rtm, (int)rtiles, (uint16_t*)out);
   } else if (x_kind == KRQ_X_FP8)
