@@ -184,8 +184,21 @@ KRQ_DEV void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <int BM, int BN>
-__global__ __launch_bounds__(kThreads, 1) void k_gemm_ring(const uint8_t* __restrict__ a, const float* __restrict__ asc,
+// scheduling pattern of a stage: product U, then its share of the NR fragment reads
+template <int U, int NP, int NR>
+struct StagePattern {
+  static KRQ_DEV void apply() {
+    if constexpr (U < NP) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      constexpr int c = (U + 1) * NR / NP - U * NR / NP;
+      if constexpr (c > 0) __builtin_amdgcn_sched_group_barrier(0x100, c, 0);
+      StagePattern<U + 1, NP, NR>::apply();
+    }
+  }
+};
+
+template <int BM, int BN, int OCC>
+__global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __restrict__ a, const float* __restrict__ asc,
                                                            int a_per_row, const uint8_t* __restrict__ b,
                                                            const float* __restrict__ bsc, int b_per_row, int M, int N,
                                                            int K, int tiles_m, int tiles, uint16_t* __restrict__ out) {
@@ -198,14 +211,15 @@ __global__ __launch_bounds__(kThreads, 1) void k_gemm_ring(const uint8_t* __rest
   constexpr int QA = BM / 64, QB = BN / 64;          // 1 KB loads per wave per stage
   constexpr int kVm = QA + QB;
   constexpr int NF = FI + FJ;                 // fragments per stage, two 16-byte reads each
-  constexpr int kScl = (BM + BN) / 64 / 4;    // 256-byte scale loads per wave per tile
+  constexpr int kSI = (BM + BN) / 64;          // 64-scale loads per tile
+  constexpr int kScl = (kSI + 3) / 4;          // per wave (the surplus goes to the sink)
   constexpr int RB = BN;                      // bytes per row of a wave's output quarter (BN/2 bf16)
   constexpr int CPR = RB / 16;                // 16-byte chunks per such row
   constexpr int kStores = FI * 32 * CPR / 64;  // 16-byte stores per lane per tile
-  static_assert(2 * NF <= FI * FJ && 2 * kVm <= FI * FJ, "one fragment read and one load per product");
-  static_assert((BM + BN) % 256 == 0, "scale loads");
+  static_assert((BM + BN) % 64 == 0, "scale loads");
   static_assert(2 * kVm + kStores + kVm < 64, "vmcnt range");
-  static_assert(4 * 32 * RB <= kStageBytes, "output staging fits one ring buffer");
+  constexpr int CR = kStageBytes >= 4 * 32 * RB ? 32 : 16;  // output rows per staging chunk
+  static_assert(4 * CR * RB <= kStageBytes, "output staging fits one ring buffer");
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x, bid = blockIdx.x;
   const int wm = (wave & 1) * (BM / 2), wn = (wave >> 1) * (BN / 2);
@@ -252,9 +266,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_gemm_ring(const uint8_t* __rest
   auto tile_loads = [&](int sb) {
 #pragma unroll
     for (int k = 0; k < kScl; ++k) {
-      const int e = (4 * k + wave) * 64 + lane;
-      dma4(e < BM ? asc + (a_per_row ? min(m0 + e, M - 1) : 0) : bsc + (b_per_row ? n0 + e - BM : 0),
-           lscl + 4 * (sb * (BM + BN) + (4 * k + wave) * 64));
+      const int li = 4 * k + wave, e = li * 64 + lane;
+      dma4(e < BM ? asc + (a_per_row ? min(m0 + e, M - 1) : 0) : bsc + (b_per_row ? min(n0 + e - BM, N - 1) : 0),
+           li < kSI ? lscl + 4 * (sb * (BM + BN) + li * 64) : lsink);
     }
 #pragma unroll
     for (int p = 0; p < 3; ++p)
@@ -273,30 +287,32 @@ __global__ __launch_bounds__(kThreads, 1) void k_gemm_ring(const uint8_t* __rest
   };
   v16f acc[FI][FJ];
 
-  // One stage: the products of stage s from register set `set`, each followed by one read of stage
-  // s + 1's fragments (buffer bn = (s + 1) % 4) into the other set. An odd stage s also loads stages
-  // s + 3 and s + 4, one load after each product: they are adjacent 64-byte halves of the same
-  // 128-byte lines (the second half is then served by the vector cache), and their buffers are the
-  // ones stages s - 1 and s used. The last stage (odd) reads and loads nothing.
+  // One stage: the products of stage s from register set `set`, the 2 NF reads of stage s + 1's
+  // fragments (buffer bn = (s + 1) % 4) into the other set spread evenly after them. An odd stage s
+  // also loads stages s + 3 and s + 4, spread the same way: they are adjacent 64-byte halves of the
+  // same 128-byte lines (the second half is then served by the vector cache), and their buffers
+  // are the ones stages s - 1 and s used. The last stage (odd) reads and loads nothing.
+  constexpr int NP = FI * FJ, NR = 2 * NF, NL = 2 * kVm;
   auto body = [&](auto set_c, auto loads_c, auto reads_c, int s, int bn) __attribute__((always_inline)) {
     constexpr int set = decltype(set_c)::value;
     constexpr bool LOADS = decltype(loads_c)::value, READS = decltype(reads_c)::value;
 #pragma unroll
-    for (int u = 0; u < FI * FJ; ++u) {
+    for (int u = 0; u < NP; ++u) {
       const int i = u / FJ, j = u % FJ;
       acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
           pack_v8i(fh[set][FI + j][0], fh[set][FI + j][1]), pack_v8i(fh[set][i][0], fh[set][i][1]), acc[i][j], 0, 0,
           0, 0, 0, 0);
-      if (LOADS && u < 2 * kVm) ring_load(u % kVm, u < kVm ? s + 3 : s + 4, (bn + (u < kVm ? 2 : 3)) & 3);
-      if (READS && u < 2 * NF) read(set ^ 1, u >> 1, u & 1, bn);
-    }
-    if (READS) {
+      if (LOADS) {
 #pragma unroll
-      for (int u = 0; u < FI * FJ; ++u) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (u < 2 * NF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        for (int l = u * NL / NP; l < (u + 1) * NL / NP; ++l)
+          ring_load(l % kVm, l < kVm ? s + 3 : s + 4, (bn + (l < kVm ? 2 : 3)) & 3);
+      }
+      if (READS) {
+#pragma unroll
+        for (int r = u * NR / NP; r < (u + 1) * NR / NP; ++r) read(set ^ 1, r >> 1, r & 1, bn);
       }
     }
+    if (READS) StagePattern<0, NP, NR>::apply();
   };
   using yes = std::true_type;
   using no = std::false_type;
@@ -306,34 +322,43 @@ __global__ __launch_bounds__(kThreads, 1) void k_gemm_ring(const uint8_t* __rest
   // Epilogue. acc[i][j] element e of lane l is the output at row m = wm + 32 i + l % 32 and column
   // n = wn + 32 j + 8 (e / 4) + 4 (l / 32) + e % 4 (B is the first product operand): a lane holds
   // four adjacent columns of a row. Ring buffer 3 is idle here (the next tile's loads fill buffers
-  // 0 .. 2), so each wave stages 32 rows of its quarter at a time in its own 8 KB of it (rows of
-  // BN bytes, 16-byte chunk c of row r at c ^ (r % 16)), 8 bytes per lane, then reads them back
-  // along rows and stores 16 bytes per lane: each store writes four whole row segments. The stores
+  // 0 .. 2), so each wave stages CR rows of its quarter at a time in its own part of it (rows of
+  // BN bytes, 16-byte chunk c of row r at c ^ (r % (BN / 16))), 8 bytes per lane, then reads them
+  // back along rows and stores 16 bytes per lane: each store writes whole row segments. The stores
   // drain while the block's next tile runs. Rounding to bf16 is the hardware convert (nearest
   // even, as f32_to_bf16 for every non-NaN value).
   auto epilogue = [&](int cm0, int cn0, const float* sc) {
-    uint8_t* tq = ring + (ST - 1) * kStageBytes + wave * 32 * RB;
+    uint8_t* tq = ring + (ST - 1) * kStageBytes + wave * CR * RB;
+    const int r = lane & 31;
 #pragma unroll
     for (int i = 0; i < FI; ++i) {
-      const int r = lane & 31;
       const float sav = sc[wm + 32 * i + r];
 #pragma unroll
-      for (int j = 0; j < FJ; ++j)
+      for (int h = 0; h < 32 / CR; ++h) {
+        if (r / CR == h) {
+          const int rl = r % CR;
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const int n = wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
-          const float4 sb4 = *reinterpret_cast<const float4*>(sc + BM + n);
-          const uint32_t lo = pack_bf16x2(acc[i][j][4 * g4 + 0] * sav * sb4.x, acc[i][j][4 * g4 + 1] * sav * sb4.y);
-          const uint32_t hi = pack_bf16x2(acc[i][j][4 * g4 + 2] * sav * sb4.z, acc[i][j][4 * g4 + 3] * sav * sb4.w);
-          const int c = 4 * j + g4;  // 16-byte chunk of the quarter's row
-          *reinterpret_cast<uint2*>(tq + r * RB + 16 * (c ^ (r & (CPR - 1))) + 8 * (lane >> 5)) = make_uint2(lo, hi);
+          for (int j = 0; j < FJ; ++j)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              const int n = wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
+              const float4 sb4 = *reinterpret_cast<const float4*>(sc + BM + n);
+              const uint32_t lo =
+                  pack_bf16x2(acc[i][j][4 * g4 + 0] * sav * sb4.x, acc[i][j][4 * g4 + 1] * sav * sb4.y);
+              const uint32_t hi =
+                  pack_bf16x2(acc[i][j][4 * g4 + 2] * sav * sb4.z, acc[i][j][4 * g4 + 3] * sav * sb4.w);
+              const int c = 4 * j + g4;  // 16-byte chunk of the quarter's row
+              *reinterpret_cast<uint2*>(tq + rl * RB + 16 * (c ^ (rl & (CPR - 1))) + 8 * (lane >> 5)) =
+                  make_uint2(lo, hi);
+            }
         }
 #pragma unroll
-      for (int it = 0; it < 32 * CPR / 64; ++it) {
-        const int rr = it * (64 / CPR) + lane / CPR, c = lane % CPR;
-        const uint4 v = *reinterpret_cast<const uint4*>(tq + rr * RB + 16 * (c ^ (rr & (CPR - 1))));
-        const int m = cm0 + wm + 32 * i + rr;
-        if (m < M) *reinterpret_cast<uint4*>(out + (int64_t)m * N + cn0 + wn + 8 * c) = v;
+        for (int it = 0; it < CR * CPR / 64; ++it) {
+          const int rr = it * (64 / CPR) + lane / CPR, c = lane % CPR;
+          const uint4 v = *reinterpret_cast<const uint4*>(tq + rr * RB + 16 * (c ^ (rr & (CPR - 1))));
+          const int m = cm0 + wm + 32 * i + CR * h + rr;
+          if (m < M) *reinterpret_cast<uint4*>(out + (int64_t)m * N + cn0 + wn + 8 * c) = v;
+        }
       }
     }
   };
@@ -405,6 +430,27 @@ __global__ __launch_bounds__(kThreads, 1) void k_gemm_ring(const uint8_t* __rest
 
 }  // namespace ring
 
+// Tile shape of the ring kernel for an e4m3 GEMM, a pure function of the shape. Measured at the
+// Qwen3-4B projections (M = 256 .. 4096): a round of 256 x 256 tiles (one block per compute unit)
+// takes 1.45x as long as a round of 128 x 128 tiles running two blocks per compute unit, and does
+// four times their products; 128 x 256 tiles were never faster than one of the two. The plan
+// takes the one with fewer estimated round-lengths, counting the tiles of the busiest compute
+// unit. The 128 x 128 ring kernel also beat the register-staged one on grids of 40 tiles (M = 256:
+// O 15.8 against 41.0 us, down 44.8 against 93.4), so bm == 0 only where N is not a multiple of
+// 128.
+struct RingPlan {
+  int bm, bn, occ;
+};
+RingPlan ring_plan(int64_t M, int64_t N, int cus) {
+  const int64_t t256 = N % 256 == 0 ? ((M + 255) / 256) * (N / 256) : 0;
+  const int64_t t128 = N % 128 == 0 ? ((M + 127) / 128) * (N / 128) : 0;
+  const double c256 = (double)((t256 + cus - 1) / cus);               // rounds of 256 x 256
+  const double c128 = 0.69 * (double)((t128 + cus - 1) / cus) / 2.0;  // two blocks per unit
+  if (t256 >= cus / 2 && (t128 == 0 || c256 <= c128)) return {256, 256, 1};
+  if (t128 > 0) return {128, 128, 2};
+  return {0, 0, 0};
+}
+
 }  // namespace
 
 extern "C" int krq_gemm_fp8(const void* x, int x_kind, const float* x_scale, const float* x_inv, int x_per_row,
@@ -426,19 +472,28 @@ extern "C" int krq_gemm_fp8(const void* x, int x_kind, const float* x_scale, con
   // The ring kernel's 256 x 256 tiles pay where a launch has at least half as many tiles as the
   // chip has compute units (M = 4096: 1.2-1.3x faster than the 128 x 128 kernel at the Qwen3-4B
   // projections); on fewer tiles most compute units would idle, and the 128 x 128 kernel is faster.
-  const int rtm = static_cast<int>((M + 255) / 256);
-  const int64_t rtiles = (int64_t)rtm * (N / 256);
-  if (x_kind == KRQ_X_FP8 && N % 256 == 0 && K % 128 == 0 && K >= 256 && aligned16(out) && rtiles >= 128) {
-    // persistent: one block per compute unit, each looping over its tiles
+  if (x_kind == KRQ_X_FP8 && K % 128 == 0 && K >= 256 && aligned16(out)) {
     int dev = 0, cus = 0;
     KRQ_REQUIRE(hipGetDevice(&dev) == hipSuccess &&
                     hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0,
                 "gemm_fp8: device query failed");
-    const int64_t blocks_r = rtiles < cus ? rtiles : cus;
-    hipLaunchKernelGGL((ring::k_gemm_ring<256, 256>), dim3(static_cast<unsigned>(blocks_r)), dim3(ring::kThreads), 0, s,
-                       (const uint8_t*)x, x_scale, x_per_row, (const uint8_t*)w8, w_scale, w_per_row, (int)M, (int)N,
-                       (int)K, rtm, (int)rtiles, (uint16_t*)out);
-  } else if (x_kind == KRQ_X_FP8)
+    const RingPlan rp = ring_plan(M, N, cus);
+    if (rp.bm > 0) {
+      const int rtm = static_cast<int>((M + rp.bm - 1) / rp.bm);
+      const int64_t rtiles = (int64_t)rtm * (N / rp.bn);
+      const int64_t slots = (int64_t)cus * rp.occ;
+      const dim3 rgrid(static_cast<unsigned>(rtiles < slots ? rtiles : slots));
+#define KRQ_RING(BM_, BN_, OCC_)                                                                                 \
+  hipLaunchKernelGGL((ring::k_gemm_ring<BM_, BN_, OCC_>), rgrid, dim3(ring::kThreads), 0, s, (const uint8_t*)x,   \
+                     x_scale, x_per_row, (const uint8_t*)w8, w_scale, w_per_row, (int)M, (int)N, (int)K, rtm,      \
+                     (int)rtiles, (uint16_t*)out)
+      if (rp.bm == 256) KRQ_RING(256, 256, 1);
+      else KRQ_RING(128, 128, 2);
+#undef KRQ_RING
+      return krq_check_launch("gemm_fp8");
+    }
+  }
+  if (x_kind == KRQ_X_FP8)
     hipLaunchKernelGGL(k_gemm_fp8<KRQ_X_FP8>, grid, dim3(kThreads), 0, s, (const uint8_t*)x, x_scale, x_inv, x_per_row,
                        (const uint8_t*)w8, w_scale, w_per_row, (int)M, (int)N, (int)K, tiles_m, (uint16_t*)out);
   else
