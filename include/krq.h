@@ -315,6 +315,18 @@ int krq_gemm_fp8(const void* x, int x_kind, const float* x_scale, const float* x
                  const void* w8, const float* w_scale, int w_per_row, int64_t M, int64_t N, int64_t K,
                  void* out, void* stream);
 
+/* krq_gemm_fp8 with a caller workspace for split K (the same product, torch._scaled_mm in
+ * engine/kernels/fp8.py:105-106): with e4m3 activations and a grid of fewer 128 x 128 tiles than
+ * the device has compute units, K is split and fp32 partials go to ws before one more launch sums
+ * them in split order and applies the scales. ws: at least krq_gemm_fp8_ws_bytes(x_kind, M, N, K)
+ * bytes, 16-byte aligned (overwritten; calls that overlap must not share it); with a smaller ws (or
+ * NULL, 0) K is not split. krq_gemm_fp8_ws_bytes returns 0 when no split is planned for the
+ * current device and -1 when the device query fails. */
+int krq_gemm_fp8_ws(const void* x, int x_kind, const float* x_scale, const float* x_inv, int x_per_row,
+                    const void* w8, const float* w_scale, int w_per_row, int64_t M, int64_t N, int64_t K,
+                    void* ws, int64_t ws_bytes, void* out, void* stream);
+int64_t krq_gemm_fp8_ws_bytes(int x_kind, int64_t M, int64_t N, int64_t K);
+
 /* Tiled <-> row-major weight copies (byte permutations; see "tiled" above). For a bf16 [N, K]
  * matrix pass its [N, 2K] byte view (K -> 2K). */
 int krq_pack_fp8(const void* w8_rowmajor, int64_t N, int64_t K, void* w8_tiled, void* stream);

@@ -197,11 +197,15 @@ struct StagePattern {
   }
 };
 
-template <int BM, int BN, int OCC>
+// PART: each work unit is (tile, split): the tile's products over K / splits bytes of K, written
+// as fp32 to plane `split` of ws [splits][M][N] (k_splitk_reduce finishes them); otherwise one
+// unit per tile over all of K, written as bf16 with its scales applied.
+template <int BM, int BN, int OCC, bool PART>
 __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __restrict__ a, const float* __restrict__ asc,
                                                            int a_per_row, const uint8_t* __restrict__ b,
                                                            const float* __restrict__ bsc, int b_per_row, int M, int N,
-                                                           int K, int tiles_m, int tiles, uint16_t* __restrict__ out) {
+                                                           int K, int tiles_m, int tiles, int splits,
+                                                           float* __restrict__ ws, uint16_t* __restrict__ out) {
   constexpr int ST = 4;                        // ring buffers
   constexpr int kStageBytes = (BM + BN) * BK;  // A rows, then B rows
   __shared__ __align__(1024) uint8_t ring[ST * kStageBytes];
@@ -213,7 +217,8 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
   constexpr int NF = FI + FJ;                 // fragments per stage, two 16-byte reads each
   constexpr int kSI = (BM + BN) / 64;          // 64-scale loads per tile
   constexpr int kScl = (kSI + 3) / 4;          // per wave (the surplus goes to the sink)
-  constexpr int RB = BN;                      // bytes per row of a wave's output quarter (BN/2 bf16)
+  constexpr int EB = PART ? 4 : 2;           // output element bytes
+  constexpr int RB = BN / 2 * EB;             // bytes per row of a wave's output quarter
   constexpr int CPR = RB / 16;                // 16-byte chunks per such row
   constexpr int kStores = FI * 32 * CPR / 64;  // 16-byte stores per lane per tile
   static_assert((BM + BN) % 64 == 0, "scale loads");
@@ -223,33 +228,38 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x, bid = blockIdx.x;
   const int wm = (wave & 1) * (BM / 2), wn = (wave >> 1) * (BN / 2);
-  const int nk = K / BK;
+  const int nk = K / BK / splits;  // stages of a work unit
+  const int units = tiles * splits;
 
-  // This block's k-th tile: tiles in M-fastest order; in each round of G tiles the blocks of one
-  // XCD (b, b + 8, ...) take a contiguous run of them.
+  // This block's k-th work unit (unit u: tile u % tiles, split u / tiles): units in order, tiles
+  // M-fastest; in each round of G units the blocks of one XCD (b, b + 8, ...) take a contiguous
+  // run of them.
   auto tile_of = [&](int k) {
     const int base = k * G;
-    if (base + bid >= tiles) return -1;
-    if ((G & 7) == 0 && tiles - base >= G) return base + (bid & 7) * (G >> 3) + (bid >> 3);
+    if (base + bid >= units) return -1;
+    if ((G & 7) == 0 && units - base >= G) return base + (bid & 7) * (G >> 3) + (bid >> 3);
     return base + bid;
   };
 
   // load q of this wave covers rows 16 (wave + 4 q) .. + 15 of A (q < QA) or of B; lane -> row
   // + lane / 4, position lane % 4
-  int m0 = 0, n0 = 0;
+  int m0 = 0, n0 = 0, sp = 0;
   const uint8_t* gsrc[kVm];
-  auto set_tile = [&](int p) {
+  auto set_tile = [&](int u) {
+    const int p = u % tiles;
+    sp = u / tiles;
     m0 = (p % tiles_m) * BM;
     n0 = (p / tiles_m) * BN;
+    const int64_t kb = (int64_t)sp * nk * BK;
 #pragma unroll
     for (int q = 0; q < QA; ++q) {
       const int row = 16 * (wave + 4 * q) + (lane >> 2);
-      gsrc[q] = a + (int64_t)min(m0 + row, M - 1) * K + 16 * ((lane & 3) ^ ((row >> 2) & 3));
+      gsrc[q] = a + (int64_t)min(m0 + row, M - 1) * K + kb + 16 * ((lane & 3) ^ ((row >> 2) & 3));
     }
 #pragma unroll
     for (int q = 0; q < QB; ++q) {
       const int row = 16 * (wave + 4 * q) + (lane >> 2);
-      gsrc[QA + q] = b + (int64_t)(n0 + row) * K + 16 * ((lane & 3) ^ ((row >> 2) & 3));
+      gsrc[QA + q] = b + (int64_t)(n0 + row) * K + kb + 16 * ((lane & 3) ^ ((row >> 2) & 3));
     }
   };
   const uint32_t lbase = lds_addr(ring) + 1024 * wave, lsink = lds_addr(sink);
@@ -327,7 +337,7 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
   // back along rows and stores 16 bytes per lane: each store writes whole row segments. The stores
   // drain while the block's next tile runs. Rounding to bf16 is the hardware convert (nearest
   // even, as f32_to_bf16 for every non-NaN value).
-  auto epilogue = [&](int cm0, int cn0, const float* sc) {
+  auto epilogue = [&](int cm0, int cn0, int csp, const float* sc) {
     uint8_t* tq = ring + (ST - 1) * kStageBytes + wave * CR * RB;
     const int r = lane & 31;
 #pragma unroll
@@ -341,15 +351,22 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
           for (int j = 0; j < FJ; ++j)
 #pragma unroll
             for (int g4 = 0; g4 < 4; ++g4) {
-              const int n = wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
-              const float4 sb4 = *reinterpret_cast<const float4*>(sc + BM + n);
-              const uint32_t lo =
-                  pack_bf16x2(acc[i][j][4 * g4 + 0] * sav * sb4.x, acc[i][j][4 * g4 + 1] * sav * sb4.y);
-              const uint32_t hi =
-                  pack_bf16x2(acc[i][j][4 * g4 + 2] * sav * sb4.z, acc[i][j][4 * g4 + 3] * sav * sb4.w);
-              const int c = 4 * j + g4;  // 16-byte chunk of the quarter's row
-              *reinterpret_cast<uint2*>(tq + rl * RB + 16 * (c ^ (rl & (CPR - 1))) + 8 * (lane >> 5)) =
-                  make_uint2(lo, hi);
+              if constexpr (PART) {
+                const int c = 8 * j + 2 * g4 + (lane >> 5);  // 16-byte chunk of the quarter's row
+                *reinterpret_cast<float4*>(tq + rl * RB + 16 * (c ^ (rl & (CPR - 1)))) =
+                    make_float4(acc[i][j][4 * g4 + 0], acc[i][j][4 * g4 + 1], acc[i][j][4 * g4 + 2],
+                                acc[i][j][4 * g4 + 3]);
+              } else {
+                const int n = wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
+                const float4 sb4 = *reinterpret_cast<const float4*>(sc + BM + n);
+                const uint32_t lo =
+                    pack_bf16x2(acc[i][j][4 * g4 + 0] * sav * sb4.x, acc[i][j][4 * g4 + 1] * sav * sb4.y);
+                const uint32_t hi =
+                    pack_bf16x2(acc[i][j][4 * g4 + 2] * sav * sb4.z, acc[i][j][4 * g4 + 3] * sav * sb4.w);
+                const int c = 4 * j + g4;  // 16-byte chunk of the quarter's row
+                *reinterpret_cast<uint2*>(tq + rl * RB + 16 * (c ^ (rl & (CPR - 1))) + 8 * (lane >> 5)) =
+                    make_uint2(lo, hi);
+              }
             }
         }
 #pragma unroll
@@ -357,7 +374,12 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
           const int rr = it * (64 / CPR) + lane / CPR, c = lane % CPR;
           const uint4 v = *reinterpret_cast<const uint4*>(tq + rr * RB + 16 * (c ^ (rr & (CPR - 1))));
           const int m = cm0 + wm + 32 * i + CR * h + rr;
-          if (m < M) *reinterpret_cast<uint4*>(out + (int64_t)m * N + cn0 + wn + 8 * c) = v;
+          if (m < M) {
+            if constexpr (PART)
+              *reinterpret_cast<uint4*>(ws + ((int64_t)csp * M + m) * N + cn0 + wn + 4 * c) = v;
+            else
+              *reinterpret_cast<uint4*>(out + (int64_t)m * N + cn0 + wn + 8 * c) = v;
+          }
         }
       }
     }
@@ -388,7 +410,7 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
       for (int j = 0; j < FJ; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-    const int cm0 = m0, cn0 = n0;
+    const int cm0 = m0, cn0 = n0, csp = sp;
     const int next = tile_of(k + 1);
     // stage 0 (needs stage 1) and stage 1 (needs stage 2, loads stages 4 and 5)
     if (k == 0) wait_vm<2 * kVm>();
@@ -422,40 +444,89 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
       tile_loads((k + 1) & 1);
     }
     body(set1{}, no{}, no{}, nk - 1, 0);
-    epilogue(cm0, cn0, scl[k & 1]);
+    epilogue(cm0, cn0, csp, scl[k & 1]);
     if (next < 0) break;
   }
   wait_vm<0>();  // no load into LDS outlives the block
 }
 
+// out[m][n] = bf16((sum over s of ws[s][m][n], s in order) * x_scale[m] * w_scale[n]), four
+// columns per thread
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ ws, int splits, int M, int N,
+                                                       const float* __restrict__ asc, int a_per_row,
+                                                       const float* __restrict__ bsc, int b_per_row,
+                                                       uint16_t* __restrict__ out) {
+  const int64_t e = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  const int64_t plane = (int64_t)M * N;
+  if (e >= plane) return;
+  const int m = static_cast<int>(e / N), n = static_cast<int>(e % N);
+  float4 acc = *reinterpret_cast<const float4*>(ws + e);
+  for (int sp = 1; sp < splits; ++sp) {
+    const float4 v = *reinterpret_cast<const float4*>(ws + sp * plane + e);
+    acc.x += v.x;
+    acc.y += v.y;
+    acc.z += v.z;
+    acc.w += v.w;
+  }
+  const float sa = asc[a_per_row ? m : 0];
+  const float4 sb = b_per_row ? *reinterpret_cast<const float4*>(bsc + n) : make_float4(bsc[0], bsc[0], bsc[0], bsc[0]);
+  *reinterpret_cast<uint2*>(out + e) =
+      make_uint2(pack_bf16x2(acc.x * sa * sb.x, acc.y * sa * sb.y), pack_bf16x2(acc.z * sa * sb.z, acc.w * sa * sb.w));
+}
+
 }  // namespace ring
 
-// Tile shape of the ring kernel for an e4m3 GEMM, a pure function of the shape. Measured at the
-// Qwen3-4B projections (M = 256 .. 4096): a round of 256 x 256 tiles (one block per compute unit)
-// takes 1.45x as long as a round of 128 x 128 tiles running two blocks per compute unit, and does
-// four times their products; 128 x 256 tiles were never faster than one of the two. The plan
-// takes the one with fewer estimated round-lengths, counting the tiles of the busiest compute
-// unit. The 128 x 128 ring kernel also beat the register-staged one on grids of 40 tiles (M = 256:
-// O 15.8 against 41.0 us, down 44.8 against 93.4), so bm == 0 only where N is not a multiple of
-// 128.
+// Tile shape of the ring kernel for an e4m3 GEMM, a pure function of the shape and the device's
+// compute-unit count. Measured at the Qwen3-4B projections (M = 256 .. 4096): a round of
+// 256 x 256 tiles (one block per compute unit) takes 1.45x as long as a round of 128 x 128 tiles
+// running two blocks per compute unit, and does four times their products; 128 x 256 tiles were
+// never faster than one of the two. The plan takes the one with fewer estimated round-lengths,
+// counting the tiles of the busiest compute unit. The 128 x 128 ring kernel also beat the
+// register-staged one on grids of 40 tiles (M = 256: O 15.8 against 41.0 us, down 44.8 against
+// 93.4), so bm == 0 only where N is not a multiple of 128.
+//
+// Split K: a 128 x 128 grid of at most a quarter as many tiles as compute units splits K into
+// `splits` equal parts (the most of 8, 4, 2 with an even number of 64-byte stages and at least
+// 2 KB of K per part) when the fp32 partials (splits x M x N x 4 bytes, written once and read
+// once) are no more bytes than the weights (N x K). Measured at M = 256 (40 tiles): down 44.5 ->
+// 19.8 us with 4 parts (27.3 with 2), O 15.7 -> 15.0 us with 2; at 96 tiles (QKV, 2 parts) and 160
+// (M = 1024 down) the partials cost more than the parts gained (11.9 -> 18.5, 44.4 -> 49.8 us).
 struct RingPlan {
-  int bm, bn, occ;
+  int bm, bn, occ, splits;
 };
-RingPlan ring_plan(int64_t M, int64_t N, int cus) {
+RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int cus) {
   const int64_t t256 = N % 256 == 0 ? ((M + 255) / 256) * (N / 256) : 0;
   const int64_t t128 = N % 128 == 0 ? ((M + 127) / 128) * (N / 128) : 0;
   const double c256 = (double)((t256 + cus - 1) / cus);               // rounds of 256 x 256
   const double c128 = 0.69 * (double)((t128 + cus - 1) / cus) / 2.0;  // two blocks per unit
-  if (t256 >= cus / 2 && (t128 == 0 || c256 <= c128)) return {256, 256, 1};
-  if (t128 > 0) return {128, 128, 2};
-  return {0, 0, 0};
+  if (t256 >= cus / 2 && (t128 == 0 || c256 <= c128)) return {256, 256, 1, 1};
+  if (t128 == 0) return {0, 0, 0, 0};
+  int splits = 1;
+  if (t128 <= cus / 4) {
+    const int64_t nk = K / 64;
+    for (int sp = 8; sp >= 2; sp /= 2)
+      if (nk % (2 * sp) == 0 && K / sp >= 2048 && sp * M * 4 <= K) {
+        splits = sp;
+        break;
+      }
+  }
+  return {128, 128, 2, splits};
 }
 
-}  // namespace
+int query_cus(int* cus) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || *cus <= 0)
+    return KRQ_EHIP;
+  return KRQ_OK;
+}
 
-extern "C" int krq_gemm_fp8(const void* x, int x_kind, const float* x_scale, const float* x_inv, int x_per_row,
-                            const void* w8, const float* w_scale, int w_per_row, int64_t M, int64_t N, int64_t K,
-                            void* out, void* stream) {
+// the ring kernels take e4m3 activations and K of at least four 64-byte stages
+bool ring_fits(int x_kind, int64_t K) { return x_kind == KRQ_X_FP8 && K % 128 == 0 && K >= 256; }
+
+int gemm_run(const void* x, int x_kind, const float* x_scale, const float* x_inv, int x_per_row, const void* w8,
+             const float* w_scale, int w_per_row, int64_t M, int64_t N, int64_t K, void* ws, int64_t ws_bytes,
+             void* out, void* stream) {
   KRQ_REQUIRE(x && w8 && w_scale && x_scale && out, "gemm_fp8: null pointer");
   KRQ_REQUIRE(x_kind == KRQ_X_FP8 || x_kind == KRQ_X_BF16_STATIC, "gemm_fp8: x_kind must be FP8 or BF16_STATIC");
   KRQ_REQUIRE(x_kind != KRQ_X_BF16_STATIC || x_inv, "gemm_fp8: x_inv is required");
@@ -464,35 +535,41 @@ extern "C" int krq_gemm_fp8(const void* x, int x_kind, const float* x_scale, con
                   K % BK == 0,
               "gemm_fp8: shape M=%lld N=%lld K=%lld (N and K multiples of 128)", (long long)M, (long long)N,
               (long long)K);
+  KRQ_REQUIRE(ws_bytes >= 0 && (ws_bytes == 0 || ws), "gemm_fp8: workspace pointer and size disagree");
   const int tiles_m = static_cast<int>((M + BM - 1) / BM);
   const int64_t blocks = (int64_t)tiles_m * (N / BN);
   KRQ_REQUIRE(blocks <= 0x7fffffff, "gemm_fp8: grid too large");
-  const dim3 grid(static_cast<unsigned>(blocks));
   hipStream_t s = (hipStream_t)stream;
-  // The ring kernel's 256 x 256 tiles pay where a launch has at least half as many tiles as the
-  // chip has compute units (M = 4096: 1.2-1.3x faster than the 128 x 128 kernel at the Qwen3-4B
-  // projections); on fewer tiles most compute units would idle, and the 128 x 128 kernel is faster.
-  if (x_kind == KRQ_X_FP8 && K % 128 == 0 && K >= 256 && aligned16(out)) {
-    int dev = 0, cus = 0;
-    KRQ_REQUIRE(hipGetDevice(&dev) == hipSuccess &&
-                    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0,
-                "gemm_fp8: device query failed");
-    const RingPlan rp = ring_plan(M, N, cus);
+  if (ring_fits(x_kind, K) && aligned16(out)) {
+    int cus = 0;
+    KRQ_REQUIRE(query_cus(&cus) == KRQ_OK, "gemm_fp8: device query failed");
+    RingPlan rp = ring_plan(M, N, K, cus);
+    if (rp.splits > 1 && (!aligned16(ws) || ws_bytes < (int64_t)rp.splits * M * N * 4)) rp.splits = 1;
     if (rp.bm > 0) {
       const int rtm = static_cast<int>((M + rp.bm - 1) / rp.bm);
       const int64_t rtiles = (int64_t)rtm * (N / rp.bn);
-      const int64_t slots = (int64_t)cus * rp.occ;
-      const dim3 rgrid(static_cast<unsigned>(rtiles < slots ? rtiles : slots));
-#define KRQ_RING(BM_, BN_, OCC_)                                                                                 \
-  hipLaunchKernelGGL((ring::k_gemm_ring<BM_, BN_, OCC_>), rgrid, dim3(ring::kThreads), 0, s, (const uint8_t*)x,   \
-                     x_scale, x_per_row, (const uint8_t*)w8, w_scale, w_per_row, (int)M, (int)N, (int)K, rtm,      \
-                     (int)rtiles, (uint16_t*)out)
-      if (rp.bm == 256) KRQ_RING(256, 256, 1);
-      else KRQ_RING(128, 128, 2);
+      const int64_t units = rtiles * rp.splits, slots = (int64_t)cus * rp.occ;
+      const dim3 rgrid(static_cast<unsigned>(units < slots ? units : slots));
+#define KRQ_RING(BM_, BN_, OCC_, PART_)                                                                              \
+  hipLaunchKernelGGL((ring::k_gemm_ring<BM_, BN_, OCC_, PART_>), rgrid, dim3(ring::kThreads), 0, s, (const uint8_t*)x, \
+                     x_scale, x_per_row, (const uint8_t*)w8, w_scale, w_per_row, (int)M, (int)N, (int)K, rtm,          \
+                     (int)rtiles, rp.splits, (float*)ws, (uint16_t*)out)
+      if (rp.bm == 256) {
+        KRQ_RING(256, 256, 1, false);
+      } else if (rp.splits == 1) {
+        KRQ_RING(128, 128, 2, false);
+      } else {
+        KRQ_RING(128, 128, 2, true);
+        const int64_t threads = M * N / 4;
+        hipLaunchKernelGGL(ring::k_splitk_reduce, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s,
+                           (const float*)ws, rp.splits, (int)M, (int)N, x_scale, x_per_row, w_scale, w_per_row,
+                           (uint16_t*)out);
+      }
 #undef KRQ_RING
       return krq_check_launch("gemm_fp8");
     }
   }
+  const dim3 grid(static_cast<unsigned>(blocks));
   if (x_kind == KRQ_X_FP8)
     hipLaunchKernelGGL(k_gemm_fp8<KRQ_X_FP8>, grid, dim3(kThreads), 0, s, (const uint8_t*)x, x_scale, x_inv, x_per_row,
                        (const uint8_t*)w8, w_scale, w_per_row, (int)M, (int)N, (int)K, tiles_m, (uint16_t*)out);
@@ -501,4 +578,26 @@ extern "C" int krq_gemm_fp8(const void* x, int x_kind, const float* x_scale, con
                        x_per_row, (const uint8_t*)w8, w_scale, w_per_row, (int)M, (int)N, (int)K, tiles_m,
                        (uint16_t*)out);
   return krq_check_launch("gemm_fp8");
+}
+
+}  // namespace
+
+extern "C" int krq_gemm_fp8(const void* x, int x_kind, const float* x_scale, const float* x_inv, int x_per_row,
+                            const void* w8, const float* w_scale, int w_per_row, int64_t M, int64_t N, int64_t K,
+                            void* out, void* stream) {
+  return gemm_run(x, x_kind, x_scale, x_inv, x_per_row, w8, w_scale, w_per_row, M, N, K, nullptr, 0, out, stream);
+}
+
+extern "C" int krq_gemm_fp8_ws(const void* x, int x_kind, const float* x_scale, const float* x_inv, int x_per_row,
+                               const void* w8, const float* w_scale, int w_per_row, int64_t M, int64_t N, int64_t K,
+                               void* ws, int64_t ws_bytes, void* out, void* stream) {
+  return gemm_run(x, x_kind, x_scale, x_inv, x_per_row, w8, w_scale, w_per_row, M, N, K, ws, ws_bytes, out, stream);
+}
+
+extern "C" int64_t krq_gemm_fp8_ws_bytes(int x_kind, int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || N <= 0 || K <= 0 || N % BN != 0 || K % BK != 0 || !ring_fits(x_kind, K)) return 0;
+  int cus = 0;
+  if (query_cus(&cus) != KRQ_OK) return -1;
+  const RingPlan rp = ring_plan(M, N, K, cus);
+  return rp.splits > 1 ? (int64_t)rp.splits * M * N * 4 : 0;
 }

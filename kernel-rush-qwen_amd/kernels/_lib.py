@@ -58,6 +58,8 @@ EXPORTS = {
     "krq_rmsnorm_quant_rows": (_i32, [_vp, _vp, _vp, _f32, _i64, _i64, _vp, _vp, _vp]),
     "krq_rmsnorm_quant_rows_tiled": (_i32, [_vp, _vp, _vp, _f32, _i64, _i64, _vp, _vp, _vp]),
     "krq_gemm_fp8": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64, _vp, _vp]),
+    "krq_gemm_fp8_ws": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "krq_gemm_fp8_ws_bytes": (_i64, [_i32, _i64, _i64, _i64]),
     "krq_pack_fp8": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "krq_unpack_fp8": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "krq_version": (ctypes.c_char_p, []),

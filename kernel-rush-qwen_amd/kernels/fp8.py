@@ -370,7 +370,7 @@ def swiglu_cast_fp8(x, q, out_a, a=None, xs=None):
 
 
 def gemm_fp8(x, q, a=None, xs=None):
-    """Prefill FP8 GEMM (krq_gemm_fp8): bf16 [M, N] = bf16(x8 . w8^T * x_scale[m] * w_scale[n]),
+    """Prefill FP8 GEMM (krq_gemm_fp8_ws): bf16 [M, N] = bf16(x8 . w8^T * x_scale[m] * w_scale[n]),
     the product torch._scaled_mm gives linear_fp8 (engine/kernels/fp8.py:105-106).
     x is bf16 [M, K] with an ActScale / SharedScale `a` (the cast is fused into the GEMM's A-tile
     staging) or float8_e4m3fn [M, K] with its scale xs (1 or M values); q from quantize_weight /
@@ -394,8 +394,12 @@ def gemm_fp8(x, q, a=None, xs=None):
     L.require_device(x_scale, x_inv)
     xpr = 1 if (x_scale.numel() == M and M > 1) else 0
     out = torch.empty((M, N), device=x.device, dtype=torch.bfloat16)
-    L.call("krq_gemm_fp8", L.ptr(xin), kind, L.ptr(x_scale), L.ptr(x_inv), xpr, L.ptr(w8), L.ptr(ws),
-           1 if ws.numel() > 1 else 0, M, N, K, L.ptr(out), L.stream(xin))
+    nbytes = L.lib().krq_gemm_fp8_ws_bytes(kind, M, N, K)
+    if nbytes < 0:
+        raise RuntimeError("krq_gemm_fp8_ws_bytes: device query failed")
+    work = torch.empty(nbytes, device=x.device, dtype=torch.uint8) if nbytes else None
+    L.call("krq_gemm_fp8_ws", L.ptr(xin), kind, L.ptr(x_scale), L.ptr(x_inv), xpr, L.ptr(w8), L.ptr(ws),
+           1 if ws.numel() > 1 else 0, M, N, K, L.ptr(work), nbytes, L.ptr(out), L.stream(xin))
     return out
 
 

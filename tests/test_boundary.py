@@ -139,6 +139,17 @@ def test_invalid_arguments_fail_before_any_launch():
     assert rc == L.KRQ_EINVAL and b"x_inv" in lib.krq_last_error()
     rc = lib.krq_gemm_fp8(p, L.X_BF16_DYN, p, p, 0, p, p, 1, 256, 256, 256, p, _null())
     assert rc == L.KRQ_EINVAL and b"x_kind" in lib.krq_last_error()
+    # the workspace form: the same checks, and a size that disagrees with its pointer is refused;
+    # no split (0 bytes) where the ring kernels do not run (bf16 activations, K below 256)
+    rc = lib.krq_gemm_fp8_ws(p, L.X_FP8, p, None, 0, p, p, 1, 256, 200, 256, p, 0, p, _null())
+    assert rc == L.KRQ_EINVAL and b"multiples of 128" in lib.krq_last_error()
+    rc = lib.krq_gemm_fp8_ws(p, L.X_FP8, p, None, 0, p, p, 1, 256, 256, 256, None, 1024, p, _null())
+    assert rc == L.KRQ_EINVAL and b"workspace" in lib.krq_last_error()
+    rc = lib.krq_gemm_fp8_ws(p, L.X_FP8, p, None, 0, p, p, 1, 256, 256, 256, p, -1, p, _null())
+    assert rc == L.KRQ_EINVAL and b"workspace" in lib.krq_last_error()
+    assert lib.krq_gemm_fp8_ws_bytes(L.X_BF16_STATIC, 256, 2560, 9728) == 0
+    assert lib.krq_gemm_fp8_ws_bytes(L.X_FP8, 256, 2560, 128) == 0
+    assert lib.krq_gemm_fp8_ws_bytes(L.X_FP8, 256, 200, 9728) == 0
 
 
 def test_fused_buffers_and_mlp_contracts():

@@ -49,6 +49,32 @@ def test_gemm_fp8_matches_oracle(dev, M, N, K, per_row):
     assert e <= TOL
 
 
+@pytest.mark.parametrize("M,N,K,splits", [(256, 2560, 9728, 4), (200, 2560, 9728, 4), (300, 2560, 4096, 2),
+                                          (130, 1024, 8192, 4)])
+def test_gemm_split_k(dev, M, N, K, splits):
+    """Split K (krq_gemm_fp8_ws with its workspace) and the unsplit kernel (krq_gemm_fp8, or the
+    workspace form given too little workspace, which must then equal it bit for bit): both within
+    the bar of the oracle."""
+    from kernels import _lib as L
+    lib = L.lib()
+    assert lib.krq_gemm_fp8_ws_bytes(L.X_FP8, M, N, K) == splits * M * N * 4
+    q = F.quantize(bf((N, K), 11, 0.02).to(dev))
+    x8, xs = F.quant_rows(bf((M, K), 12).to(dev))
+    _, ref = O.fp8_matmul(codes(x8), xs.cpu().numpy().reshape(-1), codes(q[0]), q[1].cpu().numpy())
+    y_split = F.gemm_fp8(x8, q, xs=xs)
+    args = (L.ptr(x8), L.X_FP8, L.ptr(xs), None, 1, L.ptr(q[0]), L.ptr(q[1]), 1, M, N, K)
+    y_plain = torch.empty_like(y_split)
+    L.call("krq_gemm_fp8", *args, L.ptr(y_plain), L.stream(x8))
+    small = torch.empty(splits * M * N * 4 - 16, device=dev, dtype=torch.uint8)
+    y_small = torch.empty_like(y_split)
+    L.call("krq_gemm_fp8_ws", *args, L.ptr(small), small.numel(), L.ptr(y_small), L.stream(x8))
+    assert torch.equal(y_small, y_plain)
+    for y in (y_split, y_plain):
+        e = rel_err(y.float().cpu().numpy(), ref)
+        print(f"gemm M={M} N={N} K={K} splits={splits}: max-rel {e:.2e}")
+        assert e <= TOL
+
+
 @pytest.mark.parametrize("M,N,K", [(200, 256, 384), (512, 2560, 4096)])
 def test_gemm_fused_cast_is_cast_then_gemm(dev, M, N, K):
     """bf16 x with an ActScale: the in-kernel cast equals fp8._cast + the e4m3 GEMM bit for bit,
