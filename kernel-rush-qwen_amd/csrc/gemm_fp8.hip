@@ -2,17 +2,18 @@
 // the product the reference computes with torch._scaled_mm in linear_fp8 (engine/kernels/fp8.py
 // :97-106) for prefill (engine/engine.py:670-677).
 //
-// Tiles. A block owns a 128 x 128 output tile and walks K in steps of 128 bytes; its four waves
-// each own a 64 x 64 quarter, a 4 x 4 grid of v_mfma_f32_16x16x128_f8f6f4 products (lane l holds
-// 32 bytes of row l % 16 of each operand fragment; the k order inside a lane is the same for A
-// and B, which is all the product needs - gemv_common.h). The A (activation) and B (weight) tiles
-// of a step are staged in LDS with 16 bytes of padding per 128-byte row, so the sixteen rows a
-// fragment read touches fall in distinct banks; the next step's tiles are loaded into registers
-// while the current one is multiplied.
-//
-// Activations arrive as e4m3 (KRQ_X_FP8, with their scale) or as bf16 with an inverse scale
-// (KRQ_X_BF16_STATIC: ActScale / SharedScale): the block then quantizes its A tile on the way
-// into LDS, e4m3(clamp(x * inv)), the reference's cast fused into the GEMM.
+// Two kernels. k_gemm_ring (below) takes e4m3 activations with K >= 256: persistent blocks, an LDS
+// ring of direct global->LDS loads, 256 x 256 or 128 x 128 tiles and split K for small grids.
+// k_gemm_fp8 takes the rest (K = 128, or bf16 activations cast on the way into LDS): a block owns
+// a 128 x 128 output tile and walks K in steps of 128 bytes; its four waves each own a 64 x 64
+// quarter, a 4 x 4 grid of v_mfma_f32_16x16x128_f8f6f4 products (lane l holds 32 bytes of row
+// l % 16 of each operand fragment; the k order inside a lane is the same for A and B, which is
+// all the product needs - gemv_common.h). Its A (activation) and B (weight) tiles of a step are
+// staged in LDS with 16 bytes of padding per 128-byte row, so the sixteen rows a fragment read
+// touches fall in distinct banks; the next step's tiles are loaded into registers while the
+// current one is multiplied. With bf16 activations and an inverse scale (KRQ_X_BF16_STATIC:
+// ActScale / SharedScale) the block quantizes its A tile on the way into LDS, e4m3(clamp(x * inv)),
+// the reference's cast fused into the GEMM.
 #include <type_traits>
 
 #include "gemv_common.h"
@@ -487,10 +488,11 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
 //
 // Split K: a 128 x 128 grid of at most a quarter as many tiles as compute units splits K into
 // `splits` equal parts (the most of 8, 4, 2 with an even number of 64-byte stages and at least
-// 2 KB of K per part) when the fp32 partials (splits x M x N x 4 bytes, written once and read
-// once) are no more bytes than the weights (N x K). Measured at M = 256 (40 tiles): down 44.5 ->
-// 19.8 us with 4 parts (27.3 with 2), O 15.7 -> 15.0 us with 2; at 96 tiles (QKV, 2 parts) and 160
-// (M = 1024 down) the partials cost more than the parts gained (11.9 -> 18.5, 44.4 -> 49.8 us).
+// 2 KB of K per part) when the parts then number at least half the compute units and the fp32
+// partials (splits x M x N x 4 bytes, written once and read once) are no more bytes than the
+// weights (N x K). Measured at M = 256 (40 tiles): down 44.5 -> 15.5 + 4.6 us (the sum) with 4
+// parts, 27.3 with 2; O (2 parts, 80 units) 15.7 -> 12.1 + 4.7 us; at 96 tiles (QKV, 2 parts) and
+// 160 (M = 1024 down) the partials cost more than the parts gained (11.9 -> 18.5, 44.4 -> 49.8 us).
 struct RingPlan {
   int bm, bn, occ, splits;
 };
@@ -505,7 +507,7 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int cus) {
   if (t128 <= cus / 4) {
     const int64_t nk = K / 64;
     for (int sp = 8; sp >= 2; sp /= 2)
-      if (nk % (2 * sp) == 0 && K / sp >= 2048 && sp * M * 4 <= K) {
+      if (nk % (2 * sp) == 0 && K / sp >= 2048 && sp * M * 4 <= K && t128 * sp >= cus / 2) {
         splits = sp;
         break;
       }

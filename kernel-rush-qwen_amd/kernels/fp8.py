@@ -372,9 +372,11 @@ def swiglu_cast_fp8(x, q, out_a, a=None, xs=None):
 def gemm_fp8(x, q, a=None, xs=None):
     """Prefill FP8 GEMM (krq_gemm_fp8_ws): bf16 [M, N] = bf16(x8 . w8^T * x_scale[m] * w_scale[n]),
     the product torch._scaled_mm gives linear_fp8 (engine/kernels/fp8.py:105-106).
-    x is bf16 [M, K] with an ActScale / SharedScale `a` (the cast is fused into the GEMM's A-tile
-    staging) or float8_e4m3fn [M, K] with its scale xs (1 or M values); q from quantize_weight /
-    quantize, N and K multiples of 128."""
+    x is bf16 [M, K] with an ActScale / SharedScale `a`, or float8_e4m3fn [M, K] with its scale xs
+    (1 or M values); q from quantize_weight / quantize, N and K multiples of 128. bf16 rows are cast
+    once (krq_cast_fp8) and multiplied by the e4m3 kernels where those run (K >= 256), else the
+    cast is fused into the 128 x 128 kernel's A staging; both give the bytes of the reference's
+    cast followed by the e4m3 product."""
     w8, ws = q[0], q[1]
     L.require_device(x, w8, ws)
     if w8.dtype != torch.float8_e4m3fn or w8.dim() != 2 or not w8.is_contiguous():
@@ -390,6 +392,8 @@ def gemm_fp8(x, q, a=None, xs=None):
     else:
         if a is None:
             raise ValueError("bf16 activations need an ActScale / SharedScale a")
+        if K % 128 == 0 and K >= 256:
+            return gemm_fp8(_cast_hip(_rows(x), a), q, xs=a.scale.reshape(1))
         kind, xin, x_scale, x_inv = L.X_BF16_STATIC, _rows(x), a.scale.reshape(1), a.inv.reshape(1)
     L.require_device(x_scale, x_inv)
     xpr = 1 if (x_scale.numel() == M and M > 1) else 0

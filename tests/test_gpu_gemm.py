@@ -49,8 +49,8 @@ def test_gemm_fp8_matches_oracle(dev, M, N, K, per_row):
     assert e <= TOL
 
 
-@pytest.mark.parametrize("M,N,K,splits", [(256, 2560, 9728, 4), (200, 2560, 9728, 4), (300, 2560, 4096, 2),
-                                          (130, 1024, 8192, 4)])
+@pytest.mark.parametrize("M,N,K,splits", [(256, 2560, 9728, 4), (200, 2560, 9728, 4), (300, 2560, 8192, 4),
+                                          (130, 4096, 8192, 4)])
 def test_gemm_split_k(dev, M, N, K, splits):
     """Split K (krq_gemm_fp8_ws with its workspace) and the unsplit kernel (krq_gemm_fp8, or the
     workspace form given too little workspace, which must then equal it bit for bit): both within
@@ -75,10 +75,13 @@ def test_gemm_split_k(dev, M, N, K, splits):
         assert e <= TOL
 
 
-@pytest.mark.parametrize("M,N,K", [(200, 256, 384), (512, 2560, 4096)])
+@pytest.mark.parametrize("M,N,K", [(200, 256, 128), (200, 256, 384), (512, 2560, 4096)])
 def test_gemm_fused_cast_is_cast_then_gemm(dev, M, N, K):
-    """bf16 x with an ActScale: the in-kernel cast equals fp8._cast + the e4m3 GEMM bit for bit,
-    and linear_fp8 (prefill) is within the bar of the oracle."""
+    """bf16 x with an ActScale: gemm_fp8 (the cast fused into the 128 x 128 kernel at K = 128,
+    the HIP cast then the e4m3 kernels otherwise) equals fp8._cast + the e4m3 GEMM bit for bit; the
+    C ABI's fused-cast kernel (krq_gemm_fp8 on bf16 rows) and linear_fp8 (prefill) are within the
+    bar of the oracle."""
+    from kernels import _lib as L
     w = bf((N, K), 3, 0.02).to(dev)
     q = F.quantize_weight(w)
     x = bf((M, K), 4).to(dev)
@@ -86,9 +89,13 @@ def test_gemm_fused_cast_is_cast_then_gemm(dev, M, N, K):
     y = F.gemm_fp8(x, q, a)
     y2 = F.gemm_fp8(F._cast(x, a), q, xs=a.scale.reshape(1))
     assert torch.equal(y, y2)
+    y3 = torch.empty_like(y)
+    L.call("krq_gemm_fp8", L.ptr(x), L.X_BF16_STATIC, L.ptr(a.scale), L.ptr(a.inv), 0, L.ptr(q[0]), L.ptr(q[1]), 0,
+           M, N, K, L.ptr(y3), L.stream(x))
     _, ref = O.fp8_matmul(codes(F._cast(x, a)), a.scale.cpu().numpy(), codes(q[0]), q[1].cpu().numpy())
     assert rel_err(F.linear_fp8(x, q).float().cpu().numpy(), ref) <= TOL
     assert rel_err(y.float().cpu().numpy(), ref) <= TOL
+    assert rel_err(y3.float().cpu().numpy(), ref) <= TOL
 
 
 def test_gemm_matches_library_gemm(dev):
