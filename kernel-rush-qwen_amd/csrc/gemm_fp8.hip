@@ -136,18 +136,21 @@ __global__ __launch_bounds__(kThreads) void k_gemm_fp8(const uint8_t* __restrict
 // v_mfma_f32_32x32x64_f8f6f4 with the B (weight) fragment as its first operand (lane l holds 32
 // bytes of row l % 32 of each operand fragment, k bytes 32 (l / 32) .. +31 of the 64-byte stage;
 // the product's element e of lane l belongs to first-operand row 8 (e / 4) + 4 (l / 32) + e % 4 and
-// second-operand row l % 32). K advances 64 bytes per stage through an LDS ring of ST stages.
-// Global bytes reach LDS with global_load_lds_dwordx4: one instruction
-// writes 1 KB, 16 rows of 64 bytes, lane i at byte 16 i, so a lane's global address picks which
-// 16-byte chunk of which row lands at that position. Chunk c of row r sits at position
-// c ^ ((r >> 2) & 3) of its row: a ds_read_b128 serves 16 lanes (256 bytes) per cycle, and the
-// 16 rows those lanes read then start on 16 distinct 16-byte bank groups (with the chunk taken
-// from row bits 1-2 instead, rows r and r + 8 collide and half the LDS cycles were conflicts).
+// second-operand row l % 32). K advances 64 bytes per stage; stages come in pairs whose 128 bytes
+// of each row fill one of two LDS pair buffers. Global bytes reach LDS with
+// global_load_lds_dwordx4: one instruction writes 1 KB, 8 rows of 128 bytes (whole lines), lane i
+// at byte 16 i, so a lane's global address picks which 16-byte chunk of which row lands at that
+// position. Chunk c of row r sits at position c ^ ((r >> 1) & 7) of its row: a ds_read_b128 serves
+// 16 lanes (256 bytes) per cycle, and the 16 rows those lanes read then start on 16 distinct
+// 16-byte bank groups. (With 64-byte rows, one stage per buffer and a chunk taken from row bits
+// 1-2, rows r and r + 8 collided and half the LDS cycles were conflicts; loading a line's two
+// halves with separate instructions sent both to L2.)
 //
-// Per stage s: wait for this wave's loads of stage s + 1, barrier (every wave's loads of s + 1
-// have landed and every wave is done with stage s - 1's buffer), issue the loads of stage
-// s + ST - 1 into that buffer, read stage s + 1's fragments into the other register set, and
-// multiply stage s. Past the last stage the loads go to a sink (one cached KB, same count).
+// Per pair of stages (2j, 2j + 1): the even stage multiplies from registers and reads the odd
+// stage's fragments; the odd stage waits for the next pair's loads, passes a barrier (every wave's
+// loads have landed and every wave is done with pair j's buffer), issues the loads of pair j + 2
+// into that buffer, reads the next even stage's fragments and multiplies. Past the last stage the
+// loads go to a sink (one cached KB, same count).
 namespace ring {
 
 constexpr int BK = 64, kThreads = 256;
@@ -165,6 +168,11 @@ KRQ_DEV uint32_t lds_addr(const uint8_t* p) {
 // kernel waits for them itself (wait_vm) and no other global load is in flight in the main loop.
 KRQ_DEV void dma16(const uint8_t* g, uint32_t l) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(l), "v"(g) : "memory", "m0");
+}
+
+// the same from a wave-uniform base plus a 32-bit per-lane byte offset
+KRQ_DEV void dma16s(const uint8_t* base, uint32_t voff, uint32_t l) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(voff), "s"(base) : "memory", "m0");
 }
 
 // global_load_lds_dword: 4 bytes per lane from g into LDS at l + 4 * lane (same waits as dma16)
@@ -207,29 +215,28 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
                                                            const float* __restrict__ bsc, int b_per_row, int M, int N,
                                                            int K, int tiles_m, int tiles, int splits,
                                                            float* __restrict__ ws, uint16_t* __restrict__ out) {
-  constexpr int ST = 4;                        // ring buffers
-  constexpr int kStageBytes = (BM + BN) * BK;  // A rows, then B rows
-  __shared__ __align__(1024) uint8_t ring[ST * kStageBytes];
+  constexpr int kPairBytes = (BM + BN) * 2 * BK;  // two stages: 128 bytes of K per row, A rows then B rows
+  __shared__ __align__(1024) uint8_t ring[2 * kPairBytes];
   __shared__ __align__(1024) float scl[2][BM + BN];  // per tile (alternating): row scales, then column scales
   __shared__ __align__(1024) uint8_t sink[1024];     // where the loads of stages past the last one land
   constexpr int FI = BM / 64, FJ = BN / 64;          // 32-row fragments of a wave's quarter
-  constexpr int QA = BM / 64, QB = BN / 64;          // 1 KB loads per wave per stage
+  constexpr int QA = BM / 32, QB = BN / 32;          // 1 KB loads (8 rows x 128 B) per wave per pair
   constexpr int kVm = QA + QB;
-  constexpr int NF = FI + FJ;                 // fragments per stage, two 16-byte reads each
+  constexpr int NF = FI + FJ;                  // fragments per stage, two 16-byte reads each
   constexpr int kSI = (BM + BN) / 64;          // 64-scale loads per tile
   constexpr int kScl = (kSI + 3) / 4;          // per wave (the surplus goes to the sink)
-  constexpr int EB = PART ? 4 : 2;           // output element bytes
-  constexpr int RB = BN / 2 * EB;             // bytes per row of a wave's output quarter
-  constexpr int CPR = RB / 16;                // 16-byte chunks per such row
+  constexpr int EB = PART ? 4 : 2;             // output element bytes
+  constexpr int RB = BN / 2 * EB;              // bytes per row of a wave's output quarter
+  constexpr int CPR = RB / 16;                 // 16-byte chunks per such row
   constexpr int kStores = FI * 32 * CPR / 64;  // 16-byte stores per lane per tile
+  constexpr int CR = kPairBytes >= 4 * 32 * RB ? 32 : 16;  // output rows per staging chunk
   static_assert((BM + BN) % 64 == 0, "scale loads");
-  static_assert(2 * kVm + kStores + kVm < 64, "vmcnt range");
-  constexpr int CR = kStageBytes >= 4 * 32 * RB ? 32 : 16;  // output rows per staging chunk
-  static_assert(4 * CR * RB <= kStageBytes, "output staging fits one ring buffer");
+  static_assert(kVm + kStores < 64, "vmcnt range");
+  static_assert(4 * CR * RB <= kPairBytes, "output staging fits one pair buffer");
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x, bid = blockIdx.x;
   const int wm = (wave & 1) * (BM / 2), wn = (wave >> 1) * (BN / 2);
-  const int nk = K / BK / splits;  // stages of a work unit
+  const int nk = K / BK / splits;  // stages of a work unit (even)
   const int units = tiles * splits;
 
   // This block's k-th work unit (unit u: tile u % tiles, split u / tiles): units in order, tiles
@@ -242,38 +249,45 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
     return base + bid;
   };
 
-  // load q of this wave covers rows 16 (wave + 4 q) .. + 15 of A (q < QA) or of B; lane -> row
-  // + lane / 4, position lane % 4
+  // load q of this wave covers rows 8 (wave + 4 q) .. + 7 of A (q < QA) or of B, 128 bytes of K
+  // each: lane -> row + lane / 8, position lane % 8 of the row. Addresses are a wave-uniform base
+  // (the tile's first A or B row, its split's first K byte) plus a 32-bit offset per lane (the
+  // operands are below 2 GiB, checked at launch).
   int m0 = 0, n0 = 0, sp = 0;
-  const uint8_t* gsrc[kVm];
+  const uint8_t* abase = a;
+  const uint8_t* bbase = b;
+  uint32_t goff[kVm];
   auto set_tile = [&](int u) {
     const int p = u % tiles;
     sp = u / tiles;
     m0 = (p % tiles_m) * BM;
     n0 = (p / tiles_m) * BN;
     const int64_t kb = (int64_t)sp * nk * BK;
+    abase = a + (int64_t)m0 * K + kb;
+    bbase = b + (int64_t)n0 * K + kb;
 #pragma unroll
     for (int q = 0; q < QA; ++q) {
-      const int row = 16 * (wave + 4 * q) + (lane >> 2);
-      gsrc[q] = a + (int64_t)min(m0 + row, M - 1) * K + kb + 16 * ((lane & 3) ^ ((row >> 2) & 3));
+      const int row = 8 * (wave + 4 * q) + (lane >> 3);
+      goff[q] = static_cast<uint32_t>((min(m0 + row, M - 1) - m0) * K + 16 * ((lane & 7) ^ ((row >> 1) & 7)));
     }
 #pragma unroll
     for (int q = 0; q < QB; ++q) {
-      const int row = 16 * (wave + 4 * q) + (lane >> 2);
-      gsrc[QA + q] = b + (int64_t)(n0 + row) * K + kb + 16 * ((lane & 3) ^ ((row >> 2) & 3));
+      const int row = 8 * (wave + 4 * q) + (lane >> 3);
+      goff[QA + q] = static_cast<uint32_t>(row * K + 16 * ((lane & 7) ^ ((row >> 1) & 7)));
     }
   };
   const uint32_t lbase = lds_addr(ring) + 1024 * wave, lsink = lds_addr(sink);
   const uint32_t lscl = lds_addr(reinterpret_cast<const uint8_t*>(&scl[0][0]));
-  // a stage's load q, or past the last stage the same count of loads of one cached KB of B into the
-  // sink, chosen without a branch so that every stage issues the same loads and waits alike
-  auto ring_load = [&](int q, int s, int buf) {
-    const bool real = s < nk;
-    dma16(real ? gsrc[q] + (int64_t)s * BK : b + 16 * lane,
-          real ? lbase + buf * kStageBytes + (q < QA ? 4096 * q : BM * BK + 4096 * (q - QA)) : lsink);
+  // load q of pair j (stages 2j and 2j + 1) into pair buffer pb, or past the last stage the same
+  // count of loads of one cached KB of B into the sink, chosen without a branch so that every
+  // odd stage issues the same loads and waits alike
+  auto pair_load = [&](int q, int j, int pb) {
+    const bool real = 2 * j < nk;
+    dma16s(real ? (q < QA ? abase : bbase) + j * 2 * BK : b, real ? goff[q] : 16u * lane,
+           real ? lbase + pb * kPairBytes + (q < QA ? 4096 * q : BM * 2 * BK + 4096 * (q - QA)) : lsink);
   };
   // the tile's scales (kScl loads of 64 per wave; a per-tensor scale is loaded by every lane), then
-  // its stages 0 .. 2 into buffers 0 .. 2
+  // its first pair of stages into pair buffer 0
   auto tile_loads = [&](int sb) {
 #pragma unroll
     for (int k = 0; k < kScl; ++k) {
@@ -282,30 +296,36 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
            li < kSI ? lscl + 4 * (sb * (BM + BN) + li * 64) : lsink);
     }
 #pragma unroll
-    for (int p = 0; p < 3; ++p)
-#pragma unroll
-      for (int q = 0; q < kVm; ++q) ring_load(q, p, p);
+    for (int q = 0; q < kVm; ++q) pair_load(q, 0, 0);
   };
 
-  // fragment f (A for f < FI, else B) of a stage: row (lane & 31) of its 32-row block, logical
-  // chunks 2 (lane >> 5) (h = 0) and + 1 (h = 1)
-  const int fr = lane & 31, sw = (lane >> 2) & 3;
-  const int off[2] = {fr * BK + 16 * ((2 * (lane >> 5)) ^ sw), fr * BK + 16 * ((2 * (lane >> 5) + 1) ^ sw)};
+  // Fragment f (A for f < FI, else B) of stage s: row (lane & 31) of its 32-row block, the 64-byte
+  // half s % 2 of the row's 128 bytes, logical chunks 2 (lane >> 5) (hh = 0) and + 1 (hh = 1) of
+  // that half. Chunk c (0 .. 7) of row r sits at c ^ ((r >> 1) & 7): the 16 rows a ds_read_b128
+  // phase reads then start on 16 distinct 16-byte bank groups.
+  const int sw = ((lane & 31) >> 1) & 7;
+  int off[2][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) off[h][hh] = (lane & 31) * 2 * BK + 16 * ((4 * h + 2 * (lane >> 5) + hh) ^ sw);
   uint4 fh[2][NF][2];
-  auto read = [&](int set, int f, int h, int buf) {
-    const uint8_t* p = ring + buf * kStageBytes + (f < FI ? (wm + 32 * f) * BK : BM * BK + (wn + 32 * (f - FI)) * BK);
-    fh[set][f][h] = *reinterpret_cast<const uint4*>(p + off[h]);
+  auto read = [&](int set, int f, int hh, int h, int pb) {
+    const uint8_t* p =
+        ring + pb * kPairBytes + (f < FI ? (wm + 32 * f) * 2 * BK : BM * 2 * BK + (wn + 32 * (f - FI)) * 2 * BK);
+    fh[set][f][hh] = *reinterpret_cast<const uint4*>(p + off[h][hh]);
   };
   v16f acc[FI][FJ];
 
-  // One stage: the products of stage s from register set `set`, the 2 NF reads of stage s + 1's
-  // fragments (buffer bn = (s + 1) % 4) into the other set spread evenly after them. An odd stage s
-  // also loads stages s + 3 and s + 4, spread the same way: they are adjacent 64-byte halves of the
-  // same 128-byte lines (the second half is then served by the vector cache), and their buffers
-  // are the ones stages s - 1 and s used. The last stage (odd) reads and loads nothing.
-  constexpr int NP = FI * FJ, NR = 2 * NF, NL = 2 * kVm;
-  auto body = [&](auto set_c, auto loads_c, auto reads_c, int s, int bn) __attribute__((always_inline)) {
-    constexpr int set = decltype(set_c)::value;
+  // One stage s (register set s % 2): its products, the 2 NF reads of stage s + 1's fragments
+  // (pair buffer pbn, half (s + 1) % 2) into the other set spread evenly after them, and for an odd
+  // stage the loads of the pair after next (stages s + 3 and s + 4) into pair buffer pbl, the one
+  // stages s - 1 and s used, spread the same way. An even stage's data arrived with the odd
+  // stage's before it, so only odd stages wait and pass a barrier. The last stage reads and loads
+  // nothing.
+  constexpr int NP = FI * FJ, NR = 2 * NF, NL = kVm;
+  auto body = [&](auto par_c, auto loads_c, auto reads_c, int s, int pbn, int pbl) __attribute__((always_inline)) {
+    constexpr int set = decltype(par_c)::value;
     constexpr bool LOADS = decltype(loads_c)::value, READS = decltype(reads_c)::value;
 #pragma unroll
     for (int u = 0; u < NP; ++u) {
@@ -315,31 +335,30 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
           0, 0, 0, 0);
       if (LOADS) {
 #pragma unroll
-        for (int l = u * NL / NP; l < (u + 1) * NL / NP; ++l)
-          ring_load(l % kVm, l < kVm ? s + 3 : s + 4, (bn + (l < kVm ? 2 : 3)) & 3);
+        for (int l = u * NL / NP; l < (u + 1) * NL / NP; ++l) pair_load(l, (s + 3) / 2, pbl);
       }
       if (READS) {
 #pragma unroll
-        for (int r = u * NR / NP; r < (u + 1) * NR / NP; ++r) read(set ^ 1, r >> 1, r & 1, bn);
+        for (int r = u * NR / NP; r < (u + 1) * NR / NP; ++r) read(set ^ 1, r >> 1, r & 1, set ^ 1, pbn);
       }
     }
     if (READS) StagePattern<0, NP, NR>::apply();
   };
   using yes = std::true_type;
   using no = std::false_type;
-  using set0 = std::integral_constant<int, 0>;
-  using set1 = std::integral_constant<int, 1>;
+  using even = std::integral_constant<int, 0>;
+  using odd = std::integral_constant<int, 1>;
 
   // Epilogue. acc[i][j] element e of lane l is the output at row m = wm + 32 i + l % 32 and column
   // n = wn + 32 j + 8 (e / 4) + 4 (l / 32) + e % 4 (B is the first product operand): a lane holds
-  // four adjacent columns of a row. Ring buffer 3 is idle here (the next tile's loads fill buffers
-  // 0 .. 2), so each wave stages CR rows of its quarter at a time in its own part of it (rows of
+  // four adjacent columns of a row. Pair buffer 1 is idle here (the next tile's first loads fill
+  // buffer 0), so each wave stages CR rows of its quarter at a time in its own part of it (rows of
   // BN bytes, 16-byte chunk c of row r at c ^ (r % (BN / 16))), 8 bytes per lane, then reads them
   // back along rows and stores 16 bytes per lane: each store writes whole row segments. The stores
   // drain while the block's next tile runs. Rounding to bf16 is the hardware convert (nearest
   // even, as f32_to_bf16 for every non-NaN value).
   auto epilogue = [&](int cm0, int cn0, int csp, const float* sc) {
-    uint8_t* tq = ring + (ST - 1) * kStageBytes + wave * CR * RB;
+    uint8_t* tq = ring + kPairBytes + wave * CR * RB;
     const int r = lane & 31;
 #pragma unroll
     for (int i = 0; i < FI; ++i) {
@@ -391,19 +410,19 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
   set_tile(p);
   tile_loads(0);
   for (int k = 0;; ++k) {
-    // Stage 3 goes into buffer 3 once every wave is done with the previous epilogue's staging.
-    // In flight, oldest first: the scales and stages 0 .. 2, the previous tile's kStores stores
-    // (k > 0), stage 3.
+    // The second pair goes into buffer 1 once every wave is done with the previous epilogue's
+    // staging. In flight, oldest first: the scales and the first pair, the previous tile's kStores
+    // stores (k > 0), the second pair.
     lds_barrier();
 #pragma unroll
-    for (int q = 0; q < kVm; ++q) ring_load(q, 3, 3);
-    if (k == 0) wait_vm<3 * kVm>();
-    else wait_vm<3 * kVm + kStores>();
+    for (int q = 0; q < kVm; ++q) pair_load(q, 1, 1);
+    if (k == 0) wait_vm<kVm>();
+    else wait_vm<kVm + kStores>();
     lds_barrier();
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-      read(0, f, 0, 0);
-      read(0, f, 1, 0);
+      read(0, f, 0, 0, 0);
+      read(0, f, 1, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < FI; ++i)
@@ -413,38 +432,21 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
         for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
     const int cm0 = m0, cn0 = n0, csp = sp;
     const int next = tile_of(k + 1);
-    // stage 0 (needs stage 1) and stage 1 (needs stage 2, loads stages 4 and 5)
-    if (k == 0) wait_vm<2 * kVm>();
-    else wait_vm<2 * kVm + kStores>();
-    lds_barrier();
-    body(set0{}, no{}, yes{}, 0, 1);
-    if (k == 0) wait_vm<kVm>();
-    else wait_vm<kVm + kStores>();
-    lds_barrier();
-    body(set1{}, yes{}, yes{}, 1, 2);
-    // stages 2 .. nk - 2: an even stage waits for the next one with the following two in flight,
-    // an odd stage with one
-    int bn = 3;
-    for (int s = 2; s < nk - 2; s += 2) {
-      wait_vm<2 * kVm>();
+    for (int s = 0; s < nk - 2; s += 2) {
+      const int pb = (s >> 1) & 1;
+      body(even{}, no{}, yes{}, s, pb, 0);
+      wait_vm<0>();  // the pair of stages s + 2, s + 3
       lds_barrier();
-      body(set0{}, no{}, yes{}, s, bn);
-      bn = (bn + 1) & 3;
-      wait_vm<kVm>();
-      lds_barrier();
-      body(set1{}, yes{}, yes{}, s + 1, bn);
-      bn = (bn + 1) & 3;
+      body(odd{}, yes{}, yes{}, s + 1, pb ^ 1, pb);
     }
-    wait_vm<2 * kVm>();
-    lds_barrier();
-    body(set0{}, no{}, yes{}, nk - 2, bn);
+    body(even{}, no{}, yes{}, nk - 2, ((nk - 2) >> 1) & 1, 0);
     // last stage: once every wave is past this barrier the ring is free; the next tile starts loading
     lds_barrier();
     if (next >= 0) {
       set_tile(next);
       tile_loads((k + 1) & 1);
     }
-    body(set1{}, no{}, no{}, nk - 1, 0);
+    body(odd{}, no{}, no{}, nk - 1, 0, 0);
     epilogue(cm0, cn0, csp, scl[k & 1]);
     if (next < 0) break;
   }
@@ -542,7 +544,7 @@ int gemm_run(const void* x, int x_kind, const float* x_scale, const float* x_inv
   const int64_t blocks = (int64_t)tiles_m * (N / BN);
   KRQ_REQUIRE(blocks <= 0x7fffffff, "gemm_fp8: grid too large");
   hipStream_t s = (hipStream_t)stream;
-  if (ring_fits(x_kind, K) && aligned16(out)) {
+  if (ring_fits(x_kind, K) && aligned16(out) && M * K < 0x7fffffff && N * K < 0x7fffffff) {
     int cus = 0;
     KRQ_REQUIRE(query_cus(&cus) == KRQ_OK, "gemm_fp8: device query failed");
     RingPlan rp = ring_plan(M, N, K, cus);
