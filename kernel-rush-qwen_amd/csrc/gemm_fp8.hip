@@ -481,10 +481,12 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
 
 // Tile shape of the ring kernel for an e4m3 GEMM, a pure function of the shape and the device's
 // compute-unit count. Measured at the Qwen3-4B projections (M = 256 .. 4096): a round of
-// 256 x 256 tiles (one block per compute unit) takes 1.45x as long as a round of 128 x 128 tiles
-// running two blocks per compute unit, and does four times their products; 128 x 256 tiles were
-// never faster than one of the two. The plan takes the one with fewer estimated round-lengths,
-// counting the tiles of the busiest compute unit. The 128 x 128 ring kernel also beat the
+// 256 x 256 tiles (one block per compute unit) takes 1.75x as long as a round of two 128 x 128
+// tiles on each compute unit, and does twice their products (gate_up at M = 4096: 204 us for 5
+// rounds against 220 us for 9.5); 128 x 256 tiles were never faster than one of the two. The
+// plan takes the one with fewer estimated round-lengths, counting the tiles of the busiest
+// compute unit (128 x 128 ones two at a time). It picks the faster of the two measured kernels at
+// all twelve shapes of the prefill bench. The 128 x 128 ring kernel also beat the
 // register-staged one on grids of 40 tiles (M = 256: O 15.8 against 41.0 us, down 44.8 against
 // 93.4), so bm == 0 only where N is not a multiple of 128.
 //
@@ -502,7 +504,7 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int cus) {
   const int64_t t256 = N % 256 == 0 ? ((M + 255) / 256) * (N / 256) : 0;
   const int64_t t128 = N % 128 == 0 ? ((M + 127) / 128) * (N / 128) : 0;
   const double c256 = (double)((t256 + cus - 1) / cus);               // rounds of 256 x 256
-  const double c128 = 0.69 * (double)((t128 + cus - 1) / cus) / 2.0;  // two blocks per unit
+  const double c128 = 0.57 * (double)(((t128 + cus - 1) / cus + 1) / 2);  // two blocks per unit
   if (t256 >= cus / 2 && (t128 == 0 || c256 <= c128)) return {256, 256, 1, 1};
   if (t128 == 0) return {0, 0, 0, 0};
   int splits = 1;
