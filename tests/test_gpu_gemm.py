@@ -36,7 +36,9 @@ def bf(shape, seed, scale=1.0):
                                            # 256 x 256 ring tiles (>= 128 of them): ragged M, a tile count
                                            # that is not a multiple of the 8 XCDs, several tiles per CU
                                            (2000, 4096, 2560, True), (2100, 4352, 256, True),
-                                           (4096, 8192, 384, False)])
+                                           (4096, 8192, 384, False),
+                                           # 192 x 256 tiles: ragged M (20 full row tiles + 160 rows)
+                                           (4000, 2560, 512, True), (4096, 2560, 4096, False)])
 def test_gemm_fp8_matches_oracle(dev, M, N, K, per_row):
     w = bf((N, K), 1, 0.02).to(dev)
     q = F.quantize(w) if per_row else F.quantize_weight(w)
