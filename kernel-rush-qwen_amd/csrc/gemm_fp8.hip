@@ -493,13 +493,13 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
 // register-staged one on grids of 40 tiles (M = 256: O 15.8 against 41.0 us, down 44.8 against
 // 93.4), so bm == 0 only where N is not a multiple of 128.
 //
-// Split K: a 128 x 128 grid of at most a quarter as many tiles as compute units splits K into
-// `splits` equal parts (the most of 8, 4, 2 with an even number of 64-byte stages and at least
-// 2 KB of K per part) when the parts then number at least half the compute units and the fp32
-// partials (splits x M x N x 4 bytes, written once and read once) are no more bytes than the
-// weights (N x K). Measured at M = 256 (40 tiles): down 44.5 -> 15.5 + 4.6 us (the sum) with 4
-// parts, 27.3 with 2; O (2 parts, 80 units) 15.7 -> 12.1 + 4.7 us; at 96 tiles (QKV, 2 parts) and
-// 160 (M = 1024 down) the partials cost more than the parts gained (11.9 -> 18.5, 44.4 -> 49.8 us).
+// Split K: a 128 x 128 grid of fewer tiles than compute units splits K into `splits` equal parts
+// (the most of 8, 4, 2 with an even number of 64-byte stages and at least 2 KB of K per part)
+// when the parts then number at least half the compute units and the fp32 partials
+// (splits x M x N x 4 bytes, written once and read once) are no more bytes than the weights
+// (N x K). Measured: M = 256 down (40 tiles) 44.5 -> 16.3 + 4.8 us (the sum) with 4 parts, 27.3
+// with 2; M = 1024 down (160 tiles) 49.3 -> 38.5 us with 2; O at M = 256 (2 parts, 80 units)
+// 15.7 -> 12.1 + 4.7 us, and QKV at M = 256 (2 parts) 11.9 -> 18.5 us, which the rules exclude.
 struct RingPlan {
   int bm, bn, occ, splits;
 };
@@ -515,7 +515,7 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int cus) {
   if (ok256 && (t128 == 0 || c256 <= c128)) return {256, 256, 1, 1};
   if (t128 == 0) return {0, 0, 0, 0};
   int splits = 1;
-  if (t128 <= cus / 4) {
+  if (t128 < cus) {
     const int64_t nk = K / 64;
     for (int sp = 8; sp >= 2; sp /= 2)
       if (nk % (2 * sp) == 0 && K / sp >= 2048 && sp * M * 4 <= K && t128 * sp >= cus / 2) {
