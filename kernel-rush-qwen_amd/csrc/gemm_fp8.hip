@@ -500,6 +500,8 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
 // (N x K). Measured: M = 256 down (40 tiles) 44.5 -> 16.3 + 4.8 us (the sum) with 4 parts, 27.3
 // with 2; M = 1024 down (160 tiles) 49.3 -> 38.5 us with 2; O at M = 256 (2 parts, 80 units)
 // 15.7 -> 12.1 + 4.7 us, and QKV at M = 256 (2 parts) 11.9 -> 18.5 us, which the rules exclude.
+// A grid of fewer 128 x 128 tiles than compute units that does not split runs 64 x 64 tiles, four
+// blocks per compute unit: M = 256 O 14.4 -> 10.1 us, QKV 11.2 -> 10.2, M = 1024 O 22.6 -> 20.2.
 struct RingPlan {
   int bm, bn, occ, splits;
 };
@@ -514,8 +516,9 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int cus) {
   if (ok192 && c192 < c256 && (t128 == 0 || c192 <= c128)) return {192, 256, 1, 1};
   if (ok256 && (t128 == 0 || c256 <= c128)) return {256, 256, 1, 1};
   if (t128 == 0) return {0, 0, 0, 0};
+  if (t128 >= cus) return {128, 128, 2, 1};
   int splits = 1;
-  if (t128 < cus) {
+  {
     const int64_t nk = K / 64;
     for (int sp = 8; sp >= 2; sp /= 2)
       if (nk % (2 * sp) == 0 && K / sp >= 2048 && sp * M * 4 <= K && t128 * sp >= cus / 2) {
@@ -523,7 +526,8 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int cus) {
         break;
       }
   }
-  return {128, 128, 2, splits};
+  if (splits > 1) return {128, 128, 2, splits};
+  return {64, 64, 4, 1};
 }
 
 int query_cus(int* cus) {
@@ -571,6 +575,8 @@ int gemm_run(const void* x, int x_kind, const float* x_scale, const float* x_inv
         KRQ_RING(256, 256, 1, false);
       } else if (rp.bm == 192) {
         KRQ_RING(192, 256, 1, false);
+      } else if (rp.bm == 64) {
+        KRQ_RING(64, 64, 4, false);
       } else if (rp.splits == 1) {
         KRQ_RING(128, 128, 2, false);
       } else {

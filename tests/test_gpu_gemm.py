@@ -38,7 +38,9 @@ def bf(shape, seed, scale=1.0):
                                            (2000, 4096, 2560, True), (2100, 4352, 256, True),
                                            (4096, 8192, 384, False),
                                            # 192 x 256 tiles: ragged M (20 full row tiles + 160 rows)
-                                           (4000, 2560, 512, True), (4096, 2560, 4096, False)])
+                                           (4000, 2560, 512, True), (4096, 2560, 4096, False),
+                                           # 64 x 64 tiles: small grids that do not split K
+                                           (256, 2560, 4096, True), (100, 1024, 512, False)])
 def test_gemm_fp8_matches_oracle(dev, M, N, K, per_row):
     w = bf((N, K), 1, 0.02).to(dev)
     q = F.quantize(w) if per_row else F.quantize_weight(w)
