@@ -493,15 +493,17 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
 // register-staged one on grids of 40 tiles (M = 256: O 15.8 against 41.0 us, down 44.8 against
 // 93.4), so bm == 0 only where N is not a multiple of 128.
 //
-// Split K: a 128 x 128 grid of fewer tiles than compute units splits K into `splits` equal parts
-// (the most of 8, 4, 2 with an even number of 64-byte stages and at least 2 KB of K per part)
-// when the parts then number at least half the compute units and the fp32 partials
-// (splits x M x N x 4 bytes, written once and read once) are no more bytes than the weights
-// (N x K). Measured: M = 256 down (40 tiles) 44.5 -> 16.3 + 4.8 us (the sum) with 4 parts, 27.3
-// with 2; M = 1024 down (160 tiles) 49.3 -> 38.5 us with 2; O at M = 256 (2 parts, 80 units)
-// 15.7 -> 12.1 + 4.7 us, and QKV at M = 256 (2 parts) 11.9 -> 18.5 us, which the rules exclude.
-// A grid of fewer 128 x 128 tiles than compute units that does not split runs 64 x 64 tiles, four
-// blocks per compute unit: M = 256 O 14.4 -> 10.1 us, QKV 11.2 -> 10.2, M = 1024 O 22.6 -> 20.2.
+// Split K: a 128 x 128 grid of fewer tiles than compute units, with K of at least 8 KB, splits K
+// into `splits` equal parts (the most of 8, 4, 2 with an even number of 64-byte stages and at
+// least 2 KB of K per part) when the parts then number at least half the compute units and the
+// fp32 partials (splits x M x N x 4 bytes, written once and read once) are no more bytes than the
+// weights (N x K). Otherwise such a grid runs 64 x 64 tiles, four blocks per compute unit, split by
+// the same rules where 128 x 128 ones could not be. Measured (us, Qwen3-4B shapes):
+//   down (K = 9728): M = 256 44.5 -> 16.0 + 4.8 (128 x 128 in 4 parts; 27.3 in 2), M = 1024
+//     49.3 -> 38.5 (2 parts), M = 128 34.0 -> 15.6 and M = 64 19.1 -> 13.5 (64 x 64 in 4 parts);
+//   O (K = 4096) gained from no split: 64 x 64 tiles took M = 256 from 14.4 to 9.9 us, where 2 parts
+//     of 64 x 64 took 12.7 and 2 of 128 x 128 16.8; M = 1024 22.6 -> 20.3;
+//   QKV (K = 2560) at M = 256: 64 x 64 tiles 11.2 -> 10.2, 2 parts 18.5.
 struct RingPlan {
   int bm, bn, occ, splits;
 };
@@ -517,17 +519,17 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int cus) {
   if (ok256 && (t128 == 0 || c256 <= c128)) return {256, 256, 1, 1};
   if (t128 == 0) return {0, 0, 0, 0};
   if (t128 >= cus) return {128, 128, 2, 1};
-  int splits = 1;
-  {
+  // the most parts (8, 4, 2) a grid of `tiles` may split K into, or 1
+  auto parts = [&](int64_t tiles) {
     const int64_t nk = K / 64;
+    if (K < 8192) return 1;
     for (int sp = 8; sp >= 2; sp /= 2)
-      if (nk % (2 * sp) == 0 && K / sp >= 2048 && sp * M * 4 <= K && t128 * sp >= cus / 2) {
-        splits = sp;
-        break;
-      }
-  }
-  if (splits > 1) return {128, 128, 2, splits};
-  return {64, 64, 4, 1};
+      if (nk % (2 * sp) == 0 && K / sp >= 2048 && sp * M * 4 <= K && tiles * sp >= cus / 2) return sp;
+    return 1;
+  };
+  const int s128 = parts(t128);
+  if (s128 > 1) return {128, 128, 2, s128};
+  return {64, 64, 4, parts(((M + 63) / 64) * (N / 64))};
 }
 
 int query_cus(int* cus) {
@@ -575,8 +577,14 @@ int gemm_run(const void* x, int x_kind, const float* x_scale, const float* x_inv
         KRQ_RING(256, 256, 1, false);
       } else if (rp.bm == 192) {
         KRQ_RING(192, 256, 1, false);
-      } else if (rp.bm == 64) {
+      } else if (rp.bm == 64 && rp.splits == 1) {
         KRQ_RING(64, 64, 4, false);
+      } else if (rp.bm == 64) {
+        KRQ_RING(64, 64, 4, true);
+        const int64_t threads = M * N / 4;
+        hipLaunchKernelGGL(ring::k_splitk_reduce, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s,
+                           (const float*)ws, rp.splits, (int)M, (int)N, x_scale, x_per_row, w_scale, w_per_row,
+                           (uint16_t*)out);
       } else if (rp.splits == 1) {
         KRQ_RING(128, 128, 2, false);
       } else {

@@ -54,7 +54,9 @@ def test_gemm_fp8_matches_oracle(dev, M, N, K, per_row):
 
 
 @pytest.mark.parametrize("M,N,K,splits", [(256, 2560, 9728, 4), (200, 2560, 9728, 4), (300, 2560, 8192, 4),
-                                          (130, 4096, 8192, 4), (1024, 2560, 9728, 2)])
+                                          (130, 4096, 8192, 4), (1024, 2560, 9728, 2),
+                                          # 64 x 64 tiles split (too few 128 x 128 ones to split)
+                                          (64, 2560, 9728, 4), (100, 2560, 9728, 4)])
 def test_gemm_split_k(dev, M, N, K, splits):
     """Split K (krq_gemm_fp8_ws with its workspace) and the unsplit kernel (krq_gemm_fp8, or the
     workspace form given too little workspace, which must then equal it bit for bit): both within
