@@ -162,20 +162,17 @@ KRQ_DEV uint32_t lds_addr(const uint8_t* p) {
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t*)p)));
 }
 
-// global_load_lds_dwordx4: 16 bytes per lane from g into LDS at l + 16 * lane. Issued from inline
-// assembly so that the compiler, which cannot tell the ring's buffers apart once a loop holds more
-// of these loads than it tracks, does not wait for every load in flight before each LDS read; the
-// kernel waits for them itself (wait_vm) and no other global load is in flight in the main loop.
-KRQ_DEV void dma16(const uint8_t* g, uint32_t l) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(l), "v"(g) : "memory", "m0");
-}
-
-// the same from a wave-uniform base plus a 32-bit per-lane byte offset
+// global_load_lds_dwordx4: 16 bytes per lane from base + voff into LDS at l + 16 * lane (base
+// wave-uniform, voff a 32-bit per-lane byte offset). Issued from inline assembly so that the
+// compiler, which cannot tell the ring's buffers apart once a loop holds more of these loads than
+// it tracks, does not wait for every load in flight before each LDS read; the kernel waits for
+// them itself (wait_vm). Other global loads the compiler adds (spill reloads) only make those
+// waits stricter: vector memory operations complete in order.
 KRQ_DEV void dma16s(const uint8_t* base, uint32_t voff, uint32_t l) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(voff), "s"(base) : "memory", "m0");
 }
 
-// global_load_lds_dword: 4 bytes per lane from g into LDS at l + 4 * lane (same waits as dma16)
+// global_load_lds_dword: 4 bytes per lane from g into LDS at l + 4 * lane (waited for like dma16s)
 KRQ_DEV void dma4(const float* g, uint32_t l) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(l), "v"(g) : "memory", "m0");
 }

@@ -46,14 +46,19 @@ def pack(w):
     t = torch.empty((N * K * 2,), device=w.device, dtype=torch.uint8)
     L.call("krq_pack_fp8", L.ptr(w), N, 2 * K, L.ptr(t), L.stream(w))
     w.krq_tiled = t
+    w.krq_tiled_version = w._version
     return w
 
 
 def _weight(w):
-    """(pointer tensor, layout) of the bf16 weight the kernels read."""
+    """(pointer tensor, layout) of the bf16 weight the kernels read: the tiled copy pack() made,
+    unless w has been modified in place since (its version counter moved), in which case the copy
+    is dropped and w itself is read."""
     t = getattr(w, "krq_tiled", None)
     if t is not None:
-        return t, L.W_TILED
+        if getattr(w, "krq_tiled_version", None) == w._version:
+            return t, L.W_TILED
+        w.krq_tiled = None
     return (w if w.is_contiguous() else w.contiguous()), L.W_ROWMAJOR
 
 

@@ -665,6 +665,11 @@ def test_bf16_tiled_layout_matches_rowmajor(dev):
     assert torch.equal(G.gemv(x1.to(dev), wt), ref1)
     assert torch.equal(G.gemv(x16.to(dev), wt, 4), ref16)
     assert torch.equal(G.gemv_swiglu(x16.to(dev), wt), G.gemv_swiglu(x16.to(dev), wr))
+    # an in-place change after pack(): the stale tiled copy is not read
+    wt.mul_(2)
+    wr.mul_(2)
+    assert torch.equal(G.gemv(x16.to(dev), wt, 4), G.gemv(x16.to(dev), wr, 4))
+    assert getattr(wt, "krq_tiled", None) is None
 
 
 @pytest.mark.parametrize("M", [1, 16])
