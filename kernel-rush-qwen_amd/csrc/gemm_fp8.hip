@@ -394,8 +394,9 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
           if (m < M) {
             if constexpr (PART)
               *reinterpret_cast<uint4*>(ws + ((int64_t)csp * M + m) * N + cn0 + wn + 4 * c) = v;
-            else
-              *reinterpret_cast<uint4*>(out + (int64_t)m * N + cn0 + wn + 8 * c) = v;
+            else  // streamed past the caches: nothing reads it back in this launch
+              __builtin_nontemporal_store(v4u{v.x, v.y, v.z, v.w},
+                                          reinterpret_cast<v4u*>(out + (int64_t)m * N + cn0 + wn + 8 * c));
           }
         }
       }
