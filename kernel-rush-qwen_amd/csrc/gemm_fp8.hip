@@ -168,13 +168,16 @@ KRQ_DEV uint32_t lds_addr(const uint8_t* p) {
 // it tracks, does not wait for every load in flight before each LDS read; the kernel waits for
 // them itself (wait_vm). Other global loads the compiler adds (spill reloads) only make those
 // waits stricter: vector memory operations complete in order.
+// (s_nop 0: an LDS DMA reading M0 right after a scalar write of it needs one wait state on this
+// generation - the compiler inserts it for its own instructions, not inside assembly)
 KRQ_DEV void dma16s(const uint8_t* base, uint32_t voff, uint32_t l) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(voff), "s"(base) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(voff), "s"(base)
+               : "memory", "m0");
 }
 
 // global_load_lds_dword: 4 bytes per lane from g into LDS at l + 4 * lane (waited for like dma16s)
 KRQ_DEV void dma4(const float* g, uint32_t l) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(l), "v"(g) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(l), "v"(g) : "memory", "m0");
 }
 
 template <int N>
@@ -262,15 +265,20 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
     const int64_t kb = (int64_t)sp * nk * BK;
     abase = a + (int64_t)m0 * K + kb;
     bbase = b + (int64_t)n0 * K + kb;
+    // ln: the lane index made opaque here, so that these offsets are computed per tile instead of
+    // hoisted out of the tile loop and kept live across it (they were, and spilled to scratch;
+    // without any scratch gate_up at M = 4096 went from 202 to 175 us)
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
 #pragma unroll
     for (int q = 0; q < QA; ++q) {
-      const int row = 8 * (wave + 4 * q) + (lane >> 3);
-      goff[q] = static_cast<uint32_t>((min(m0 + row, M - 1) - m0) * K + 16 * ((lane & 7) ^ ((row >> 1) & 7)));
+      const int row = 8 * (wave + 4 * q) + (ln >> 3);
+      goff[q] = static_cast<uint32_t>((min(m0 + row, M - 1) - m0) * K + 16 * ((ln & 7) ^ ((row >> 1) & 7)));
     }
 #pragma unroll
     for (int q = 0; q < QB; ++q) {
-      const int row = 8 * (wave + 4 * q) + (lane >> 3);
-      goff[QA + q] = static_cast<uint32_t>(row * K + 16 * ((lane & 7) ^ ((row >> 1) & 7)));
+      const int row = 8 * (wave + 4 * q) + (ln >> 3);
+      goff[QA + q] = static_cast<uint32_t>(row * K + 16 * ((ln & 7) ^ ((row >> 1) & 7)));
     }
   };
   const uint32_t lbase = lds_addr(ring) + 1024 * wave, lsink = lds_addr(sink);
@@ -355,8 +363,10 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
   // drain while the block's next tile runs. Rounding to bf16 is the hardware convert (nearest
   // even, as f32_to_bf16 for every non-NaN value).
   auto epilogue = [&](int cm0, int cn0, int csp, const float* sc) {
+    int le = lane;  // opaque for the same reason as in set_tile
+    asm volatile("" : "+v"(le));
     uint8_t* tq = ring + kPairBytes + wave * CR * RB;
-    const int r = lane & 31;
+    const int r = le & 31;
 #pragma unroll
     for (int i = 0; i < FI; ++i) {
       const float sav = sc[wm + 32 * i + r];
@@ -369,26 +379,26 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
 #pragma unroll
             for (int g4 = 0; g4 < 4; ++g4) {
               if constexpr (PART) {
-                const int c = 8 * j + 2 * g4 + (lane >> 5);  // 16-byte chunk of the quarter's row
+                const int c = 8 * j + 2 * g4 + (le >> 5);  // 16-byte chunk of the quarter's row
                 *reinterpret_cast<float4*>(tq + rl * RB + 16 * (c ^ (rl & (CPR - 1)))) =
                     make_float4(acc[i][j][4 * g4 + 0], acc[i][j][4 * g4 + 1], acc[i][j][4 * g4 + 2],
                                 acc[i][j][4 * g4 + 3]);
               } else {
-                const int n = wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
+                const int n = wn + 32 * j + 8 * g4 + 4 * (le >> 5);
                 const float4 sb4 = *reinterpret_cast<const float4*>(sc + BM + n);
                 const uint32_t lo =
                     pack_bf16x2(acc[i][j][4 * g4 + 0] * sav * sb4.x, acc[i][j][4 * g4 + 1] * sav * sb4.y);
                 const uint32_t hi =
                     pack_bf16x2(acc[i][j][4 * g4 + 2] * sav * sb4.z, acc[i][j][4 * g4 + 3] * sav * sb4.w);
                 const int c = 4 * j + g4;  // 16-byte chunk of the quarter's row
-                *reinterpret_cast<uint2*>(tq + rl * RB + 16 * (c ^ (rl & (CPR - 1))) + 8 * (lane >> 5)) =
+                *reinterpret_cast<uint2*>(tq + rl * RB + 16 * (c ^ (rl & (CPR - 1))) + 8 * (le >> 5)) =
                     make_uint2(lo, hi);
               }
             }
         }
 #pragma unroll
         for (int it = 0; it < CR * CPR / 64; ++it) {
-          const int rr = it * (64 / CPR) + lane / CPR, c = lane % CPR;
+          const int rr = it * (64 / CPR) + le / CPR, c = le % CPR;
           const uint4 v = *reinterpret_cast<const uint4*>(tq + rr * RB + 16 * (c ^ (rr & (CPR - 1))));
           const int m = cm0 + wm + 32 * i + CR * h + rr;
           if (m < M) {
@@ -482,12 +492,12 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
 //
 // Tile shape of the ring kernel for an e4m3 GEMM, a pure function of the shape and the device's
 // compute-unit count. Measured at the Qwen3-4B projections (M = 256 .. 4096): a round of
-// 256 x 256 tiles (one block per compute unit) takes 1.75x as long as a round of two 128 x 128
-// tiles on each compute unit, and does twice their products (gate_up at M = 4096: 204 us for 5
-// rounds against 220 us for 9.5); 128 x 256 tiles were never faster than one of the two. The
-// plan takes the one with fewer estimated round-lengths, counting the tiles of the busiest
-// compute unit (128 x 128 ones two at a time). It picks the faster of the two measured kernels at
-// all twelve shapes of the prefill bench. The 128 x 128 ring kernel also beat the
+// 256 x 256 tiles (one block per compute unit) takes about 1.45x as long as a round of two
+// 128 x 128 tiles on each compute unit, and does twice their products (gate_up at M = 4096: 175 us
+// for 5 rounds; QKV: 68 us for 2 rounds against 76 us for 3 of 128 x 128); 128 x 256 tiles were
+// never faster than one of the two. The plan takes the one with fewer estimated round-lengths,
+// counting the tiles of the busiest compute unit (128 x 128 ones two at a time). It picks the
+// faster of the measured kernels at the shapes of the prefill bench. The 128 x 128 ring kernel also beat the
 // register-staged one on grids of 40 tiles (M = 256: O 15.8 against 41.0 us, down 44.8 against
 // 93.4), so bm == 0 only where N is not a multiple of 128.
 //
@@ -511,7 +521,7 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int cus) {
   const int64_t t128 = N % 128 == 0 ? ((M + 127) / 128) * (N / 128) : 0;
   const double c256 = (double)((t256 + cus - 1) / cus);                   // rounds of 256 x 256
   const double c192 = 0.75 * (double)((t192 + cus - 1) / cus);            // 192-row tiles
-  const double c128 = 0.57 * (double)(((t128 + cus - 1) / cus + 1) / 2);  // two blocks per unit
+  const double c128 = 0.70 * (double)(((t128 + cus - 1) / cus + 1) / 2);  // two blocks per unit
   const bool ok256 = t256 >= cus / 2, ok192 = t192 >= cus / 2;
   if (ok192 && c192 < c256 && (t128 == 0 || c192 <= c128)) return {192, 256, 1, 1};
   if (ok256 && (t128 == 0 || c256 <= c128)) return {256, 256, 1, 1};
