@@ -136,8 +136,9 @@ def static_mlp(torch, fp8, dev, M):
 
 def prefill(torch, fp8, dev_rows):
     """FP8 prefill GEMM at the four Qwen3-4B projections, M = dev_rows: krq_gemm_fp8 on e4m3
-    activations against torch._scaled_mm (hipBLASLt) on the same operands, and the reference's
-    whole linear_fp8 (ActScale + cast + library GEMM). Prints one JSON line for gate_up."""
+    activations against torch._scaled_mm (hipBLASLt) on the same operands, and the whole
+    linear_fp8 (ActScale + cast + this GEMM from 128 rows, the library GEMM below). Prints one JSON
+    line for gate_up."""
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     M = dev_rows

@@ -213,7 +213,7 @@ template <int BM, int BN, int OCC, bool PART>
 __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __restrict__ a, const float* __restrict__ asc,
                                                            int a_per_row, const uint8_t* __restrict__ b,
                                                            const float* __restrict__ bsc, int b_per_row, int M, int N,
-                                                           int K, int tiles_m, int tiles, int splits,
+                                                           int K, int tiles_m, int tiles, int splits, int ldo,
                                                            float* __restrict__ ws, uint16_t* __restrict__ out) {
   constexpr int kPairBytes = (BM + BN) * 2 * BK;  // two stages: 128 bytes of K per row, A rows then B rows
   __shared__ __align__(1024) uint8_t ring[2 * kPairBytes];
@@ -406,7 +406,7 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
               *reinterpret_cast<uint4*>(ws + ((int64_t)csp * M + m) * N + cn0 + wn + 4 * c) = v;
             else  // streamed past the caches: nothing reads it back in this launch
               __builtin_nontemporal_store(v4u{v.x, v.y, v.z, v.w},
-                                          reinterpret_cast<v4u*>(out + (int64_t)m * N + cn0 + wn + 8 * c));
+                                          reinterpret_cast<v4u*>(out + (int64_t)m * ldo + cn0 + wn + 8 * c));
           }
         }
       }
@@ -514,6 +514,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
 //   QKV (K = 2560) at M = 256: 64 x 64 tiles 11.2 -> 10.2, 2 parts 18.5.
 struct RingPlan {
   int bm, bn, occ, splits;
+  int tail;  // 256 x 256: whole rounds over the first columns, then 128 x 128 tiles over the rest
 };
 RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int cus) {
   const int64_t t256 = N % 256 == 0 ? ((M + 255) / 256) * (N / 256) : 0;
@@ -523,10 +524,17 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int cus) {
   const double c192 = 0.75 * (double)((t192 + cus - 1) / cus);            // 192-row tiles
   const double c128 = 0.70 * (double)(((t128 + cus - 1) / cus + 1) / 2);  // two blocks per unit
   const bool ok256 = t256 >= cus / 2, ok192 = t192 >= cus / 2;
-  if (ok192 && c192 < c256 && (t128 == 0 || c192 <= c128)) return {192, 256, 1, 1};
-  if (ok256 && (t128 == 0 || c256 <= c128)) return {256, 256, 1, 1};
-  if (t128 == 0) return {0, 0, 0, 0};
-  if (t128 >= cus) return {128, 128, 2, 1};
+  // whole rounds of 256 x 256 tiles, when they cover whole columns of tiles, then the rest of the
+  // columns in 128 x 128 tiles (two per unit): a partial round of 256 x 256 tiles at up to half the
+  // chip costs a whole one, as 128 x 128 tiles 0.7 of one
+  const int64_t r256 = t256 / cus, rest = t256 % cus, tm256 = (M + 255) / 256;
+  const double ctail = (double)r256 + 0.70 * (double)((2 * rest + cus - 1) / cus);
+  const bool tail = r256 >= 1 && rest > 0 && (r256 * cus) % tm256 == 0 && t128 > 0;
+  if (ok192 && c192 < c256 && (t128 == 0 || c192 <= c128) && !(tail && ctail < c192)) return {192, 256, 1, 1, 0};
+  if (tail && ctail < c256 && ctail < c128) return {256, 256, 1, 1, 1};
+  if (ok256 && (t128 == 0 || c256 <= c128)) return {256, 256, 1, 1, 0};
+  if (t128 == 0) return {0, 0, 0, 0, 0};
+  if (t128 >= cus) return {128, 128, 2, 1, 0};
   // the most parts (8, 4, 2) a grid of `tiles` may split K into, or 1
   auto parts = [&](int64_t tiles) {
     const int64_t nk = K / 64;
@@ -536,8 +544,8 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int cus) {
     return 1;
   };
   const int s128 = parts(t128);
-  if (s128 > 1) return {128, 128, 2, s128};
-  return {64, 64, 4, parts(((M + 63) / 64) * (N / 64))};
+  if (s128 > 1) return {128, 128, 2, s128, 0};
+  return {64, 64, 4, parts(((M + 63) / 64) * (N / 64)), 0};
 }
 
 int query_cus(int* cus) {
@@ -573,30 +581,39 @@ int gemm_run(const void* x, int x_kind, const float* x_scale, const float* x_inv
     RingPlan rp = ring_plan(M, N, K, cus);
     if (rp.splits > 1 && (!aligned16(ws) || ws_bytes < (int64_t)rp.splits * M * N * 4)) rp.splits = 1;
     if (rp.bm > 0) {
-      const int rtm = static_cast<int>((M + rp.bm - 1) / rp.bm);
-      const int64_t rtiles = (int64_t)rtm * (N / rp.bn);
-      const int64_t units = rtiles * rp.splits, slots = (int64_t)cus * rp.occ;
-      const dim3 rgrid(static_cast<unsigned>(units < slots ? units : slots));
-#define KRQ_RING(BM_, BN_, OCC_, PART_)                                                                              \
-  hipLaunchKernelGGL((ring::k_gemm_ring<BM_, BN_, OCC_, PART_>), rgrid, dim3(ring::kThreads), 0, s, (const uint8_t*)x, \
-                     x_scale, x_per_row, (const uint8_t*)w8, w_scale, w_per_row, (int)M, (int)N, (int)K, rtm,          \
-                     (int)rtiles, rp.splits, (float*)ws, (uint16_t*)out)
-      if (rp.bm == 256) {
-        KRQ_RING(256, 256, 1, false);
+      // one launch over columns [n_lo, n_hi) of the output (ldo = N)
+#define KRQ_RING(BM_, BN_, OCC_, PART_, n_lo, n_hi)                                                                  \
+  do {                                                                                                             \
+    const int64_t nn = (n_hi) - (n_lo), tm_ = (M + (BM_)-1) / (BM_), tiles_ = tm_ * (nn / (BN_));                   \
+    const int64_t units_ = tiles_ * rp.splits, slots_ = (int64_t)cus * (OCC_);                                     \
+    hipLaunchKernelGGL((ring::k_gemm_ring<BM_, BN_, OCC_, PART_>), dim3(static_cast<unsigned>(units_ < slots_ ? units_ : slots_)), \
+                       dim3(ring::kThreads), 0, s, (const uint8_t*)x, x_scale, x_per_row,                           \
+                       (const uint8_t*)w8 + (n_lo) * K, w_scale + (w_per_row ? (n_lo) : 0), w_per_row, (int)M,     \
+                       (int)nn, (int)K, (int)tm_, (int)tiles_, rp.splits, (int)N, (float*)ws,                       \
+                       (uint16_t*)out + (n_lo));                                                                   \
+  } while (0)
+      if (rp.bm == 256 && rp.tail) {
+        // the whole rounds' tiles (M-fastest) fill whole columns of tiles: the first n_split columns
+        const int64_t tm256 = (M + 255) / 256, rounds = (N / 256) * tm256 / cus;
+        const int64_t n_split = rounds * cus / tm256 * 256;
+        KRQ_RING(256, 256, 1, false, 0, n_split);
+        KRQ_RING(128, 128, 2, false, n_split, N);
+      } else if (rp.bm == 256) {
+        KRQ_RING(256, 256, 1, false, 0, N);
       } else if (rp.bm == 192) {
-        KRQ_RING(192, 256, 1, false);
+        KRQ_RING(192, 256, 1, false, 0, N);
       } else if (rp.bm == 64 && rp.splits == 1) {
-        KRQ_RING(64, 64, 4, false);
+        KRQ_RING(64, 64, 4, false, 0, N);
       } else if (rp.bm == 64) {
-        KRQ_RING(64, 64, 4, true);
+        KRQ_RING(64, 64, 4, true, 0, N);
         const int64_t threads = M * N / 4;
         hipLaunchKernelGGL(ring::k_splitk_reduce, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s,
                            (const float*)ws, rp.splits, (int)M, (int)N, x_scale, x_per_row, w_scale, w_per_row,
                            (uint16_t*)out);
       } else if (rp.splits == 1) {
-        KRQ_RING(128, 128, 2, false);
+        KRQ_RING(128, 128, 2, false, 0, N);
       } else {
-        KRQ_RING(128, 128, 2, true);
+        KRQ_RING(128, 128, 2, true, 0, N);
         const int64_t threads = M * N / 4;
         hipLaunchKernelGGL(ring::k_splitk_reduce, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s,
                            (const float*)ws, rp.splits, (int)M, (int)N, x_scale, x_per_row, w_scale, w_per_row,

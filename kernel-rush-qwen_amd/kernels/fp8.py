@@ -27,6 +27,9 @@ from . import _lib as L
 FP8_MAX = 448.0
 HEADROOM = float(os.environ.get("ENGINE_FP8_HEADROOM", "4"))
 DECODE_MAX_ROWS = 32  # rows handled by one launch of the skinny kernels
+# From this many rows linear_fp8 runs gemm_fp8: per Qwen3-4B decoder layer (the four projections)
+# it takes 0.80x-0.995x hipBLASLt's time on MI355X from M = 128 to 4096, and 1.09x at M = 64.
+PREFILL_MIN_ROWS = 128
 
 
 class FP8Weight(tuple):
@@ -410,9 +413,10 @@ def gemm_fp8(x, q, a=None, xs=None):
 def linear_fp8(x, q, a=None, amax_out=None):
     """bf16 [M, N] ~= x @ W^T with q = quantize_weight(W); a = given scale, or
     None to scale by this tensor's own range (running max kept in amax_out).
-    Reference: engine/kernels/fp8.py:97-106. Decode sizes (M <= 32) run the HIP GEMV; larger M
-    (prefill) keep the reference's library GEMM, torch._scaled_mm (hipBLASLt on ROCm), which is
-    2-5x faster on MI355X than this library's MFMA tile GEMM (gemm_fp8) at the Qwen3-4B shapes."""
+    Reference: engine/kernels/fp8.py:97-106. Decode sizes (M <= 32) run the HIP GEMV; prefill
+    rows from PREFILL_MIN_ROWS up run this library's GEMM (gemm_fp8) where its e4m3 kernels take
+    the weight (N and K multiples of 128, K >= 256); the rest keep the reference's library GEMM,
+    torch._scaled_mm (hipBLASLt on ROCm)."""
     w8, ws = q[0], q[1]
     if a is None:
         a = ActScale(x)
@@ -423,4 +427,12 @@ def linear_fp8(x, q, a=None, amax_out=None):
     x8 = _cast(x, a)
     if x.shape[0] <= DECODE_MAX_ROWS:
         return gemv_fp8_launch(x8, a.scale.reshape(1), q, 1, L.OUT_BF16)
+    if x.shape[0] >= PREFILL_MIN_ROWS and _ring_gemm_fits(w8):
+        return gemm_fp8(x8, q, xs=a.scale.reshape(1))
     return torch._scaled_mm(x8, w8.t(), scale_a=a.scale, scale_b=ws, out_dtype=torch.bfloat16)
+
+
+def _ring_gemm_fits(w8):
+    """The weight shapes gemm_fp8 multiplies with its ring kernels on e4m3 rows."""
+    return (w8.dtype == torch.float8_e4m3fn and w8.dim() == 2 and w8.is_contiguous() and w8.shape[0] % 128 == 0
+            and w8.shape[1] % 128 == 0 and w8.shape[1] >= 256)

@@ -40,7 +40,11 @@ def bf(shape, seed, scale=1.0):
                                            # 192 x 256 tiles: ragged M (20 full row tiles + 160 rows)
                                            (4000, 2560, 512, True), (4096, 2560, 4096, False),
                                            # 64 x 64 tiles: small grids that do not split K
-                                           (256, 2560, 4096, True), (100, 1024, 512, False)])
+                                           (256, 2560, 4096, True), (100, 1024, 512, False),
+                                           # a whole round of 256 x 256 tiles over the first 4096
+                                           # columns, then 128 x 128 tiles over the last 2048 (two
+                                           # launches into one output), also with ragged M
+                                           (4096, 6144, 512, False), (3900, 6144, 384, True)])
 def test_gemm_fp8_matches_oracle(dev, M, N, K, per_row):
     w = bf((N, K), 1, 0.02).to(dev)
     q = F.quantize(w) if per_row else F.quantize_weight(w)
@@ -102,6 +106,24 @@ def test_gemm_fused_cast_is_cast_then_gemm(dev, M, N, K):
     assert rel_err(F.linear_fp8(x, q).float().cpu().numpy(), ref) <= TOL
     assert rel_err(y.float().cpu().numpy(), ref) <= TOL
     assert rel_err(y3.float().cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 2560, 4096), (300, 6144, 2560), (64, 2560, 4096), (200, 256, 128)])
+def test_linear_fp8_prefill_route(dev, M, N, K):
+    """linear_fp8 above the decode sizes (engine/kernels/fp8.py:105-106): from PREFILL_MIN_ROWS rows,
+    on weights the ring kernels take, it is gemm_fp8 on the cast rows bit for bit; below that (or
+    for K = 128) the library's torch._scaled_mm bit for bit. Both within the bar of the oracle."""
+    q = F.quantize_weight(bf((N, K), 31, 0.02).to(dev))
+    x = bf((M, K), 32).to(dev)
+    a = F.ActScale(x)
+    y = F.linear_fp8(x, q, a)
+    x8 = F._cast(x, a)
+    if M >= F.PREFILL_MIN_ROWS and K >= 256:
+        assert torch.equal(y, F.gemm_fp8(x8, q, xs=a.scale.reshape(1)))
+    else:
+        assert torch.equal(y, torch._scaled_mm(x8, q[0].t(), scale_a=a.scale, scale_b=q[1], out_dtype=torch.bfloat16))
+    _, ref = O.fp8_matmul(codes(x8), a.scale.cpu().numpy(), codes(q[0]), q[1].cpu().numpy())
+    assert rel_err(y.float().cpu().numpy(), ref) <= TOL
 
 
 def test_gemm_matches_library_gemm(dev):
