@@ -44,6 +44,7 @@ for p in (ROOT, os.path.join(ROOT, "kernel-rush-qwen_amd")):
 HBM_PEAK = 8.0e12
 H, I, NQKV, NQD, V = 2560, 9728, 6144, 4096, 151936
 LAYERS = 36
+PREFILL_MS = (1024, 4096)  # prompt lengths of the prefill GEMM summary in the default line
 METRIC = "FP8 skinny-GEMM HBM GB/s (% of 8 TB/s peak) at Qwen3-4B shapes, M=1 and M=16"
 # (name, N rows of W, K, split, mode)
 PROJ = [("qkv", NQKV, H, 2, "partial"), ("o", H, NQD, 4, "partial"),
@@ -134,14 +135,13 @@ def static_mlp(torch, fp8, dev, M):
     return fused, unfused, nbytes
 
 
-def prefill(torch, fp8, dev_rows):
-    """FP8 prefill GEMM at the four Qwen3-4B projections, M = dev_rows: krq_gemm_fp8 on e4m3
-    activations against torch._scaled_mm (hipBLASLt) on the same operands, and the whole
-    linear_fp8 (ActScale + cast + this GEMM from 128 rows, the library GEMM below). Prints one JSON
-    line for gate_up."""
+def prefill_times(torch, fp8, M, lin=True):
+    """FP8 prefill GEMM at the four Qwen3-4B projections, M rows: krq_gemm_fp8 on e4m3 activations
+    against torch._scaled_mm (hipBLASLt) on the same operands, and (lin) the whole linear_fp8
+    (ActScale + cast + this GEMM from 128 rows, the library GEMM below). Returns name -> (us ours,
+    us library, us linear_fp8 or None, flops), each the minimum over replays of a graph of 20."""
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    M = dev_rows
     out = {}
     for p, (name, N, K, _, _) in enumerate(PROJ):
         g = torch.Generator(device=dev).manual_seed(4000 + p)
@@ -152,11 +152,19 @@ def prefill(torch, fp8, dev_rows):
         t_ours = graph_time(torch, lambda i: fp8.gemm_fp8(x8, q, xs=xs), 20)[0]
         t_lib = graph_time(torch, lambda i: torch._scaled_mm(x8, q[0].t(), scale_a=a.scale, scale_b=q[1],
                                                              out_dtype=torch.bfloat16), 20)[0]
-        t_lin = graph_time(torch, lambda i: fp8.linear_fp8(x, q), 20)[0]
+        t_lin = graph_time(torch, lambda i: fp8.linear_fp8(x, q), 20)[0] if lin else None
         fl = 2.0 * M * N * K
         out[name] = (t_ours, t_lib, t_lin, fl)
         log(f"[bench] prefill M={M} {name:<8} krq_gemm_fp8 {t_ours:8.1f} us ({fl / t_ours / 1e6:6.0f} TFLOP/s) | "
-            f"hipBLASLt {t_lib:8.1f} us ({fl / t_lib / 1e6:6.0f} TFLOP/s) | linear_fp8 {t_lin:8.1f} us")
+            f"hipBLASLt {t_lib:8.1f} us ({fl / t_lib / 1e6:6.0f} TFLOP/s)"
+            + (f" | linear_fp8 {t_lin:8.1f} us" if lin else ""))
+    return out
+
+
+def prefill(torch, fp8, dev_rows):
+    """--config prefill: prefill_times at M = dev_rows, one JSON line for gate_up."""
+    M = dev_rows
+    out = prefill_times(torch, fp8, M)
     t_ours, t_lib, t_lin, fl = out["gate_up"]
     tf = fl / t_ours / 1e6
     print(json.dumps({
@@ -456,6 +464,7 @@ def main():
     ap.add_argument("--reps", type=int, default=72, help="launches per graph in the kernel table")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill GEMM summary of the default line")
     ap.add_argument("--no-table", action="store_true", help="skip the per-kernel tables (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 256 MiB device copy (known bytes) to scale HBM counters")
@@ -622,6 +631,18 @@ def main():
     cpu = None
     if not args.no_cpu and cfg in ("decode", "c2", "c3", "c3m32"):
         cpu = cpu_baseline(torch, Ms, args.cpu_seconds)
+    pre = None
+    if cfg == "decode" and not args.no_prefill:
+        # the prefill GEMM next to the library's, per decoder layer (the four projections summed)
+        pre = {"M": list(PREFILL_MS), "layer_us": [], "hipblaslt_layer_us": [], "ratio": []}
+        for pm in PREFILL_MS:
+            t = prefill_times(torch, fp8, pm, lin=False)
+            ours, lib = sum(v[0] for v in t.values()), sum(v[1] for v in t.values())
+            pre["layer_us"].append(round(ours, 1))
+            pre["hipblaslt_layer_us"].append(round(lib, 1))
+            pre["ratio"].append(round(ours / lib, 3))
+        log(f"[bench] prefill GEMM per layer, M={list(PREFILL_MS)}: {pre['layer_us']} us against hipBLASLt "
+            f"{pre['hipblaslt_layer_us']} us")
 
     print(json.dumps({
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
@@ -632,7 +653,7 @@ def main():
                    "layout": args.layout, "pct_of_hbm_peak": round(100 * value / 8000.0, 2),
                    "replays": args.replays, "ms_per_step_min": round(t_min / steps, 5),
                    "value_best": round(step_bytes * steps / (t_min * 1e-3) / 1e9, 1)},
-        "per_m": per_m or None,
+        "per_m": per_m or None, "prefill": pre,
         "roofline": roofline, "cpu_baseline": cpu}), flush=True)
 
 
