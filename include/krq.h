@@ -310,9 +310,10 @@ int krq_rmsnorm_quant_rows_tiled(const void* x, const float* ss_in, const void* 
  * 97-106, prefill call site engine/engine.py:670-677). x_kind KRQ_X_FP8: x is e4m3 [M, K];
  * KRQ_X_BF16_STATIC: x is bf16 [M, K], quantized in the kernel as e4m3(clamp(x * x_inv)) (x_inv per
  * tensor, or per row with x_per_row). w8 row-major e4m3 [N, K]. N and K multiples of 128.
- * e4m3 rows with K >= 256 (and out 16-byte aligned) run the persistent ring kernels (256 x 256 or
- * 128 x 128 tiles, chosen from the shape and the device's compute units); other inputs a 128 x 128
- * kernel with register-staged loads.
+ * e4m3 rows with K >= 256 (and out 16-byte aligned) run the persistent ring kernels (256 x 256,
+ * 192 x 256, 128 x 128 or 64 x 64 tiles, chosen from the shape and the device's compute units; a
+ * partial last round of 256 x 256 tiles as 128 x 128 tiles in a second launch); other inputs a
+ * 128 x 128 kernel with register-staged loads.
  */
 int krq_gemm_fp8(const void* x, int x_kind, const float* x_scale, const float* x_inv, int x_per_row,
                  const void* w8, const float* w_scale, int w_per_row, int64_t M, int64_t N, int64_t K,

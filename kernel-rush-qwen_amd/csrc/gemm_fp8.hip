@@ -3,7 +3,8 @@
 // :97-106) for prefill (engine/engine.py:670-677).
 //
 // Two kernels. k_gemm_ring (below) takes e4m3 activations with K >= 256: persistent blocks, an LDS
-// ring of direct global->LDS loads, 256 x 256 or 128 x 128 tiles and split K for small grids.
+// ring of direct global->LDS loads, 256 x 256 / 192 x 256 / 128 x 128 / 64 x 64 tiles and split K
+// for small grids.
 // k_gemm_fp8 takes the rest (K = 128, or bf16 activations cast on the way into LDS): a block owns
 // a 128 x 128 output tile and walks K in steps of 128 bytes; its four waves each own a 64 x 64
 // quarter, a 4 x 4 grid of v_mfma_f32_16x16x128_f8f6f4 products (lane l holds 32 bytes of row
