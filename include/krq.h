@@ -96,6 +96,15 @@ int krq_cast_fp8(const void* x_bf16, int64_t M, int64_t K, const float* inv, int
                  void* x8, void* stream);
 
 /*
+ * krq_act_scale (per tensor) then krq_cast_fp8 with its inverse: the first two steps of linear_fp8
+ * without a given scale (reference engine/kernels/fp8.py:97-104: a = ActScale(x), then _cast(x, a)).
+ * The same amax, inv, scale and bytes, in two launches where the alignment allows (the fold of the
+ * partial maxima runs inside the cast), else three. ws: krq_act_scale_ws_floats(M, K) floats.
+ */
+int krq_act_scale_cast_fp8(const void* x_bf16, int64_t M, int64_t K, float headroom, float* amax, float* inv,
+                           float* scale, float* ws, void* x8, void* stream);
+
+/*
  * Per-token dynamic quantization in one launch: fp8.quant_rows as called by the reference's
  * experiments/modal_fp8.py:84-85 (x8, xs for torch._scaled_mm scale_a); ActScale per row plus
  * the cast above. xs[m] = scale of row m (amax[m]/448 as above).

@@ -107,6 +107,23 @@ __global__ __launch_bounds__(kQT) void k_absmax_partial(const uint16_t* __restri
   if (threadIdx.x == 0) ws[blockIdx.x] = as_f32(mb);
 }
 
+// pass 1 on 16-byte chunks of 8 bf16 (x 16-byte aligned, n8 chunks): four loads in flight per
+// thread and a packed 16-bit bit-max (absmax8_bits) - the scalar pass above reads 2 bytes per lane
+// per load and streamed at ~1.7 TB/s on MI355X
+__global__ __launch_bounds__(kQT) void k_absmax_partial_vec(const uint4* __restrict__ x, int64_t n8,
+                                                            float* __restrict__ ws) {
+  u16x2 m{0, 0};
+  const int64_t stride = (int64_t)gridDim.x * kQT;
+  int64_t i = blockIdx.x * (int64_t)kQT + threadIdx.x;
+  for (; i + 3 * stride < n8; i += 4 * stride) {
+    const uint4 a0 = x[i], a1 = x[i + stride], a2 = x[i + 2 * stride], a3 = x[i + 3 * stride];
+    m = absmax8_bits(a3, absmax8_bits(a2, absmax8_bits(a1, absmax8_bits(a0, m))));
+  }
+  for (; i < n8; i += stride) m = absmax8_bits(x[i], m);
+  const uint32_t mb = block_max_u32<kQT>(bits_max_to_u32(m));
+  if (threadIdx.x == 0) ws[blockIdx.x] = as_f32(mb);
+}
+
 // per tensor pass 2
 __global__ __launch_bounds__(1024) void k_act_fold(const float* __restrict__ ws, int g,
                                                    float headroom, float* amax, float* inv,
@@ -315,6 +332,27 @@ __global__ __launch_bounds__(kQT) void k_cast_vec(const uint16_t* __restrict__ x
   }
 }
 
+// pass 2 folded into the cast (linear_fp8 without a given scale): every block reduces the g
+// partials itself (g <= kActPartials, 4 KB from L2), finishes the scale as k_act_fold does (block 0
+// stores amax, inv, scale) and casts its chunks as k_cast_vec with that inverse - the bytes of
+// pass 2 then the cast, one launch fewer
+__global__ __launch_bounds__(kQT) void k_cast_fold_vec(const uint16_t* __restrict__ x, int64_t nch,
+                                                       const float* __restrict__ ws, int g, float headroom,
+                                                       float* amax, float* inv, float* scale,
+                                                       uint8_t* __restrict__ x8) {
+  uint32_t mb = 0;
+  for (int i = threadIdx.x; i < g; i += kQT) mb = umax32(mb, mag_bits(ws[i]));
+  const float a = clamp_min_nan(as_f32(block_max_u32<kQT>(mb)), 1e-6f) * headroom;
+  const float iv = inv_from_amax(a);
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    amax[0] = a;
+    inv[0] = iv;
+    scale[0] = scale_from_amax(a);
+  }
+  for (int64_t i = blockIdx.x * (int64_t)kQT + threadIdx.x; i < nch; i += (int64_t)gridDim.x * kQT)
+    *reinterpret_cast<uint2*>(x8 + 8 * i) = quant8(ld16(reinterpret_cast<const uint8_t*>(x) + 16 * i), iv);
+}
+
 bool vec_ok(const void* p, int64_t K, int64_t ld) {
   return K % 8 == 0 && ld % 8 == 0 && K <= kVecMaxK && aligned16(p);
 }
@@ -371,6 +409,16 @@ extern "C" int krq_quant_fp8_tensor(const void* w_bf16, int64_t N, int64_t K, in
 
 static constexpr int kActPartials = 1024;
 
+// per-tensor pass 1 into ws[0 .. g): the vector pass where x allows it; returns g
+static int absmax_partials(const void* x_bf16, int64_t M, int64_t K, float* ws, hipStream_t s) {
+  const int g = grid_for(M * K, kQT * 16, kActPartials);
+  if (aligned16(x_bf16) && (M * K) % 8 == 0)
+    hipLaunchKernelGGL(k_absmax_partial_vec, dim3(g), dim3(kQT), 0, s, (const uint4*)x_bf16, M * K / 8, ws);
+  else
+    hipLaunchKernelGGL(k_absmax_partial, dim3(g), dim3(kQT), 0, s, (const uint16_t*)x_bf16, M * K, ws);
+  return g;
+}
+
 extern "C" int64_t krq_act_scale_ws_floats(int64_t M, int64_t K) {
   return grid_for(M * K, kQT * 16, kActPartials);
 }
@@ -390,11 +438,28 @@ extern "C" int krq_act_scale(const void* x_bf16, int64_t M, int64_t K, int per_r
                          headroom, amax, inv, scale, nullptr);
   } else {
     KRQ_REQUIRE(ws != nullptr, "act_scale: per-tensor scale needs a workspace");
-    const int g = grid_for(M * K, kQT * 16, kActPartials);
-    hipLaunchKernelGGL(k_absmax_partial, dim3(g), dim3(kQT), 0, s, (const uint16_t*)x_bf16, M * K, ws);
+    const int g = absmax_partials(x_bf16, M, K, ws, s);
     hipLaunchKernelGGL(k_act_fold, dim3(1), dim3(1024), 0, s, ws, g, headroom, amax, inv, scale);
   }
   return krq_check_launch("act_scale");
+}
+
+extern "C" int krq_act_scale_cast_fp8(const void* x_bf16, int64_t M, int64_t K, float headroom, float* amax,
+                                      float* inv, float* scale, float* ws, void* x8, void* stream) {
+  KRQ_REQUIRE(x_bf16 && amax && inv && scale && ws && x8, "act_scale_cast: null pointer");
+  KRQ_REQUIRE(M > 0 && K > 0, "act_scale_cast: bad shape M=%lld K=%lld", (long long)M, (long long)K);
+  hipStream_t s = (hipStream_t)stream;
+  const int g = absmax_partials(x_bf16, M, K, ws, s);
+  if (vec_ok(x_bf16, K, K) && aligned16(x8)) {
+    const int gc = grid_for(M * K / 8, kQT, 8192);
+    hipLaunchKernelGGL(k_cast_fold_vec, dim3(gc), dim3(kQT), 0, s, (const uint16_t*)x_bf16, M * K / 8, ws, g,
+                       headroom, amax, inv, scale, (uint8_t*)x8);
+  } else {  // the two passes and the scalar cast
+    hipLaunchKernelGGL(k_act_fold, dim3(1), dim3(1024), 0, s, ws, g, headroom, amax, inv, scale);
+    const int gc = grid_for(M * K, kQT * 4, 8192);
+    hipLaunchKernelGGL(k_cast, dim3(gc), dim3(kQT), 0, s, (const uint16_t*)x_bf16, M, K, inv, 0, (uint8_t*)x8);
+  }
+  return krq_check_launch("act_scale_cast");
 }
 
 extern "C" int krq_cast_fp8(const void* x_bf16, int64_t M, int64_t K, const float* inv, int per_row,

@@ -155,6 +155,23 @@ def _cast_hip(x, a):
     return y
 
 
+def _act_scale_cast(x, headroom=1.0):
+    """(ActScale(x, headroom), _cast_hip(x, a)) through krq_act_scale_cast_fp8: the same scale and
+    bytes, one launch fewer (the fold of the partial maxima runs inside the cast)."""
+    x2 = _rows(x)
+    M, K = x2.shape
+    dev = x2.device
+    a = ActScale.__new__(ActScale)
+    a.amax = torch.empty((), device=dev, dtype=torch.float32)
+    a.inv = torch.empty((1,), device=dev, dtype=torch.float32)
+    a.scale = torch.empty((), device=dev, dtype=torch.float32)
+    ws = torch.empty((max(1, L.lib().krq_act_scale_ws_floats(M, K)),), device=dev, dtype=torch.float32)
+    y = torch.empty(x.shape, device=x.device, dtype=torch.float8_e4m3fn)
+    L.call("krq_act_scale_cast_fp8", L.ptr(x2), M, K, float(headroom), L.ptr(a.amax), L.ptr(a.inv),
+           L.ptr(a.scale), L.ptr(ws), L.ptr(y), L.stream(x2))
+    return a, y
+
+
 def _cast_torch(x, a):
     return (x.float() * a.inv).clamp_(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
 
@@ -418,13 +435,18 @@ def linear_fp8(x, q, a=None, amax_out=None):
     the weight (N and K multiples of 128, K >= 256); the rest keep the reference's library GEMM,
     torch._scaled_mm (hipBLASLt on ROCm)."""
     w8, ws = q[0], q[1]
+    x8 = None
     if a is None:
-        a = ActScale(x)
+        if x.dim() == 2 and x.shape[0] > DECODE_MAX_ROWS and _cast is _cast_hip:
+            a, x8 = _act_scale_cast(x)
+        else:
+            a = ActScale(x)
         if amax_out is not None:
             amax_out.copy_(torch.maximum(amax_out, a.amax.reshape(1)))
-    if _fits_fused(x, 1, a):
+    if x8 is None and _fits_fused(x, 1, a):
         return gemv_fp8_bf16_launch(x, q, 1, L.OUT_BF16, a)
-    x8 = _cast(x, a)
+    if x8 is None:
+        x8 = _cast(x, a)
     if x.shape[0] <= DECODE_MAX_ROWS:
         return gemv_fp8_launch(x8, a.scale.reshape(1), q, 1, L.OUT_BF16)
     if x.shape[0] >= PREFILL_MIN_ROWS and _ring_gemm_fits(w8):

@@ -117,6 +117,11 @@ def test_linear_fp8_prefill_route(dev, M, N, K):
     x = bf((M, K), 32).to(dev)
     a = F.ActScale(x)
     y = F.linear_fp8(x, q, a)
+    # without a given scale linear_fp8 takes its own (ActScale and the cast in two launches),
+    # the same bits, and records amax in amax_out
+    amax_out = torch.zeros(1, device=dev)
+    assert torch.equal(F.linear_fp8(x, q, amax_out=amax_out), y)
+    assert torch.equal(amax_out, a.amax.reshape(1))
     x8 = F._cast(x, a)
     if M >= F.PREFILL_MIN_ROWS and K >= 256:
         assert torch.equal(y, F.gemm_fp8(x8, q, xs=a.scale.reshape(1)))

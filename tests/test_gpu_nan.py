@@ -143,6 +143,29 @@ def test_act_scale_nan_inf(dev, v):
     assert_codes(u8(fp8._cast_hip(xd, a)), u8(fp8._cast_torch(xd, a)))
 
 
+@pytest.mark.parametrize("v", [None, NAN, INF, -INF])
+@pytest.mark.parametrize("M,K", [(40, 2560), (300, 9728), (33, 100), (64, 4104)])
+def test_act_scale_cast_is_act_scale_then_cast(dev, M, K, v):
+    """linear_fp8's first steps without a given scale (engine/kernels/fp8.py:97-104) in two
+    launches (krq_act_scale_cast_fp8: the vector maximum pass, then the cast folding the partial
+    maxima itself; M K % 8 != 0 takes the scalar passes): the scale and bytes of ActScale then
+    _cast_hip, and of the oracle, NaN and inf included."""
+    x = act(M, K, 36 + M)
+    if v is not None:
+        x[M // 2, K // 3] = v
+    xd = x.to(dev)
+    a, y = fp8._act_scale_cast(xd)
+    a2 = fp8.ActScale(xd)
+    assert_f32(a.amax.cpu().numpy(), a2.amax.cpu().numpy())
+    assert_f32(a.inv.cpu().numpy(), a2.inv.cpu().numpy())
+    assert_f32(a.scale.cpu().numpy(), a2.scale.cpu().numpy())
+    assert_codes(u8(y), u8(fp8._cast_hip(xd, a2)))
+    amax, inv, scale = O.act_scale(u16(x))
+    assert_f32(a.amax.cpu().numpy(), amax)
+    assert_f32(a.scale.cpu().numpy(), scale)
+    assert_codes(u8(y), O.cast(u16(x), inv))
+
+
 # 512-thread kernel (K % 16 == 0), 8-value chunk kernel (K % 16 == 8), scalar kernel (K % 8 != 0,
 # and rows longer than the vector kernels hold)
 @pytest.mark.parametrize("M,K", [(16, 2560), (12, 200), (11, 100), (10, 20000)])
