@@ -66,6 +66,11 @@ def test_invalid_arguments_fail_before_any_launch():
     # tiled activations take the matrix-core kernel; their quantizer needs K % 64 == 0
     rc = lib.krq_gemv_fp8(p, L.X_FP8_TILED, p, None, 0, p, 1, p, 1, 1, 64, 256, 1, 0, 2, p, _null())
     assert rc == L.KRQ_EINVAL and b"tiled activations" in lib.krq_last_error()
+    # the activation scale with its cast: every pointer, a real shape
+    rc = lib.krq_act_scale_cast_fp8(p, 16, 2560, 1.0, p, p, p, None, p, _null())
+    assert rc == L.KRQ_EINVAL and b"null pointer" in lib.krq_last_error()
+    rc = lib.krq_act_scale_cast_fp8(p, 0, 2560, 1.0, p, p, p, p, p, _null())
+    assert rc == L.KRQ_EINVAL and b"bad shape" in lib.krq_last_error()
     rc = lib.krq_quant_rows_tiled(p, 16, 100, p, p, _null())
     assert rc == L.KRQ_EINVAL and b"K=100" in lib.krq_last_error()
     rc = lib.krq_quant_rows_tiled(p, 16, 16384 + 64, p, p, _null())
