@@ -131,6 +131,32 @@ def test_linear_fp8_prefill_route(dev, M, N, K):
     assert rel_err(y.float().cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("M,N,K", [(4096, 6144, 512), (256, 2560, 9728), (300, 6144, 2560)])
+def test_gemm_graph_replays(dev, M, N, K):
+    """gemm_fp8 captured in a graph (the two-launch tail plan, split K with its reduce and the
+    workspace, a plain ring launch): every replay, with eager work between them, equals the eager
+    result bit for bit."""
+    q = F.quantize(bf((N, K), 41, 0.02).to(dev))
+    x8, xs = F.quant_rows(bf((M, K), 42).to(dev))
+    want = F.gemm_fp8(x8, q, xs=xs)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        F.gemm_fp8(x8, q, xs=xs)  # warm-up on a side stream, as before any capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = F.gemm_fp8(x8, q, xs=xs)
+    for r in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want), f"replay {r}"
+        F.gemm_fp8(x8, q, xs=xs).sum().item()  # eager work between the replays
+        y.zero_()
+        torch.cuda.synchronize()
+
+
 def test_gemm_matches_library_gemm(dev):
     """Against torch._scaled_mm (hipBLASLt) on the same operands: both within the bar of the oracle,
     and within a few bf16 ulps of each other."""
