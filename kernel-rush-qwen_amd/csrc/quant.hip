@@ -124,6 +124,22 @@ __global__ __launch_bounds__(kQT) void k_absmax_partial_vec(const uint4* __restr
   if (threadIdx.x == 0) ws[blockIdx.x] = as_f32(mb);
 }
 
+// per tensor in one launch for small tensors (decode rows): one 1,024-thread block takes the whole
+// maximum (16-byte chunks when x allows, else 2 bytes per load) and finishes the scale as k_act_fold
+__global__ __launch_bounds__(1024) void k_act_scale_small(const uint16_t* __restrict__ x, int64_t n, int vec,
+                                                          float headroom, float* amax, float* inv, float* scale) {
+  uint32_t mb = 0;
+  if (vec) {
+    u16x2 m{0, 0};
+    for (int64_t i = threadIdx.x; i < n / 8; i += 1024) m = absmax8_bits(reinterpret_cast<const uint4*>(x)[i], m);
+    mb = bits_max_to_u32(m);
+  } else {
+    for (int64_t i = threadIdx.x; i < n; i += 1024) mb = umax32(mb, mag_bits(bf16_to_f32(x[i])));
+  }
+  mb = block_max_u32<1024>(mb);
+  if (threadIdx.x == 0) act_finish(as_f32(mb), headroom, amax, inv, scale, 0);
+}
+
 // per tensor pass 2
 __global__ __launch_bounds__(1024) void k_act_fold(const float* __restrict__ ws, int g,
                                                    float headroom, float* amax, float* inv,
@@ -408,6 +424,7 @@ extern "C" int krq_quant_fp8_tensor(const void* w_bf16, int64_t N, int64_t K, in
 }
 
 static constexpr int kActPartials = 1024;
+static constexpr int64_t kActSmall = 65536;  // elements one block takes in one launch (krq_act_scale)
 
 // per-tensor pass 1 into ws[0 .. g): the vector pass where x allows it; returns g
 static int absmax_partials(const void* x_bf16, int64_t M, int64_t K, float* ws, hipStream_t s) {
@@ -438,8 +455,14 @@ extern "C" int krq_act_scale(const void* x_bf16, int64_t M, int64_t K, int per_r
                          headroom, amax, inv, scale, nullptr);
   } else {
     KRQ_REQUIRE(ws != nullptr, "act_scale: per-tensor scale needs a workspace");
-    const int g = absmax_partials(x_bf16, M, K, ws, s);
-    hipLaunchKernelGGL(k_act_fold, dim3(1), dim3(1024), 0, s, ws, g, headroom, amax, inv, scale);
+    if (M * K <= kActSmall) {
+      const int vec = aligned16(x_bf16) && (M * K) % 8 == 0;
+      hipLaunchKernelGGL(k_act_scale_small, dim3(1), dim3(1024), 0, s, (const uint16_t*)x_bf16, M * K, vec, headroom,
+                         amax, inv, scale);
+    } else {
+      const int g = absmax_partials(x_bf16, M, K, ws, s);
+      hipLaunchKernelGGL(k_act_fold, dim3(1), dim3(1024), 0, s, ws, g, headroom, amax, inv, scale);
+    }
   }
   return krq_check_launch("act_scale");
 }
