@@ -87,22 +87,23 @@ void launch_row(int awc, int u, dim3 grid, dim3 block, size_t smem, hipStream_t 
 #undef KRQ_ROW_U
 }
 
-// 1 < M <= 16 on e4m3 rows (tiled or row-major), one row block per workgroup, rows_ring's slots
-template <int MODE, int LAYOUT, int XK>
+// 1 < M <= 32 on e4m3 rows (tiled or row-major), one row block per workgroup, rows_ring's slots; MT
+// 16-row tiles (2 above M = 16)
+template <int MODE, int LAYOUT, int XK, int MT>
 void launch_rows(int u, dim3 grid, dim3 block, size_t smem, hipStream_t s, const uint8_t* xb,
                  const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
                  const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out,
                  void* aux) {
   constexpr bool one = MODE != KRQ_OUT_SWIGLU;
   if constexpr (XK == KRQ_X_FP8 || XK == KRQ_X_FP8_TILED) {
-    if (one && u == 10)
+    if (MT == 1 && one && u == 10)
       hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, one ? 10 : 5, 1, 0>), grid, block, smem, s,
                          KRQ_GEMV_ARGS);
-    else if (one && u == 8)
+    else if (MT == 1 && one && u == 8)
       hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, one ? 8 : 5, 1, 0>), grid, block, smem, s,
                          KRQ_GEMV_ARGS);
     else
-      hipLaunchKernelGGL((k_gemv_fp8<1, MODE, LAYOUT, XK, 1, 5, 1, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
+      hipLaunchKernelGGL((k_gemv_fp8<MT, MODE, LAYOUT, XK, 1, 5, 1, 0>), grid, block, smem, s, KRQ_GEMV_ARGS);
   }
 }
 
@@ -114,7 +115,10 @@ int launch(int algo, int pb, int awc, int u, bool rows, int M, dim3 grid, int nt
   const dim3 block(nthreads);
   constexpr int PB2 = MODE == KRQ_OUT_SWIGLU ? 1 : 2;  // no paired variant of the SwiGLU kernel
   if (rows) {
-    launch_rows<MODE, LAYOUT, XK>(u, grid, block, smem, s, KRQ_GEMV_ARGS);
+    if (M > 16)
+      launch_rows<MODE, LAYOUT, XK, 2>(u, grid, block, smem, s, KRQ_GEMV_ARGS);
+    else
+      launch_rows<MODE, LAYOUT, XK, 1>(u, grid, block, smem, s, KRQ_GEMV_ARGS);
     return 0;
   }
   if constexpr (XK == KRQ_X_BF16_DYN) {  // (M == 1)
@@ -222,11 +226,19 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   const int MT = (algo == 2 || M <= 16) ? 1 : 2;
   const int64_t blocks = NO / 16 / pb * split;
   // Multi-row blocks on e4m3 rows (1 < M <= 16, one row block per workgroup, matrix cores) take
-  // rows_ring.
-  const bool rows = M > 1 && M <= 16 && pb == 1 && algo == 1 && (x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED);
+  // rows_ring. So do 16 < M <= 32 (two row tiles) on splits of more than 8 steps, with five-slot
+  // waves (ten slots with two row tiles spill): at M = 32 QKV 6.99 -> 6.67 us, gate_up 13.70 ->
+  // 13.12, down 9.82 -> 9.51, while O (8 steps) lost with it (5.77 -> 6.49) and keeps the ring
+  // of two.
+  const bool rows = M > 1 && (M <= 16 || (M <= 32 && (nsteps > 8 || mode == KRQ_OUT_SWIGLU))) && pb == 1 &&
+                    algo == 1 && (x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED);
   int awc = 0, u = 0, nw = 0, na = 0;
   if (rows) {
     rows_ring(nsteps, P, &u, &nw);
+    if (M > 16 && u > 5) {
+      u = 5;
+      nw = (nsteps + 4) / 5;
+    }
   } else {
     // one-row kind: an activation wave holding the whole row (K <= 10240), else every wave takes
     // part in the prologue. Measured at M = 1: QKV 5.92 -> 5.29 us, O 5.15 -> 4.41, down 7.91 ->
