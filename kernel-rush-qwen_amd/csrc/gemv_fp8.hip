@@ -228,8 +228,8 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   // Multi-row blocks on e4m3 rows (1 < M <= 16, one row block per workgroup, matrix cores) take
   // rows_ring. So do 16 < M <= 32 (two row tiles) on splits of more than 8 steps, with five-slot
   // waves (ten slots with two row tiles spill): at M = 32 QKV 6.99 -> 6.67 us, gate_up 13.70 ->
-  // 13.12, down 9.82 -> 9.51, while O (8 steps) lost with it (5.77 -> 6.49) and keeps the ring
-  // of two.
+  // 13.12, down 9.82 -> 9.51, while O (8 steps) lost with it (5.77 -> 6.49 with one wave of 8
+  // slots, 6.39 with two of 5) and keeps the ring of two.
   const bool rows = M > 1 && (M <= 16 || (M <= 32 && (nsteps > 8 || mode == KRQ_OUT_SWIGLU))) && pb == 1 &&
                     algo == 1 && (x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED);
   int awc = 0, u = 0, nw = 0, na = 0;
