@@ -182,7 +182,7 @@ SEEDS = {"qkv": 0, "o": 1, "down": 3, "small": 5}
 
 
 @pytest.mark.parametrize("name", list(SHAPES))
-@pytest.mark.parametrize("M", [1, 2, 16, 32])
+@pytest.mark.parametrize("M", [1, 2, 16, 23, 32])  # 23: the two-row-tile rings with a ragged second tile
 def test_gemv_fp8(dev, name, M):
     N, K = SHAPES[name]
     w, x = _fp8_case(N, K, M, SEEDS[name])
@@ -253,7 +253,7 @@ def test_gemv_fp8_layouts_and_algos(dev, layout, algo):
         assert rel_err(y, yref) <= TOL
 
 
-@pytest.mark.parametrize("M", [1, 16, 32])
+@pytest.mark.parametrize("M", [1, 16, 23, 32])
 def test_gemv_swiglu_fp8(dev, M):
     N, K = GATE_UP
     I = N // 2
