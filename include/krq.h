@@ -120,6 +120,11 @@ int krq_quant_rows(const void* x_bf16, int64_t M, int64_t K, void* x8, float* xs
  * x8_tiled holds MP * K bytes; K % 64 == 0. xs as krq_quant_rows (M values).
  */
 int krq_quant_rows_tiled(const void* x_bf16, int64_t M, int64_t K, void* x8_tiled, float* xs, void* stream);
+/* krq_cast_fp8 with a given per-tensor inverse (ActScale / SharedScale, the static scales of the
+ * engine's FP8 decode, engine/engine.py:977-981 through linear_fp8) written in that tiled layout:
+ * the bytes of _cast(x, a) (reference engine/kernels/fp8.py:52-56) permuted, pad rows zero, for the
+ * GEMV on KRQ_X_FP8_TILED rows at 1 < M <= 32. Same shape rules as krq_quant_rows_tiled. */
+int krq_cast_fp8_tiled(const void* x_bf16, int64_t M, int64_t K, const float* inv, void* x8_tiled, void* stream);
 
 /*
  * FP8 skinny GEMM/GEMV, M <= 32: replaces linear_fp8 -> torch._scaled_mm (reference

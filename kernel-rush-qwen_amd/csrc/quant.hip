@@ -337,6 +337,30 @@ __global__ __launch_bounds__(NT) void k_act_rows_fast(const uint16_t* __restrict
   }
 }
 
+// the cast with a given inverse (krq_cast_fp8's bytes) into the tiled activation layout of
+// k_act_rows_fast<NT, true>: one block per row of the M rows padded to a multiple of 16, 16 values
+// per thread piece, the pad rows written as zeros
+template <int NT>
+__global__ __launch_bounds__(NT) void k_cast_rows_tiled(const uint16_t* __restrict__ x, int64_t M, int64_t K,
+                                                        const float* __restrict__ inv, uint8_t* __restrict__ x8) {
+  constexpr int C = static_cast<int>(kVecMaxK / 16 / NT);
+  const int64_t r = blockIdx.x;
+  const float iv = inv[0];
+  const uint8_t* row = reinterpret_cast<const uint8_t*>(x + r * K);
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int64_t e = 16 * (int64_t)(threadIdx.x + c * NT);
+    if (e < K) {
+      uint4 o = zero4();
+      if (r < M) {
+        const uint2 lo = quant8(ld16(row + 2 * e), iv), hi = quant8(ld16(row + 2 * e + 16), iv);
+        o = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      }
+      *reinterpret_cast<uint4*>(x8 + tiled_offset(r, e, K)) = o;
+    }
+  }
+}
+
 // cast, one 16-byte chunk (8 values) per thread
 __global__ __launch_bounds__(kQT) void k_cast_vec(const uint16_t* __restrict__ x, int64_t M, int64_t K,
                                                   const float* __restrict__ inv, int per_row,
@@ -529,6 +553,19 @@ extern "C" int krq_quant_rows_tiled(const void* x_bf16, int64_t M, int64_t K, vo
   hipLaunchKernelGGL((k_act_rows_fast<kRowNT, true>), dim3(static_cast<unsigned>(mp)), dim3(kRowNT), 0,
                      (hipStream_t)stream, (const uint16_t*)x_bf16, M, K, xs, (uint8_t*)x8_tiled);
   return krq_check_launch("quant_rows_tiled");
+}
+
+extern "C" int krq_cast_fp8_tiled(const void* x_bf16, int64_t M, int64_t K, const float* inv, void* x8_tiled,
+                                  void* stream) {
+  KRQ_REQUIRE(x_bf16 && inv && x8_tiled, "cast_fp8_tiled: null pointer");
+  KRQ_REQUIRE(M > 0 && M <= 0x7fffffe0 && K > 0 && K % 64 == 0,
+              "cast_fp8_tiled: bad shape M=%lld K=%lld (K a multiple of 64)", (long long)M, (long long)K);
+  KRQ_REQUIRE(vec_ok(x_bf16, K, K) && aligned16(x8_tiled),
+              "cast_fp8_tiled: x and x8_tiled must be 16-byte aligned and K at most %lld", (long long)kVecMaxK);
+  const int64_t mp = (M + 15) / 16 * 16;
+  hipLaunchKernelGGL((k_cast_rows_tiled<kRowNT>), dim3(static_cast<unsigned>(mp)), dim3(kRowNT), 0,
+                     (hipStream_t)stream, (const uint16_t*)x_bf16, M, K, inv, (uint8_t*)x8_tiled);
+  return krq_check_launch("cast_fp8_tiled");
 }
 
 extern "C" int krq_pack_fp8(const void* w8_rowmajor, int64_t N, int64_t K, void* w8_tiled,

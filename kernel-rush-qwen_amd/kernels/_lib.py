@@ -33,6 +33,7 @@ EXPORTS = {
     "krq_act_scale_cast_fp8": (_i32, [_vp, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "krq_quant_rows": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "krq_quant_rows_tiled": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    "krq_cast_fp8_tiled": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "krq_gemv_fp8": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64,
                             _i32, _i32, _i32, _vp, _vp]),
     "krq_gemv_swiglu_fp8_cast": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64,

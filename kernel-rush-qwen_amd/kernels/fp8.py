@@ -146,6 +146,19 @@ def quant_rows_tiled(x):
     return x8t, xs
 
 
+def cast_tiled(x, a):
+    """_cast(x, a) in the tiled activation layout of quant_rows_tiled (krq_cast_fp8_tiled): the
+    static- or per-call-scale rows for the GEMV on X_FP8_TILED (from TILED_MIN_ROWS to 32 rows).
+    Returns uint8 [16 * ceil(M / 16) * K]; the bytes are _cast's, permuted, pad rows zero."""
+    x2 = _rows(x)
+    M, K = x2.shape
+    L.require_device(a.inv)
+    mp = (M + 15) // 16 * 16
+    x8t = torch.empty((mp * K,), device=x2.device, dtype=torch.uint8)
+    L.call("krq_cast_fp8_tiled", L.ptr(x2), M, K, L.ptr(a.inv.reshape(1)), L.ptr(x8t), L.stream(x2))
+    return x8t
+
+
 def _cast_hip(x, a):
     x2 = _rows(x)
     M, K = x2.shape
@@ -283,12 +296,16 @@ def gemv_fp8_bf16_launch(x, q, split=1, mode=L.OUT_BF16, a=None, algo=L.ALGO_AUT
 
 
 def _fits_fused(x, split, a):
+    """One row quantized in the GEMV's prologue (its activation wave). More rows with a given
+    scale are cast first (row-major, or tiled from TILED_MIN_ROWS): quantizing them in the prologue
+    measured slower on MI355X at every M > 1 (split 1, us, prologue / cast + GEMV): QKV M = 4
+    9.19 / 6.92, M = 8 10.62 / 7.19; gate_up M = 4 15.78 / 11.33, M = 8 23.66 / 11.90."""
     M, K = x.shape
-    if x.dtype != torch.bfloat16 or M > DECODE_MAX_ROWS or K % 64:
+    if x.dtype != torch.bfloat16 or M != 1 or K % 64:
         return False
     if a is None:
-        return M == 1 and K <= FUSED_MAX_ELEMS_DYN
-    return M * (K // split) <= FUSED_MAX_ELEMS
+        return K <= FUSED_MAX_ELEMS_DYN
+    return K // split <= FUSED_MAX_ELEMS
 
 
 def _activation_fp8(x, a, xs):
@@ -305,13 +322,29 @@ def _activation_fp8(x, a, xs):
     return x8, s.reshape(-1)
 
 
+# From this many rows the GEMV reads tiled e4m3 rows (padded to 16-row tiles); below, row-major ones.
+# Measured on MI355X (graph of 72 launches over 12 weight sets, per-token scales with the decode
+# splits / a given scale at split 1), row-major against tiled, us: QKV M = 12 7.28 / 7.40, M = 16
+# 7.52 / 7.40; gate_up M = 4 12.64 / 13.47, M = 16 14.19 / 13.70; down M = 4 9.70 / 10.35, M = 16
+# 11.24 / 10.83; given scale M = 8 QKV 7.19 / 7.60, M = 16 8.25 / 7.68, M = 32 10.47 / 9.29.
+TILED_MIN_ROWS = 13
+
+
 def _tiled_rows(x, a, xs, algo):
-    """bf16 rows scaled per token at 1 < M <= 32 go through quant_rows_tiled and the GEMV on tiled
-    activations (the same operands as quant_rows + the row-major e4m3 GEMV, contiguous loads);
-    rows longer than quant_rows_tiled takes use quant_rows and the row-major e4m3 GEMV."""
+    """bf16 rows at TILED_MIN_ROWS <= M <= 32 go through quant_rows_tiled (scaled per token) or
+    cast_tiled (a given scale) and the GEMV on tiled activations (the operands of quant_rows / _cast
+    + the row-major e4m3 GEMV, with contiguous loads); fewer rows, and rows longer than the tiled
+    kernels take, use the row-major kernels."""
     M, K = x.shape
-    return (xs is None and a is None and x.dtype == torch.bfloat16 and 1 < M <= DECODE_MAX_ROWS
+    return (xs is None and x.dtype == torch.bfloat16 and TILED_MIN_ROWS <= M <= DECODE_MAX_ROWS
             and K % 64 == 0 and K <= TILED_ROWS_MAX_K and algo != L.ALGO_VALU)
+
+
+def _tiled_operand(x, a):
+    """(x8 tiled, x_scale) for _tiled_rows inputs: per token, or with the given scale."""
+    if a is None:
+        return quant_rows_tiled(x)
+    return cast_tiled(x, a), a.scale.reshape(1)
 
 
 def _chunked(x8, xs, fn):
@@ -337,7 +370,7 @@ def gemv_fp8(x, q, split=1, a=None, xs=None, algo=L.ALGO_AUTO):
     if xs is None and _fits_fused(x, split, a):
         return gemv_fp8_bf16_launch(x, q, split, mode, a, algo)
     if _tiled_rows(x, a, xs, algo):
-        x8t, s = quant_rows_tiled(x)
+        x8t, s = _tiled_operand(x, a)
         return gemv_fp8_tiled_launch(x8t, s, q, M, split, mode)
     x8, s = _activation_fp8(x, a, xs)
     return _chunked(x8, s, lambda xc, sc: gemv_fp8_launch(xc, sc, q, split, mode, algo))
@@ -350,7 +383,7 @@ def gemv_swiglu_fp8(x, q, a=None, xs=None, algo=L.ALGO_AUTO):
     if xs is None and _fits_fused(x, 1, a):
         return gemv_fp8_bf16_launch(x, q, 1, L.OUT_SWIGLU, a, algo)
     if _tiled_rows(x, a, xs, algo):
-        x8t, s = quant_rows_tiled(x)
+        x8t, s = _tiled_operand(x, a)
         return gemv_fp8_tiled_launch(x8t, s, q, x.shape[0], 1, L.OUT_SWIGLU)
     x8, s = _activation_fp8(x, a, xs)
     return _chunked(x8, s, lambda xc, sc: gemv_fp8_launch(xc, sc, q, 1, L.OUT_SWIGLU, algo))
@@ -375,7 +408,7 @@ def swiglu_cast_fp8(x, q, out_a, a=None, xs=None):
         kind, x_scale, x_inv = (L.X_BF16_DYN, None, None) if a is None else \
             (L.X_BF16_STATIC, a.scale.reshape(1), a.inv.reshape(1))
     elif _tiled_rows(x, a, xs, L.ALGO_AUTO):
-        xin, x_scale = quant_rows_tiled(x)
+        xin, x_scale = _tiled_operand(x, a)
         kind, x_inv = L.X_FP8_TILED, None
     else:
         xin, x_scale = _activation_fp8(x, a, xs)
@@ -445,6 +478,8 @@ def linear_fp8(x, q, a=None, amax_out=None):
             amax_out.copy_(torch.maximum(amax_out, a.amax.reshape(1)))
     if x8 is None and _fits_fused(x, 1, a):
         return gemv_fp8_bf16_launch(x, q, 1, L.OUT_BF16, a)
+    if x8 is None and _tiled_rows(x, a, None, L.ALGO_AUTO):
+        return gemv_fp8_tiled_launch(cast_tiled(x, a), a.scale.reshape(1), q, x.shape[0], 1, L.OUT_BF16)
     if x8 is None:
         x8 = _cast(x, a)
     if x.shape[0] <= DECODE_MAX_ROWS:

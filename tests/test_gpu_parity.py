@@ -566,6 +566,56 @@ def test_quant_rows_tiled(dev, M, K):
     assert np.array_equal(xs.cpu().numpy().reshape(-1), rs.reshape(-1))
 
 
+@pytest.mark.parametrize("M", [2, 5, 16, 17, 32])
+@pytest.mark.parametrize("K", [64, 2560, 9728])
+def test_cast_tiled(dev, M, K):
+    """cast_tiled (krq_cast_fp8_tiled) writes _cast's bytes with a given scale in the tiled
+    activation layout: the oracle's cast rows, padded with zero rows to a multiple of 16, through
+    O.tile, bit for bit, with clamped codes and a NaN among them."""
+    x = act(M, K, 400 + M + K)
+    x[M - 1, K // 2] = float("nan")
+    a = fp8.SharedScale(torch.tensor([448.0 / 2.0], device=dev), torch.tensor(2.0 / 448.0, device=dev))
+    x8t = fp8.cast_tiled(x.to(dev), a)
+    mp = (M + 15) // 16 * 16
+    pad = np.zeros((mp, K), dtype=np.uint8)
+    pad[:M] = O.cast(u16(x), np.float32(448.0 / 2.0))
+    assert np.array_equal(x8t.cpu().numpy(), O.tile(pad).reshape(-1))
+
+
+@pytest.mark.parametrize("M", [4, 12, 13, 16, 23])
+def test_static_scale_multi_row_routes(dev, M):
+    """A given scale at 1 < M <= 32 (the engine's FP8 decode, engine/engine.py:977-981): linear_fp8,
+    gemv_fp8 (partials) and gemv_swiglu_fp8 cast the rows first - row-major below TILED_MIN_ROWS,
+    tiled (cast_tiled) from there - and run that GEMV: the same bits as those launches called
+    directly, within the bar of the oracle."""
+    a = fp8.SharedScale(torch.tensor([448.0 / 5.0], device=dev), torch.tensor(5.0 / 448.0, device=dev))
+    sc = a.scale.reshape(1)
+
+    def direct(xd, q, split, mode):
+        if M >= fp8.TILED_MIN_ROWS:
+            return fp8.gemv_fp8_tiled_launch(fp8.cast_tiled(xd, a), sc, q, M, split, mode)
+        return fp8.gemv_fp8_launch(fp8._cast_hip(xd, a), sc, q, split, mode)
+
+    for name, split in (("qkv", 2), ("down", 4)):
+        N, K = SHAPES[name]
+        w, x = _fp8_case(N, K, M, 70 + SEEDS[name])
+        q = fp8.quantize_weight(w.to(dev))
+        xd = x.to(dev)
+        y = fp8.linear_fp8(xd, q, a)
+        assert torch.equal(y, direct(xd, q, 1, L.OUT_BF16))
+        p = fp8.gemv_fp8(xd, q, split, a)
+        assert torch.equal(p, direct(xd, q, split, L.OUT_PARTIAL))
+        r8, rs = O.quantize_weight(u16(w))
+        _, yref = O.fp8_matmul(O.cast(u16(x), np.float32(448.0 / 5.0)), np.float32(5.0 / 448.0), r8, rs)
+        assert rel_err(y.float().cpu().numpy(), yref) <= TOL
+        assert rel_err(_sum_partials(p), yref) <= TOL
+    N, K = GATE_UP
+    w, x = _fp8_case(N, K, M, 77)
+    q = fp8.quantize(w.to(dev))
+    xd = x.to(dev)
+    assert torch.equal(fp8.gemv_swiglu_fp8(xd, q, a), direct(xd, q, 1, L.OUT_SWIGLU))
+
+
 TILED_SHAPES = {"qkv": (QKV, (1, 2)), "o": (O_PROJ, (4,)), "down": (DOWN, (4,)), "small": ((64, 384), (1, 2))}
 
 
