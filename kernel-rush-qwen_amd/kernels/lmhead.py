@@ -6,7 +6,8 @@ reference's fused form keeps the same rule (engine/kernels/mega.py:412-436).
 
 FP8 heads take the activation scaling of the weight's form:
   per-channel weights (fp8.quantize, BASELINE's per-channel lm_head): h scaled per token, inside
-      the GEMV at M == 1, else by fp8.quant_rows_tiled (rows in the tiled activation layout);
+      the GEMV at M == 1, else by fp8.quant_rows (row-major rows) or, from fp8.TILED_MIN_ROWS,
+      fp8.quant_rows_tiled (rows in the tiled activation layout);
   per-tensor weights (fp8.quantize_weight, the engine's lm8 = quantize_weight(lm_head),
       engine.py:504-505): exactly linear_fp8(h, lm8) followed by torch.argmax (engine.py:989,
       :1022) - one ActScale over all of h (at M == 1 the same as per token, so inside the GEMV),
@@ -35,19 +36,22 @@ def _fp8_operands(h, w, a, h_layout):
     if ws.numel() == 1:          # linear_fp8's own ActScale over the whole of h
         a = _fp8.ActScale(h)
         return _fp8._cast(_fp8._rows(h), a), a.scale.reshape(1), 0, L.LM_FP8
-    if K % 64 == 0 and K <= _fp8.TILED_ROWS_MAX_K and h_layout == "tiled":   # tiled e4m3 rows
+    tiled = h_layout == "tiled" or (h_layout == "auto" and M >= _fp8.TILED_MIN_ROWS)
+    if K % 64 == 0 and K <= _fp8.TILED_ROWS_MAX_K and tiled:   # tiled e4m3 rows
         h8, hs = _fp8.quant_rows_tiled(h)
         return h8, hs.reshape(-1), 1, L.LM_FP8_TILED_H
     h8, hs = _fp8.quant_rows(h)
     return h8, hs.reshape(-1), 1, L.LM_FP8
 
 
-def lm_head_argmax(h, w, return_logits=False, h_layout="tiled", a=None):
+def lm_head_argmax(h, w, return_logits=False, h_layout="auto", a=None):
     """h [M, K] bf16 (M <= 32); w the tied embedding, bf16 [V, K], or an FP8Weight from
     fp8.quantize (per channel) or fp8.quantize_weight (per tensor). Returns int64 [M] token ids,
-    or (ids, bf16 logits [M, V]) with return_logits=True. h_layout ("tiled" or "rowmajor"): how a
-    per-channel FP8 head's per-token rows are laid out at M > 1 (the same operands either way;
-    tiled loads are contiguous). a: an ActScale / SharedScale for the FP8 head's activations (as
+    or (ids, bf16 logits [M, V]) with return_logits=True. h_layout ("auto", "tiled" or
+    "rowmajor"): how a per-channel FP8 head's per-token rows are laid out at M > 1 (the same
+    operands either way); "auto" takes tiled rows from fp8.TILED_MIN_ROWS (measured on MI355X at
+    V = 151,936, us tiled / row-major: M = 2 68.4 / 63.8, M = 8 72.9 / 71.5, M = 12 75.5 / 75.4,
+    M = 16 77.5 / 80.7). a: an ActScale / SharedScale for the FP8 head's activations (as
     linear_fp8 takes), instead of the scaling described in the module docstring."""
     L.require_device(h)
     M, K = h.shape

@@ -141,9 +141,10 @@ def test_lmhead_fp8_per_channel_argmax_seeds(dev, head, M):
         assert np.array_equal(idx, O.argmax_lowest(lg))
         assert rel_err(lg, y) <= TOL
         inside += check_rows(idx, y, S, f"fp8/channel M={M} seed {seed}")
-        if M > 1 and seed == 0:  # tiled e4m3 rows (the default) and row-major ones: the same logits
-            idx_r, logits_r = lmhead.lm_head_argmax(hd, q, return_logits=True, h_layout="rowmajor")
-            assert torch.equal(logits_r, logits) and np.array_equal(idx_r.cpu().numpy(), idx)
+        if M > 1 and seed == 0:  # tiled e4m3 rows and row-major ones: the same logits
+            for lay in ("rowmajor", "tiled"):
+                idx_r, logits_r = lmhead.lm_head_argmax(hd, q, return_logits=True, h_layout=lay)
+                assert torch.equal(logits_r, logits) and np.array_equal(idx_r.cpu().numpy(), idx), lay
     print(f"fp8 per-channel M={M}: {inside} of {M * len(SEEDS)} rows inside the fp32 bound")
     assert inside <= M * len(SEEDS) // 2
 
