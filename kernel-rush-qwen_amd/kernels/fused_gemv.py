@@ -134,16 +134,19 @@ def _launch_fp8(x, q, split, mode, norm, ep, eps, a, out):
     fits = L.lib().krq_gemv_fp8_fused_fits
     kind = L.X_BF16_STATIC if a is not None else L.X_BF16_DYN
     if not fits(M, N, K, split, mode, kind, 1 if norm is not None else 0):
-        # stage outside: normalize (and quantize) the rows first, then e4m3 activations
-        # (per-token scales: the rows in the tiled activation layout, read as one KiB per operand)
-        tiled = a is None and K % 64 == 0
+        # stage outside: normalize (and quantize) the rows first, then e4m3 activations, row-major
+        # or (from fp8.TILED_MIN_ROWS rows) in the tiled activation layout, as fp8's GEMVs choose
+        tiled = K % 64 == 0 and K <= _fp8.TILED_ROWS_MAX_K and M >= _fp8.TILED_MIN_ROWS
         if norm is not None:
-            if tiled:
+            if tiled and a is None:
                 x8 = torch.empty(((M + 15) // 16 * 16 * K,), device=x.device, dtype=torch.uint8)
                 xs = torch.empty((M,), device=x.device, dtype=torch.float32)
                 L.call("krq_rmsnorm_quant_rows_tiled", L.ptr(x), L.ptr(ss), L.ptr(ln), float(eps), M, K,
                        L.ptr(x8), L.ptr(xs), L.stream(x))
                 return _fp8.gemv_fp8_tiled_launch(x8, xs, q, M, split, mode, out)
+            if tiled:
+                x8t = _fp8.cast_tiled(_rmsnorm(x, ln, ss, eps), a)
+                return _fp8.gemv_fp8_tiled_launch(x8t, a.scale.reshape(1), q, M, split, mode, out)
             if a is None:
                 x8 = torch.empty((M, K), device=x.device, dtype=torch.float8_e4m3fn)
                 xs = torch.empty((M,), device=x.device, dtype=torch.float32)
@@ -153,7 +156,7 @@ def _launch_fp8(x, q, split, mode, norm, ep, eps, a, out):
                 x8, xs = _fp8._cast(_rmsnorm(x, ln, ss, eps), a), a.scale.reshape(1)
             return _fp8.gemv_fp8_launch(x8, xs, q, split, mode, L.ALGO_MFMA, out)
         if tiled:
-            x8, xs = _fp8.quant_rows_tiled(x)
+            x8, xs = _fp8._tiled_operand(x, a)
             kind, xin, x_scale, x_inv = L.X_FP8_TILED, x8, xs.reshape(-1), None
         else:
             x8, xs = _fp8._activation_fp8(x, a, None)
