@@ -37,7 +37,8 @@ constexpr int kU = 4;  // steps per load batch
 
 // Internal output mode (not part of the C ABI's modes): the lm-head epilogue. Logits are rounded
 // to bf16 (optionally stored to `out`) and each block writes, per output row m, the largest
-// logit of its 16 columns and the lowest column index holding it to `aux` ([row block][M] Best).
+// logit of its 16 columns and the lowest column index holding it to `aux` ([M][row block] Best:
+// each token row's candidates are contiguous, so the fold reads them as whole lines).
 constexpr int kOutArgmax = 3;
 
 struct Best {
@@ -266,7 +267,7 @@ KRQ_DEV void epilogue(const float* red, int p0, int nw, int M, int64_t NO, int64
         const Best c = shfl_best(b, o);
         if (better(c.v, c.i, b.v, b.i)) b = c;
       }
-      if (valid && (ln & 15) == 0) reinterpret_cast<Best*>(aux)[rb * M + m] = b;
+      if (valid && (ln & 15) == 0) reinterpret_cast<Best*>(aux)[(int64_t)m * (NO >> 4) + rb] = b;
       continue;
     }
     if (MODE == KRQ_OUT_SWIGLU && cast) {
@@ -506,7 +507,7 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 int plan_waves(int nsteps, int P, int U, int64_t blocks, bool act_wave = false);
 
 // Validated launches shared by the C ABI entry points (gemv_fp8.hip, gemv_bf16.hip); mode may
-// also be kOutArgmax (then split == 1, aux = [N/16][M] Best, out = optional bf16 logits).
+// also be kOutArgmax (then split == 1, aux = [M][N/16] Best, out = optional bf16 logits).
 int gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const float* x_inv, int x_per_row,
                  const void* w8, int w_layout, const float* w_scale, int w_per_row, int64_t M,
                  int64_t N, int64_t K, int split, int mode, int algo, void* out, void* aux,

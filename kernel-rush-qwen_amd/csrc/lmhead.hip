@@ -57,20 +57,22 @@ KRQ_DEV uint64_t readlane_u64(uint64_t k, int l) {
   return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
-// One block per token row: every candidate load of a batch is issued before the first is used
-// (one memory round trip), the keys are reduced with DPP steps inside each wave and across the
+// One block per token row (its [nrb] candidates are contiguous, so each wave's load is 512 bytes of
+// whole lines): every candidate load of a batch is issued before the first is used (one memory
+// round trip), the keys are reduced with DPP steps inside each wave and across the
 // block's 16 waves by wave 0.
 __global__ __launch_bounds__(kFoldThreads) void k_argmax_fold(const Best* __restrict__ cand, int64_t nrb,
                                                               int M, int64_t* __restrict__ idx_out) {
   __shared__ uint64_t wk[kFoldThreads / 64];
   const int m = blockIdx.x, lane = threadIdx.x & 63;
+  const Best* __restrict__ row = cand + (int64_t)m * nrb;  // token row m's candidates, contiguous
   uint64_t best = 0;  // below every candidate's key
   for (int64_t base = 0; base < nrb; base += (int64_t)kFoldPer * kFoldThreads) {
     Best c[kFoldPer];
 #pragma unroll
     for (int q = 0; q < kFoldPer; ++q) {
       const int64_t rb = min(base + threadIdx.x + (int64_t)q * kFoldThreads, nrb - 1);  // clamped, valid
-      c[q] = cand[rb * M + m];
+      c[q] = row[rb];
     }
 #pragma unroll
     for (int q = 0; q < kFoldPer; ++q) {
