@@ -732,3 +732,30 @@ def test_lmhead_bf16_tiled(dev, M):
     G.pack(Ed)
     idx_t, lg_t = lmhead.lm_head_argmax(h.to(dev), Ed, return_logits=True)
     assert torch.equal(idx_t, idx_r) and torch.equal(lg_t, lg_r)
+
+
+@pytest.mark.parametrize("K", [16448, 16512])
+def test_rows_longer_than_tiled_kernels_fall_back(dev, K):
+    """M = 16 rows longer than krq_quant_rows_tiled takes (K > fp8.TILED_ROWS_MAX_K) go through
+    the row-major quant_rows + e4m3 GEMV instead of raising: gemv_fp8 at every split that tiles K,
+    and the per-channel FP8 lm_head (ids and bf16 logits against the oracle)."""
+    assert K > fp8.TILED_ROWS_MAX_K
+    M, N = 16, 64
+    w, x = weight(N, K, 41), act(M, K, 42)
+    q = fp8.quantize(w.to(dev))
+    r8, rs = O.quantize(u16(w))
+    x8r, xsr = O.quant_rows(u16(x))
+    _, yref = O.fp8_matmul(x8r, xsr, r8, rs)
+    xd = x.to(dev)
+    for split in (1, 2):
+        if (K // split) % 64:
+            continue
+        y = fp8.gemv_fp8(xd, q, split)
+        y = _sum_partials(y) if split > 1 else y.float().cpu().numpy()
+        e = rel_err(y, yref)
+        print(f"K={K} M={M} split={split}: max-rel {e:.2e}")
+        assert e <= TOL
+    idx, lg = lmhead.lm_head_argmax(xd, q, return_logits=True)
+    assert rel_err(lg.float().cpu().numpy(), yref) <= TOL
+    ref_ids = O.argmax_lowest(O.bf16_to_f32(u16(lg)).reshape(M, N))  # the fold over its own logits
+    assert np.array_equal(idx.cpu().numpy(), ref_ids)
