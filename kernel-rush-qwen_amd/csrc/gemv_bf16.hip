@@ -12,7 +12,8 @@ using namespace krq;
 
 namespace {
 
-// PB = 2: two adjacent row blocks per block sharing the activation loads (as in gemv_fp8.hip).
+// PB = 2 or 4: adjacent row blocks per block sharing the activation loads (as in gemv_fp8.hip;
+// 4 for the multi-row lm_head, where every 16-column block re-reads the bf16 rows from L2).
 template <int MT, int MODE, int LAYOUT, int ALGO, int U, int PB>
 __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x,
                                                   const uint8_t* __restrict__ w, int M, int64_t NO,
@@ -21,26 +22,31 @@ __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x
   extern __shared__ float red[];
   __shared__ float ones[32];
   static_assert(PB == 1 || (MODE != KRQ_OUT_SWIGLU && ALGO != 2), "paired row blocks: MFMA, no SwiGLU");
-  constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : PB;
+  static_assert(PB == 1 || PB == 2 || PB == 4, "one, two or four row blocks per block");
+  constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : PB;  // weight row blocks streamed per step
+  constexpr int NV = MT * 256;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int64_t rb = (int64_t)blockIdx.x * PB, rbu = MODE == KRQ_OUT_SWIGLU ? rb + (NO >> 4) : rb + 1;
+  const int64_t rb = (int64_t)blockIdx.x * PB;
   const int sidx = blockIdx.y;
   const int nsteps = (kts + 1) >> 1;
   const int64_t tbase = (int64_t)sidx * kts;
   const int64_t rowb = 2 * K;
   const int jcount = wave < nsteps ? (nsteps - wave + nw - 1) / nw : 0;
   if (threadIdx.x < 32) ones[threadIdx.x] = 1.0f;
+  // weight set p: the up half of the SwiGLU, else the p-th row block of this block
+  auto rbp = [&](int p) -> int64_t { return MODE == KRQ_OUT_SWIGLU && p == 1 ? rb + (NO >> 4) : rb + p; };
 
-  v4f acc[MT], accu[MT];
+  v4f acc[P][MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
-    accu[mt] = v4f{0.f, 0.f, 0.f, 0.f};
-  }
-  float s0 = 0.f, s1 = 0.f, q0 = 0.f, q1 = 0.f;
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[p][mt] = v4f{0.f, 0.f, 0.f, 0.f};
+  float sv[P][2];  // vector-ALU partial sums (ALGO 2) of the low and high tile of each step
+#pragma unroll
+  for (int p = 0; p < P; ++p) sv[p][0] = sv[p][1] = 0.f;
   // a ring of U step slots: consume slot u (step cc), then refill it with step cc + U
-  uint4 wl[U], wh[U], ul[U], uh[U], xl[U][MT], xh[U][MT];
+  uint4 wl[P][U], wh[P][U], xl[U][MT], xh[U][MT];
   // Every slot load is issued unconditionally (a branch around a load makes the compiler drain all
   // outstanding loads at the join): a slot past this wave's last step reloads that step (already
   // in flight or cached) and is masked where consumed; rows m >= M read row M - 1, whose products
@@ -49,11 +55,10 @@ __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x
     const int j = jcount > 0 ? wave + min(cc, jcount - 1) * nw : 0;
     const int64_t t0 = tbase + 2 * j;
     const int64_t t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
-    wl[u] = ld16nt(w_addr<LAYOUT>(w, rb, t0, rowb, lane));
-    wh[u] = ld16nt(w_addr<LAYOUT>(w, rb, t1, rowb, lane));
-    if (P == 2) {
-      ul[u] = ld16nt(w_addr<LAYOUT>(w, rbu, t0, rowb, lane));
-      uh[u] = ld16nt(w_addr<LAYOUT>(w, rbu, t1, rowb, lane));
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      wl[p][u] = ld16nt(w_addr<LAYOUT>(w, rbp(p), t0, rowb, lane));
+      wh[p][u] = ld16nt(w_addr<LAYOUT>(w, rbp(p), t1, rowb, lane));
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -66,26 +71,17 @@ __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x
   auto consume_slot = [&](int u, int cc) {
     const int j = jcount > 0 ? wave + min(cc, jcount - 1) * nw : 0;
     const bool ok = cc < jcount, hi = ok && (2 * j + 1 < kts);
-    const uint4 bl = sel4(ok, wl[u]), bh = sel4(hi, wh[u]);
-    if (ALGO == 2) {
-      s0 = dot8_bf16(bl, xl[u][0], s0);
-      s1 = dot8_bf16(bh, xh[u][0], s1);
-      if (P == 2) {
-        q0 = dot8_bf16(sel4(ok, ul[u]), xl[u][0], q0);
-        q1 = dot8_bf16(sel4(hi, uh[u]), xh[u][0], q1);
-      }
-    } else {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xl[u][mt]), as_v8bf(bl), acc[mt], 0, 0, 0);
-        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xh[u][mt]), as_v8bf(bh), acc[mt], 0, 0, 0);
-      }
-      if (P == 2) {
-        const uint4 cl = sel4(ok, ul[u]), ch = sel4(hi, uh[u]);
+    for (int p = 0; p < P; ++p) {
+      const uint4 bl = sel4(ok, wl[p][u]), bh = sel4(hi, wh[p][u]);
+      if (ALGO == 2) {
+        sv[p][0] = dot8_bf16(bl, xl[u][0], sv[p][0]);
+        sv[p][1] = dot8_bf16(bh, xh[u][0], sv[p][1]);
+      } else {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xl[u][mt]), as_v8bf(cl), accu[mt], 0, 0, 0);
-          accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xh[u][mt]), as_v8bf(ch), accu[mt], 0, 0, 0);
+          acc[p][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xl[u][mt]), as_v8bf(bl), acc[p][mt], 0, 0, 0);
+          acc[p][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(xh[u][mt]), as_v8bf(bh), acc[p][mt], 0, 0, 0);
         }
       }
     }
@@ -106,18 +102,31 @@ __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x
 #pragma unroll
   for (int u = 0; u < U; ++u) consume_slot(u, base + u);
   if (ALGO == 2) {
-    float a = s0 + s1, au = q0 + q1;
-    a += __shfl_xor(a, 16, kWave);
-    a += __shfl_xor(a, 32, kWave);
-    au += __shfl_xor(au, 16, kWave);
-    au += __shfl_xor(au, 32, kWave);
-    acc[0] = v4f{g == 0 ? a : 0.f, 0.f, 0.f, 0.f};
-    accu[0] = v4f{g == 0 ? au : 0.f, 0.f, 0.f, 0.f};
+    // the four lanes of row r (g = 0..3) hold partial sums of disjoint k: add them; lanes 0..15
+    // then carry columns 16 rb + lane in MFMA slot (mt 0, i 0), i.e. output row m = 0
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      float a = sv[p][0] + sv[p][1];
+      a += __shfl_xor(a, 16, kWave);
+      a += __shfl_xor(a, 32, kWave);
+      acc[p][0] = v4f{g == 0 ? a : 0.f, 0.f, 0.f, 0.f};
+    }
   }
-  stash<MT, P>(red, wave, lane, acc, accu);
+  // the P accumulator sets of each wave, in the layout epilogue() reads
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[(wave * P + p) * NV + mt * 256 + i * 64 + lane] = acc[p][mt][i];
   __syncthreads();
-  epilogue<MT, MODE, P>(red, 0, nw, M, NO, rb, sidx, ones, ColScales{1.0f, 1.0f}, out, aux);
-  if (PB == 2) epilogue<MT, MODE, P>(red, 1, nw, M, NO, rbu, sidx, ones, ColScales{1.0f, 1.0f}, out, aux);
+  if (MODE == KRQ_OUT_SWIGLU) {
+    epilogue<MT, MODE, P>(red, 0, nw, M, NO, rb, sidx, ones, ColScales{1.0f, 1.0f}, out, aux);
+  } else {
+#pragma unroll
+    for (int p = 0; p < PB; ++p)
+      epilogue<MT, MODE, P>(red, p, nw, M, NO, rb + p, sidx, ones, ColScales{1.0f, 1.0f}, out, aux);
+  }
 }
 
 // Persistent row partition (the reference's gemv_rows, engine/kernels/gemv.py:270-348): exactly
@@ -229,10 +238,13 @@ void launch(int M, int pb, dim3 grid, int nw, size_t smem, hipStream_t s, const 
             const uint8_t* w, int m, int64_t NO, int64_t K, int kts, void* out, void* aux) {
   const dim3 block(nw * 64);
   constexpr int PB2 = MODE == KRQ_OUT_SWIGLU ? 1 : 2;
+  constexpr int PB4 = MODE == kOutArgmax ? 4 : 1;  // (pb is 4 only for the argmax epilogue)
   if (M == 1)
     hipLaunchKernelGGL((k_gemv_bf16<1, MODE, LAYOUT, 2, 4, 1>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
   else if (M <= 4)
     hipLaunchKernelGGL((k_gemv_bf16<1, MODE, LAYOUT, 1, 4, 1>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
+  else if (M <= 16 && pb == 4)
+    hipLaunchKernelGGL((k_gemv_bf16<1, MODE, LAYOUT, 1, 2, PB4>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
   else if (M <= 16 && pb == 2)
     hipLaunchKernelGGL((k_gemv_bf16<1, MODE, LAYOUT, 1, 2, PB2>), grid, block, smem, s, x, w, m, NO, K, kts, out, aux);
   else if (M <= 16)
@@ -273,9 +285,11 @@ int krq::gemv_bf16_run(const void* x, const void* w, int w_layout, int64_t M, in
               "gemv_bf16: no tiling divides N=%lld (output columns must be a multiple of 16)", (long long)N);
   KRQ_REQUIRE(NO / 16 <= 0x7fffffff && split <= 65535, "gemv_bf16: grid too large");
   const int kts = static_cast<int>(K / split / 32);
-  // paired only where halving the blocks still leaves thousands (the lm_head), as in gemv_fp8.hip
-  const int pb = (mode != KRQ_OUT_SWIGLU && M > 4 && (NO / 16) % 2 == 0 &&
-                  (NO / 16) * split >= 4096) ? 2 : 1;
+  // paired only where halving the blocks still leaves thousands (the lm_head), as in gemv_fp8.hip;
+  // the lm_head's argmax launch at 4 < M <= 16 takes four row blocks per block
+  int pb = (mode != KRQ_OUT_SWIGLU && M > 4 && (NO / 16) % 2 == 0 &&
+            (NO / 16) * split >= 4096) ? 2 : 1;
+  if (pb == 2 && mode == kOutArgmax && M <= 16 && (NO / 16) % 4 == 0) pb = 4;
   const int P = mode == KRQ_OUT_SWIGLU ? 2 : pb;
   const int MT = M <= 16 ? 1 : 2;
   const int nw = plan_waves((kts + 1) / 2, P, M <= 4 ? 4 : 2, NO / 16 / pb * split);  // U of launch()'s variant
