@@ -41,6 +41,13 @@ constexpr int kU = 4;  // steps per load batch
 // each token row's candidates are contiguous, so the fold reads them as whole lines).
 constexpr int kOutArgmax = 3;
 
+// Internal output mode: the SwiGLU of KRQ_OUT_SWIGLU by a half-pair block b, which owns the 8 output
+// columns 8 b .. 8 b + 7: one matrix-core B operand holds both weight halves of them (its columns
+// 0-7 gate rows 8 b + c, its columns 8-15 the matching up rows NO + 8 b + c), with the steps per wave
+// of the two-matrix block, so the sums are the same bit for bit. A SwiGLU launch runs its last
+// column blocks this way (k_gemv_fp8_swiglu_mixed) to even out the bytes per compute unit.
+constexpr int kOutSwiGluHalf = 5;
+
 struct Best {
   float v;
   int i;
@@ -98,6 +105,18 @@ template <int LAYOUT>
 KRQ_DEV const uint8_t* w_addr(const uint8_t* w, int64_t rb, int64_t t, int64_t row_bytes, int lane) {
   if (LAYOUT == KRQ_W_TILED) return w + ((rb * (row_bytes >> 6) + t) * 64 + lane) * 16;
   return w + (rb * 16 + (lane & 15)) * row_bytes + t * 64 + (lane >> 4) * 16;
+}
+
+// The B-operand address of half-pair block b (kOutSwiGluHalf): lane column c < 8 reads gate row
+// 8 b + c, c >= 8 the up row NO + 8 b + c - 8; both are row 8 (b % 2) + c % 8 of 16-row block b / 2
+// of their matrix, so in the tiled layout a lane reads that row's 16 bytes of the tile.
+template <int LAYOUT>
+KRQ_DEV const uint8_t* w_addr_hp(const uint8_t* w, int64_t b, int64_t NO, int64_t t, int64_t row_bytes, int lane) {
+  const int c = lane & 15;
+  const int64_t rbx = (b >> 1) + (c >> 3) * (NO >> 4);
+  const int rr = 8 * static_cast<int>(b & 1) + (c & 7);
+  if (LAYOUT == KRQ_W_TILED) return w + ((rbx * (row_bytes >> 6) + t) * 64 + (lane & 48) + rr) * 16;
+  return w + (rbx * 16 + rr) * row_bytes + t * 64 + (lane >> 4) * 16;
 }
 
 // Hardware fp32 -> OCP e4m3 pair conversion after the reference's clamp to +-448. Bit-identical to
@@ -226,6 +245,11 @@ struct ColScales {
 template <int MODE, int PB>
 KRQ_DEV ColScales load_col_scales(const float* __restrict__ wsc, int w_per_row, int64_t NO, int64_t rb) {
   ColScales c{1.0f, 1.0f};
+  if (MODE == kOutSwiGluHalf) {  // rb = b: the scale of this lane column's gate or up row
+    const int col = threadIdx.x & 15;
+    c.g = wsc[w_per_row ? (col >> 3) * NO + rb * 8 + (col & 7) : 0];
+    return c;
+  }
   const int64_t n = rb * 16 + (threadIdx.x & 15);
   c.g = wsc[w_per_row ? n : 0];
   if (MODE == KRQ_OUT_SWIGLU) c.u = wsc[w_per_row ? NO + n : 0];
@@ -241,7 +265,7 @@ template <int MT, int MODE, int P>
 KRQ_DEV void epilogue(const float* red, int p0, int nw, int M, int64_t NO, int64_t rb, int split_idx,
                       const float* xs, ColScales cs, void* __restrict__ out, void* __restrict__ aux) {
   constexpr int NV = MT * 256;
-  const bool cast = MODE == KRQ_OUT_SWIGLU && aux != nullptr;
+  const bool cast = (MODE == KRQ_OUT_SWIGLU || MODE == kOutSwiGluHalf) && aux != nullptr;
   const float cinv = cast ? *static_cast<const float*>(aux) : 0.0f;
   for (int v = threadIdx.x; v < NV; v += blockDim.x) {
     const int mt = v >> 8, i = (v >> 6) & 3, ln = v & 63;
@@ -254,6 +278,27 @@ KRQ_DEV void epilogue(const float* red, int p0, int nw, int M, int64_t NO, int64
       if (MODE == KRQ_OUT_SWIGLU) au += red[(w * P + p0 + 1) * NV + v];
     }
     const float x = valid ? xs[m] : 0.0f;
+    if (MODE == kOutSwiGluHalf) {
+      // lane column c < 8 holds gate output 8 rb + c of row m, lane column c + 8 its up value: each
+      // rounded as KRQ_OUT_SWIGLU rounds it, then the gate lanes combine them
+      const float t = round_bf16(a * x * cs.g);
+      const float uu = __shfl_xor(t, 8, kWave);
+      if (ln & 8) continue;
+      const int64_t n8 = rb * 8 + (ln & 7);
+      if (cast) {
+        uint8_t q = 0;  // pad rows m >= M
+        if (valid) {
+          const float sl = round_bf16(t / (1.0f + expf(-t)));
+          q = clamp_to_e4m3(round_bf16(sl * uu) * cinv);
+        }
+        const int64_t tile = (int64_t)(m >> 4) * (NO >> 6) + (n8 >> 6);
+        reinterpret_cast<uint8_t*>(out)[tile * 1024 + 16 * (16 * ((n8 & 63) >> 4) + (m & 15)) + (n8 & 15)] = q;
+      } else if (valid) {
+        const float sl = round_bf16(t / (1.0f + expf(-t)));
+        reinterpret_cast<uint16_t*>(out)[(int64_t)m * NO + n8] = f32_to_bf16(sl * uu);
+      }
+      continue;
+    }
     if (MODE == kOutArgmax) {
       // the 16 lanes sharing (mt, i, g) hold the 16 columns of one output row: fold them
       Best b{-INFINITY, 0x7fffffff};

@@ -171,6 +171,36 @@ void launch_xk(int xk, int algo, int pb, int awc, int u, bool rows, int M, dim3 
 #undef KRQ_XK_ARGS
 }
 
+// The SwiGLU as k_gemv_fp8_swiglu_mixed (nfull two-matrix blocks, then half-pair blocks) for the
+// kernels the plan picked: the one-row kernel beside its activation wave (five-slot rings) or the
+// multi-row ring on e4m3 rows (M <= 16). False for any other plan, which keeps the plain launch.
+template <int XK>
+bool launch_swiglu_mixed(int awc, int u, bool rows, int M, int nfull, dim3 grid, int nthreads, size_t smem,
+                         hipStream_t s, const uint8_t* xb, const float* x_scale, const float* x_inv, int x_per_row,
+                         const uint8_t* wb, const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K,
+                         int kts, void* out, void* aux) {
+  const dim3 block(nthreads);
+  if constexpr (XK == KRQ_X_FP8 || XK == KRQ_X_FP8_TILED) {
+    if (!rows || M > 16 || u != 5) return false;
+    hipLaunchKernelGGL((k_gemv_fp8_swiglu_mixed<KRQ_W_TILED, XK, 1, 5, 0>), grid, block, smem, s, KRQ_GEMV_ARGS,
+                       nfull);
+  } else {
+    if (M != 1 || u != kSwiU) return false;
+    if (awc == kAwRow)
+      hipLaunchKernelGGL((k_gemv_fp8_swiglu_mixed<KRQ_W_TILED, XK, 1, kSwiU, kAwRow>), grid, block, smem, s,
+                         KRQ_GEMV_ARGS, nfull);
+    else if (awc == kAwSmall)
+      hipLaunchKernelGGL((k_gemv_fp8_swiglu_mixed<KRQ_W_TILED, XK, 1, kSwiU, kAwSmall>), grid, block, smem, s,
+                         KRQ_GEMV_ARGS, nfull);
+    else if (awc == kAwLarge)
+      hipLaunchKernelGGL((k_gemv_fp8_swiglu_mixed<KRQ_W_TILED, XK, 1, kSwiU, kAwLarge>), grid, block, smem, s,
+                         KRQ_GEMV_ARGS, nfull);
+    else
+      return false;
+  }
+  return true;
+}
+
 // Activation-wave chunks per lane holding `span` bf16 elements (0: too long for one wave).
 int aw_chunks(int64_t span) {
   return span <= 512 * kAwRow ? kAwRow : span <= 512 * kAwSmall ? kAwSmall : span <= 512 * kAwLarge ? kAwLarge : 0;
@@ -282,6 +312,26 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) + slice;
   const dim3 grid(static_cast<unsigned>(NO / 16 / pb), static_cast<unsigned>(split));
   const int nthreads = (nw + na) * 64;
+  // A SwiGLU grid of column blocks a little over a multiple of the CUs (gate_up: 608 = 2 x 256 +
+  // 96) runs its last ones as half-pair blocks in the same launch, so no CU streams a third full
+  // block (same steps per wave, so the same output bits).
+  if (mode == KRQ_OUT_SWIGLU && algo == 1 && w_layout == KRQ_W_TILED) {
+    const int64_t nrbs = NO / 16, rem = nrbs % kCUs;
+    if (nrbs > 2 * kCUs && rem != 0 && 2 * rem <= kCUs) {
+      const int nfull = static_cast<int>(nrbs - rem);
+      const dim3 gm(static_cast<unsigned>(nfull + 2 * rem), 1);
+#define KRQ_MIXED(XKV)                                                                                         \
+  launch_swiglu_mixed<XKV>(awc, u, rows, m, nfull, gm, nthreads, smem, s, xb, x_scale, x_inv, x_per_row, wb, \
+                           w_scale, w_per_row, m, NO, K, kts, out, aux)
+      bool ok = false;
+      if (x_kind == KRQ_X_FP8) ok = KRQ_MIXED(KRQ_X_FP8);
+      else if (x_kind == KRQ_X_FP8_TILED) ok = KRQ_MIXED(KRQ_X_FP8_TILED);
+      else if (x_kind == KRQ_X_BF16_DYN) ok = KRQ_MIXED(KRQ_X_BF16_DYN);
+      else ok = KRQ_MIXED(KRQ_X_BF16_STATIC);
+#undef KRQ_MIXED
+      if (ok) return krq_check_launch("gemv_fp8");
+    }
+  }
 #define KRQ_FP8_CASE(MODE, LAYOUT)                                                                          \
   launch_xk<MODE, LAYOUT>(x_kind, algo, pb, awc, u, rows, m, grid, nthreads, smem, s, xb, x_scale, x_inv, \
                           x_per_row, wb, w_scale, w_per_row, m, NO, K, kts, out, aux)

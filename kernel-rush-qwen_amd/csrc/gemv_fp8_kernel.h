@@ -146,13 +146,14 @@ template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, int PB, bool NO
 KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restrict__ xsc,
                            const float* __restrict__ xinv, int x_per_row, const uint8_t* __restrict__ w8,
                            const float* __restrict__ wsc, int w_per_row, int M, int64_t NO, int64_t K,
-                           int kts, void* __restrict__ out, void* __restrict__ aux, const FusedArgs& fa) {
+                           int kts, void* __restrict__ out, void* __restrict__ aux, const FusedArgs& fa,
+                           int64_t bx) {
   // nw*P*MT*256 partial sums | e4m3 activation slice [M][ks] | (NORM) sum-of-squares [M][K/16]
   extern __shared__ float red[];
   __shared__ float xs_l[32], rstd_s[32];
   __shared__ uint32_t amax_w[kMaxThreads / 64];
   __shared__ uint32_t last_s;
-  static_assert(PB == 1 || (MODE != KRQ_OUT_SWIGLU && MODE != kOutResidual && ALGO != 2),
+  static_assert(PB == 1 || (MODE != KRQ_OUT_SWIGLU && MODE != kOutSwiGluHalf && MODE != kOutResidual && ALGO != 2),
                 "paired row blocks: MFMA, no SwiGLU or residual epilogue");
   static_assert(!NORM || (XK != KRQ_X_FP8 && XK != KRQ_X_FP8_TILED), "the RMSNorm prologue takes bf16 activations");
   constexpr bool AW = AWC > 0;
@@ -172,7 +173,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   // nw = the waves that stream weights (all but the activation wave)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x >> 6) - (AW ? 1 : 0);
   const int r = lane & 15, g = lane >> 4;
-  const int64_t rb = (int64_t)blockIdx.x * PB, rbu = MODE == KRQ_OUT_SWIGLU ? rb + (NO >> 4) : rb + 1;
+  const int64_t rb = bx * PB, rbu = MODE == KRQ_OUT_SWIGLU ? rb + (NO >> 4) : rb + 1;
   const int sidx = blockIdx.y;
   const int nsteps = (kts + 1) >> 1;
   const int64_t tbase = (int64_t)sidx * kts;
@@ -244,8 +245,13 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
     const int j = jcount > 0 ? wave + min(cc, jcount - 1) * nw : 0;
     const int64_t t0 = tbase + 2 * j;
     const int64_t t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
-    wl[u] = ld16nt(w_addr<LAYOUT>(w8, rb, t0, K, lane));
-    wh[u] = ld16nt(w_addr<LAYOUT>(w8, rb, t1, K, lane));
+    if constexpr (MODE == kOutSwiGluHalf) {
+      wl[u] = ld16nt(w_addr_hp<LAYOUT>(w8, rb, NO, t0, K, lane));
+      wh[u] = ld16nt(w_addr_hp<LAYOUT>(w8, rb, NO, t1, K, lane));
+    } else {
+      wl[u] = ld16nt(w_addr<LAYOUT>(w8, rb, t0, K, lane));
+      wh[u] = ld16nt(w_addr<LAYOUT>(w8, rb, t1, K, lane));
+    }
     if (P == 2) {
       ul[u] = ld16nt(w_addr<LAYOUT>(w8, rbu, t0, K, lane));
       uh[u] = ld16nt(w_addr<LAYOUT>(w8, rbu, t1, K, lane));
@@ -451,14 +457,31 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
 template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, int PB, int AWC>
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(KRQ_FP8_KERNEL_PARAMS) {
   gemv_fp8_body<MT, MODE, LAYOUT, XK, ALGO, U, PB, false, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M, NO,
-                                                               K, kts, out, aux, FusedArgs{});
+                                                               K, kts, out, aux, FusedArgs{}, blockIdx.x);
+}
+
+// The SwiGLU launch with its last column blocks split in half: workgroups below nfull are the
+// two-matrix blocks of output columns 16 i .. 16 i + 15; workgroup nfull + j is half-pair block
+// 2 nfull + j (columns 8 (2 nfull + j) ..), which streams half the bytes with the same steps per
+// wave. Workgroup i runs on compute unit i mod 256, so nfull = 512 puts two full blocks on every CU
+// and at most one half block more, instead of a third full block on some CUs.
+template <int LAYOUT, int XK, int ALGO, int U, int AWC>
+__global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8_swiglu_mixed(KRQ_FP8_KERNEL_PARAMS, int nfull) {
+  if (static_cast<int>(blockIdx.x) < nfull)
+    gemv_fp8_body<1, KRQ_OUT_SWIGLU, LAYOUT, XK, ALGO, U, 1, false, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row,
+                                                                         M, NO, K, kts, out, aux, FusedArgs{},
+                                                                         blockIdx.x);
+  else
+    gemv_fp8_body<1, kOutSwiGluHalf, LAYOUT, XK, ALGO, U, 1, false, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row,
+                                                                         M, NO, K, kts, out, aux, FusedArgs{},
+                                                                         (int64_t)blockIdx.x + nfull);
 }
 
 // the fused kernel (fused_fp8.hip): RMSNorm prologue and / or residual epilogue
 template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, bool NORM, int AWC>
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8_fused(KRQ_FP8_KERNEL_PARAMS, FusedArgs fa) {
   gemv_fp8_body<MT, MODE, LAYOUT, XK, ALGO, U, 1, NORM, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M, NO,
-                                                             K, kts, out, aux, fa);
+                                                             K, kts, out, aux, fa, blockIdx.x);
 }
 
 }  // namespace
