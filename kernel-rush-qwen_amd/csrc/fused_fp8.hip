@@ -121,6 +121,17 @@ void launch(int M, int awc, int u, dim3 grid, int nw, size_t smem, hipStream_t s
     constexpr int DU = MODE == KRQ_OUT_SWIGLU ? kSwiU : kDeepU, MU = MODE == KRQ_OUT_SWIGLU ? kSwiU : kMidU;
     if constexpr (XK == KRQ_X_BF16_DYN || XK == KRQ_X_BF16_STATIC) {
       if (u > 0 && awc == kAwSmall) {
+        // the SwiGLU's last column blocks as half-pair blocks, as the plain launch runs them
+        const int64_t nrbs = NO / 16, rem = nrbs % kCUs;
+        if constexpr (MODE == KRQ_OUT_SWIGLU) {
+          if (u == MU && grid.y == 1 && nrbs > 2 * kCUs && rem != 0 && 2 * rem <= kCUs) {
+            const int nfull = static_cast<int>(nrbs - rem);
+            const dim3 gm(static_cast<unsigned>(nfull + 2 * rem), 1);
+            hipLaunchKernelGGL((k_gemv_fp8_fused_swiglu_mixed<LAYOUT, XK, MU, NORM, kAwSmall>), gm, block, smem, s,
+                               KRQ_FUSED_FP8_ARGS, nfull);
+            return;
+          }
+        }
         if (u == MU)
           hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, MU, NORM, kAwSmall>), grid, block, smem, s,
                              KRQ_FUSED_FP8_ARGS);

@@ -169,7 +169,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   // (one bare barrier) took the M = 1 QKV + RMSNorm launch from 6.58 to 5.22 us; the plain one-row
   // kernels (row loads only: QKV 4.71 -> 5.01 us) and the two-round SwiGLU block (gate_up +
   // RMSNorm 10.5 -> 10.75 us) measured slower with it, so they keep issuing at once.
-  constexpr bool ORDER = AWC > 0 && NORM && MODE != KRQ_OUT_SWIGLU;
+  constexpr bool ORDER = AWC > 0 && NORM && MODE != KRQ_OUT_SWIGLU && MODE != kOutSwiGluHalf;
   // nw = the waves that stream weights (all but the activation wave)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x >> 6) - (AW ? 1 : 0);
   const int r = lane & 15, g = lane >> 4;
@@ -482,6 +482,20 @@ template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, bool NORM, int 
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8_fused(KRQ_FP8_KERNEL_PARAMS, FusedArgs fa) {
   gemv_fp8_body<MT, MODE, LAYOUT, XK, ALGO, U, 1, NORM, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M, NO,
                                                              K, kts, out, aux, fa, blockIdx.x);
+}
+
+
+// The fused kernel's SwiGLU with its last column blocks split in half (as k_gemv_fp8_swiglu_mixed).
+template <int LAYOUT, int XK, int U, bool NORM, int AWC>
+__global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8_fused_swiglu_mixed(KRQ_FP8_KERNEL_PARAMS, FusedArgs fa,
+                                                                            int nfull) {
+  if (static_cast<int>(blockIdx.x) < nfull)
+    gemv_fp8_body<1, KRQ_OUT_SWIGLU, LAYOUT, XK, 1, U, 1, NORM, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M,
+                                                                     NO, K, kts, out, aux, fa, blockIdx.x);
+  else
+    gemv_fp8_body<1, kOutSwiGluHalf, LAYOUT, XK, 1, U, 1, NORM, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M,
+                                                                     NO, K, kts, out, aux, fa,
+                                                                     (int64_t)blockIdx.x + nfull);
 }
 
 }  // namespace
