@@ -14,11 +14,11 @@ namespace {
 
 // PB = 2 or 4: adjacent row blocks per block sharing the activation loads (as in gemv_fp8.hip;
 // 4 for the multi-row lm_head, where every 16-column block re-reads the bf16 rows from L2).
+// bx: the column block this workgroup owns (its two-matrix, paired or single row block, or with
+// MODE kOutSwiGluHalf its half-pair block).
 template <int MT, int MODE, int LAYOUT, int ALGO, int U, int PB>
-__global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x,
-                                                  const uint8_t* __restrict__ w, int M, int64_t NO,
-                                                  int64_t K, int kts, void* __restrict__ out,
-                                                  void* __restrict__ aux) {
+KRQ_DEV void gemv_bf16_body(const uint8_t* __restrict__ x, const uint8_t* __restrict__ w, int M, int64_t NO,
+                            int64_t K, int kts, void* __restrict__ out, void* __restrict__ aux, int64_t bx) {
   extern __shared__ float red[];
   __shared__ float ones[32];
   static_assert(PB == 1 || (MODE != KRQ_OUT_SWIGLU && ALGO != 2), "paired row blocks: MFMA, no SwiGLU");
@@ -27,7 +27,7 @@ __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x
   constexpr int NV = MT * 256;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int64_t rb = (int64_t)blockIdx.x * PB;
+  const int64_t rb = bx * PB;
   const int sidx = blockIdx.y;
   const int nsteps = (kts + 1) >> 1;
   const int64_t tbase = (int64_t)sidx * kts;
@@ -55,10 +55,15 @@ __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x
     const int j = jcount > 0 ? wave + min(cc, jcount - 1) * nw : 0;
     const int64_t t0 = tbase + 2 * j;
     const int64_t t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
+    if constexpr (MODE == kOutSwiGluHalf) {
+      wl[0][u] = ld16nt(w_addr_hp<LAYOUT>(w, rb, NO, t0, rowb, lane));
+      wh[0][u] = ld16nt(w_addr_hp<LAYOUT>(w, rb, NO, t1, rowb, lane));
+    } else {
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      wl[p][u] = ld16nt(w_addr<LAYOUT>(w, rbp(p), t0, rowb, lane));
-      wh[p][u] = ld16nt(w_addr<LAYOUT>(w, rbp(p), t1, rowb, lane));
+      for (int p = 0; p < P; ++p) {
+        wl[p][u] = ld16nt(w_addr<LAYOUT>(w, rbp(p), t0, rowb, lane));
+        wh[p][u] = ld16nt(w_addr<LAYOUT>(w, rbp(p), t1, rowb, lane));
+      }
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -127,6 +132,29 @@ __global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x
     for (int p = 0; p < PB; ++p)
       epilogue<MT, MODE, P>(red, p, nw, M, NO, rb + p, sidx, ones, ColScales{1.0f, 1.0f}, out, aux);
   }
+}
+
+template <int MT, int MODE, int LAYOUT, int ALGO, int U, int PB>
+__global__ __launch_bounds__(512) void k_gemv_bf16(const uint8_t* __restrict__ x,
+                                                  const uint8_t* __restrict__ w, int M, int64_t NO,
+                                                  int64_t K, int kts, void* __restrict__ out,
+                                                  void* __restrict__ aux) {
+  gemv_bf16_body<MT, MODE, LAYOUT, ALGO, U, PB>(x, w, M, NO, K, kts, out, aux, blockIdx.x);
+}
+
+// The SwiGLU with its last column blocks split in half, as k_gemv_fp8_swiglu_mixed: workgroups
+// below nfull are two-matrix blocks, workgroup nfull + j is half-pair block 2 nfull + j (the same
+// steps per wave, so the same output bits).
+template <int LAYOUT, int ALGO, int U>
+__global__ __launch_bounds__(512) void k_gemv_bf16_swiglu_mixed(const uint8_t* __restrict__ x,
+                                                               const uint8_t* __restrict__ w, int M, int64_t NO,
+                                                               int64_t K, int kts, void* __restrict__ out,
+                                                               void* __restrict__ aux, int nfull) {
+  if (static_cast<int>(blockIdx.x) < nfull)
+    gemv_bf16_body<1, KRQ_OUT_SWIGLU, LAYOUT, ALGO, U, 1>(x, w, M, NO, K, kts, out, aux, blockIdx.x);
+  else
+    gemv_bf16_body<1, kOutSwiGluHalf, LAYOUT, ALGO, U, 1>(x, w, M, NO, K, kts, out, aux,
+                                                          (int64_t)blockIdx.x + nfull);
 }
 
 // Persistent row partition (the reference's gemv_rows, engine/kernels/gemv.py:270-348): exactly
@@ -264,6 +292,36 @@ void launch_layout(int layout, int M, int pb, dim3 grid, int nw, size_t smem, hi
     launch<MODE, KRQ_W_ROWMAJOR>(M, pb, grid, nw, smem, s, x, w, m, NO, K, kts, out, aux);
 }
 
+constexpr int64_t kCUs = 256;  // compute units of the MI355X (workgroup b runs on CU b mod 256)
+
+// k_gemv_bf16_swiglu_mixed for M <= 16 when the SwiGLU's column blocks number a little over a
+// multiple of the CUs (gate_up: 608 = 2 x 256 + 96), with the variant launch() would pick; false
+// otherwise.
+bool launch_swiglu_mixed(int layout, int M, int64_t NO, int nw, size_t smem, hipStream_t s, const uint8_t* x,
+                         const uint8_t* w, int64_t K, int kts, void* out) {
+  const int64_t nrbs = NO / 16, rem = nrbs % kCUs;
+  if (M > 16 || nrbs <= 2 * kCUs || rem == 0 || 2 * rem > kCUs) return false;
+  const int nfull = static_cast<int>(nrbs - rem);
+  const dim3 grid(static_cast<unsigned>(nfull + 2 * rem), 1), block(nw * 64);
+#define KRQ_BF16_MIXED(LAYOUT)                                                                                   \
+  if (M == 1)                                                                                                    \
+    hipLaunchKernelGGL((k_gemv_bf16_swiglu_mixed<LAYOUT, 2, 4>), grid, block, smem, s, x, w, M, NO, K, kts, out, \
+                       nullptr, nfull);                                                                          \
+  else if (M <= 4)                                                                                               \
+    hipLaunchKernelGGL((k_gemv_bf16_swiglu_mixed<LAYOUT, 1, 4>), grid, block, smem, s, x, w, M, NO, K, kts, out, \
+                       nullptr, nfull);                                                                          \
+  else                                                                                                           \
+    hipLaunchKernelGGL((k_gemv_bf16_swiglu_mixed<LAYOUT, 1, 2>), grid, block, smem, s, x, w, M, NO, K, kts, out, \
+                       nullptr, nfull);
+  if (layout == KRQ_W_TILED) {
+    KRQ_BF16_MIXED(KRQ_W_TILED)
+  } else {
+    KRQ_BF16_MIXED(KRQ_W_ROWMAJOR)
+  }
+#undef KRQ_BF16_MIXED
+  return true;
+}
+
 }  // namespace
 
 int krq::gemv_bf16_run(const void* x, const void* w, int w_layout, int64_t M, int64_t N, int64_t K,
@@ -301,6 +359,8 @@ int krq::gemv_bf16_run(const void* x, const void* w, int w_layout, int64_t M, in
   hipStream_t s = (hipStream_t)stream;
   if (mode == KRQ_OUT_BF16) launch_layout<KRQ_OUT_BF16>(w_layout, m, pb, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
   else if (mode == KRQ_OUT_PARTIAL) launch_layout<KRQ_OUT_PARTIAL>(w_layout, m, pb, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
+  else if (mode == KRQ_OUT_SWIGLU && launch_swiglu_mixed(w_layout, m, NO, nw, smem, s, xb, wb, K, kts, out))
+    ;  // the mixed launch below 17 rows on grids a little over a multiple of the CUs
   else if (mode == KRQ_OUT_SWIGLU) launch_layout<KRQ_OUT_SWIGLU>(w_layout, m, pb, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
   else launch_layout<kOutArgmax>(w_layout, m, pb, grid, nw, smem, s, xb, wb, m, NO, K, kts, out, aux);
   return krq_check_launch("gemv_bf16");
