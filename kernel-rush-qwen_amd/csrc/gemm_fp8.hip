@@ -418,14 +418,17 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
   if (p < 0) return;
   set_tile(p);
   tile_loads(0);
+  bool ragged = false;  // the previous tile had rows past M
   for (int k = 0;; ++k) {
     // The second pair goes into buffer 1 once every wave is done with the previous epilogue's
-    // staging. In flight, oldest first: the scales and the first pair, the previous tile's kStores
-    // stores (k > 0), the second pair.
+    // staging. In flight, oldest first: the scales and the first pair, the previous tile's stores
+    // (k > 0), the second pair. A tile whose rows all lie below M issued exactly kStores stores per
+    // lane; one with rows past M may have issued fewer (a wave whose chunk rows are all past M
+    // branches around its store), so after such a tile the wait counts only the second pair.
     lds_barrier();
 #pragma unroll
     for (int q = 0; q < kVm; ++q) pair_load(q, 1, 1);
-    if (k == 0) wait_vm<kVm>();
+    if (k == 0 || ragged) wait_vm<kVm>();
     else wait_vm<kVm + kStores>();
     lds_barrier();
 #pragma unroll
@@ -457,6 +460,7 @@ __global__ __launch_bounds__(kThreads, OCC) void k_gemm_ring(const uint8_t* __re
     }
     body(odd{}, no{}, no{}, nk - 1, 0, 0);
     epilogue(cm0, cn0, csp, scl[k & 1]);
+    ragged = cm0 + BM > M;
     if (next < 0) break;
   }
   wait_vm<0>();  // no load into LDS outlives the block

@@ -57,6 +57,31 @@ def test_gemm_fp8_matches_oracle(dev, M, N, K, per_row):
     assert e <= TOL
 
 
+@pytest.mark.parametrize("M,N,K,pad", [(4000, 19456, 2560, 4096),   # 256 x 256, ~5 tiles per block
+                                       (3900, 19456, 2560, 4096),
+                                       (2000, 19456, 2560, 2048),   # 256 x 256 rounds + 128 x 128 tail
+                                       (3000, 6144, 2560, 3072)])   # 192 x 256, a second tile after a ragged one
+def test_gemm_ragged_multi_tile(dev, M, N, K, pad):
+    """More ring tiles than blocks with M not a multiple of the tile height (gate_up and QKV
+    shapes), so blocks run tiles after one with rows past M: within the bar of the oracle on a
+    sample of rows (the last 256, which hold the ragged row tile, and every 61st row), and bit for
+    bit the rows of a run on M padded to a whole number of tiles (the same tile plan, no ragged
+    tile; each output is the same sum of the same products in the same order)."""
+    w = bf((N, K), 51, 0.02).to(dev)
+    q = F.quantize(w)
+    x = bf((pad, K), 52).to(dev)
+    x8p, xsp = F.quant_rows(x)
+    x8, xs = x8p[:M].contiguous(), xsp[:M].contiguous()
+    y = F.gemm_fp8(x8, q, xs=xs)
+    y_pad = F.gemm_fp8(x8p, q, xs=xsp)
+    assert torch.equal(y, y_pad[:M])
+    rows = np.unique(np.concatenate([np.arange(0, M, 61), np.arange(M - 256, M)]))
+    _, ref = O.fp8_matmul(codes(x8)[rows], xs.cpu().numpy().reshape(-1)[rows], codes(q[0]), q[1].cpu().numpy())
+    e = rel_err(y.float().cpu().numpy()[rows], ref)
+    print(f"gemm ragged M={M} N={N} K={K}: max-rel {e:.2e} on {rows.size} rows")
+    assert e <= TOL
+
+
 @pytest.mark.parametrize("M,N,K,splits", [(256, 2560, 9728, 4), (200, 2560, 9728, 4), (300, 2560, 8192, 4),
                                           (130, 4096, 8192, 4), (1024, 2560, 9728, 2),
                                           # 64 x 64 tiles split (too few 128 x 128 ones to split)
