@@ -376,6 +376,45 @@ def measured_traffic(cfg, name):
         return None, None
 
 
+def kernel_template(name):
+    """A rocprofv3 kernel name without its argument list and namespaces: 'k_gemv_fp8<1, 3, ...>'."""
+    name = name.replace("void ", "").replace("(anonymous namespace)::", "")
+    return name[:name.index("(")] if "(" in name else name
+
+
+def summarize_trace(csv_path):
+    """Per-kernel durations of a rocprofv3 --kernel-trace CSV (End - Start per dispatch, us).
+    'b2b' counts only dispatches whose neighbours in time are the same kernel: the launches of
+    the kernel table's graphs (72 back-to-back launches of one kernel), which are what roofline_of
+    times with hipEvents. In such a run each dispatch starts when the previous one ends, so its
+    traced duration is its share of the run, launch overhead included, like the hipEvents figure.
+    'all' counts every dispatch, including those of the mixed step graphs, where the profiler's
+    per-dispatch work sits between kernels and stretches the traced spans."""
+    import csv
+    rows = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), kernel_template(r["Kernel_Name"]))
+                  for r in csv.DictReader(open(csv_path)))
+    out = {}
+    for i, (s, e, k) in enumerate(rows):
+        d = out.setdefault(k, {"all": [], "b2b": []})
+        d["all"].append((e - s) / 1000.0)
+        if 0 < i < len(rows) - 1 and rows[i - 1][2] == k and rows[i + 1][2] == k:
+            d["b2b"].append((e - s) / 1000.0)
+
+    def stats(v):
+        return {"n": len(v), "avg_us": round(sum(v) / len(v), 3), "median_us": round(median(sorted(v)), 3)} if v else None
+    return {k: {"all": stats(d["all"]), "b2b": stats(d["b2b"])} for k, d in out.items() if k.startswith("k_")}
+
+
+def traced_us(kernel):
+    """Average traced duration (us) of `kernel` over its back-to-back dispatches, from the committed
+    kernel-trace summary profiles/gemv_fp8_decode_trace.json (bench.py --summarize-trace), or None."""
+    try:
+        k = json.load(open(os.path.join(ROOT, "profiles", "gemv_fp8_decode_trace.json")))["kernels"][kernel]
+        return k["b2b"]["avg_us"]
+    except (OSError, KeyError, ValueError, TypeError):
+        return None
+
+
 def timed_graph(torch, step, steps, warmup, replays):
     """W untimed eager steps, then K steps captured into one graph, replayed once untimed and then
     `replays` times, each replay timed with hipEvents between synchronizations.
@@ -427,11 +466,16 @@ def roofline_of(rows, M, L, layout, cfg):
     dom = max((r for r in rows if r["name"] in ("qkv", "o", "gate_up", "down")), key=lambda r: r["us_med"])
     traffic, kernel = measured_traffic(cfg, dom["name"]) if layout == "tiled" else (None, None)
     a = dom["bytes"] / dom["us_med"] / 1e3
+    tr = traced_us(kernel) if kernel else None
     return {"bound": "hbm", "achieved": round(a, 1), "peak": 8000.0, "unit": "GB/s",
             "frac": round(a / 8000.0, 4), "traffic": traffic,
             "kernel": f"gemv_fp8 {dom['name']} [{dom['N']}x{dom['K']}] M={M}" + (f" ({kernel})" if kernel else ""),
             "bytes_per_launch": dom["bytes"], "us_per_launch": round(dom["us_med"], 3),
-            "us_per_launch_min": round(dom["us_min"], 3)}
+            "us_per_launch_min": round(dom["us_min"], 3),
+            # headline: hipEvents median of this run; beside it the committed kernel trace's average
+            # over the same back-to-back launches (profiles/gemv_fp8_decode_trace.json)
+            "us_per_launch_trace": tr,
+            "frac_trace": round(dom["bytes"] / tr / 1e3 / 8000.0, 4) if tr else None}
 
 
 def per_m_summary(M, ts, steps, step_bytes, rows, roof):
@@ -468,7 +512,16 @@ def main():
     ap.add_argument("--no-table", action="store_true", help="skip the per-kernel tables (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 256 MiB device copy (known bytes) to scale HBM counters")
+    ap.add_argument("--summarize-trace", metavar="CSV", default=None,
+                    help="no GPU work: print the per-kernel duration summary of a rocprofv3 kernel-trace CSV "
+                    "(this build's kernels; the JSON of profiles/gemv_fp8_decode_trace.json) and exit")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(json.dumps({"source": "rocprofv3 --kernel-trace --stats --output-format csv -d <out> -o kt -- "
+                          "python3 bench.py --no-cpu --no-prefill; then python3 bench.py --summarize-trace "
+                          "<out>/kt_kernel_trace.csv", "kernels": summarize_trace(args.summarize_trace)},
+                         indent=1, sort_keys=True))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the path runs on one GPU; sharding across "
               "GPUs is a design note, not an implementation); run with --gpus 1", file=sys.stderr)
