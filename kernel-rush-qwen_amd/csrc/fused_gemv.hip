@@ -37,7 +37,7 @@ __global__ __launch_bounds__(kMaxNT) void k_gemv_fused(const uint8_t* __restrict
                                                        const uint8_t* __restrict__ w, int M, int64_t NO,
                                                        int64_t K, int kts, void* __restrict__ out,
                                                        FusedArgs fa) {
-  extern __shared__ float red[];  // nw*P*MT*256 floats | (NORM) x slice bf16 [M][ks], ss [M][T]
+  extern __shared__ __align__(16) float red[];  // nw*P*MT*256 floats | (NORM) x slice bf16 [M][ks], ss [M][T]
   __shared__ float rstd_s[32], ones[32];
   __shared__ uint32_t last_s;
   constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : 1;

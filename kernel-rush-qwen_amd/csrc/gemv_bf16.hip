@@ -19,7 +19,7 @@ namespace {
 template <int MT, int MODE, int LAYOUT, int ALGO, int U, int PB>
 KRQ_DEV void gemv_bf16_body(const uint8_t* __restrict__ x, const uint8_t* __restrict__ w, int M, int64_t NO,
                             int64_t K, int kts, void* __restrict__ out, void* __restrict__ aux, int64_t bx) {
-  extern __shared__ float red[];
+  extern __shared__ __align__(16) float red[];
   __shared__ float ones[32];
   static_assert(PB == 1 || (MODE != KRQ_OUT_SWIGLU && ALGO != 2), "paired row blocks: MFMA, no SwiGLU");
   static_assert(PB == 1 || PB == 2 || PB == 4, "one, two or four row blocks per block");
