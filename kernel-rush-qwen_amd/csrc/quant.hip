@@ -286,28 +286,18 @@ __global__ __launch_bounds__(kQT) void k_act_rows_vec(const uint16_t* __restrict
   }
 }
 
-// quant_rows / quant_rows_tiled (K % 16 == 0): 16 values per thread piece (two 16-byte loads, one
-// 16-byte store), the row amax as DPP wave maxima and one barrier, 512 threads. Measured on MI355X
+// quant_rows (K % 16 == 0): 16 values per thread piece (two 16-byte loads, one 16-byte store), the
+// row amax as DPP wave maxima and one barrier, 512 threads, one block per row. Measured on MI355X
 // (graph of 72 launches, M = 16; K = 2,560 / 4,096 / 9,728): 2.47 / 2.54 / 3.11 us against 2.87 /
 // 2.90 / 3.64 for k_act_rows_vec (256 threads, 8-value pieces, shuffle reductions, two barriers);
-// 256 and 1,024 threads measured slower. TILED: x8 in the tiled activation layout (tiled_offset,
-// the weights' tiling), one block per row of the M rows padded to a multiple of 16, the pad rows
-// written as zeros.
+// 256 and 1,024 threads measured slower.
 constexpr int kRowNT = 512;
-template <int NT, bool TILED>
+template <int NT>
 __global__ __launch_bounds__(NT) void k_act_rows_fast(const uint16_t* __restrict__ x, int64_t M, int64_t K,
                                                       float* __restrict__ scale, uint8_t* __restrict__ x8) {
   constexpr int C = static_cast<int>(kVecMaxK / 16 / NT);
   __shared__ uint32_t red[NT / 64];
   const int64_t r = blockIdx.x;
-  if (TILED && r >= M) {
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-      const int64_t e = 16 * (int64_t)(threadIdx.x + c * NT);
-      if (e < K) *reinterpret_cast<uint4*>(x8 + tiled_offset(r, e, K)) = zero4();
-    }
-    return;
-  }
   const uint8_t* row = reinterpret_cast<const uint8_t*>(x + r * K);
   uint4 v[C][2];
   uint32_t mb = 0;
@@ -332,13 +322,61 @@ __global__ __launch_bounds__(NT) void k_act_rows_fast(const uint16_t* __restrict
     const int64_t e = 16 * (int64_t)(threadIdx.x + c * NT);
     if (e < K) {
       const uint2 lo = quant8(v[c][0], iv), hi = quant8(v[c][1], iv);
-      *reinterpret_cast<uint4*>(x8 + (TILED ? tiled_offset(r, e, K) : r * K + e)) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      *reinterpret_cast<uint4*>(x8 + r * K + e) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    }
+  }
+}
+
+// quant_rows_tiled by single-wave workgroups: workgroup (s, r) reads row r whole (16-element pieces
+// p = lane + 64 c, two 16-byte loads each, every load in flight; lanes past the row repeat its last
+// piece), takes the row's amax with DPP steps (no LDS, no barrier), and quantizes and writes only
+// its pieces c in [s sp, (s + 1) sp) into the tiled layout; pad rows r >= M get zeros. The same
+// arithmetic as k_act_rows_fast (quant_rows: the row's fp32 magnitude bits, the ActScale inverse,
+// the hardware convert), so the same bytes and scales, permuted. Single-wave workgroups with one
+// piece per lane each (ch workgroups per row) measured fastest at M = 16, K = 2,560 / 4,096 /
+// 9,728 (graph of 72 launches): 2.36 / 2.39 / 2.87 us, against 2.47 / 2.54 / 3.09 for one
+// 512-thread block per row (the row-major kernel above with a tiled store), 2.65 / 2.80 / 3.28
+// with two pieces per lane and 3.21 / 3.69 / 6.60 with one workgroup per row.
+template <int CH>
+__global__ __launch_bounds__(64) void k_act_rows_wave(const uint16_t* __restrict__ x, int64_t M, int64_t K, int sp,
+                                                      float* __restrict__ scale, uint8_t* __restrict__ x8) {
+  const int lane = threadIdx.x, s = blockIdx.x;
+  const int64_t r = blockIdx.y;
+  const int np = static_cast<int>(K >> 4), c0 = s * sp;
+  if (r >= M) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int p = lane + 64 * c;
+      if (c >= c0 && c < c0 + sp && p < np) *reinterpret_cast<uint4*>(x8 + tiled_offset(r, 16 * (int64_t)p, K)) = zero4();
+    }
+    return;
+  }
+  const uint8_t* row = reinterpret_cast<const uint8_t*>(x + r * K);
+  uint4 v[CH][2];
+  uint32_t mb = 0;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int p = min(lane + 64 * c, np - 1);
+    v[c][0] = ld16(row + 32 * (int64_t)p);
+    v[c][1] = ld16(row + 32 * (int64_t)p + 16);
+  }
+#pragma unroll
+  for (int c = 0; c < CH; ++c) mb = absmax8(v[c][1], absmax8(v[c][0], mb));
+  const float a = clamp_min_nan(as_f32(wave_max_u32_dpp(mb)), 1e-6f);
+  const float iv = inv_from_amax(a);
+  if (s == 0 && lane == 0) scale[r] = scale_from_amax(a);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int p = lane + 64 * c;
+    if (c >= c0 && c < c0 + sp && p < np) {
+      const uint2 lo = quant8(v[c][0], iv), hi = quant8(v[c][1], iv);
+      *reinterpret_cast<uint4*>(x8 + tiled_offset(r, 16 * (int64_t)p, K)) = make_uint4(lo.x, lo.y, hi.x, hi.y);
     }
   }
 }
 
 // the cast with a given inverse (krq_cast_fp8's bytes) into the tiled activation layout of
-// k_act_rows_fast<NT, true>: one block per row of the M rows padded to a multiple of 16, 16 values
+// quant_rows_tiled: one block per row of the M rows padded to a multiple of 16, 16 values
 // per thread piece, the pad rows written as zeros
 template <int NT>
 __global__ __launch_bounds__(NT) void k_cast_rows_tiled(const uint16_t* __restrict__ x, int64_t M, int64_t K,
@@ -531,7 +569,7 @@ extern "C" int krq_quant_rows(const void* x_bf16, int64_t M, int64_t K, void* x8
   KRQ_REQUIRE(M > 0 && K > 0 && M <= 0x7fffffff, "quant_rows: bad shape M=%lld K=%lld",
               (long long)M, (long long)K);
   if (vec_ok(x_bf16, K, K) && aligned16(x8) && K % 16 == 0)
-    hipLaunchKernelGGL((k_act_rows_fast<kRowNT, false>), dim3(static_cast<unsigned>(M)), dim3(kRowNT), 0,
+    hipLaunchKernelGGL((k_act_rows_fast<kRowNT>), dim3(static_cast<unsigned>(M)), dim3(kRowNT), 0,
                        (hipStream_t)stream, (const uint16_t*)x_bf16, M, K, xs, (uint8_t*)x8);
   else if (vec_ok(x_bf16, K, K) && aligned16(x8))
     hipLaunchKernelGGL(k_act_rows_vec, dim3(static_cast<unsigned>(M)), dim3(kQT), 0, (hipStream_t)stream,
@@ -550,8 +588,18 @@ extern "C" int krq_quant_rows_tiled(const void* x_bf16, int64_t M, int64_t K, vo
   KRQ_REQUIRE(vec_ok(x_bf16, K, K) && aligned16(x8_tiled),
               "quant_rows_tiled: x and x8_tiled must be 16-byte aligned and K at most %lld", (long long)kVecMaxK);
   const int64_t mp = (M + 15) / 16 * 16;  // rows padded to whole 16-row tiles
-  hipLaunchKernelGGL((k_act_rows_fast<kRowNT, true>), dim3(static_cast<unsigned>(mp)), dim3(kRowNT), 0,
-                     (hipStream_t)stream, (const uint16_t*)x_bf16, M, K, xs, (uint8_t*)x8_tiled);
+  const int np = static_cast<int>(K / 16), ch = (np + 63) / 64;  // pieces per lane of a whole row (<= 16)
+  const int sp = 1;                                               // pieces each workgroup stores per lane
+  const dim3 grid(static_cast<unsigned>((ch + sp - 1) / sp), static_cast<unsigned>(mp));
+#define KRQ_ROWS_WAVE(CH)                                                                                         \
+  hipLaunchKernelGGL((k_act_rows_wave<CH>), grid, dim3(64), 0, (hipStream_t)stream, (const uint16_t*)x_bf16, M, K, \
+                     sp, xs, (uint8_t*)x8_tiled)
+  if (ch <= 3) KRQ_ROWS_WAVE(3);
+  else if (ch <= 4) KRQ_ROWS_WAVE(4);
+  else if (ch <= 8) KRQ_ROWS_WAVE(8);
+  else if (ch <= 10) KRQ_ROWS_WAVE(10);
+  else KRQ_ROWS_WAVE(16);
+#undef KRQ_ROWS_WAVE
   return krq_check_launch("quant_rows_tiled");
 }
 
