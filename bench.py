@@ -262,7 +262,7 @@ def graph_time(torch, fn, reps, iters=5):
     return ts[0], ts[len(ts) // 2]
 
 
-def kernel_table(torch, fp8, L, layers, xs, M, reps):
+def kernel_table(torch, fp8, L, layers, xs, M, reps, compare=True):
     """Each kernel of the step alone, back-to-back launches cycling layers (hipEvents around a
     graph replay), each projection the way the step runs it: at M = 1 the GEMV scales its bf16 row
     per token itself (one kernel per projection); at M > 1 quant_rows_tiled runs first and the GEMV
@@ -298,7 +298,7 @@ def kernel_table(torch, fp8, L, layers, xs, M, reps):
             add(name, N, K, split, mode, bf16_fn(x, name, split, m, L.ALGO_AUTO), 2 * M * K)
         else:
             add(name, N, K, split, mode, tiled_fn(x, name, split, m), M * K)
-    for name, N, K, split, mode in PROJ:
+    for name, N, K, split, mode in PROJ if compare else ():
         x, m = xs[name], modes[mode]
         if M == 1:
             add(name + "/valu", N, K, split, mode, bf16_fn(x, name, split, m, L.ALGO_VALU), 2 * M * K)
@@ -492,6 +492,79 @@ def per_m_summary(M, ts, steps, step_bytes, rows, roof):
             "roofline": roof}
 
 
+# BASELINE's stated fractions of 8 TB/s per config (C2 / C4 at M = 1: 80%, C3 / C4 at M = 16: 70%)
+TARGET = {1: 0.80, 16: 0.70}
+
+
+def lmhead_summary(torch, fp8, lmhead, G, dev, Ms=(1, 16)):
+    """C4: the tied lm_head [V x H] GEMV fused with greedy argmax, BF16 and per-channel FP8
+    weights, at each M (graph of 8 launches, min and median of 5 replays)."""
+    g = torch.Generator(device=dev).manual_seed(7)
+    E = (torch.randn(V, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    q8 = fp8.quantize(E)
+    G.pack(E)
+    out = {}
+    for M in Ms:
+        h = torch.randn(M, H, generator=torch.Generator().manual_seed(100 + M)).to(torch.bfloat16).to(dev)
+        for kind, w in (("bf16", E), ("fp8", q8)):
+            tmin, tmed = graph_time(torch, lambda i: lmhead.lm_head_argmax(h, w), 8)
+            b = lm_bytes(M, kind)
+            pct = 100 * b / (tmed * 1e-6) / HBM_PEAK
+            out[f"{kind}_m{M}"] = {"us_med": round(tmed, 2), "us_min": round(tmin, 2), "bytes": b,
+                                   "gbs": round(b / tmed / 1e3, 1), "pct_of_hbm_peak": round(pct, 2),
+                                   "target_pct": round(100 * TARGET.get(M, 0.70), 1)}
+            log(f"[bench] C4 lm_head {kind} M={M}: {tmed:.2f} us (min {tmin:.2f}), {b / tmed / 1e3:.0f} GB/s, "
+                f"{pct:.1f}% of 8 TB/s")
+    return out, E
+
+
+def c5_summary(torch, lmhead, layer_step, layer_bytes, E, dev, Ms=(1, 16)):
+    """C5: the full decode-step weight stream, 36 layers x (QKV, O, gate_up, down) FP8 + the BF16
+    lm_head with argmax, one hipGraph of 5 steps, min and median of 5 replays, at each M."""
+    out = {}
+    for M in Ms:
+        h = torch.randn(M, H, generator=torch.Generator().manual_seed(100 + M)).to(torch.bfloat16).to(dev)
+        layer = layer_step(M)
+
+        def step(i):
+            for li in range(LAYERS):
+                layer(li)
+            lmhead.lm_head_argmax(h, E)
+        b = LAYERS * layer_bytes(M) + lm_bytes(M, "bf16")
+        ts = timed_graph(torch, step, 5, 1, 5)
+        tmed, tmin = median(ts) / 5, ts[0] / 5
+        pct = 100 * b / (tmed * 1e-3) / HBM_PEAK
+        out[str(M)] = {"ms_per_step": round(tmed, 4), "ms_per_step_min": round(tmin, 4), "bytes_per_step": b,
+                       "gbs": round(b / (tmed * 1e-3) / 1e9, 1), "pct_of_hbm_peak": round(pct, 2)}
+        log(f"[bench] C5 full step M={M}: {tmed * 1e3:.1f} us (min {tmin * 1e3:.1f}), "
+            f"{b / (tmed * 1e-3) / 1e9:.0f} GB/s, {pct:.1f}% of 8 TB/s")
+    return out
+
+
+def m32_summary(torch, fp8, L, layers, layer_step, layer_bytes, dev, reps):
+    """C3's second size, M = 32 (16 x 2 tree-verify rows): the step (quant_rows_tiled + GEMV per
+    projection, cycling the layers) and each projection's GEMV beside hipBLASLt (torch._scaled_mm)
+    on the same shape."""
+    M = 32
+    xs = make_inputs(torch, dev, M)
+    ts = timed_graph(torch, layer_step(M, xs={M: xs}), 72, 2, 5)
+    tmed = median(ts) / 72 * 1e3
+    rows = kernel_table(torch, fp8, L, layers, xs, M, reps, compare=False)
+    lib = prefill_times(torch, fp8, M, lin=False)
+    proj = {}
+    for r in rows:
+        if r["name"] in lib:
+            proj[r["name"]] = {"gemv_us": round(r["us_med"], 3), "hipblaslt_us": round(lib[r["name"]][1], 3),
+                               "ratio": round(r["us_med"] / lib[r["name"]][1], 3)}
+        elif r["name"].startswith("quant"):
+            proj[r["name"]] = {"us": round(r["us_med"], 3)}
+    b = layer_bytes(M)
+    log(f"[bench] M=32 step {tmed:.2f} us, {b / tmed / 1e3:.0f} GB/s; GEMV / hipBLASLt per projection: "
+        + ", ".join(f"{k} {v['gemv_us']:.2f}/{v['hipblaslt_us']:.2f}" for k, v in proj.items() if "gemv_us" in v))
+    return {"us_per_step": round(tmed, 3), "bytes_per_step": b, "gbs": round(b / tmed / 1e3, 1),
+            "pct_of_hbm_peak": round(100 * b / (tmed * 1e-6) / HBM_PEAK, 2), "projections": proj}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -510,6 +583,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill GEMM summary of the default line")
     ap.add_argument("--no-table", action="store_true", help="skip the per-kernel tables (profiling runs)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the C4 / C5 / M = 32 summaries of the default line (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 256 MiB device copy (known bytes) to scale HBM counters")
     ap.add_argument("--summarize-trace", metavar="CSV", default=None,
@@ -567,7 +642,7 @@ def main():
     def layer_bytes(M):
         return sum(proj_bytes(M, N, K, split, mode) for _, N, K, split, mode in PROJ)
 
-    def layer_step(M, offset=0):
+    def layer_step(M, offset=0, xs=xs):
         def step(i):
             Lw = layers[(i + offset) % LAYERS]
             for name, N, K, split, mode in PROJ:
@@ -696,6 +771,13 @@ def main():
             pre["ratio"].append(round(ours / lib, 3))
         log(f"[bench] prefill GEMM per layer, M={list(PREFILL_MS)}: {pre['layer_us']} us against hipBLASLt "
             f"{pre['hipblaslt_layer_us']} us")
+    extra = {}
+    if cfg == "decode" and not args.no_extra:
+        # BASELINE's other configs beside the headline: C4 (lm_head + argmax), C5 (full step), M = 32
+        extra["c4"], E_lm = lmhead_summary(torch, fp8, lmhead, G, dev)
+        extra["c5"] = c5_summary(torch, lmhead, layer_step, layer_bytes, E_lm, dev)
+        del E_lm
+        extra["c3m32"] = m32_summary(torch, fp8, L, layers, layer_step, layer_bytes, dev, args.reps)
 
     print(json.dumps({
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
@@ -706,7 +788,7 @@ def main():
                    "layout": args.layout, "pct_of_hbm_peak": round(100 * value / 8000.0, 2),
                    "replays": args.replays, "ms_per_step_min": round(t_min / steps, 5),
                    "value_best": round(step_bytes * steps / (t_min * 1e-3) / 1e9, 1)},
-        "per_m": per_m or None, "prefill": pre,
+        "per_m": per_m or None, "prefill": pre, **extra,
         "roofline": roofline, "cpu_baseline": cpu}), flush=True)
 
 

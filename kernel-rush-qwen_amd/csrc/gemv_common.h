@@ -119,15 +119,6 @@ KRQ_DEV const uint8_t* w_addr_hp(const uint8_t* w, int64_t b, int64_t NO, int64_
   return w + (rbx * 16 + rr) * row_bytes + t * 64 + (lane >> 4) * 16;
 }
 
-// The B-operand address of a half block (8 rows 8 hsel .. 8 hsel + 7 of row block rb): lane column
-// c reads row 8 hsel + c % 8 (the caller picks the tile t for c < 8 and c >= 8).
-template <int LAYOUT>
-KRQ_DEV const uint8_t* w_addr_half(const uint8_t* w, int64_t rb, int hsel, int64_t t, int64_t row_bytes, int lane) {
-  const int rr = 8 * hsel + (lane & 7);
-  if (LAYOUT == KRQ_W_TILED) return w + ((rb * (row_bytes >> 6) + t) * 64 + (lane & 48) + rr) * 16;
-  return w + (rb * 16 + rr) * row_bytes + t * 64 + (lane >> 4) * 16;
-}
-
 // Hardware fp32 -> OCP e4m3 pair conversion after the reference's clamp to +-448. Bit-identical to
 // f32_to_e4m3 (round to nearest even) on the clamped range; NaN stays NaN.
 KRQ_DEV float clamp448(float v) { return v != v ? v : fminf(fmaxf(v, -kFp8Max), kFp8Max); }

@@ -201,36 +201,6 @@ bool launch_swiglu_mixed(int awc, int u, bool rows, int M, int nfull, dim3 grid,
   return true;
 }
 
-// The one-row split-K launch as k_gemv_fp8_mixed (nfull full blocks, then half blocks) for the
-// kernels the plan picked: beside an activation wave with a deep ring (8, 10 or 20 slots; the half
-// blocks take half as many), or the e4m3 row with four-slot rings (two for the half blocks). False
-// for any other plan, which keeps the plain launch.
-template <int XK>
-bool launch_mixed(int awc, int u, int nfull, int nrb, dim3 grid, int nthreads, size_t smem, hipStream_t s,
-                  const uint8_t* xb, const float* x_scale, const float* x_inv, int x_per_row, const uint8_t* wb,
-                  const float* w_scale, int w_per_row, int m, int64_t NO, int64_t K, int kts, void* out, void* aux) {
-  const dim3 block(nthreads);
-#define KRQ_MIX(UF, AWC)                                                                                          hipLaunchKernelGGL((k_gemv_fp8_mixed<KRQ_OUT_PARTIAL, KRQ_W_TILED, XK, UF, (UF) / 2, AWC>), grid, block, smem, s,                      KRQ_GEMV_ARGS, nfull, nrb)
-  if constexpr (XK == KRQ_X_FP8 || XK == KRQ_X_FP8_TILED) {
-    if (awc != 0 || u != 4) return false;
-    KRQ_MIX(4, 0);
-  } else {
-#define KRQ_MIX_U(AWC)                    if (u == kMidU) KRQ_MIX(kMidU, AWC);     else if (u == kDeepU) KRQ_MIX(kDeepU, AWC);   else if (u == kBigU) KRQ_MIX(kBigU, AWC);     else return false;
-    if (awc == kAwRow) {
-      KRQ_MIX_U(kAwRow)
-    } else if (awc == kAwSmall) {
-      KRQ_MIX_U(kAwSmall)
-    } else if (awc == kAwLarge) {
-      KRQ_MIX_U(kAwLarge)
-    } else {
-      return false;
-    }
-#undef KRQ_MIX_U
-  }
-#undef KRQ_MIX
-  return true;
-}
-
 // Activation-wave chunks per lane holding `span` bf16 elements (0: too long for one wave).
 int aw_chunks(int64_t span) {
   return span <= 512 * kAwRow ? kAwRow : span <= 512 * kAwSmall ? kAwSmall : span <= 512 * kAwLarge ? kAwLarge : 0;
@@ -342,24 +312,6 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) + slice;
   const dim3 grid(static_cast<unsigned>(NO / 16 / pb), static_cast<unsigned>(split));
   const int nthreads = (nw + na) * 64;
-  // A one-row split-K grid of (row block, split) pairs a little over a multiple of the CUs (O and
-  // down at split 4: 640 = 2 x 256 + 128) runs its last pairs as half blocks in the same launch
-  // (k_gemv_fp8_mixed), so no CU streams a third full block.
-  if (mode == KRQ_OUT_PARTIAL && algo == 1 && M == 1 && !rows && pb == 1 && w_layout == KRQ_W_TILED) {
-    const int64_t rem = blocks % kCUs;
-    if (blocks > 2 * kCUs && rem != 0 && 2 * rem <= kCUs && blocks <= 0x7fffffff) {
-      const int nfull = static_cast<int>(blocks - rem);
-      const dim3 gm(static_cast<unsigned>(nfull + 2 * rem), 1);
-#define KRQ_MIXED(XKV)                                                                                           launch_mixed<XKV>(awc, u, nfull, static_cast<int>(NO / 16), gm, nthreads, smem, s, xb, x_scale, x_inv,                           x_per_row, wb, w_scale, w_per_row, m, NO, K, kts, out, aux)
-      bool ok = false;
-      if (x_kind == KRQ_X_FP8) ok = KRQ_MIXED(KRQ_X_FP8);
-      else if (x_kind == KRQ_X_FP8_TILED) ok = KRQ_MIXED(KRQ_X_FP8_TILED);
-      else if (x_kind == KRQ_X_BF16_DYN) ok = KRQ_MIXED(KRQ_X_BF16_DYN);
-      else ok = KRQ_MIXED(KRQ_X_BF16_STATIC);
-#undef KRQ_MIXED
-      if (ok) return krq_check_launch("gemv_fp8");
-    }
-  }
   // A SwiGLU grid of column blocks a little over a multiple of the CUs (gate_up: 608 = 2 x 256 +
   // 96) runs its last ones as half-pair blocks in the same launch, so no CU streams a third full
   // block (same steps per wave, so the same output bits).

@@ -142,27 +142,16 @@ KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restr
 // the weight steps, and every row block re-reads them).
 // AWC > 0 (one-row kind without RMSNorm): the block's last wave is the activation wave above and
 // the others stream weights; AWC = 0: every wave takes part in the activation prologue.
-// bx, sy: the block's row block and K split.
-// HALF (one row, single matrix, KRQ_OUT_BF16 / KRQ_OUT_PARTIAL): a half block, which owns the 8
-// output columns 16 bx + 8 hsel .. + 7 of split sy and streams their weights over both halves of
-// the split's K range at once. Its unit of work is a pair of steps (j, j + nh), nh = ceil(steps / 2):
-// matrix-core B column c < 8 holds weight row 8 hsel + c at step j, column c >= 8 the same row at
-// step j + nh; A row 0 holds the activation slice at step j, row 1 (every odd row) at step j + nh.
-// Then C[0][c] (c < 8) is the first half's sum and C[1][c + 8] the second half's, and the output is
-// their sum. Half the loads of a full block for half its bytes, so a launch can give every compute
-// unit the same work (k_gemv_fp8_mixed). The fp32 sums of the matrix-core step results are exact
-// here whatever their grouping (the one-row kernels with one and with two weight waves give the
-// same bits), so the half blocks' outputs equal the full blocks' bit for bit.
-template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, int PB, bool NORM, int AWC, bool HALF = false>
+template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, int PB, bool NORM, int AWC>
 KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restrict__ xsc,
                            const float* __restrict__ xinv, int x_per_row, const uint8_t* __restrict__ w8,
                            const float* __restrict__ wsc, int w_per_row, int M, int64_t NO, int64_t K,
                            int kts, void* __restrict__ out, void* __restrict__ aux, const FusedArgs& fa,
-                           int64_t bx, int sy, int hsel) {
+                           int64_t bx) {
   // nw*P*MT*256 partial sums | e4m3 activation slice [M][ks] | (NORM) sum-of-squares [M][K/16].
   // 16-byte aligned: the slice is read 16 bytes per lane. (Without it the dynamic region starts
-  // right after the static variables, at a 4-byte boundary when they total 132 bytes, as in
-  // k_gemv_fp8_mixed, and the one-row slice's 8- and 16-byte accesses were misaligned.)
+  // right after the static variables, at a 4-byte boundary when they total 132 bytes, as in the
+  // two-row-tile argmax kernels, and the slice's 8- and 16-byte accesses are misaligned.)
   extern __shared__ __align__(16) float red[];
   __shared__ float xs_l[32], rstd_s[32];
   __shared__ uint32_t amax_w[kMaxThreads / 64];
@@ -173,8 +162,6 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   constexpr bool AW = AWC > 0;
   static_assert(!AW || (XK != KRQ_X_FP8 && XK != KRQ_X_FP8_TILED && MT == 1), "activation wave: one bf16 row");
   static_assert(XK != KRQ_X_FP8_TILED || ALGO != 2, "tiled activations: matrix-core kernels");
-  static_assert(!HALF || (MT == 1 && PB == 1 && ALGO == 1 && !NORM && (MODE == KRQ_OUT_BF16 || MODE == KRQ_OUT_PARTIAL)),
-                "half blocks: one row tile, one matrix, matrix cores, plain outputs");
   constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : PB;  // weight row blocks streamed per step
   constexpr bool XT = XK == KRQ_X_FP8_TILED;
   constexpr bool FUSED = XK != KRQ_X_FP8 && !XT;  // bf16 activations quantized into LDS
@@ -190,18 +177,16 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x >> 6) - (AW ? 1 : 0);
   const int r = lane & 15, g = lane >> 4;
   const int64_t rb = bx * PB, rbu = MODE == KRQ_OUT_SWIGLU ? rb + (NO >> 4) : rb + 1;
-  const int sidx = sy;
+  const int sidx = blockIdx.y;
   const int nsteps = (kts + 1) >> 1;
-  const int nst = HALF ? (nsteps + 1) >> 1 : nsteps;  // work units of the block (HALF: step pairs)
   const int64_t tbase = (int64_t)sidx * kts;
   const int64_t k0 = tbase * 64;  // first K element of this split
   const int ks = kts * 64;        // K elements of this split
   const int T = (int)(K >> 4);    // sum-of-squares partials per row
   uint8_t* xq = reinterpret_cast<uint8_t*>(red + nw * P * MT * 256);
-  const int jcount = wave < nst ? (nst - wave + nw - 1) / nw : 0;
+  const int jcount = wave < nsteps ? (nsteps - wave + nw - 1) / nw : 0;
   KRQ_STAMP(0, threadIdx.x == 0);
-  const ColScales cs = HALF ? ColScales{wsc[w_per_row ? rb * 16 + 8 * hsel + (threadIdx.x & 7) : 0], 1.0f}
-                            : load_col_scales<MODE, PB>(wsc, w_per_row, NO, rb);
+  const ColScales cs = load_col_scales<MODE, PB>(wsc, w_per_row, NO, rb);
 
   // ---- fused activation prologue, part 1: activation loads ahead of the weight stream ----
   // Every load of the prologue and of the step ring is issued unconditionally, at a clamped (valid)
@@ -263,25 +248,6 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
     const int j = jcount > 0 ? wave + min(cc, jcount - 1) * nw : 0;
     const int64_t t0 = tbase + 2 * j;
     const int64_t t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
-    if constexpr (HALF) {
-      // the pair's second step (clamped past the last: its loads repeat that step, masked below)
-      const int jb = min(j + nst, nsteps - 1);
-      const int64_t s0 = tbase + 2 * jb, s1 = (2 * jb + 1 < kts) ? s0 + 1 : s0;
-      const bool wsec = r >= 8, xsec = r & 1;
-      wl[u] = ld16nt(w_addr_half<LAYOUT>(w8, rb, hsel, wsec ? s0 : t0, K, lane));
-      wh[u] = ld16nt(w_addr_half<LAYOUT>(w8, rb, hsel, wsec ? s1 : t1, K, lane));
-      if (!FUSED) {  // row 0 of the activations (M == 1), at the step of this lane's A row
-        const int64_t a0 = xsec ? s0 : t0, a1 = xsec ? s1 : t1;
-        if (XT) {
-          xl[u][0] = ld16(x + (a0 * 64 + (lane & 48)) * 16);
-          xh[u][0] = ld16(x + (a1 * 64 + (lane & 48)) * 16);
-        } else {
-          xl[u][0] = ld16(x + g * 16 + a0 * 64);
-          xh[u][0] = ld16(x + g * 16 + a1 * 64);
-        }
-      }
-      return;
-    }
     if constexpr (MODE == kOutSwiGluHalf) {
       wl[u] = ld16nt(w_addr_hp<LAYOUT>(w8, rb, NO, t0, K, lane));
       wh[u] = ld16nt(w_addr_hp<LAYOUT>(w8, rb, NO, t1, K, lane));
@@ -393,21 +359,6 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   auto consume_slot = [&](int u, int cc) {
     const int j = jcount > 0 ? wave + min(cc, jcount - 1) * nw : 0;
     const bool ok = cc < jcount, hi = ok && (2 * j + 1 < kts);
-    if constexpr (HALF) {
-      const int jb = min(j + nst, nsteps - 1);
-      const bool okb = ok && j + nst < nsteps, hib = okb && (2 * jb + 1 < kts);
-      if (FUSED) {  // A row r: the slice at step j (even r) or jb (odd r)
-        const int js = (r & 1) ? jb : j;
-        const uint8_t* xr = xq + g * 16;
-        xl[u][0] = *reinterpret_cast<const uint4*>(xr + (2 * js) * 64);
-        xh[u][0] = sel4(2 * js + 1 < kts, *reinterpret_cast<const uint4*>(xr + min(2 * js + 1, kts - 1) * 64));
-      }
-      const bool sec = r >= 8;
-      const v8i B = pack_v8i(sel4(sec ? okb : ok, wl[u]), sel4(sec ? hib : hi, wh[u]));
-      acc[0] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(pack_v8i(xl[u][0], xh[u][0]), B, acc[0], 0, 0, 0, 0,
-                                                                0, 0);
-      return;
-    }
     if (FUSED) {
       // the quantized slice ends at ks: the high tile of an odd last step is zero (not stale LDS)
 #pragma unroll
@@ -467,29 +418,6 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
     accu[0] = v4f{g == 0 ? au : 0.f, 0.f, 0.f, 0.f};
   }
   KRQ_STAMP(2, threadIdx.x == 0);
-  if (direct && HALF) {
-    // lanes 0-15: element 0 = C[0][l] (first half of K), element 1 = C[1][l] (second half); lane
-    // c < 8 adds lane c + 8's second-half sum of the same weight row (DPP row_ror:8 within each row
-    // of 16 lanes). Elements 2 and 3 are not needed, but all four stay live until the store: an
-    // element that dies at the matrix-core instruction frees its register for the next vector-ALU
-    // result while the instruction may still be writing it, and the compiler placed no wait for
-    // that (the lane-index arithmetic of a ds_bpermute shuffle landed there and read back garbage
-    // on some launches).
-    if constexpr (DIRECT_OK) {
-      const float c1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc[0][1]), 0x128, 0xf, 0xf, false));
-      if (lane < 8) {
-        const int64_t n = rb * 16 + 8 * hsel + lane;
-        const float y = (acc[0][0] + c1) * xs_l[0] * cs.g;
-        if (MODE == KRQ_OUT_BF16)
-          reinterpret_cast<uint16_t*>(out)[n] = f32_to_bf16(y);
-        else
-          reinterpret_cast<float*>(out)[(int64_t)sidx * NO + n] = y;
-      }
-      asm volatile("" ::"v"(acc[0]));
-    }
-    KRQ_STAMP(3, threadIdx.x == 0);
-    return;
-  }
   if (direct) {
     // lane l, element i holds output row 4 (l / 16) + i, column 16 rb + l % 16 (xs_l is in LDS:
     // written by this wave, or by the activation wave before the barrier above)
@@ -513,23 +441,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   stash<MT, P>(red, wave, lane, acc, accu);
   }  // weight waves
   __syncthreads();
-  if constexpr (HALF) {
-    // the waves' sums as in epilogue(): thread c < 8 takes C[0][c] and C[1][c + 8] of each wave
-    const int t = threadIdx.x;
-    if (t < 8) {
-      float a0 = 0.0f, a1 = 0.0f;
-      for (int w = 0; w < nw; ++w) {
-        a0 += red[w * 256 + t];
-        a1 += red[w * 256 + 64 + t + 8];
-      }
-      const int64_t n = rb * 16 + 8 * hsel + t;
-      const float y = (a0 + a1) * xs_l[0] * cs.g;
-      if (MODE == KRQ_OUT_BF16)
-        reinterpret_cast<uint16_t*>(out)[n] = f32_to_bf16(y);
-      else
-        reinterpret_cast<float*>(out)[(int64_t)sidx * NO + n] = y;
-    }
-  } else if constexpr (MODE == kOutResidual) {
+  if constexpr (MODE == kOutResidual) {
     residual_epilogue<MT>(red, nw, M, NO, rb, sidx, gridDim.y, xs_l, cs.g, reinterpret_cast<float*>(out), fa,
                           &last_s);
   } else {
@@ -548,7 +460,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
 template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, int PB, int AWC>
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(KRQ_FP8_KERNEL_PARAMS) {
   gemv_fp8_body<MT, MODE, LAYOUT, XK, ALGO, U, PB, false, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M, NO,
-                                                               K, kts, out, aux, FusedArgs{}, blockIdx.x, blockIdx.y, 0);
+                                                               K, kts, out, aux, FusedArgs{}, blockIdx.x);
 }
 
 // The SwiGLU launch with its last column blocks split in half: workgroups below nfull are the
@@ -561,39 +473,18 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8_swiglu_mixed(KRQ_FP8_K
   if (static_cast<int>(blockIdx.x) < nfull)
     gemv_fp8_body<1, KRQ_OUT_SWIGLU, LAYOUT, XK, ALGO, U, 1, false, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row,
                                                                          M, NO, K, kts, out, aux, FusedArgs{},
-                                                                         blockIdx.x, 0, 0);
+                                                                         blockIdx.x);
   else
     gemv_fp8_body<1, kOutSwiGluHalf, LAYOUT, XK, ALGO, U, 1, false, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row,
                                                                          M, NO, K, kts, out, aux, FusedArgs{},
-                                                                         (int64_t)blockIdx.x + nfull, 0, 0);
-}
-
-// A one-row, single-matrix launch whose (row block, split) pairs number a little over a multiple of
-// the compute units (O and down at split 4: 640 = 2 x 256 + 128): workgroups below nfull are the
-// full blocks of pairs 0 .. nfull - 1 (pair p: row block p % nrb, split p / nrb, the order of the
-// plain launch's two-dimensional grid); workgroup nfull + h is half block h % 2 of pair
-// nfull + h / 2. Workgroup i runs on compute unit i mod 256, so with nfull = 512 every CU streams
-// two full blocks and one half block instead of some streaming three full ones. UF / UH: the step
-// slots per weight wave of the full and the half blocks (both hold their whole ring at once).
-template <int MODE, int LAYOUT, int XK, int UF, int UH, int AWC>
-__global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8_mixed(KRQ_FP8_KERNEL_PARAMS, int nfull, int nrb) {
-  const int w = static_cast<int>(blockIdx.x);
-  if (w < nfull) {
-    gemv_fp8_body<1, MODE, LAYOUT, XK, 1, UF, 1, false, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M, NO, K,
-                                                             kts, out, aux, FusedArgs{}, w % nrb, w / nrb, 0);
-  } else {
-    const int h = w - nfull, p = nfull + (h >> 1);
-    gemv_fp8_body<1, MODE, LAYOUT, XK, 1, UH, 1, false, AWC, true>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M,
-                                                                   NO, K, kts, out, aux, FusedArgs{}, p % nrb,
-                                                                   p / nrb, h & 1);
-  }
+                                                                         (int64_t)blockIdx.x + nfull);
 }
 
 // the fused kernel (fused_fp8.hip): RMSNorm prologue and / or residual epilogue
 template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, bool NORM, int AWC>
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8_fused(KRQ_FP8_KERNEL_PARAMS, FusedArgs fa) {
   gemv_fp8_body<MT, MODE, LAYOUT, XK, ALGO, U, 1, NORM, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M, NO,
-                                                             K, kts, out, aux, fa, blockIdx.x, blockIdx.y, 0);
+                                                             K, kts, out, aux, fa, blockIdx.x);
 }
 
 
@@ -603,11 +494,11 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8_fused_swiglu_mixed(KRQ
                                                                             int nfull) {
   if (static_cast<int>(blockIdx.x) < nfull)
     gemv_fp8_body<1, KRQ_OUT_SWIGLU, LAYOUT, XK, 1, U, 1, NORM, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M,
-                                                                     NO, K, kts, out, aux, fa, blockIdx.x, 0, 0);
+                                                                     NO, K, kts, out, aux, fa, blockIdx.x);
   else
     gemv_fp8_body<1, kOutSwiGluHalf, LAYOUT, XK, 1, U, 1, NORM, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row, M,
                                                                      NO, K, kts, out, aux, fa,
-                                                                     (int64_t)blockIdx.x + nfull, 0, 0);
+                                                                     (int64_t)blockIdx.x + nfull);
 }
 
 }  // namespace

@@ -340,8 +340,8 @@ __global__ __launch_bounds__(NT) void k_act_rows_fast(const uint16_t* __restrict
 template <int CH>
 __global__ __launch_bounds__(64) void k_act_rows_wave(const uint16_t* __restrict__ x, int64_t M, int64_t K, int sp,
                                                       float* __restrict__ scale, uint8_t* __restrict__ x8) {
-  const int lane = threadIdx.x, s = blockIdx.x;
-  const int64_t r = blockIdx.y;
+  const int lane = threadIdx.x, s = blockIdx.y;
+  const int64_t r = blockIdx.x;
   const int np = static_cast<int>(K >> 4), c0 = s * sp;
   if (r >= M) {
 #pragma unroll
@@ -590,7 +590,7 @@ extern "C" int krq_quant_rows_tiled(const void* x_bf16, int64_t M, int64_t K, vo
   const int64_t mp = (M + 15) / 16 * 16;  // rows padded to whole 16-row tiles
   const int np = static_cast<int>(K / 16), ch = (np + 63) / 64;  // pieces per lane of a whole row (<= 16)
   const int sp = 1;                                               // pieces each workgroup stores per lane
-  const dim3 grid(static_cast<unsigned>((ch + sp - 1) / sp), static_cast<unsigned>(mp));
+  const dim3 grid(static_cast<unsigned>(mp), static_cast<unsigned>((ch + sp - 1) / sp));
 #define KRQ_ROWS_WAVE(CH)                                                                                         \
   hipLaunchKernelGGL((k_act_rows_wave<CH>), grid, dim3(64), 0, (hipStream_t)stream, (const uint16_t*)x_bf16, M, K, \
                      sp, xs, (uint8_t*)x8_tiled)

@@ -485,43 +485,6 @@ def test_graph_replay_matches_eager(dev):
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("name", ["o", "down"])
-def test_half_blocks_match_full_blocks(dev, name):
-    """O and down at M = 1, split 4: 640 (row block, split) pairs, 2 x 256 + 128. On tiled weights
-    the GEMV runs the last 128 pairs as 256 half blocks in the same launch (k_gemv_fp8_mixed). A
-    half block sums the two halves of its K range in separate matrix-core rows and adds them at the
-    end. On row-major weights every pair is a full block, with other rings and wave counts. For each
-    activation kind the partials are equal bit for bit, and within the bar of the exact oracle. The
-    kinds are per-token scaling in the kernel, a static inverse scale, e4m3 rows and tiled e4m3 rows."""
-    N, K = SHAPES[name]
-    w, x = _fp8_case(N, K, 1, 60 + SEEDS[name])
-    q = fp8.quantize(w.to(dev))
-    qr = fp8.FP8Weight(q[0], q[1], None)
-    xd = x.to(dev)
-    x8, xs = fp8.quant_rows(xd)
-    x8t, xst = fp8.quant_rows_tiled(xd)
-    a = fp8.SharedScale(torch.tensor([448.0 / 4.0], device=dev), torch.tensor(4.0 / 448.0, device=dev))
-    runs = {
-        "dyn": lambda qq: fp8.gemv_fp8_bf16_launch(xd, qq, 4, L.OUT_PARTIAL),
-        "static": lambda qq: fp8.gemv_fp8_bf16_launch(xd, qq, 4, L.OUT_PARTIAL, a),
-        "fp8": lambda qq: fp8.gemv_fp8_launch(x8, xs, qq, 4, L.OUT_PARTIAL),
-        "tiled": lambda qq: fp8.gemv_fp8_tiled_launch(x8t, xst, qq, 1, 4, L.OUT_PARTIAL),
-    }
-    r8, rs = O.quantize(u16(w))
-    _, yref = O.fp8_matmul(u8(x8), xs.cpu().numpy(), r8, rs)
-    _, yref_s = O.fp8_matmul(u8(fp8._cast_hip(xd, a)), np.float32(4.0 / 448.0), r8, rs)
-    outs = {}
-    for kind, fn in runs.items():
-        mixed, plain = fn(q), fn(qr)
-        d = (mixed - plain).abs().max().item()
-        print(f"{name} {kind}: mixed vs plain max |diff| {d:.3e}")
-        assert torch.equal(mixed, plain), kind
-        assert rel_err(_sum_partials(mixed), yref_s if kind == "static" else yref) <= TOL, kind
-        outs[kind] = mixed
-    # one row scaled in the kernel = quant_rows then the e4m3 GEMV, either activation layout
-    assert torch.equal(outs["dyn"], outs["fp8"]) and torch.equal(outs["fp8"], outs["tiled"])
-
-
 def test_deterministic(dev):
     N, K = DOWN
     w, x = _fp8_case(N, K, 32, 4)
