@@ -190,6 +190,27 @@ def out_bytes(M, N, split, mode):
     return 2 * M * N
 
 
+def chained_mlp(torch, fp8, dev, layers, x):
+    """The decode MLP at M = 1 two ways on the same operands: the chained launch
+    (PersistentMLP(chained=True), krq_mlp_chain_fp8: gate_up's SwiGLU blocks and down's split-K
+    blocks in one launch, the down blocks waiting in the kernel for act) and the two-launch pair
+    (gemv_swiglu_fp8, then gemv_fp8 split 4; PersistentMLP's default form). Returns (chained step,
+    pair step, algorithmic bytes per step: both weights, scales, x, act written and read, the
+    fp32 partials)."""
+    from kernels.mlp import PersistentMLP
+    pm = PersistentMLP(1, H, I, dev, split=4, chained=True)
+
+    def chain(i):
+        Lw = layers[i % LAYERS]
+        return pm(x, Lw["gate_up"], Lw["down"])
+
+    def pair(i):
+        Lw = layers[i % LAYERS]
+        return fp8.gemv_fp8(fp8.gemv_swiglu_fp8(x, Lw["gate_up"]), Lw["down"], 4)
+    nbytes = proj_bytes(1, 2 * I, H, 1, "swiglu") + proj_bytes(1, H, I, 4, "partial")
+    return chain, pair, nbytes
+
+
 def proj_bytes(M, N, K, split, mode):
     return N * K + 4 * N + 2 * M * K + 4 * M + out_bytes(M, N, split, mode)
 
@@ -572,7 +593,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--replays", type=int, default=7, help="timed replays of the step graph (>= 5)")
     ap.add_argument("--config", default="decode",
-                    choices=["decode", "c2", "c3", "c3m32", "c4", "c5", "layer", "mlp_static", "prefill"])
+                    choices=["decode", "c2", "c3", "c3m32", "c4", "c5", "layer", "mlp_static", "mlp_chain",
+                             "prefill"])
     ap.add_argument("--m", type=int, default=None, help="rows for --config c4 / c5 / layer (default 1) "
                     "and prefill (default 1024)")
     ap.add_argument("--lm", default="bf16", choices=["bf16", "fp8"], help="lm head weights (c4)")
@@ -672,6 +694,10 @@ def main():
         step, unfused_step, step_bytes = static_mlp(torch, fp8, dev, Ms[0])
         work = (f"static-scale FP8 decode MLP at M={Ms[0]} (engine.py:977-981: gate_up with SiLU*up and the "
                 f"down input's cast in one launch, then down), per-tensor weights, cycling {LAYERS} layers")
+    elif cfg == "mlp_chain":
+        step, pair_step, step_bytes = chained_mlp(torch, fp8, dev, layers, xs[1]["gate_up"])
+        work = (f"chained FP8 decode MLP at M=1 (gate_up with SwiGLU and down's split-K partials in one launch, "
+                f"the down workgroups waiting in the kernel for act), per-token scales, cycling {LAYERS} layers")
     elif cfg == "c4":
         w_lm = E if E is not None else q8
         step = lambda i: lmhead.lm_head_argmax(h, w_lm)
@@ -729,6 +755,19 @@ def main():
                     "frac": round(a / 8000.0, 4), "traffic": None, "kernel": f"static-scale FP8 MLP M={Ms[0]}",
                     "bytes_per_launch": step_bytes, "us_per_launch": round(tmed_f, 3),
                     "unfused_us": round(tmed_u, 3)}
+    if cfg == "mlp_chain":
+        res = {}
+        for rnd in range(2):  # alternating, so both forms see the same box state
+            for name, fn in (("pair", pair_step), ("chained", step)):
+                res.setdefault(name, []).append(graph_time(torch, fn, args.reps))
+        (cmin, cmed), (pmin, pmed) = min(res["chained"]), min(res["pair"])
+        log(f"[bench] FP8 MLP M=1 (graph of {args.reps}, cycling {LAYERS} layers): chained (one launch) "
+            f"{cmed:.2f} us (min {cmin:.2f}); pair (SwiGLU GEMV, down GEMV) {pmed:.2f} us (min {pmin:.2f})")
+        a = step_bytes / cmed / 1e3
+        roofline = {"bound": "hbm", "achieved": round(a, 1), "peak": 8000.0, "unit": "GB/s",
+                    "frac": round(a / 8000.0, 4), "traffic": None, "kernel": "k_mlp_chain_fp8 M=1",
+                    "bytes_per_launch": step_bytes, "us_per_launch": round(cmed, 3),
+                    "pair_us": round(pmed, 3)}
     if cfg == "layer":
         rows = []
         for name, fn, nbytes in fused_stages:

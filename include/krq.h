@@ -260,6 +260,29 @@ int krq_mlp_fp8_bounded(const void* x, int x_kind, const float* x_scale, const v
 int64_t krq_mlp_ctl_words(void);
 
 /*
+ * The decode MLP at M == 1 in ONE launch, with the result of the default two-launch pair
+ * (reference engine/kernels/mlp.py:22-118 PersistentMLP.__call__, as its consumer
+ * engine/engine.py:911-915 uses it): act = SwiGLU(x . [gate; up]^T) (bf16 [1, I], bit-identical
+ * to krq_gemv_fp8 KRQ_OUT_SWIGLU on the bf16 row), then out = the fp32 [split, 1, H] split-K
+ * partials of act . w_down^T with act scaled per token (krq_gemv_fp8, KRQ_X_BF16_DYN).
+ * Both weights KRQ_W_TILED with per-row (or per-tensor) scales; x bf16 [1, H].
+ * The down workgroups issue their weight loads first and wait in the kernel for every gate_up
+ * workgroup's act (a done flag in ctl, polled at most max_polls times, each poll one memory
+ * round trip). The partial sums equal krq_gemv_fp8's to fp32 rounding (two weight waves per
+ * split instead of one).
+ * ctl: krq_mlp_chain_ctl_words() uint32 words, zero before the first call; every launch leaves
+ *      them zero again, except word 513, which a wait that gave up sets to 1 (that block's
+ *      partials are then NaN; zero ctl again before the next call). Calls sharing ctl must not
+ *      overlap.
+ * Needs H % 64 == 0, I % 64 == 0, (I/split) % 64 == 0, H and I at most 10240, and at most 20
+ * steps of 128 elements per split (I/split <= 2560).
+ */
+int krq_mlp_chain_fp8(const void* x, const void* w_gu, const float* gu_scale, int gu_per_row,
+                      const void* w_down, const float* down_scale, int down_per_row, int64_t H, int64_t I,
+                      int split, void* act, uint32_t* ctl, uint32_t max_polls, void* out, void* stream);
+int64_t krq_mlp_chain_ctl_words(void);
+
+/*
  * BF16 GEMV with the RMSNorm prologue and the residual epilogue folded in: gemv_fused /
  * gemv_swiglu_fused (reference engine/kernels/fused_gemv.py:48-221, called at
  * engine/engine.py:953-961).

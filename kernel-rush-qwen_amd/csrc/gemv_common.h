@@ -257,11 +257,19 @@ KRQ_DEV ColScales load_col_scales(const float* __restrict__ wsc, int w_per_row, 
   return c;
 }
 
+// a bf16 output element; WT: written through to memory (agent scope), for a reader on another XCD
+// in the same launch
+template <bool WT>
+KRQ_DEV void store_bf16(uint16_t* p, uint16_t v) {
+  if constexpr (WT) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *p = v;
+}
+
 // P accumulator sets per wave in red; this call reads set p0 (and p0 + 1 for SwiGLU) and writes
 // row block rb. SwiGLU with aux = a device float `inv`: out receives the next projection's input,
 // e4m3(clamp(act * inv, +-448)) of the bf16 act, in the tiled activation layout (rows padded to
 // 16 MT, pad rows 0; NO % 64 == 0) instead of bf16 act.
-template <int MT, int MODE, int P>
+template <int MT, int MODE, int P, bool WT = false>
 KRQ_DEV void epilogue(const float* red, int p0, int nw, int M, int64_t NO, int64_t rb, int split_idx,
                       const float* xs, ColScales cs, void* __restrict__ out, void* __restrict__ aux) {
   constexpr int NV = MT * 256;
@@ -295,7 +303,7 @@ KRQ_DEV void epilogue(const float* red, int p0, int nw, int M, int64_t NO, int64
         reinterpret_cast<uint8_t*>(out)[tile * 1024 + 16 * (16 * ((n8 & 63) >> 4) + (m & 15)) + (n8 & 15)] = q;
       } else if (valid) {
         const float sl = round_bf16(t / (1.0f + expf(-t)));
-        reinterpret_cast<uint16_t*>(out)[(int64_t)m * NO + n8] = f32_to_bf16(sl * uu);
+        store_bf16<WT>(reinterpret_cast<uint16_t*>(out) + (int64_t)m * NO + n8, f32_to_bf16(sl * uu));
       }
       continue;
     }
@@ -333,7 +341,7 @@ KRQ_DEV void epilogue(const float* red, int p0, int nw, int M, int64_t NO, int64
       const float gg = round_bf16(a * x * cs.g);
       const float uu = round_bf16(au * x * cs.u);
       const float sl = round_bf16(gg / (1.0f + expf(-gg)));
-      reinterpret_cast<uint16_t*>(out)[(int64_t)m * NO + n] = f32_to_bf16(sl * uu);
+      store_bf16<WT>(reinterpret_cast<uint16_t*>(out) + (int64_t)m * NO + n, f32_to_bf16(sl * uu));
     } else {
       const float y = a * x * cs.g;
       if (MODE == KRQ_OUT_BF16)
@@ -397,8 +405,24 @@ struct FusedArgs {
   const uint16_t* res_in;  // residual epilogue: bf16 [M][N] residual rows
   uint16_t* res_out;       // bf16 [M][N] new residual rows
   float* ss_out;           // [M][N/16] per-tile sums of squares of res_out
-  uint32_t* cnt;           // [N/16] split-arrival counters (zero between launches)
+  uint32_t* cnt;           // [N/16] split-arrival counters (zero between launches); chained MLP: kChainWords control words
+  uint32_t max_polls;      // chained MLP: polls of the first stage's done flag before a block gives up
+  int n_first;             // chained MLP: first workgroup index of the second stage
+  int n_second;            // chained MLP: workgroups of the second stage
 };
+
+// Control words of the chained MLP (uint32, zero between launches). Group g < kChainGroups owns
+// the line at word 64 g: [0] first-stage arrivals, [1] second-stage exits. Word kChainArr counts
+// the first-stage groups complete, kChainExit the second-stage groups done, and kChainErr records
+// a wait that gave up. The first stage's done flag goes to kChainReps replicas kChainRepStride
+// words (4,352 bytes) apart from word kChainRep, and a waiting workgroup polls replica
+// blockIdx.x % kChainReps: a few hundred workgroups polling one word saturate the memory channel
+// that holds it, and every weight stream, which is interleaved over all channels, slows with it
+// (measured: the gate_up stage took 240 us instead of 10).
+constexpr int kChainGroups = 8, kChainTop = kChainGroups * 64, kChainExit = kChainTop, kChainErr = kChainTop + 1,
+              kChainArr = kChainTop + 2, kChainRep = kChainTop + 64, kChainReps = 64, kChainRepStride = 1088,
+              kChainWords = kChainRep + kChainReps * kChainRepStride;
+static_assert(kChainReps == 64, "one replica per lane of the publishing wave");
 
 typedef float v2f __attribute__((ext_vector_type(2)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));

@@ -3,6 +3,8 @@
 // epilogue conventions: gemv_common.h.
 #include "gemv_fp8_kernel.h"
 
+#include <algorithm>
+
 using namespace krq;
 
 namespace krq {
@@ -369,6 +371,68 @@ extern "C" int krq_gemv_swiglu_fp8_cast(const void* x, int x_kind, const float* 
   return gemv_fp8_run(x, x_kind, x_scale, x_inv, x_per_row, w8, w_layout, w_scale, w_per_row, M, N, K, 1,
                       KRQ_OUT_SWIGLU, 0, x8_tiled, const_cast<float*>(out_inv), stream);
 }
+
+// The chained FP8 MLP at M = 1 (k_mlp_chain_fp8): act = SwiGLU(x . Wgu^T) and the split-K partials
+// of act . Wd^T in one launch, the down blocks streaming their weights before act is complete.
+extern "C" int krq_mlp_chain_fp8(const void* x, const void* w_gu, const float* gu_scale, int gu_per_row,
+                                 const void* w_down, const float* down_scale, int down_per_row, int64_t H, int64_t I,
+                                 int split, void* act, uint32_t* ctl, uint32_t max_polls, void* out, void* stream) {
+  KRQ_REQUIRE(x && w_gu && gu_scale && w_down && down_scale && act && ctl && out, "mlp_chain_fp8: null pointer");
+  KRQ_REQUIRE(aligned16(x) && aligned16(w_gu) && aligned16(w_down) && aligned16(act),
+              "mlp_chain_fp8: x, weights and act must be 16-byte aligned");
+  KRQ_REQUIRE(H > 0 && I > 0 && H % 64 == 0 && I % 64 == 0 && split >= 1 && I % split == 0 && (I / split) % 64 == 0,
+              "mlp_chain_fp8: shape H=%lld I=%lld split=%d (H, I and I/split multiples of 64)", (long long)H,
+              (long long)I, split);
+  KRQ_REQUIRE(H <= 512 * kAwLarge && I <= 512 * kAwLarge, "mlp_chain_fp8: rows longer than %d elements",
+              512 * kAwLarge);
+  KRQ_REQUIRE(max_polls > 0, "mlp_chain_fp8: max_polls must be positive");
+  const int awg = aw_chunks(H), awd = aw_chunks(I);
+  // gate_up: the SwiGLU launch's plan (two-matrix blocks, the last ones as half-pair blocks)
+  const int64_t nrbs = I / 16, rem = nrbs % kCUs;
+  const bool mixed = nrbs > 2 * kCUs && rem != 0 && 2 * rem <= kCUs;
+  const int64_t nfull = mixed ? nrbs - rem : nrbs, n_first = mixed ? nfull + 2 * rem : nrbs;
+  const int64_t nrb2 = H / 16, n_second = nrb2 * split;
+  KRQ_REQUIRE(n_first + n_second <= 0x7fffffff, "mlp_chain_fp8: grid too large");
+  // down: two weight waves of kDeepU slots, every step of the split in flight before the wait for
+  // act. (The standalone down GEMV's single wave of kBigU slots would take the chained kernel to
+  // 256 VGPRs, two waves per SIMD, and two resident blocks per CU instead of four.) The partial
+  // sums are those of two waves, so they differ from the standalone GEMV's in fp32 rounding only.
+  constexpr int NWG = 2, NWD = 2;
+  const int kts_g = static_cast<int>(H / 64), kts_d = static_cast<int>(I / split / 64);
+  KRQ_REQUIRE((kts_d + 1) / 2 <= NWD * kDeepU,
+              "mlp_chain_fp8: down's split of I/split=%lld elements exceeds the ring (at most %d steps of 128)",
+              (long long)(I / split), NWD * kDeepU);
+  // LDS: the larger stage's partial sums and quantized slice
+  const size_t smem = std::max((size_t)NWG * 2 * 256 * sizeof(float) + (size_t)H,
+                               (size_t)NWD * 256 * sizeof(float) + (size_t)(I / split));
+  FusedArgs fa{};
+  fa.cnt = ctl;
+  fa.max_polls = max_polls;
+  fa.n_first = static_cast<int>(n_first);
+  fa.n_second = static_cast<int>(n_second);
+  const dim3 grid(static_cast<unsigned>(n_first + n_second)), block((NWG + 1) * 64);
+  hipStream_t s = (hipStream_t)stream;
+#define KRQ_CHAIN(AG, AD)                                                                                            \
+  hipLaunchKernelGGL((k_mlp_chain_fp8<kSwiU, AG, kDeepU, AD, NWG, NWD>), grid, block, smem, s, (const uint8_t*)x,    \
+                     (const uint8_t*)w_gu, gu_scale, gu_per_row, (const uint8_t*)w_down, down_scale, down_per_row, I, H, \
+                     kts_g, kts_d, static_cast<int>(nfull), static_cast<int>(nrb2), (uint16_t*)act, (float*)out, fa)
+#define KRQ_CHAIN_D(AG)                     \
+  if (awd == kAwRow) KRQ_CHAIN(AG, kAwRow); \
+  else if (awd == kAwSmall) KRQ_CHAIN(AG, kAwSmall); \
+  else KRQ_CHAIN(AG, kAwLarge);
+  if (awg == kAwRow) {
+    KRQ_CHAIN_D(kAwRow)
+  } else if (awg == kAwSmall) {
+    KRQ_CHAIN_D(kAwSmall)
+  } else {
+    KRQ_CHAIN_D(kAwLarge)
+  }
+#undef KRQ_CHAIN_D
+#undef KRQ_CHAIN
+  return krq_check_launch("mlp_chain_fp8");
+}
+
+extern "C" int64_t krq_mlp_chain_ctl_words(void) { return kChainWords; }
 
 #ifdef KRQ_TIMELINE
 // Timeline build only: copy the stamps of this file's GEMV kernels (8 slots per block, block

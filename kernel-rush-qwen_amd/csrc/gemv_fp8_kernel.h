@@ -74,12 +74,35 @@ constexpr int64_t kCUs = 256;  // compute units of the MI355X
 // row's sum-of-squares partials in the canonical order (K <= 4096: T = K / 16 <= 64 * kSsPerLane).
 // ORDER: the wave meets the weight waves at a bare s_barrier (no fence, no wait) once all of its
 // loads are issued, and the weight waves issue their ring only after it; see gemv_fp8_body.
-template <int XK, int AWC, bool NORM, bool ORDER>
+// CH (second stage of the chained MLP, KRQ_X_BF16_DYN): the row is written in this launch by the
+// first stage's workgroups, on every XCD. The wave first polls its replica of the first stage's
+// done flag with a scalar load (which does not queue behind the vector memory traffic of the
+// weight stream), until it is set or fa.max_polls polls pass; then it reads the row with
+// agent-scope (sc1) buffer loads, which read memory instead of a stale line of this XCD's L2. A
+// wait that gives up records kChainErr and makes the scale NaN, so every output of the block is
+// NaN.
+template <int XK, int AWC, bool NORM, bool ORDER, bool CH = false>
 KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restrict__ xsc,
                              const float* __restrict__ xinv, int64_t K, int64_t k0, int ks, int lane,
                              uint8_t* xq, float* xs_l, const FusedArgs& fa) {
   constexpr int LC = NORM ? AWC : 1;
   constexpr int SC = NORM ? kSsPerLane : 1;
+  static_assert(!CH || (XK == KRQ_X_BF16_DYN && !NORM), "chained stage: one bf16 row scaled per token");
+  bool chain_bad = false;
+  if constexpr (CH) {
+    // this workgroup's replica of the done flag (an address held in scalar registers)
+    const uint32_t* rep = fa.cnt + kChainRep + kChainRepStride * static_cast<int>(blockIdx.x % kChainReps);
+    uint32_t polls = 0, done = 0;
+    for (;;) {
+      // the load and its wait in one statement, the destination early-clobber (a load in flight
+      // still writes its register)
+      asm volatile("s_load_dword %0, %1, 0x0 glc\n\ts_waitcnt lgkmcnt(0)" : "=&s"(done) : "s"(rep) : "memory");
+      if (done != 0 || ++polls > fa.max_polls) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    chain_bad = done == 0;
+    if (chain_bad && lane == 0) cstore(fa.cnt + kChainErr, 1u);
+  }
   __builtin_amdgcn_s_setprio(3);
   // DYN: chunk i = lane + 64 c of the row holds elements 8i .. 8i + 7 (indices past the row repeat
   // its last chunk); STATIC: the same over the slice
@@ -93,7 +116,13 @@ KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restr
 #pragma unroll
   for (int c = 0; c < AWC; ++c) {
     const int64_t e = e0 + 8 * (int64_t)min(lane + 64 * c, last);
-    v[c] = ld16(x + 2 * e);
+    if constexpr (CH) {
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(x), (short)0,
+                                                                          static_cast<int>(2 * K), 0x00020000);
+      v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(2 * e), 0, 16));
+    } else {
+      v[c] = ld16(x + 2 * e);
+    }
     if (NORM) lv[c] = ld16(lnb + 2 * e);
   }
   if (NORM) {
@@ -123,7 +152,8 @@ KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restr
 #pragma unroll
     for (int c = 0; c < AWC; ++c)
       if (!NORM || lane + 64 * c <= last) mb = absmax8_bits(v[c], mb);
-    const float am = clamp_min_nan(as_f32(wave_max_u32_dpp(bits_max_to_u32(mb))), 1e-6f);
+    float am = clamp_min_nan(as_f32(wave_max_u32_dpp(bits_max_to_u32(mb))), 1e-6f);
+    if (CH && chain_bad) am = __builtin_nanf("");
     inv = inv_from_amax(am);
     if (lane == 0) xs_l[0] = scale_from_amax(am);
   }
@@ -137,17 +167,68 @@ KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restr
   __builtin_amdgcn_s_setprio(0);
 }
 
+// End of a chained-MLP block (every thread of the block, or every thread of its wave 0, calls it).
+// First stage: once every thread's act stores have completed, one arrival on the block's group
+// counter; the group's last arrival counts the group complete, and the last group complete sets
+// every replica of the done flag (one store per lane of wave 0). Second stage: one exit on its
+// group; the group's last exit counts the group done, and the last group done zeroes every control
+// word. By then every second-stage block has passed its wait, so no word is read again in this
+// launch. (Counters that only grow, with the launch number published instead of a flag, need no
+// zeroing but measured slower: 32 against 19 us per Qwen3-4B MLP.)
+template <bool FIRST>
+KRQ_DEV void chain_tail(const FusedArgs& fa) {
+  const int g = static_cast<int>(blockIdx.x) % kChainGroups;
+  const int lane = threadIdx.x & 63;
+  // workgroups lo .. hi - 1 whose index is q mod kChainGroups
+  auto in_group = [](int q, int lo, int hi) {
+    const int first = lo + ((q - lo % kChainGroups) % kChainGroups + kChainGroups) % kChainGroups;
+    return first < hi ? (hi - 1 - first) / kChainGroups + 1 : 0;
+  };
+  auto groups_of = [&](int lo, int hi) {
+    int n = 0;
+    for (int q = 0; q < kChainGroups; ++q) n += in_group(q, lo, hi) > 0 ? 1 : 0;
+    return n;
+  };
+  if constexpr (FIRST) {
+    stores_done();
+    __syncthreads();
+  }
+  if (threadIdx.x >= 64) return;
+  uint32_t last = 0;
+  if (lane == 0) {
+    const int lo = FIRST ? 0 : fa.n_first, hi = FIRST ? fa.n_first : fa.n_first + fa.n_second;
+    if (cadd(fa.cnt + 64 * g + (FIRST ? 0 : 1), 1u) == static_cast<uint32_t>(in_group(g, lo, hi) - 1))
+      last = cadd(fa.cnt + (FIRST ? kChainArr : kChainExit), 1u) == static_cast<uint32_t>(groups_of(lo, hi) - 1);
+  }
+  if (!__shfl(last, 0, kWave)) return;
+  if constexpr (FIRST) {
+    cstore(fa.cnt + kChainRep + kChainRepStride * lane, 1u);
+  } else {
+    cstore(fa.cnt + kChainRep + kChainRepStride * lane, 0u);
+    if (lane < 2 * kChainGroups) cstore(fa.cnt + 64 * (lane >> 1) + (lane & 1), 0u);
+    if (lane == 0) {
+      cstore(fa.cnt + kChainArr, 0u);
+      cstore(fa.cnt + kChainExit, 0u);
+    }
+  }
+}
+
 // PB = 2 (MFMA kernels, modes other than SwiGLU): the block owns two adjacent row blocks, so each
 // activation load feeds two matrix-core products (at M > 1 the activation slices are as large as
 // the weight steps, and every row block re-reads them).
 // AWC > 0 (one-row kind without RMSNorm): the block's last wave is the activation wave above and
 // the others stream weights; AWC = 0: every wave takes part in the activation prologue.
-template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, int PB, bool NORM, int AWC>
+// CHAIN (the chained MLP, k_mlp_chain_fp8): a SwiGLU block writes act through to memory and then
+// counts itself into the first-stage counters; a split-K (partials) block is a second-stage
+// block whose activation wave waits for the first stage's done flag (activation_wave<..., CH>)
+// and which counts its exit, the last one out zeroing the control words (chain_tail). sy >= 0 / nwo > 0: the block's K split and its
+// weight-wave count, given (the chained kernel's one-dimensional grid and common block size).
+template <int MT, int MODE, int LAYOUT, int XK, int ALGO, int U, int PB, bool NORM, int AWC, bool CHAIN = false>
 KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restrict__ xsc,
                            const float* __restrict__ xinv, int x_per_row, const uint8_t* __restrict__ w8,
                            const float* __restrict__ wsc, int w_per_row, int M, int64_t NO, int64_t K,
                            int kts, void* __restrict__ out, void* __restrict__ aux, const FusedArgs& fa,
-                           int64_t bx) {
+                           int64_t bx, int sy = -1, int nwo = 0) {
   // nw*P*MT*256 partial sums | e4m3 activation slice [M][ks] | (NORM) sum-of-squares [M][K/16].
   // 16-byte aligned: the slice is read 16 bytes per lane. (Without it the dynamic region starts
   // right after the static variables, at a 4-byte boundary when they total 132 bytes, as in the
@@ -174,10 +255,15 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   // RMSNorm 10.5 -> 10.75 us) measured slower with it, so they keep issuing at once.
   constexpr bool ORDER = AWC > 0 && NORM && MODE != KRQ_OUT_SWIGLU && MODE != kOutSwiGluHalf;
   // nw = the waves that stream weights (all but the activation wave)
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x >> 6) - (AW ? 1 : 0);
+  static_assert(!CHAIN || (MT == 1 && PB == 1 && !NORM &&
+                            ((MODE == KRQ_OUT_PARTIAL && AWC > 0 && XK == KRQ_X_BF16_DYN) ||
+                             MODE == KRQ_OUT_SWIGLU || MODE == kOutSwiGluHalf)),
+                "chained MLP: SwiGLU first stage, per-token partials second stage");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nw = nwo > 0 ? nwo : (blockDim.x >> 6) - (AW ? 1 : 0);
   const int r = lane & 15, g = lane >> 4;
   const int64_t rb = bx * PB, rbu = MODE == KRQ_OUT_SWIGLU ? rb + (NO >> 4) : rb + 1;
-  const int sidx = blockIdx.y;
+  const int sidx = sy >= 0 ? sy : static_cast<int>(blockIdx.y);
   const int nsteps = (kts + 1) >> 1;
   const int64_t tbase = (int64_t)sidx * kts;
   const int64_t k0 = tbase * 64;  // first K element of this split
@@ -227,7 +313,8 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   const bool direct = DIRECT_OK && nw == 1;
   // (wave index read as a scalar: the compiler then knows the branch is uniform per wave)
   if (AW && __builtin_amdgcn_readfirstlane(wave) == nw) {
-    activation_wave<XK, AW ? AWC : 1, NORM, ORDER>(x, xsc, xinv, K, k0, ks, lane, xq, xs_l, fa);
+    activation_wave<XK, AW ? AWC : 1, NORM, ORDER, CHAIN && MODE == KRQ_OUT_PARTIAL>(x, xsc, xinv, K, k0, ks, lane, xq,
+                                                                                 xs_l, fa);
     KRQ_STAMP(1, lane == 0);
     __syncthreads();  // the slice and its scale are in LDS
     if (direct) return;
@@ -435,6 +522,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
         }
       }
     }
+    if constexpr (CHAIN) chain_tail<false>(fa);  // (thread 0 is in this wave)
     KRQ_STAMP(3, threadIdx.x == 0);
     return;
   }
@@ -445,9 +533,10 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
     residual_epilogue<MT>(red, nw, M, NO, rb, sidx, gridDim.y, xs_l, cs.g, reinterpret_cast<float*>(out), fa,
                           &last_s);
   } else {
-    epilogue<MT, MODE, P>(red, 0, nw, M, NO, rb, sidx, xs_l, cs, out, aux);
+    epilogue<MT, MODE, P, CHAIN>(red, 0, nw, M, NO, rb, sidx, xs_l, cs, out, aux);
     if (PB == 2) epilogue<MT, MODE, P>(red, 1, nw, M, NO, rbu, sidx, xs_l, ColScales{cs.u, 1.0f}, out, aux);
   }
+  if constexpr (CHAIN) chain_tail<MODE != KRQ_OUT_PARTIAL>(fa);
   KRQ_STAMP(3, threadIdx.x == 0);
 }
 
@@ -478,6 +567,36 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8_swiglu_mixed(KRQ_FP8_K
     gemv_fp8_body<1, kOutSwiGluHalf, LAYOUT, XK, ALGO, U, 1, false, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row,
                                                                          M, NO, K, kts, out, aux, FusedArgs{},
                                                                          (int64_t)blockIdx.x + nfull);
+}
+
+// The chained FP8 MLP at M = 1 (krq_mlp_chain_fp8): act = SwiGLU(x . Wgu^T) and the split-K
+// partials of act . Wd^T in one launch. Workgroups below nfull are gate_up's two-matrix blocks and
+// those up to fa.n_first its half-pair blocks (k_gemv_fp8_swiglu_mixed's plan); the rest are
+// down's blocks, pair p = w - fa.n_first (row block p % nrb2, split p / nrb2), which issue their
+// weight ring and then wait for act (activation_wave<..., CH>). Workgroups are dispatched in index
+// order, so every first-stage block has a slot before any second-stage block waits. The block has
+// NWG weight waves and the activation wave; a second-stage block uses NWD <= NWG weight waves and
+// its waves past the activation wave end at once (a barrier waits for the surviving waves only).
+template <int UG, int AWG, int UD, int AWD, int NWG, int NWD>
+__global__ __launch_bounds__(kMaxThreads) void k_mlp_chain_fp8(
+    const uint8_t* __restrict__ x, const uint8_t* __restrict__ wgu, const float* __restrict__ gsc, int g_per_row,
+    const uint8_t* __restrict__ wd, const float* __restrict__ dsc, int d_per_row, int64_t I, int64_t H, int kts_g,
+    int kts_d, int nfull, int nrb2, uint16_t* __restrict__ act, float* __restrict__ part, FusedArgs fa) {
+  static_assert(NWD <= NWG, "the block holds the second stage's waves");
+  const int w = static_cast<int>(blockIdx.x);
+  if (w < nfull) {
+    gemv_fp8_body<1, KRQ_OUT_SWIGLU, KRQ_W_TILED, KRQ_X_BF16_DYN, 1, UG, 1, false, AWG, true>(
+        x, nullptr, nullptr, 0, wgu, gsc, g_per_row, 1, I, H, kts_g, act, nullptr, fa, w, 0, NWG);
+  } else if (w < fa.n_first) {
+    gemv_fp8_body<1, kOutSwiGluHalf, KRQ_W_TILED, KRQ_X_BF16_DYN, 1, UG, 1, false, AWG, true>(
+        x, nullptr, nullptr, 0, wgu, gsc, g_per_row, 1, I, H, kts_g, act, nullptr, fa, (int64_t)w + nfull, 0, NWG);
+  } else {
+    if (__builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)) > NWD) return;
+    const int p = w - fa.n_first;
+    gemv_fp8_body<1, KRQ_OUT_PARTIAL, KRQ_W_TILED, KRQ_X_BF16_DYN, 1, UD, 1, false, AWD, true>(
+        reinterpret_cast<const uint8_t*>(act), nullptr, nullptr, 0, wd, dsc, d_per_row, 1, H, I, kts_d, part, nullptr,
+        fa, p % nrb2, p / nrb2, NWD);
+  }
 }
 
 // the fused kernel (fused_fp8.hip): RMSNorm prologue and / or residual epilogue

@@ -50,6 +50,9 @@ EXPORTS = {
     "krq_mlp_fp8_bounded": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _i32, _i64, _i64,
                                    _i64, _i32, _vp, _vp, _i32, ctypes.c_uint32, _vp, _vp]),
     "krq_mlp_ctl_words": (_i64, []),
+    "krq_mlp_chain_fp8": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _i32, _vp, _vp,
+                                 ctypes.c_uint32, _vp, _vp]),
+    "krq_mlp_chain_ctl_words": (_i64, []),
     "krq_gemv_bf16_fused": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _f32, _vp,
                                    _vp, _vp, _vp, _vp, _vp]),
     "krq_gemv_fused_fits": (_i64, [_i64, _i64, _i64, _i32, _i32, _i32]),

@@ -18,6 +18,13 @@ reference; the library clamps it to the blocks the device holds at once (so spin
 deadlock), and `programs=None` takes one per CU. Its control words are zeroed here once and left
 zeroed by every launch; a block whose phase-1 wait gives up writes NaN partials, and failed()
 reports it.
+
+chained=True (M == 1, tiled FP8 weights) runs the two-launch pair's kernels as one launch of
+k_mlp_chain_fp8 (krq_mlp_chain_fp8): the down workgroups issue their weight loads, then wait for
+every gate_up workgroup's act through arrival counters polled by scalar loads, and read act with
+coherent loads. act is bit-identical to the pair's; the partials equal the pair's to fp32
+rounding (the down blocks sum two weight waves). A wait that gives up makes that block's
+partials NaN and failed() reports it; zero_ctl() then clears the control words.
 """
 
 import torch
@@ -30,8 +37,10 @@ from . import gemv as _gemv
 class PersistentMLP:
     """Workspace for one M. Call with (h [M, H] bf16, w_gu [2I, H], w_down [H, I]) as FP8Weight."""
 
+    CHAIN_POLLS = 1 << 20  # bound on the chained form's wait: about a second of polls
+
     def __init__(self, M, H, I, device, programs=None, split=4, bn=16, bn2=16, chunk=512,
-                 one_launch=False):
+                 one_launch=False, chained=False):
         # the reference's shape contract (engine/kernels/mlp.py:100-103)
         assert I % chunk == 0 and chunk % bn == 0 and I % split == 0
         assert (I // split) % 64 == 0 and H % bn2 == 0
@@ -42,7 +51,11 @@ class PersistentMLP:
         self.M, self.H, self.I, self.G = M, H, I, programs
         self.split, self.bn, self.bn2, self.chunk = split, bn, bn2, chunk
         self.one_launch = one_launch
-        self.ctl = torch.zeros((int(L.lib().krq_mlp_ctl_words()),), device=device, dtype=torch.int32)
+        if chained and (one_launch or M != 1):
+            raise ValueError("PersistentMLP: the chained form takes M == 1 and excludes one_launch")
+        self.chained = chained
+        words = L.lib().krq_mlp_chain_ctl_words() if chained else L.lib().krq_mlp_ctl_words()
+        self.ctl = torch.zeros((int(words),), device=device, dtype=torch.int32)
         self.act = None   # bf16 [M, I] SwiGLU activations of the last call
 
     def _bf16(self, h, w_gu, w_down):
@@ -82,6 +95,16 @@ class PersistentMLP:
         M = h2.shape[0]
         if M != self.M:
             raise ValueError(f"PersistentMLP built for M={self.M}, called with M={M}")
+        if self.chained:
+            if lay_gu != L.W_TILED:
+                raise ValueError("PersistentMLP: the chained form takes tiled weights")
+            act = torch.empty((1, I), device=h.device, dtype=torch.bfloat16)
+            out = torch.empty((S, 1, H), device=h.device, dtype=torch.float32)
+            L.call("krq_mlp_chain_fp8", L.ptr(h2), L.ptr(gu), L.ptr(gs), g_pr, L.ptr(dn), L.ptr(ds), d_pr,
+                   H, I, S, L.ptr(act), L.ptr(self.ctl), int(self.CHAIN_POLLS if max_polls is None else max_polls),
+                   L.ptr(out), L.stream(h))
+            self.act = act
+            return out
         if not self.one_launch:
             act = _fp8.gemv_swiglu_fp8(h2, w_gu)
             self.act = act
@@ -105,9 +128,16 @@ class PersistentMLP:
         return out
 
     def failed(self):
-        """True if a one-launch call flagged a phase-1 wait that timed out (its partials are NaN);
-        synchronizes the device."""
-        return bool(self.ctl[-1].item())
+        """True if a one-launch or chained call flagged a wait that timed out (its partials are
+        NaN); synchronizes the device."""
+        return bool(self.ctl[self.CHAIN_ERR if self.chained else -1].item())
+
+    CHAIN_ERR = 513  # the chained form's error word (after 8 groups of 64 words and the exit count)
+
+    def zero_ctl(self):
+        """Clear the control words (needed after a wait gave up; every good launch leaves them
+        zero)."""
+        self.ctl.zero_()
 
 
 def mlp_fp8_static(h, gu8, down8, a_gu, a_down, split=1):

@@ -256,3 +256,105 @@ def test_swiglu_cast_is_the_cast_of_act(dev, M, sites):
             yf = y.float().cpu().numpy() if split == 1 else y.double().sum(0).cpu().numpy()
             _, yref = O.fp8_matmul(ref8, np.float32(sc.item()), u8(q_d[0]), q_d[1].cpu().numpy())
             assert rel_err(yf, yref) <= TOL, (headroom, split)
+
+
+# ---- the chained form: gate_up and down in one launch at M == 1 (krq_mlp_chain_fp8) ----
+
+# (H, I, split): Qwen3-4B (mixed gate_up plan, 19 steps per down split), a grid below one block
+# per CU, and an odd tile count per split (23 tiles: the last step's high tile masked)
+CHAIN_SHAPES = [(H, I, 4), (1024, 3072, 2), (512, 1472, 1)]
+
+
+
+@pytest.mark.parametrize("h_,i_,S", CHAIN_SHAPES)
+def test_mlp_chain_matches_pair_and_oracle(dev, h_, i_, S):
+    """Two different rows in a row (a stale line of the first call's act would show in the
+    second): act bit-identical to the two-launch pair's, partials equal to the pair's to fp32
+    rounding (a down block sums two weight waves where the standalone GEMV may use one), the last
+    call within the oracle's bar; the control words are zero after every call."""
+    wgu, wd, _ = case(1, h_, i_, 110)
+    qgu, qd = fp8.quantize(wgu.to(dev)), fp8.quantize(wd.to(dev))
+    pm = PersistentMLP(1, h_, i_, dev, split=S, chunk=64, chained=True)
+    g = torch.Generator().manual_seed(111)
+    for call in range(2):
+        x = (torch.randn(1, h_, generator=g) * (1 + 3 * call)).to(torch.bfloat16)
+        xd = x.to(dev)
+        out = pm(xd, qgu, qd)
+        a = fp8.gemv_swiglu_fp8(xd, qgu)
+        sep = fp8.gemv_fp8_bf16_launch(a, qd, S, L.OUT_PARTIAL, None, L.ALGO_AUTO)  # (fp32 also at S = 1)
+        torch.cuda.synchronize()
+        assert out.shape == (S, 1, h_) and out.dtype == torch.float32
+        assert torch.equal(pm.act, a), f"call {call}: act differs from the SwiGLU GEMV's"
+        y, ys = out.cpu().numpy(), sep.cpu().numpy()
+        e_pair = max(rel_err(y[s], ys[s]) for s in range(S))
+        print(f"chain H={h_} I={i_} S={S} call {call}: partials vs pair max-rel {e_pair:.2e}, "
+              f"bit-equal {float(np.mean(y == ys)):.3f}")
+        assert e_pair <= 1e-5
+        assert not pm.failed() and int(pm.ctl.abs().sum()) == 0
+    act_ref, parts = O.mlp_fp8(u16(x), u8(qgu[0]), qgu[1].cpu().numpy(), u8(qd[0]), qd[1].cpu().numpy(), S)
+    e_parts = max(rel_err(y[s], parts[s]) for s in range(S))
+    assert rel_err(pm.act.float().cpu().numpy(), O.bf16_to_f32(act_ref)) <= TOL
+    assert e_parts <= TOL and rel_err(y.sum(0), parts.sum(0)) <= TOL
+
+
+def test_mlp_chain_graph_replays(dev):
+    """Replays of a captured chained launch, with a new row copied in between and eager calls
+    between replays: every replay equals the eager result for its row (the control words reset
+    themselves, and act is read from memory, not from a line cached by an earlier replay)."""
+    wgu, wd, _ = case(1, H, I, 120)
+    qgu, qd = fp8.quantize(wgu.to(dev)), fp8.quantize(wd.to(dev))
+    g = torch.Generator().manual_seed(121)
+    xs = [torch.randn(1, H, generator=g).to(torch.bfloat16).to(dev) for _ in range(3)]
+    pm = PersistentMLP(1, H, I, dev, chained=True)
+    eager = [pm(x, qgu, qd).clone() for x in xs]
+    static_x = xs[0].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        pm(static_x, qgu, qd)
+    torch.cuda.current_stream().wait_stream(s)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        out = pm(static_x, qgu, qd)
+    for r in range(6):
+        static_x.copy_(xs[r % 3])
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager[r % 3]), r
+        assert torch.equal(pm(xs[(r + 1) % 3], qgu, qd), eager[(r + 1) % 3]), r
+    assert not pm.failed() and int(pm.ctl.abs().sum()) == 0
+    del gr
+
+
+def test_mlp_chain_wait_timeout_poisons_partials(dev):
+    """Waits bounded at one poll (forced from the host): a down block that gives up sets the
+    error word and writes NaN partials; every other partial equals the good launch's; the launch
+    ends. After zero_ctl() the next launch is good again and leaves the words zero."""
+    wgu, wd, x = case(1, H, I, 130)
+    qgu, qd = fp8.quantize(wgu.to(dev)), fp8.quantize(wd.to(dev))
+    xd = x.to(dev)
+    pm = PersistentMLP(1, H, I, dev, chained=True)
+    good = pm(xd, qgu, qd).clone()
+    out = pm(xd, qgu, qd, max_polls=1)
+    torch.cuda.synchronize()
+    nan = torch.isnan(out)
+    print(f"timed-out partials: {int(nan.sum())} of {out.numel()}, flagged {pm.failed()}")
+    assert torch.equal(out[~nan], good[~nan])
+    assert pm.failed() == bool(nan.any())
+    pm.zero_ctl()
+    assert torch.equal(pm(xd, qgu, qd), good) and not pm.failed()
+    assert int(pm.ctl.abs().sum()) == 0
+
+
+def test_mlp_chain_rejects_bad_plans(dev):
+    """M > 1, row-major weights and splits past the ring raise instead of launching."""
+    with pytest.raises(ValueError):
+        PersistentMLP(2, H, I, dev, chained=True)
+    wgu, wd, x = case(1, 512, 3072, 140)
+    qgu, qd = fp8.quantize(wgu.to(dev)), fp8.quantize(wd.to(dev))
+    pm = PersistentMLP(1, 512, 3072, dev, split=1, chained=True)  # 24 steps of 128 in one split
+    with pytest.raises(ValueError, match="ring"):
+        pm(x.to(dev), qgu, qd)
+    rgu, rd = fp8.FP8Weight(qgu[0], qgu[1], None), fp8.FP8Weight(qd[0], qd[1], None)
+    with pytest.raises(ValueError, match="tiled"):
+        PersistentMLP(1, 512, 3072, dev, split=2, chained=True)(x.to(dev), rgu, rd)
