@@ -175,7 +175,10 @@ void launch_xk(int xk, int algo, int pb, int awc, int u, bool rows, int M, dim3 
 
 // The SwiGLU as k_gemv_fp8_swiglu_mixed (nfull two-matrix blocks, then half-pair blocks) for the
 // kernels the plan picked: the one-row kernel beside its activation wave (five-slot rings) or the
-// multi-row ring on e4m3 rows (M <= 16). False for any other plan, which keeps the plain launch.
+// multi-row ring on e4m3 rows (one or two 16-row tiles). False for any other plan, which keeps the
+// plain launch. With two row tiles the block takes 228 VGPRs, so two fit per CU and the launch's
+// last blocks run in a second round: as half-pair blocks that round is half as long (gate_up at
+// M = 32: 13.1 -> 12.7 us).
 template <int XK>
 bool launch_swiglu_mixed(int awc, int u, bool rows, int M, int nfull, dim3 grid, int nthreads, size_t smem,
                          hipStream_t s, const uint8_t* xb, const float* x_scale, const float* x_inv, int x_per_row,
@@ -183,9 +186,13 @@ bool launch_swiglu_mixed(int awc, int u, bool rows, int M, int nfull, dim3 grid,
                          int kts, void* out, void* aux) {
   const dim3 block(nthreads);
   if constexpr (XK == KRQ_X_FP8 || XK == KRQ_X_FP8_TILED) {
-    if (!rows || M > 16 || u != 5) return false;
-    hipLaunchKernelGGL((k_gemv_fp8_swiglu_mixed<KRQ_W_TILED, XK, 1, 5, 0>), grid, block, smem, s, KRQ_GEMV_ARGS,
-                       nfull);
+    if (!rows || u != 5) return false;
+    if (M > 16)
+      hipLaunchKernelGGL((k_gemv_fp8_swiglu_mixed<KRQ_W_TILED, XK, 1, 5, 0, 2>), grid, block, smem, s, KRQ_GEMV_ARGS,
+                         nfull);
+    else
+      hipLaunchKernelGGL((k_gemv_fp8_swiglu_mixed<KRQ_W_TILED, XK, 1, 5, 0>), grid, block, smem, s, KRQ_GEMV_ARGS,
+                         nfull);
   } else {
     if (M != 1 || u != kSwiU) return false;
     if (awc == kAwRow)

@@ -552,19 +552,20 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(KRQ_FP8_KERNEL_PARAMS)
                                                                K, kts, out, aux, FusedArgs{}, blockIdx.x);
 }
 
-// The SwiGLU launch with its last column blocks split in half: workgroups below nfull are the
-// two-matrix blocks of output columns 16 i .. 16 i + 15; workgroup nfull + j is half-pair block
-// 2 nfull + j (columns 8 (2 nfull + j) ..), which streams half the bytes with the same steps per
-// wave. Workgroup i runs on compute unit i mod 256, so nfull = 512 puts two full blocks on every CU
-// and at most one half block more, instead of a third full block on some CUs.
-template <int LAYOUT, int XK, int ALGO, int U, int AWC>
+// The SwiGLU launch (MT 16-row tiles) with its last column blocks split in half: workgroups
+// below nfull are the two-matrix blocks of output columns 16 i .. 16 i + 15; workgroup nfull + j
+// is half-pair block 2 nfull + j (columns 8 (2 nfull + j) ..), which streams half the bytes with
+// the same steps per wave. Workgroup i runs on compute unit i mod 256, so nfull = 512 puts two
+// full blocks on every CU and at most one half block more, instead of a third full block on some
+// CUs.
+template <int LAYOUT, int XK, int ALGO, int U, int AWC, int MT = 1>
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8_swiglu_mixed(KRQ_FP8_KERNEL_PARAMS, int nfull) {
   if (static_cast<int>(blockIdx.x) < nfull)
-    gemv_fp8_body<1, KRQ_OUT_SWIGLU, LAYOUT, XK, ALGO, U, 1, false, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row,
+    gemv_fp8_body<MT, KRQ_OUT_SWIGLU, LAYOUT, XK, ALGO, U, 1, false, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row,
                                                                          M, NO, K, kts, out, aux, FusedArgs{},
                                                                          blockIdx.x);
   else
-    gemv_fp8_body<1, kOutSwiGluHalf, LAYOUT, XK, ALGO, U, 1, false, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row,
+    gemv_fp8_body<MT, kOutSwiGluHalf, LAYOUT, XK, ALGO, U, 1, false, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row,
                                                                          M, NO, K, kts, out, aux, FusedArgs{},
                                                                          (int64_t)blockIdx.x + nfull);
 }

@@ -54,15 +54,15 @@ def _bf16_ulp(v):
     return 2.0 ** (e - 7)
 
 
-def check_rows(idx, y, S, what):
+def check_rows(idx, y, S, what, k=K):
     """idx: the kernel's int64 [M]; y: exact logits float64 [M, V]; S: scaled sums of |products|
-    [M, V]. Asserts the identical index on every row the fp32 bound decides; returns the number of
-    rows inside the bound."""
+    [M, V]; k: the products per logit. Asserts the identical index on every row the fp32 bound
+    decides; returns the number of rows inside the bound."""
     ref = O.argmax_lowest(O.round_bf16(y.astype(np.float32)))
     inside = 0
     for m in range(y.shape[0]):
         ym, sm = y[m], S[m]
-        E = K * 2.0 ** -24 * sm + 2.0 ** -22 * np.abs(ym)
+        E = k * 2.0 ** -24 * sm + 2.0 ** -22 * np.abs(ym)
         top2 = np.partition(ym, -2)[-2:]
         y1, margin = top2[1], top2[1] - top2[0]
         ulp = _bf16_ulp(y1)
@@ -195,3 +195,35 @@ def test_lmhead_fp8_static_scale(dev, head):
     S = (np.abs(xf) @ head["w_pt_abs"].T) * sc
     assert rel_err(logits.float().cpu().numpy(), y) <= TOL
     check_rows(idx.cpu().numpy(), y, S, "fp8/tensor static M=16")
+
+
+@pytest.mark.parametrize("v,k,M", [(160, 2560, 2), (2080, 2560, 13), (40000, 2560, 16), (40000, 1024, 16),
+                                   (40000, 4096, 5), (40000, 1280, 16), (40000, 2688, 16)])
+def test_lmhead_fp8_tiled_h_shapes(dev, v, k, M):
+    """The FP8 head on tiled e4m3 rows of h. Where K / 128 is a multiple of 8 or 10 and K <= 4,096
+    it runs the persistent kernel (workgroups that hold h in LDS and stream row blocks), else the
+    kernel of one row block pair per workgroup (K = 2,688). The vocabularies leave some of the
+    persistent grid's waves without a row block (V = 160, 2,080) or give some waves one row block
+    more than others (V = 40,000). Against the exact oracle: ids equal the argmax of the kernel's
+    own logits, logits within the tolerance, every id the oracle's wherever the fp32 bound decides
+    it (check_rows), and the ids without the logits output the same."""
+    g = torch.Generator().manual_seed(v + k + M)
+    W = (torch.randn(v, k, generator=g) * 0.02).to(torch.bfloat16)
+    h = torch.randn(M, k, generator=g).to(torch.bfloat16)
+    q = fp8.quantize(W.to(dev))
+    w = O.e4m3_decode(u8(q[0])).astype(np.float64)
+    s = q[1].cpu().numpy().astype(np.float64)
+    hd = h.to(dev)
+    idx, logits = lmhead.lm_head_argmax(hd, q, return_logits=True, h_layout="tiled")
+    r8, rs = O.quant_rows(u16(h))
+    xf = O.e4m3_decode(r8).astype(np.float64)
+    scale = rs.astype(np.float64)[:, None] * s[None, :]
+    y = (xf @ w.T) * scale
+    S = (np.abs(xf) @ np.abs(w).T) * scale
+    idx = idx.cpu().numpy()
+    lg = logits.float().cpu().numpy()
+    assert np.array_equal(idx, O.argmax_lowest(lg))
+    assert rel_err(lg, y) <= TOL
+    inside = check_rows(idx, y, S, f"tiled h V={v} K={k} M={M}", k=k)
+    assert inside <= max(1, M // 2)
+    assert np.array_equal(lmhead.lm_head_argmax(hd, q, h_layout="tiled").cpu().numpy(), idx)
