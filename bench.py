@@ -426,6 +426,58 @@ def summarize_trace(csv_path):
     return {k: {"all": stats(d["all"]), "b2b": stats(d["b2b"])} for k, d in out.items() if k.startswith("k_")}
 
 
+# The kernel template each step projection runs (tiled weights), per M: the keys of the counter
+# summaries profiles/traffic_c2.json / traffic_c3.json that --summarize-pmc writes.
+STEP_KERNELS = {
+    1: {"qkv": "k_gemv_fp8<1, 1, 1, 1, 1, 10, 1, 5>", "o": "k_gemv_fp8<1, 1, 1, 1, 1, 8, 1, 8>",
+        "gate_up": "k_gemv_fp8_swiglu_mixed<1, 1, 1, 5, 5, 1>", "down": "k_gemv_fp8<1, 1, 1, 1, 1, 20, 1, 20>"},
+    16: {"qkv": "k_gemv_fp8<1, 1, 1, 3, 1, 10, 1, 0>", "o": "k_gemv_fp8<1, 1, 1, 3, 1, 8, 1, 0>",
+         "gate_up": "k_gemv_fp8_swiglu_mixed<1, 3, 1, 5, 0, 1>", "down": "k_gemv_fp8<1, 1, 1, 3, 1, 5, 1, 0>"},
+}
+PMC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --output-format csv -d <out> -o pmc -- python3 bench.py "
+              "--no-cpu --no-prefill --no-extra --steps 36 --warmup 2 --reps 36 --replays 1 --calibrate-copy; "
+              "then python3 bench.py --summarize-pmc <fetch>/pmc_counter_collection.csv "
+              "<write>/pmc_counter_collection.csv <dir>")
+
+
+def summarize_pmc(fetch_csv, write_csv, out_dir):
+    """HBM bytes per dispatch of the step kernels from two rocprofv3 --pmc runs (FETCH_SIZE, then
+    WRITE_SIZE, KiB per dispatch), each scaled by what the counter reads for the run's 256 MiB
+    device copy (--calibrate-copy: 268,435,456 bytes read and written). Writes traffic_c2.json
+    (M = 1) and traffic_c3.json (M = 16) into out_dir; returns their paths."""
+    import csv
+    from collections import defaultdict
+
+    def load(path, counter):
+        vals = defaultdict(list)
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] == counter:
+                vals[kernel_template(r["Kernel_Name"])].append(float(r["Counter_Value"]))
+        return vals
+    F, W = load(fetch_csv, "FETCH_SIZE"), load(write_csv, "WRITE_SIZE")
+    copy_f = [max(v) for k, v in F.items() if "copyBuffer" in k]
+    copy_w = [max(v) for k, v in W.items() if "copyBuffer" in k]
+    if not copy_f or not copy_w:
+        raise SystemExit("summarize-pmc: no device copy in the runs (run bench.py with --calibrate-copy)")
+    fs, ws = max(copy_f) * 1024 / (256 << 20), max(copy_w) * 1024 / (256 << 20)
+    paths = []
+    for M, cfg in ((1, "c2"), (16, "c3")):
+        out = {"config": cfg, "M": M, "fetch_scale": fs, "write_scale": ws, "source": PMC_SOURCE, "projections": {}}
+        for proj, k in STEP_KERNELS[M].items():
+            if k not in F or k not in W:
+                raise SystemExit(f"summarize-pmc: {k} ({proj}, M={M}) is not in the runs")
+            f, w = sorted(F[k]), sorted(W[k])
+            out["projections"][proj] = {
+                "kernel": k, "read_bytes_median": median(f) * 1024 / fs, "write_bytes_median": median(w) * 1024 / ws,
+                "read_bytes_max": f[-1] * 1024 / fs, "dispatches": len(f), "fetch_kib_median": median(f),
+                "fetch_kib_max": f[-1], "write_kib_median": median(w)}
+        path = os.path.join(out_dir, f"traffic_{cfg}.json")
+        with open(path, "w") as fh:
+            json.dump(out, fh, indent=1)
+        paths.append(path)
+    return paths
+
+
 def traced_us(kernel):
     """Average traced duration (us) of `kernel` over its back-to-back dispatches, from the committed
     kernel-trace summary profiles/gemv_fp8_decode_trace.json (bench.py --summarize-trace), or None."""
@@ -609,14 +661,20 @@ def main():
                     help="skip the C4 / C5 / M = 32 summaries of the default line (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 256 MiB device copy (known bytes) to scale HBM counters")
+    ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "DIR"), default=None,
+                    help="write DIR/traffic_c2.json and traffic_c3.json from the two counter runs and exit")
     ap.add_argument("--summarize-trace", metavar="CSV", default=None,
                     help="no GPU work: print the per-kernel duration summary of a rocprofv3 kernel-trace CSV "
                     "(this build's kernels; the JSON of profiles/gemv_fp8_decode_trace.json) and exit")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        for path in summarize_pmc(*args.summarize_pmc):
+            print(path)
+        return
     if args.summarize_trace:
         print(json.dumps({"source": "rocprofv3 --kernel-trace --stats --output-format csv -d <out> -o kt -- "
-                          "python3 bench.py --no-cpu --no-prefill; then python3 bench.py --summarize-trace "
-                          "<out>/kt_kernel_trace.csv", "kernels": summarize_trace(args.summarize_trace)},
+                          "python3 bench.py --no-cpu --no-prefill --no-extra; then python3 bench.py "
+                          "--summarize-trace <out>/kt_kernel_trace.csv", "kernels": summarize_trace(args.summarize_trace)},
                          indent=1, sort_keys=True))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
