@@ -283,6 +283,22 @@ int krq_mlp_chain_fp8(const void* x, const void* w_gu, const float* gu_scale, in
 int64_t krq_mlp_chain_ctl_words(void);
 
 /*
+ * The decode MLP on BF16 weights in ONE launch (reference engine/kernels/mlp.py:22-118
+ * PersistentMLP.__call__ with the engine's bf16 weights, engine/engine.py:911-915): act =
+ * SwiGLU(x . [gate; up]^T) (bf16 [M, I]) and out = the fp32 [split, M, H] split-K partials of
+ * act . w_down^T, bit-identical to krq_gemv_bf16 KRQ_OUT_SWIGLU followed by krq_gemv_bf16
+ * KRQ_OUT_PARTIAL: each stage runs the plan krq_gemv_bf16 gives it. x bf16 [M, H] (1 <= M <= 32);
+ * w_gu [2I, H] and w_down [H, I] bf16, both in w_layout (KRQ_W_ROWMAJOR, or KRQ_W_TILED copies
+ * from krq_pack_fp8 over 2K-byte rows). The down workgroups issue their first weight loads, then
+ * wait for every gate_up workgroup's act (ctl and max_polls as krq_mlp_chain_fp8; a wait that
+ * gives up sets word 513 and makes that block's partials NaN).
+ * Needs H % 32 == 0, I % 16 == 0, (I/split) % 32 == 0, and fewer than 4096 down blocks
+ * (H/16 * split) above 4 rows (krq_gemv_bf16 pairs row blocks there).
+ */
+int krq_mlp_chain_bf16(const void* x, const void* w_gu, const void* w_down, int w_layout, int64_t M, int64_t H,
+                       int64_t I, int split, void* act, uint32_t* ctl, uint32_t max_polls, void* out, void* stream);
+
+/*
  * BF16 GEMV with the RMSNorm prologue and the residual epilogue folded in: gemv_fused /
  * gemv_swiglu_fused (reference engine/kernels/fused_gemv.py:48-221, called at
  * engine/engine.py:953-961).

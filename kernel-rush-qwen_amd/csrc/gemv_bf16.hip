@@ -16,19 +16,30 @@ namespace {
 // 4 for the multi-row lm_head, where every 16-column block re-reads the bf16 rows from L2).
 // bx: the column block this workgroup owns (its two-matrix, paired or single row block, or with
 // MODE kOutSwiGluHalf its half-pair block).
-template <int MT, int MODE, int LAYOUT, int ALGO, int U, int PB>
+// CHAIN (the chained BF16 MLP, k_mlp_chain_bf16): a SwiGLU block writes act through to memory and
+// counts itself into the first-stage counters; a split-K (partials) block is a second-stage block
+// on act, which issues its weight loads, waits for the first stage's done flag (chain_wait; a wait
+// that gives up makes the block's partials NaN) and then reads act with agent-scope (sc1) loads,
+// and counts its exit. sy >= 0 / nwo > 0: the block's K split and its wave count, given (the
+// chained kernel's one-dimensional grid and common block size); waves past nwo end at once.
+template <int MT, int MODE, int LAYOUT, int ALGO, int U, int PB, bool CHAIN = false>
 KRQ_DEV void gemv_bf16_body(const uint8_t* __restrict__ x, const uint8_t* __restrict__ w, int M, int64_t NO,
-                            int64_t K, int kts, void* __restrict__ out, void* __restrict__ aux, int64_t bx) {
+                            int64_t K, int kts, void* __restrict__ out, void* __restrict__ aux, int64_t bx,
+                            int sy = -1, int nwo = 0, const FusedArgs* fa = nullptr) {
   extern __shared__ __align__(16) float red[];
   __shared__ float ones[32];
   static_assert(PB == 1 || (MODE != KRQ_OUT_SWIGLU && ALGO != 2), "paired row blocks: MFMA, no SwiGLU");
   static_assert(PB == 1 || PB == 2 || PB == 4, "one, two or four row blocks per block");
+  static_assert(!CHAIN || (PB == 1 && (MODE == KRQ_OUT_SWIGLU || MODE == kOutSwiGluHalf || MODE == KRQ_OUT_PARTIAL)),
+                "chained MLP: SwiGLU first stage, partials second stage");
+  constexpr bool WAITS = CHAIN && MODE == KRQ_OUT_PARTIAL;  // (second stage)
   constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : PB;  // weight row blocks streamed per step
   constexpr int NV = MT * 256;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = nwo > 0 ? nwo : blockDim.x >> 6;
+  if (CHAIN && __builtin_amdgcn_readfirstlane(wave) >= nw) return;
   const int r = lane & 15, g = lane >> 4;
   const int64_t rb = bx * PB;
-  const int sidx = blockIdx.y;
+  const int sidx = sy >= 0 ? sy : static_cast<int>(blockIdx.y);
   const int nsteps = (kts + 1) >> 1;
   const int64_t tbase = (int64_t)sidx * kts;
   const int64_t rowb = 2 * K;
@@ -51,7 +62,10 @@ KRQ_DEV void gemv_bf16_body(const uint8_t* __restrict__ x, const uint8_t* __rest
   // outstanding loads at the join): a slot past this wave's last step reloads that step (already
   // in flight or cached) and is masked where consumed; rows m >= M read row M - 1, whose products
   // land in accumulator rows the epilogue never writes.
-  auto load_slot = [&](int u, int cc) {
+  // (WAITS: act, written in this launch on every XCD, read with sc1 loads through a buffer resource)
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(x), (short)0, WAITS ? static_cast<int>(M * rowb) : 0, 0x00020000);
+  auto load_w = [&](int u, int cc) {
     const int j = jcount > 0 ? wave + min(cc, jcount - 1) * nw : 0;
     const int64_t t0 = tbase + 2 * j;
     const int64_t t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
@@ -65,13 +79,28 @@ KRQ_DEV void gemv_bf16_body(const uint8_t* __restrict__ x, const uint8_t* __rest
         wh[p][u] = ld16nt(w_addr<LAYOUT>(w, rbp(p), t1, rowb, lane));
       }
     }
+  };
+  auto load_x = [&](int u, int cc) {
+    const int j = jcount > 0 ? wave + min(cc, jcount - 1) * nw : 0;
+    const int64_t t0 = tbase + 2 * j;
+    const int64_t t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int m = ALGO == 2 ? 0 : min(mt * 16 + r, M - 1);
-      const uint8_t* xr = x + (int64_t)m * rowb + g * 16;
-      xl[u][mt] = ld16(xr + t0 * 64);
-      xh[u][mt] = ld16(xr + t1 * 64);
+      if constexpr (WAITS) {
+        const int o = static_cast<int>((int64_t)m * rowb + g * 16);
+        xl[u][mt] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, o + static_cast<int>(t0 * 64), 0, 16));
+        xh[u][mt] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, o + static_cast<int>(t1 * 64), 0, 16));
+      } else {
+        const uint8_t* xr = x + (int64_t)m * rowb + g * 16;
+        xl[u][mt] = ld16(xr + t0 * 64);
+        xh[u][mt] = ld16(xr + t1 * 64);
+      }
     }
+  };
+  auto load_slot = [&](int u, int cc) {
+    load_w(u, cc);
+    load_x(u, cc);
   };
   auto consume_slot = [&](int u, int cc) {
     const int j = jcount > 0 ? wave + min(cc, jcount - 1) * nw : 0;
@@ -91,12 +120,32 @@ KRQ_DEV void gemv_bf16_body(const uint8_t* __restrict__ x, const uint8_t* __rest
       }
     }
   };
+  bool chain_bad = false;
+  if constexpr (WAITS) {  // the weights first, then the wait, then act
 #pragma unroll
-  for (int u = 0; u < U; ++u) load_slot(u, u);
+    for (int u = 0; u < U; ++u) load_w(u, u);
+    chain_bad = !chain_wait(*fa);
+#pragma unroll
+    for (int u = 0; u < U; ++u) load_x(u, u);
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) load_slot(u, u);
+  }
   __builtin_amdgcn_sched_barrier(0);
   // the last batch is peeled off (consume only), so no load sits behind a branch and the first
   // batch's loads stay ahead of everything else
   int base = 0;
+  if constexpr (WAITS) {
+    // One batch peeled off, unconditionally (past jcount it reloads the last step and consumes
+    // nothing): the first batch's loads went out weights first, act after the wait, and a loop
+    // entered with them in that order waits for every load on its first pass.
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      consume_slot(u, u);
+      load_slot(u, u + U);
+    }
+    base = U;
+  }
   for (; base + U < jcount; base += U) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -117,6 +166,12 @@ KRQ_DEV void gemv_bf16_body(const uint8_t* __restrict__ x, const uint8_t* __rest
       acc[p][0] = v4f{g == 0 ? a : 0.f, 0.f, 0.f, 0.f};
     }
   }
+  if (WAITS && chain_bad) {  // (the wait gave up: every partial of the block is NaN)
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[p][mt] = v4f{NAN, NAN, NAN, NAN};
+  }
   // the P accumulator sets of each wave, in the layout epilogue() reads
 #pragma unroll
   for (int p = 0; p < P; ++p)
@@ -126,12 +181,15 @@ KRQ_DEV void gemv_bf16_body(const uint8_t* __restrict__ x, const uint8_t* __rest
       for (int i = 0; i < 4; ++i) red[(wave * P + p) * NV + mt * 256 + i * 64 + lane] = acc[p][mt][i];
   __syncthreads();
   if (MODE == KRQ_OUT_SWIGLU) {
-    epilogue<MT, MODE, P>(red, 0, nw, M, NO, rb, sidx, ones, ColScales{1.0f, 1.0f}, out, aux);
+    epilogue<MT, MODE, P, CHAIN>(red, 0, nw, M, NO, rb, sidx, ones, ColScales{1.0f, 1.0f}, out, aux,
+                                 CHAIN ? nw * kWave : 0);
   } else {
 #pragma unroll
     for (int p = 0; p < PB; ++p)
-      epilogue<MT, MODE, P>(red, p, nw, M, NO, rb + p, sidx, ones, ColScales{1.0f, 1.0f}, out, aux);
+      epilogue<MT, MODE, P, CHAIN>(red, p, nw, M, NO, rb + p, sidx, ones, ColScales{1.0f, 1.0f}, out, aux,
+                                   CHAIN ? nw * kWave : 0);
   }
+  if constexpr (CHAIN) chain_tail<!WAITS>(*fa);
 }
 
 template <int MT, int MODE, int LAYOUT, int ALGO, int U, int PB>
@@ -155,6 +213,33 @@ __global__ __launch_bounds__(512) void k_gemv_bf16_swiglu_mixed(const uint8_t* _
   else
     gemv_bf16_body<1, kOutSwiGluHalf, LAYOUT, ALGO, U, 1>(x, w, M, NO, K, kts, out, aux,
                                                           (int64_t)blockIdx.x + nfull);
+}
+
+// The chained BF16 MLP (krq_mlp_chain_bf16): act = SwiGLU(x . Wgu^T) and the split-K partials of
+// act . Wd^T in one launch. Workgroups below fa.n_first are the SwiGLU launch's blocks (two-matrix
+// blocks below nfull, then half-pair blocks, as k_gemv_bf16_swiglu_mixed, when MT == 1), with
+// NWG waves; the rest are the down launch's blocks with NWD waves, block p at row block p % nrb2
+// of K split p / nrb2. Each stage keeps the standalone launch's plan, so act and the partials are
+// those of the two launches, bit for bit. The block holds max(NWG, NWD) waves; the waves a stage
+// does not use end at once (a barrier waits only for the waves that have not ended).
+template <int MT, int LAYOUT, int ALGO, int U>
+__global__ __launch_bounds__(512) void k_mlp_chain_bf16(const uint8_t* __restrict__ x, const uint8_t* __restrict__ wgu,
+                                                       const uint8_t* __restrict__ wd, int M, int64_t I, int64_t H,
+                                                       int kts_g, int kts_d, int nfull, int nrb2, int nwg, int nwd,
+                                                       uint16_t* __restrict__ act, float* __restrict__ part,
+                                                       FusedArgs fa) {
+  const int w = static_cast<int>(blockIdx.x);
+  if (w < nfull) {
+    gemv_bf16_body<MT, KRQ_OUT_SWIGLU, LAYOUT, ALGO, U, 1, true>(x, wgu, M, I, H, kts_g, act, nullptr, w, 0, nwg, &fa);
+  } else if (w < fa.n_first) {
+    if constexpr (MT == 1)
+      gemv_bf16_body<1, kOutSwiGluHalf, LAYOUT, ALGO, U, 1, true>(x, wgu, M, I, H, kts_g, act, nullptr,
+                                                                  (int64_t)w + nfull, 0, nwg, &fa);
+  } else {
+    const int p = w - fa.n_first;
+    gemv_bf16_body<MT, KRQ_OUT_PARTIAL, LAYOUT, ALGO, U, 1, true>(reinterpret_cast<const uint8_t*>(act), wd, M, H, I,
+                                                                  kts_d, part, nullptr, p % nrb2, p / nrb2, nwd, &fa);
+  }
 }
 
 // Persistent row partition (the reference's gemv_rows, engine/kernels/gemv.py:270-348): exactly
@@ -402,4 +487,66 @@ extern "C" int krq_gemv_bf16_rows(const void* x, const void* w, int64_t M, int64
       hipLaunchKernelGGL((k_gemv_bf16_rows<2, 1, 4>), grid, block, 0, s, xb, wb, m, N, K, out);
   }
   return krq_check_launch("gemv_rows");
+}
+
+// The chained BF16 MLP (k_mlp_chain_bf16): both stages of the decode MLP in one launch, each with
+// the plan krq_gemv_bf16 gives it (the SwiGLU launch and the split-K partials launch).
+extern "C" int krq_mlp_chain_bf16(const void* x, const void* w_gu, const void* w_down, int w_layout, int64_t M,
+                                  int64_t H, int64_t I, int split, void* act, uint32_t* ctl, uint32_t max_polls,
+                                  void* out, void* stream) {
+  KRQ_REQUIRE(x && w_gu && w_down && act && ctl && out, "mlp_chain_bf16: null pointer");
+  KRQ_REQUIRE(aligned16(x) && aligned16(w_gu) && aligned16(w_down) && aligned16(act),
+              "mlp_chain_bf16: x, weights and act must be 16-byte aligned");
+  KRQ_REQUIRE(w_layout == KRQ_W_ROWMAJOR || w_layout == KRQ_W_TILED, "mlp_chain_bf16: bad layout %d", w_layout);
+  KRQ_REQUIRE(M >= 1 && M <= 32, "mlp_chain_bf16: M=%lld outside 1..32", (long long)M);
+  KRQ_REQUIRE(H > 0 && I > 0 && H % 32 == 0 && I % 16 == 0 && split >= 1 && I % split == 0 &&
+                  (I / split) % 32 == 0,
+              "mlp_chain_bf16: shape H=%lld I=%lld split=%d (H and I/split multiples of 32, I of 16)",
+              (long long)H, (long long)I, split);
+  KRQ_REQUIRE(M * 2 * I <= 0x7fffffff && I / 16 <= 0x7fffffff && split <= 65535,
+              "mlp_chain_bf16: shape too large");
+  KRQ_REQUIRE(max_polls > 0, "mlp_chain_bf16: max_polls must be positive");
+  const int64_t nrb2 = H / 16, n_second = nrb2 * split;
+  // the down launch pairs row blocks on grids of thousands of blocks above 4 rows; the chained
+  // kernel keeps one row block per block, so it takes only the unpaired plan
+  KRQ_REQUIRE(!(M > 4 && nrb2 % 2 == 0 && n_second >= 4096),
+              "mlp_chain_bf16: %lld down blocks at M=%lld (the chained form takes fewer than 4096 above 4 rows)",
+              (long long)n_second, (long long)M);
+  const int U = M <= 4 ? 4 : 2, MT = M <= 16 ? 1 : 2;  // (launch()'s variant)
+  const int kts_g = static_cast<int>(H / 32), kts_d = static_cast<int>(I / split / 32);
+  // gate_up: the SwiGLU launch's plan (two-matrix blocks, the last ones as half-pair blocks)
+  const int64_t nrbs = I / 16, rem = nrbs % kCUs;
+  const bool mixed = M <= 16 && nrbs > 2 * kCUs && rem != 0 && 2 * rem <= kCUs;
+  const int64_t nfull = mixed ? nrbs - rem : nrbs, n_first = mixed ? nfull + 2 * rem : nrbs;
+  KRQ_REQUIRE(n_first + n_second <= 0x7fffffff, "mlp_chain_bf16: grid too large");
+  const int nwg = plan_waves((kts_g + 1) / 2, 2, U, nrbs), nwd = plan_waves((kts_d + 1) / 2, 1, U, n_second);
+  const int nwb = std::max(nwg, nwd);
+  const size_t smem = std::max((size_t)nwg * 2, (size_t)nwd) * MT * 256 * sizeof(float);
+  FusedArgs fa{};
+  fa.cnt = ctl;
+  fa.max_polls = max_polls;
+  fa.n_first = static_cast<int>(n_first);
+  fa.n_second = static_cast<int>(n_second);
+  const dim3 grid(static_cast<unsigned>(n_first + n_second)), block(nwb * 64);
+  hipStream_t s = (hipStream_t)stream;
+  const uint8_t* xb = (const uint8_t*)x;
+  const uint8_t* gb = (const uint8_t*)w_gu;
+  const uint8_t* db = (const uint8_t*)w_down;
+  const int m = static_cast<int>(M);
+#define KRQ_CHAIN(MT_, LAYOUT, ALGO, U_)                                                                          \
+  hipLaunchKernelGGL((k_mlp_chain_bf16<MT_, LAYOUT, ALGO, U_>), grid, block, smem, s, xb, gb, db, m, I, H, kts_g, \
+                     kts_d, static_cast<int>(nfull), static_cast<int>(nrb2), nwg, nwd, (uint16_t*)act, (float*)out, fa)
+#define KRQ_CHAIN_M(LAYOUT)                          \
+  if (M == 1) KRQ_CHAIN(1, LAYOUT, 2, 4);            \
+  else if (M <= 4) KRQ_CHAIN(1, LAYOUT, 1, 4);       \
+  else if (M <= 16) KRQ_CHAIN(1, LAYOUT, 1, 2);      \
+  else KRQ_CHAIN(2, LAYOUT, 1, 2);
+  if (w_layout == KRQ_W_TILED) {
+    KRQ_CHAIN_M(KRQ_W_TILED)
+  } else {
+    KRQ_CHAIN_M(KRQ_W_ROWMAJOR)
+  }
+#undef KRQ_CHAIN_M
+#undef KRQ_CHAIN
+  return krq_check_launch("mlp_chain_bf16");
 }

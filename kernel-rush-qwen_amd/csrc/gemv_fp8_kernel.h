@@ -89,20 +89,7 @@ KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restr
   constexpr int SC = NORM ? kSsPerLane : 1;
   static_assert(!CH || (XK == KRQ_X_BF16_DYN && !NORM), "chained stage: one bf16 row scaled per token");
   bool chain_bad = false;
-  if constexpr (CH) {
-    // this workgroup's replica of the done flag (an address held in scalar registers)
-    const uint32_t* rep = fa.cnt + kChainRep + kChainRepStride * static_cast<int>(blockIdx.x % kChainReps);
-    uint32_t polls = 0, done = 0;
-    for (;;) {
-      // the load and its wait in one statement, the destination early-clobber (a load in flight
-      // still writes its register)
-      asm volatile("s_load_dword %0, %1, 0x0 glc\n\ts_waitcnt lgkmcnt(0)" : "=&s"(done) : "s"(rep) : "memory");
-      if (done != 0 || ++polls > fa.max_polls) break;
-      __builtin_amdgcn_s_sleep(1);
-    }
-    chain_bad = done == 0;
-    if (chain_bad && lane == 0) cstore(fa.cnt + kChainErr, 1u);
-  }
+  if constexpr (CH) chain_bad = !chain_wait(fa);
   __builtin_amdgcn_s_setprio(3);
   // DYN: chunk i = lane + 64 c of the row holds elements 8i .. 8i + 7 (indices past the row repeat
   // its last chunk); STATIC: the same over the slice
@@ -165,52 +152,6 @@ KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restr
           XK == KRQ_X_BF16_DYN ? quant8_own_amax(v[c], inv) : quant8_clamped(v[c], inv);
   }
   __builtin_amdgcn_s_setprio(0);
-}
-
-// End of a chained-MLP block (every thread of the block, or every thread of its wave 0, calls it).
-// First stage: once every thread's act stores have completed, one arrival on the block's group
-// counter; the group's last arrival counts the group complete, and the last group complete sets
-// every replica of the done flag (one store per lane of wave 0). Second stage: one exit on its
-// group; the group's last exit counts the group done, and the last group done zeroes every control
-// word. By then every second-stage block has passed its wait, so no word is read again in this
-// launch. (Counters that only grow, with the launch number published instead of a flag, need no
-// zeroing but measured slower: 32 against 19 us per Qwen3-4B MLP.)
-template <bool FIRST>
-KRQ_DEV void chain_tail(const FusedArgs& fa) {
-  const int g = static_cast<int>(blockIdx.x) % kChainGroups;
-  const int lane = threadIdx.x & 63;
-  // workgroups lo .. hi - 1 whose index is q mod kChainGroups
-  auto in_group = [](int q, int lo, int hi) {
-    const int first = lo + ((q - lo % kChainGroups) % kChainGroups + kChainGroups) % kChainGroups;
-    return first < hi ? (hi - 1 - first) / kChainGroups + 1 : 0;
-  };
-  auto groups_of = [&](int lo, int hi) {
-    int n = 0;
-    for (int q = 0; q < kChainGroups; ++q) n += in_group(q, lo, hi) > 0 ? 1 : 0;
-    return n;
-  };
-  if constexpr (FIRST) {
-    stores_done();
-    __syncthreads();
-  }
-  if (threadIdx.x >= 64) return;
-  uint32_t last = 0;
-  if (lane == 0) {
-    const int lo = FIRST ? 0 : fa.n_first, hi = FIRST ? fa.n_first : fa.n_first + fa.n_second;
-    if (cadd(fa.cnt + 64 * g + (FIRST ? 0 : 1), 1u) == static_cast<uint32_t>(in_group(g, lo, hi) - 1))
-      last = cadd(fa.cnt + (FIRST ? kChainArr : kChainExit), 1u) == static_cast<uint32_t>(groups_of(lo, hi) - 1);
-  }
-  if (!__shfl(last, 0, kWave)) return;
-  if constexpr (FIRST) {
-    cstore(fa.cnt + kChainRep + kChainRepStride * lane, 1u);
-  } else {
-    cstore(fa.cnt + kChainRep + kChainRepStride * lane, 0u);
-    if (lane < 2 * kChainGroups) cstore(fa.cnt + 64 * (lane >> 1) + (lane & 1), 0u);
-    if (lane == 0) {
-      cstore(fa.cnt + kChainArr, 0u);
-      cstore(fa.cnt + kChainExit, 0u);
-    }
-  }
 }
 
 // PB = 2 (MFMA kernels, modes other than SwiGLU): the block owns two adjacent row blocks, so each

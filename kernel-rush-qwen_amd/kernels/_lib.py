@@ -53,6 +53,8 @@ EXPORTS = {
     "krq_mlp_chain_fp8": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _i32, _vp, _vp,
                                  ctypes.c_uint32, _vp, _vp]),
     "krq_mlp_chain_ctl_words": (_i64, []),
+    "krq_mlp_chain_bf16": (_i32, [_vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _vp, ctypes.c_uint32, _vp,
+                                  _vp]),
     "krq_gemv_bf16_fused": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _f32, _vp,
                                    _vp, _vp, _vp, _vp, _vp]),
     "krq_gemv_fused_fits": (_i64, [_i64, _i64, _i64, _i32, _i32, _i32]),

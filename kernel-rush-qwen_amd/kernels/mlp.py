@@ -25,6 +25,11 @@ every gate_up workgroup's act through arrival counters polled by scalar loads, a
 coherent loads. act is bit-identical to the pair's; the partials equal the pair's to fp32
 rounding (the down blocks sum two weight waves). A wait that gives up makes that block's
 partials NaN and failed() reports it; zero_ctl() then clears the control words.
+
+For BF16 weights, one_launch=True or chained=True (any M) runs the chained launch of the BF16
+GEMVs, k_mlp_chain_bf16 (krq_mlp_chain_bf16): each stage keeps its standalone launch's plan, so
+act and the partials are the two-launch pair's, bit for bit; waits, failed() and zero_ctl() as
+above.
 """
 
 import torch
@@ -51,24 +56,42 @@ class PersistentMLP:
         self.M, self.H, self.I, self.G = M, H, I, programs
         self.split, self.bn, self.bn2, self.chunk = split, bn, bn2, chunk
         self.one_launch = one_launch
-        if chained and (one_launch or M != 1):
-            raise ValueError("PersistentMLP: the chained form takes M == 1 and excludes one_launch")
+        if chained and one_launch:
+            raise ValueError("PersistentMLP: the chained form excludes one_launch")
         self.chained = chained
-        words = L.lib().krq_mlp_chain_ctl_words() if chained else L.lib().krq_mlp_ctl_words()
+        words = L.lib().krq_mlp_ctl_words()
+        self._mlp_err = int(words) - 1  # krq_mlp_fp8's error word: its last control word
+        if chained or one_launch:  # (one_launch with BF16 weights runs the chained form)
+            words = max(int(words), int(L.lib().krq_mlp_chain_ctl_words()))
         self.ctl = torch.zeros((int(words),), device=device, dtype=torch.int32)
         self.act = None   # bf16 [M, I] SwiGLU activations of the last call
+        self._err = self._mlp_err  # the error word of the form that ran last
 
-    def _bf16(self, h, w_gu, w_down):
-        H, I = self.H, self.I
+    def _bf16(self, h, w_gu, w_down, max_polls):
+        H, I, S = self.H, self.I, self.split
         if tuple(w_gu.shape) != (2 * I, H) or tuple(w_down.shape) != (H, I):
             raise ValueError(f"PersistentMLP: weights {tuple(w_gu.shape)} / {tuple(w_down.shape)} do not "
                              f"match H={H}, I={I}")
         h2 = _fp8._rows(h)
-        if h2.shape[0] != self.M:
-            raise ValueError(f"PersistentMLP built for M={self.M}, called with M={h2.shape[0]}")
-        act = _gemv.gemv_swiglu(h2, w_gu)
+        M = h2.shape[0]
+        if M != self.M:
+            raise ValueError(f"PersistentMLP built for M={self.M}, called with M={M}")
+        if not (self.chained or self.one_launch):
+            act = _gemv.gemv_swiglu(h2, w_gu)
+            self.act = act
+            return _gemv.gemv(act, w_down, S)
+        L.require_device(h2, w_gu, w_down)
+        gu, lay_gu = _gemv._weight(w_gu)
+        dn, lay_dn = _gemv._weight(w_down)
+        if lay_gu != lay_dn:
+            raise ValueError("PersistentMLP: gate/up and down weights must share a layout (pack both or neither)")
+        act = torch.empty((M, I), device=h.device, dtype=torch.bfloat16)
+        out = torch.empty((S, M, H), device=h.device, dtype=torch.float32)
+        self._err = self.CHAIN_ERR
+        L.call("krq_mlp_chain_bf16", L.ptr(h2), L.ptr(gu), L.ptr(dn), lay_gu, M, H, I, S, L.ptr(act),
+               L.ptr(self.ctl), int(self.CHAIN_POLLS if max_polls is None else max_polls), L.ptr(out), L.stream(h))
         self.act = act
-        return _gemv.gemv(act, w_down, self.split)
+        return out
 
     def __call__(self, h, w_gu, w_down, max_polls=None):
         """max_polls (one-launch form): bound on the phase-1 wait's polls (default: about a
@@ -76,7 +99,7 @@ class PersistentMLP:
         if isinstance(w_gu, torch.Tensor) and isinstance(w_down, torch.Tensor):
             if w_gu.dtype != torch.bfloat16 or w_down.dtype != torch.bfloat16:
                 raise ValueError("PersistentMLP: weights are FP8Weight tuples or bf16 tensors")
-            return self._bf16(h, w_gu, w_down)
+            return self._bf16(h, w_gu, w_down, max_polls)
         if not (isinstance(w_gu, tuple) and isinstance(w_down, tuple)):
             raise ValueError("PersistentMLP: weights are FP8Weight tuples or bf16 tensors")
         H, I, S = self.H, self.I, self.split
@@ -96,8 +119,11 @@ class PersistentMLP:
         if M != self.M:
             raise ValueError(f"PersistentMLP built for M={self.M}, called with M={M}")
         if self.chained:
+            if M != 1:
+                raise ValueError("PersistentMLP: the chained form of FP8 weights takes M == 1")
             if lay_gu != L.W_TILED:
                 raise ValueError("PersistentMLP: the chained form takes tiled weights")
+            self._err = self.CHAIN_ERR
             act = torch.empty((1, I), device=h.device, dtype=torch.bfloat16)
             out = torch.empty((S, 1, H), device=h.device, dtype=torch.float32)
             L.call("krq_mlp_chain_fp8", L.ptr(h2), L.ptr(gu), L.ptr(gs), g_pr, L.ptr(dn), L.ptr(ds), d_pr,
@@ -109,6 +135,7 @@ class PersistentMLP:
             act = _fp8.gemv_swiglu_fp8(h2, w_gu)
             self.act = act
             return _fp8.gemv_fp8(act, w_down, S)
+        self._err = self._mlp_err
         if M == 1:
             xin, kind, xs = h2, L.X_BF16_DYN, None
         else:
@@ -130,7 +157,7 @@ class PersistentMLP:
     def failed(self):
         """True if a one-launch or chained call flagged a wait that timed out (its partials are
         NaN); synchronizes the device."""
-        return bool(self.ctl[self.CHAIN_ERR if self.chained else -1].item())
+        return bool(self.ctl[self._err].item())
 
     CHAIN_ERR = 513  # the chained form's error word (after 8 groups of 64 words and the exit count)
 

@@ -348,13 +348,132 @@ def test_mlp_chain_wait_timeout_poisons_partials(dev):
 
 def test_mlp_chain_rejects_bad_plans(dev):
     """M > 1, row-major weights and splits past the ring raise instead of launching."""
-    with pytest.raises(ValueError):
-        PersistentMLP(2, H, I, dev, chained=True)
     wgu, wd, x = case(1, 512, 3072, 140)
     qgu, qd = fp8.quantize(wgu.to(dev)), fp8.quantize(wd.to(dev))
+    with pytest.raises(ValueError, match="M == 1"):
+        PersistentMLP(2, 512, 3072, dev, chained=True)(torch.cat([x, x]).to(dev), qgu, qd)
     pm = PersistentMLP(1, 512, 3072, dev, split=1, chained=True)  # 24 steps of 128 in one split
     with pytest.raises(ValueError, match="ring"):
         pm(x.to(dev), qgu, qd)
     rgu, rd = fp8.FP8Weight(qgu[0], qgu[1], None), fp8.FP8Weight(qd[0], qd[1], None)
     with pytest.raises(ValueError, match="tiled"):
         PersistentMLP(1, 512, 3072, dev, split=2, chained=True)(x.to(dev), rgu, rd)
+
+
+# ---- the chained form on BF16 weights (krq_mlp_chain_bf16), any M ----
+
+# (M, H, I, split, packed): Qwen3-4B at one row (vector-ALU blocks, mixed gate_up plan), four,
+# sixteen and 32 rows (two row tiles), on tiled and row-major weights; a grid below one block per
+# CU with four down waves beside two gate_up waves; an odd step count per split
+CHAIN_BF16_CASES = [(1, H, I, 4, True), (1, H, I, 4, False), (4, H, I, 4, True), (16, H, I, 4, True),
+                    (32, H, I, 4, False), (1, 1024, 3072, 2, True), (3, 512, 1472, 1, False)]
+
+
+def bf16_case(M, h_, i_, seed, packed):
+    from kernels import gemv as G
+    wgu, wd, _ = case(M, h_, i_, seed)
+    wgu, wd = wgu.to("cuda"), wd.to("cuda")
+    if packed:
+        G.pack(wgu)
+        G.pack(wd)
+    return wgu, wd
+
+
+@pytest.mark.parametrize("M,h_,i_,S,packed", CHAIN_BF16_CASES)
+def test_mlp_chain_bf16_matches_pair(dev, M, h_, i_, S, packed):
+    """Two different row sets in a row: act and the partials bit-identical to the two BF16 GEMV
+    launches (each stage runs its standalone plan), the control words zero after every call, and
+    the last call within the oracle's bar (bf16 matmul, SwiGLU rounding chain, bf16 matmul)."""
+    from kernels import gemv as G
+    wgu, wd = bf16_case(M, h_, i_, 600 + M, packed)
+    pm = PersistentMLP(M, h_, i_, dev, split=S, chunk=64, chained=True)
+    g = torch.Generator().manual_seed(601 + M)
+    for call in range(2):
+        x = (torch.randn(M, h_, generator=g) * (1 + 3 * call)).to(torch.bfloat16)
+        xd = x.to(dev)
+        out = pm(xd, wgu, wd)
+        a = G.gemv_swiglu(xd, wgu)
+        sep = G.gemv(a, wd, S) if S > 1 else G._launch(a, wd, 1, L.OUT_PARTIAL)
+        torch.cuda.synchronize()
+        assert out.shape == (S, M, h_) and out.dtype == torch.float32
+        assert torch.equal(pm.act, a), f"call {call}: act differs from the SwiGLU GEMV's"
+        assert torch.equal(out, sep), f"call {call}: partials differ from the down GEMV's"
+        assert not pm.failed() and int(pm.ctl.abs().sum()) == 0
+    full = O.bf16_matmul(u16(x), u16(wgu))
+    act = O.swiglu(full[:, :i_].astype(np.float32), full[:, i_:].astype(np.float32))
+    ref = O.bf16_matmul(act, u16(wd))
+    assert rel_err(pm.act.float().cpu().numpy(), O.bf16_to_f32(act)) <= TOL
+    assert rel_err(out.double().sum(0).cpu().numpy(), ref) <= TOL
+
+
+def test_mlp_bf16_one_launch_is_the_chain(dev):
+    """one_launch=True on BF16 weights runs the chained launch: the pair's partials, one launch."""
+    from kernels import gemv as G
+    wgu, wd = bf16_case(1, H, I, 610, True)
+    x = torch.randn(1, H, generator=torch.Generator().manual_seed(611)).to(torch.bfloat16).to(dev)
+    pm = PersistentMLP(1, H, I, dev, one_launch=True)
+    out = pm(x, wgu, wd)
+    assert torch.equal(out, G.gemv(G.gemv_swiglu(x, wgu), wd, 4))
+    assert not pm.failed() and int(pm.ctl.abs().sum()) == 0
+
+
+def test_mlp_chain_bf16_graph_replays(dev):
+    """Replays of a captured BF16 chained launch with a new row copied in between and eager calls
+    between replays: every replay equals the eager result for its row."""
+    wgu, wd = bf16_case(1, H, I, 620, True)
+    g = torch.Generator().manual_seed(621)
+    xs = [torch.randn(1, H, generator=g).to(torch.bfloat16).to(dev) for _ in range(3)]
+    pm = PersistentMLP(1, H, I, dev, chained=True)
+    eager = [pm(x, wgu, wd).clone() for x in xs]
+    static_x = xs[0].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        pm(static_x, wgu, wd)
+    torch.cuda.current_stream().wait_stream(s)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        out = pm(static_x, wgu, wd)
+    for r in range(6):
+        static_x.copy_(xs[r % 3])
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager[r % 3]), r
+        assert torch.equal(pm(xs[(r + 1) % 3], wgu, wd), eager[(r + 1) % 3]), r
+    assert not pm.failed() and int(pm.ctl.abs().sum()) == 0
+    del gr
+
+
+def test_mlp_chain_bf16_wait_timeout_poisons_partials(dev):
+    """Waits bounded at one poll (forced from the host): a down block that gives up sets the error
+    word and writes NaN partials, every other partial equals the good launch's, and the launch
+    ends; after zero_ctl() the next launch is good again."""
+    wgu, wd = bf16_case(1, H, I, 630, True)
+    xd = torch.randn(1, H, generator=torch.Generator().manual_seed(631)).to(torch.bfloat16).to(dev)
+    pm = PersistentMLP(1, H, I, dev, chained=True)
+    good = pm(xd, wgu, wd).clone()
+    out = pm(xd, wgu, wd, max_polls=1)
+    torch.cuda.synchronize()
+    nan = torch.isnan(out)
+    print(f"bf16 timed-out partials: {int(nan.sum())} of {out.numel()}, flagged {pm.failed()}")
+    assert torch.equal(out[~nan], good[~nan])
+    assert pm.failed() == bool(nan.any())
+    pm.zero_ctl()
+    assert torch.equal(pm(xd, wgu, wd), good) and not pm.failed()
+    assert int(pm.ctl.abs().sum()) == 0
+
+
+def test_mlp_chain_bf16_rejects_bad_plans(dev):
+    """A down grid the standalone GEMV would pair (4096 blocks above 4 rows) and mixed layouts
+    raise instead of launching."""
+    from kernels import gemv as G
+    with pytest.raises(ValueError):
+        PersistentMLP(1, H, I, dev, chained=True, one_launch=True)
+    h_, i_ = 16384, 256
+    wgu, wd = bf16_case(8, h_, i_, 640, False)
+    x = torch.zeros(8, h_, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError, match="4096"):
+        PersistentMLP(8, h_, i_, dev, split=4, chunk=64, chained=True)(x, wgu, wd)
+    G.pack(wgu)
+    with pytest.raises(ValueError, match="layout"):
+        PersistentMLP(8, h_, i_, dev, split=4, chunk=64, chained=True)(x, wgu, wd)
