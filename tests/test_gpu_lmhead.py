@@ -54,10 +54,12 @@ def _bf16_ulp(v):
     return 2.0 ** (e - 7)
 
 
-def check_rows(idx, y, S, what, k=K):
+def check_rows(idx, y, S, what, k=K, exact=True):
     """idx: the kernel's int64 [M]; y: exact logits float64 [M, V]; S: scaled sums of |products|
     [M, V]; k: the products per logit. Asserts the identical index on every row the fp32 bound
-    decides; returns the number of rows inside the bound."""
+    decides; returns the number of rows inside the bound. exact: also on the rows inside the bound
+    (the kernels are deterministic and the inputs seeded, so on these cases the kernel's index
+    either is the oracle's or is not, run after run; every such row measured on MI355X is)."""
     ref = O.argmax_lowest(O.round_bf16(y.astype(np.float32)))
     inside = 0
     for m in range(y.shape[0]):
@@ -81,6 +83,8 @@ def check_rows(idx, y, S, what, k=K):
             print(f"  {what} row {m}: inside the fp32 bound (top-2 margin {margin:.3e}, "
                   f"{cand.size} candidates, E {E[cand].max():.2e}); kernel {idx[m]}, oracle {ref[m]}")
             assert ym[idx[m]] >= y1 - 2 * E.max() - ulp
+            if exact:
+                assert idx[m] == ref[m], f"{what} row {m} (inside the bound): {idx[m]} vs oracle {ref[m]}"
     return inside
 
 
@@ -118,7 +122,7 @@ def test_lmhead_bf16_argmax_seeds(dev, head, M):
         assert rel_err(lg, y) <= TOL
         inside += check_rows(idx, y, S, f"bf16 M={M} seed {seed}")
     print(f"bf16 M={M}: {inside} of {M * len(SEEDS)} rows inside the fp32 bound")
-    assert inside <= M * len(SEEDS) // 2
+    assert inside <= M * len(SEEDS) // 4
 
 
 @pytest.mark.parametrize("M", [1, 16])
@@ -146,7 +150,7 @@ def test_lmhead_fp8_per_channel_argmax_seeds(dev, head, M):
                 idx_r, logits_r = lmhead.lm_head_argmax(hd, q, return_logits=True, h_layout=lay)
                 assert torch.equal(logits_r, logits) and np.array_equal(idx_r.cpu().numpy(), idx), lay
     print(f"fp8 per-channel M={M}: {inside} of {M * len(SEEDS)} rows inside the fp32 bound")
-    assert inside <= M * len(SEEDS) // 2
+    assert inside <= M * len(SEEDS) // 4
 
 
 @pytest.mark.parametrize("M", [1, 16])
@@ -176,7 +180,7 @@ def test_lmhead_fp8_per_tensor_engine_path(dev, head, M):
         n2 = check_rows(idx_lin, y, S, f"fp8/tensor linear_fp8 M={M} seed {seed}")
         inside += max(n1, n2)
     print(f"fp8 per-tensor M={M}: {inside} of {M * len(SEEDS)} rows inside the fp32 bound")
-    assert inside <= M * len(SEEDS) // 2
+    assert inside <= M * len(SEEDS) // 4
 
 
 def test_lmhead_fp8_static_scale(dev, head):
@@ -227,3 +231,32 @@ def test_lmhead_fp8_tiled_h_shapes(dev, v, k, M):
     inside = check_rows(idx, y, S, f"tiled h V={v} K={k} M={M}", k=k)
     assert inside <= max(1, M // 2)
     assert np.array_equal(lmhead.lm_head_argmax(hd, q, h_layout="tiled").cpu().numpy(), idx)
+
+
+@pytest.mark.parametrize("v,k,packed", [(151936, 2560, True), (151936, 2560, False), (40000, 4096, True),
+                                        (8208, 3072, False), (8208, 8192, True), (8208, 1024, True)])
+def test_lmhead_bf16_m1_shapes(dev, v, k, packed):
+    """The BF16 head at M = 1 over vocabularies and hidden sizes besides Qwen3-4B's (two and four
+    waves per row block, V = 8,208 just over 512 row blocks), tiled and row-major: its logits equal
+    the BF16 GEMV's (krq_gemv_bf16) bit for bit, its id is the argmax of those logits, and the ids
+    are the oracle's wherever the fp32 bound decides them."""
+    from kernels import gemv as G
+    g = torch.Generator().manual_seed(v + k)
+    W = (torch.randn(v, k, generator=g) * 0.02).to(torch.bfloat16)
+    h = torch.randn(1, k, generator=g).to(torch.bfloat16)
+    Wd, hd = W.to(dev), h.to(dev)
+    if packed:
+        G.pack(Wd)
+    idx, logits = lmhead.lm_head_argmax(hd, Wd, return_logits=True)
+    ref_logits = G.gemv(hd, Wd)
+    assert torch.equal(logits.view(torch.int16), ref_logits.view(torch.int16))
+    idx = idx.cpu().numpy()
+    lg = logits.float().cpu().numpy()
+    assert np.array_equal(idx, O.argmax_lowest(lg))
+    hf = O.bf16_to_f32(u16(h)).astype(np.float64)
+    Wf = O.bf16_to_f32(u16(W)).astype(np.float64)
+    y = hf @ Wf.T
+    assert rel_err(lg, y) <= TOL
+    inside = check_rows(idx, y, np.abs(hf) @ np.abs(Wf).T, f"bf16 V={v} K={k}", k=k)
+    assert inside <= 1
+    assert np.array_equal(lmhead.lm_head_argmax(hd, Wd).cpu().numpy(), idx)
