@@ -146,11 +146,19 @@ KRQ_DEV void gemv_bf16_body(const uint8_t* __restrict__ x, const uint8_t* __rest
     }
     base = U;
   }
+  // One-row single-matrix blocks pin each slot's refill right behind its products: left to itself
+  // the compiler moves the batch's loads to its end and waits for the whole ring on every pass.
+  // Measured (M = 1, split 1, graph-timed, two alternating runs on one box): QKV 9.37 -> 8.75 us,
+  // O 8.35 -> 6.89, the BF16 lm_head 125.5 -> 122.6, down (split 4) and gate_up unchanged within
+  // the runs' spread; pinning every slot of the two-matrix SwiGLU block and of the matrix-core
+  // rings (M > 1) as well measured slower (gate_up 18.5 -> 19.8 us, M = 16 lm_head 139 -> 152).
+  constexpr bool PIN = ALGO == 2 && P == 1;
   for (; base + U < jcount; base += U) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       consume_slot(u, base + u);
       load_slot(u, base + u + U);
+      if constexpr (PIN) __builtin_amdgcn_sched_barrier(0);
     }
   }
 #pragma unroll
