@@ -304,6 +304,9 @@ int krq_mlp_chain_bf16(const void* x, const void* w_gu, const void* w_down, int 
  * engine/engine.py:953-961).
  *   ln != NULL (RMSNorm): x rows are normalized on the fly, h = bf16(bf16(x * rstd) * ln) with
  *                 rstd[m] = rsqrt(sum(ss_in[m][0..K/16)) / K + eps); ss_in is [M][K/16] fp32.
+ *                 M == 1: the sum is the row's own sum of squares (every one-row normalizing
+ *                 kernel, this one, krq_rmsnorm_rows, krq_rmsnorm_quant_rows(_tiled) and
+ *                 krq_gemv_fp8_fused, takes it in one fixed order from x) and ss_in is not read.
  *   mode KRQ_OUT_BF16 / KRQ_OUT_PARTIAL / KRQ_OUT_SWIGLU: as krq_gemv_bf16, into out.
  *   mode KRQ_OUT_RESIDUAL: y = bf16(sum of the split partials in split order);
  *                 res_out = bf16(res_in + y) (bf16 [M][N]); ss_out[m][t] = sum over the 16
@@ -322,7 +325,7 @@ int krq_gemv_bf16_fused(const void* x, const void* w, int w_layout, int64_t M, i
                         const void* res_in, void* res_out, float* ss_out, uint32_t* cnt, void* out,
                         void* stream);
 int64_t krq_gemv_fused_fits(int64_t M, int64_t N, int64_t K, int split, int mode, int norm);
-/* h = bf16(bf16(x * rstd) * ln) for whole bf16 rows x [M][K], rstd as above. */
+/* h = bf16(bf16(x * rstd) * ln) for whole bf16 rows x [M][K], rstd as above (M == 1: from x). */
 int krq_rmsnorm_rows(const void* x, const float* ss_in, const void* ln, float eps, int64_t M, int64_t K,
                      void* h, void* stream);
 
@@ -337,7 +340,11 @@ int krq_rmsnorm_rows(const void* x, const float* ss_in, const void* ln, float ep
  *   mode KRQ_OUT_RESIDUAL (ln == NULL; any x_kind): one split's value is the scaled product
  *                 (x8 . w8) * x_scale[m] * w_scale[n], as the partials output holds it; then
  *                 y = bf16(sum over splits in split order) and res_out / ss_out / cnt / out as in
- *                 krq_gemv_bf16_fused.
+ *                 krq_gemv_bf16_fused. M == 1, split 4, bf16 activations (DYN or STATIC): the
+ *                 folded launch (N / 4 workgroups, each four output columns over the four
+ *                 quarters of K) computes the same four split values and y bit for bit with no
+ *                 cross-workgroup sum; it needs neither cnt nor out and leaves ss_out alone
+ *                 (one-row consumers take the sum of squares from the row).
  * krq_gemv_fp8_fused_fits() tells whether the in-kernel staging holds the launch; otherwise use
  * krq_rmsnorm_quant_rows (per token) or krq_rmsnorm_rows + a static cast, then krq_gemv_fp8 /
  * the residual mode with x_kind KRQ_X_FP8. Calls sharing cnt must not overlap.

@@ -29,9 +29,11 @@ constexpr int64_t kNormStageMax = 24 * 1024;
 // Measured on MI355X (fused FP8 layer, M = 16, against 256 threads of 8-value chunks with the
 // partials staged in LDS and four barriers): gate_up + RMSNorm 15.01 -> 14.90 us, QKV + RMSNorm
 // 9.29 -> 9.09 us. TILED: x8 in the tiled activation layout (tiled_offset), one block per row of
-// the M rows padded to a multiple of 16, the pad rows zero.
+// the M rows padded to a multiple of 16, the pad rows zero. ROWSUM (one row): the row's own chunk
+// sums (sumsq8, chunk i = elements 8 i ..) staged in LDS, and each wave takes the canonical sum over
+// them instead of over ss_in.
 constexpr int kNqThreads = 512;
-template <int NT, int SC, bool TILED>
+template <int NT, int SC, bool TILED, bool ROWSUM>
 __global__ __launch_bounds__(NT) void k_rmsnorm_quant_rows(const uint16_t* __restrict__ x,
                                                            const float* __restrict__ ss_in,
                                                            const uint16_t* __restrict__ ln, float eps,
@@ -39,6 +41,7 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_quant_rows(const uint16_t* __res
                                                            float* __restrict__ xs) {
   constexpr int C = kRowMaxK / 16 / NT;
   __shared__ uint32_t red[NT / 64];
+  __shared__ float sq[ROWSUM ? kRowMaxK / 8 : 1];
   const int64_t m = blockIdx.x;
   if (TILED && m >= M) {
 #pragma unroll
@@ -63,12 +66,25 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_quant_rows(const uint16_t* __res
     lv[c][0] = ld16(lr + 2 * e);
     lv[c][1] = ld16(lr + 2 * e + 16);
   }
-#pragma unroll
-  for (int j = 0; j < SC; ++j) sp[j] = ss_in[m * T + min(lane + 64 * j, T - 1)];
   float a = 0.0f;
+  if constexpr (ROWSUM) {
 #pragma unroll
-  for (int j = 0; j < SC; ++j)
-    if (lane + 64 * j < T) a += sp[j];
+    for (int c = 0; c < C; ++c) {
+      const int p = threadIdx.x + c * NT;  // piece p: chunks 2 p and 2 p + 1
+      if (16 * (int64_t)p < K) {
+        sq[2 * p] = sumsq8(v[c][0]);
+        sq[2 * p + 1] = sumsq8(v[c][1]);
+      }
+    }
+    __syncthreads();
+    for (int t = lane; t < (int)(K >> 3); t += 64) a += sq[t];
+  } else {
+#pragma unroll
+    for (int j = 0; j < SC; ++j) sp[j] = ss_in[m * T + min(lane + 64 * j, T - 1)];
+#pragma unroll
+    for (int j = 0; j < SC; ++j)
+      if (lane + 64 * j < T) a += sp[j];
+  }
   const float rstd = rstd_of(a, K, eps);
   uint32_t am = 0;
 #pragma unroll
@@ -98,13 +114,16 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_quant_rows(const uint16_t* __res
 template <bool TILED>
 void launch_rmsnorm_quant(int64_t rows, const void* x, const float* ss_in, const void* ln, float eps, int64_t M,
                           int64_t K, void* x8, float* x_scale, hipStream_t s) {
-  // SC partials per lane: T = K / 16 <= 64 * SC
+  // SC partials per lane: T = K / 16 <= 64 * SC; one row sums itself (ROWSUM)
   const dim3 g(static_cast<unsigned>(rows)), b(kNqThreads);
-  if (K <= 4096)
-    hipLaunchKernelGGL((k_rmsnorm_quant_rows<kNqThreads, 4, TILED>), g, b, 0, s, (const uint16_t*)x, ss_in,
+  if (M == 1)
+    hipLaunchKernelGGL((k_rmsnorm_quant_rows<kNqThreads, 1, TILED, true>), g, b, 0, s, (const uint16_t*)x, ss_in,
+                       (const uint16_t*)ln, eps, M, K, (uint8_t*)x8, x_scale);
+  else if (K <= 4096)
+    hipLaunchKernelGGL((k_rmsnorm_quant_rows<kNqThreads, 4, TILED, false>), g, b, 0, s, (const uint16_t*)x, ss_in,
                        (const uint16_t*)ln, eps, M, K, (uint8_t*)x8, x_scale);
   else
-    hipLaunchKernelGGL((k_rmsnorm_quant_rows<kNqThreads, kRowMaxK / 16 / 64, TILED>), g, b, 0, s,
+    hipLaunchKernelGGL((k_rmsnorm_quant_rows<kNqThreads, kRowMaxK / 16 / 64, TILED, false>), g, b, 0, s,
                        (const uint16_t*)x, ss_in, (const uint16_t*)ln, eps, M, K, (uint8_t*)x8, x_scale);
 }
 
@@ -165,12 +184,18 @@ void launch(int M, int awc, int u, dim3 grid, int nw, size_t smem, hipStream_t s
       return;
     }
   }
-  if (M <= 4)
+  if constexpr (NORM && XK == KRQ_X_BF16_DYN) {
+    // (not reached: plan() gives a one-row RMSNorm launch the activation wave)
+  } else if constexpr (MODE == kOutResidualFold) {  // (one row)
     hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, 4, NORM, 0>), grid, block, smem, s, KRQ_FUSED_FP8_ARGS);
-  else if (M <= 16)
-    hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, 2, NORM, 0>), grid, block, smem, s, KRQ_FUSED_FP8_ARGS);
-  else
-    hipLaunchKernelGGL((k_gemv_fp8_fused<2, MODE, LAYOUT, XK, 1, 2, NORM, 0>), grid, block, smem, s, KRQ_FUSED_FP8_ARGS);
+  } else {
+    if (M <= 4)
+      hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, 4, NORM, 0>), grid, block, smem, s, KRQ_FUSED_FP8_ARGS);
+    else if (M <= 16)
+      hipLaunchKernelGGL((k_gemv_fp8_fused<1, MODE, LAYOUT, XK, 1, 2, NORM, 0>), grid, block, smem, s, KRQ_FUSED_FP8_ARGS);
+    else
+      hipLaunchKernelGGL((k_gemv_fp8_fused<2, MODE, LAYOUT, XK, 1, 2, NORM, 0>), grid, block, smem, s, KRQ_FUSED_FP8_ARGS);
+  }
 }
 
 template <int MODE, int XK, bool NORM>
@@ -191,16 +216,17 @@ struct FusedPlan {
   int awc;      // chunks per lane of the activation wave (0: none, every wave runs the prologue)
   int u;        // step slots of the deep ring (tiled layout), 0: the default ring
   size_t smem;  // dynamic LDS bytes
+  bool fold;    // the folded one-row residual launch (kOutResidualFold)
 };
 
 // One-row launches (M == 1, bf16 activations) get the activation wave of gemv_fp8_kernel.h when
-// its registers hold what it loads: the whole row (per-token scale) or the slice (static scale),
-// K <= 4096 with RMSNorm (the row's partials, 64 x kSsPerLane). Grids of fewer blocks than CUs
-// (the one-pass residual GEMVs) keep the shared prologue.
+// its registers hold what it loads: the whole row (per-token scale, or RMSNorm, which sums the row
+// itself; K <= 4096 with RMSNorm) or the slice (static scale). Grids of fewer blocks than CUs keep
+// the shared prologue.
 int act_wave_chunks(int64_t M, int64_t K, int64_t ks, int mode, int x_kind, bool norm) {
   if (M != 1 || x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED) return 0;
   if (norm && K > 512 * kAwSmall) return 0;
-  const int64_t span = x_kind == KRQ_X_BF16_DYN ? K : ks;
+  const int64_t span = x_kind == KRQ_X_BF16_DYN || norm ? K : ks;
   return span <= 512 * kAwSmall ? kAwSmall : span <= 512 * kAwLarge ? kAwLarge : 0;
 }
 
@@ -212,7 +238,16 @@ bool plan(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind, bool
   const int64_t ks = K / split;
   const int P = mode == KRQ_OUT_SWIGLU ? 2 : 1;
   const int64_t NO = mode == KRQ_OUT_SWIGLU ? N / 2 : N;
-  const int awc = NO / 16 * split >= kCUs ? act_wave_chunks(M, K, ks, mode, x_kind, norm) : 0;
+  // The residual epilogue at M = 1 over the callers' four splits of bf16 activations runs folded:
+  // N / 4 blocks (each four output columns over the four quarters of K, one matrix-core product
+  // per step) with this plan's waves and ring, the split launch's sums bit for bit, and no cross-
+  // block reduction. Its whole row is quantized into LDS.
+  const bool fold = mode == kOutResidual && M == 1 && split == 4 &&
+                    (x_kind == KRQ_X_BF16_DYN || x_kind == KRQ_X_BF16_STATIC);
+  const int64_t kq = fold ? K : ks;  // elements of the row quantized into LDS
+  const int awc = NO / 16 * split >= kCUs ? act_wave_chunks(M, K, kq, mode, x_kind, norm) : 0;
+  // a one-row RMSNorm sums the row in the activation wave (no ss_in at M = 1)
+  if (norm && M == 1 && awc == 0) return false;
   if (awc == 0 && norm && x_kind == KRQ_X_BF16_STATIC && M * ks * 2 > kNormStageMax) return false;
   const int kts = static_cast<int>(ks / 64);
   const int MT = M <= 16 ? 1 : 2;
@@ -230,9 +265,8 @@ bool plan(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind, bool
   }
   bool staged_ss = false;  // the sum-of-squares partials staged in LDS (RMSNorm of M rows)
   if (awc == 0) {
-    const int64_t xchunks = x_kind == KRQ_X_BF16_DYN ? (K + 7) / 8 : x_kind == KRQ_X_BF16_STATIC ? M * (ks / 8) : 0;
+    const int64_t xchunks = x_kind == KRQ_X_BF16_DYN ? (K + 7) / 8 : x_kind == KRQ_X_BF16_STATIC ? M * (kq / 8) : 0;
     const int xc = x_kind == KRQ_X_BF16_DYN ? kXChunksDyn : kXChunks;
-    if (norm && x_kind == KRQ_X_BF16_DYN && K / 16 > 64 * kSsPerLane) return false;
     staged_ss = norm && x_kind == KRQ_X_BF16_STATIC;
     auto short_of = [&](int w) {
       return (int64_t)w * 64 * xc < xchunks || (staged_ss && (int64_t)w * 64 * kSsChunks * 4 < M * (K / 16));
@@ -243,10 +277,10 @@ bool plan(int64_t M, int64_t N, int64_t K, int split, int mode, int x_kind, bool
     nw = min(nw, kMaxThreads / 64 - 1);
   }
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) +
-                      (x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED ? 0 : (size_t)M * ks) +
+                      (x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED ? 0 : (size_t)M * kq) +
                       (staged_ss ? (size_t)M * (K / 16) * sizeof(float) : 0);
   if (smem > kMaxSmem) return false;
-  *out = FusedPlan{nw, awc, u, smem};
+  *out = FusedPlan{nw, awc, u, smem, fold};
   return true;
 }
 
@@ -284,7 +318,9 @@ extern "C" int krq_gemv_fp8_fused(const void* x, int x_kind, const float* x_scal
   KRQ_REQUIRE(!(norm && mode == kOutResidual), "gemv_fp8_fused: RMSNorm and the residual epilogue in one call");
   KRQ_REQUIRE(!norm || (ss_in && aligned16(ln) && aligned16(ss_in) && x_kind != KRQ_X_FP8 && x_kind != KRQ_X_FP8_TILED),
               "gemv_fp8_fused: RMSNorm needs bf16 activations, ss_in and aligned ln / ss_in");
-  KRQ_REQUIRE(mode != kOutResidual || (res_in && res_out && ss_out && (split == 1 || (cnt && out))),
+  // (at M = 1 with four splits of bf16 activations the folded form needs neither cnt nor out)
+  const bool one_row4 = M == 1 && split == 4 && (x_kind == KRQ_X_BF16_DYN || x_kind == KRQ_X_BF16_STATIC);
+  KRQ_REQUIRE(mode != kOutResidual || (res_in && res_out && ss_out && (split == 1 || one_row4 || (cnt && out))),
               "gemv_fp8_fused: the residual epilogue needs res_in, res_out, ss_out and, for split > 1, "
               "cnt and the partials buffer");
   KRQ_REQUIRE(mode == kOutResidual || out, "gemv_fp8_fused: null output");
@@ -295,8 +331,9 @@ extern "C" int krq_gemv_fp8_fused(const void* x, int x_kind, const float* x_scal
   KRQ_REQUIRE(plan(M, N, K, split, mode, x_kind, norm, &p),
               "gemv_fp8_fused: M=%lld x K/split=%lld does not fit the in-kernel staging; normalize and "
               "quantize rows first (krq_rmsnorm_quant_rows)", (long long)M, (long long)(K / split));
-  const int kts = static_cast<int>(K / split / 64);
-  const dim3 grid(static_cast<unsigned>(NO / 16), static_cast<unsigned>(split));
+  const int kts = static_cast<int>(K / split / 64);  // (folded: the tiles of one quarter of K)
+  const dim3 grid = p.fold ? dim3(static_cast<unsigned>(N / 4), 1)
+                           : dim3(static_cast<unsigned>(NO / 16), static_cast<unsigned>(split));
   const FusedArgs fa{reinterpret_cast<const uint16_t*>(ln), ss_in, eps, reinterpret_cast<const uint16_t*>(res_in),
                      reinterpret_cast<uint16_t*>(res_out), ss_out, cnt};
   const uint8_t* xb = (const uint8_t*)x;
@@ -306,7 +343,10 @@ extern "C" int krq_gemv_fp8_fused(const void* x, int x_kind, const float* x_scal
 #define KRQ_CASE(MODE, XK, NORM)                                                                          \
   launch_layout<MODE, XK, NORM>(w_layout, m, p.awc, p.u, grid, p.nw, p.smem, s, xb, x_scale, x_inv, x_per_row, wb, w_scale, \
                                 w_per_row, m, NO, K, kts, out, fa)
-  if (mode == kOutResidual) {
+  if (p.fold) {
+    if (x_kind == KRQ_X_BF16_DYN) KRQ_CASE(kOutResidualFold, KRQ_X_BF16_DYN, false);
+    else KRQ_CASE(kOutResidualFold, KRQ_X_BF16_STATIC, false);
+  } else if (mode == kOutResidual) {
     if (x_kind == KRQ_X_FP8) KRQ_CASE(kOutResidual, KRQ_X_FP8, false);
     else if (x_kind == KRQ_X_FP8_TILED) KRQ_CASE(kOutResidual, KRQ_X_FP8_TILED, false);
     else if (x_kind == KRQ_X_BF16_DYN) KRQ_CASE(kOutResidual, KRQ_X_BF16_DYN, false);

@@ -9,7 +9,8 @@
 // so instead of one accumulator per row that every 16-column tile adds into, each tile writes its
 // own partial: ss is [M][T] (T = N / 16 tiles of the producer = K / 16 of the consumer). The
 // consumer's prologue sums a row's T partials in a fixed order (deterministic; the reference's
-// atomic order is not). Every producer overwrites all T slots, so nothing needs zeroing.
+// atomic order is not). Every producer overwrites all T slots, so nothing needs zeroing. At M = 1
+// the consumer sums its row itself instead (gemv_common.h, sumsq8) and reads no ss_in.
 //
 // Split-K with the residual epilogue: each split writes its partial tile with write-through
 // (agent-scope) stores, waits for them, then bumps the tile's counter; the split that brings it to
@@ -57,11 +58,21 @@ __global__ __launch_bounds__(kMaxNT) void k_gemv_fused(const uint8_t* __restrict
   uint8_t* hq = reinterpret_cast<uint8_t*>(red + nw * P * MT * 256);
   float* sst = reinterpret_cast<float*>(hq + (size_t)M * ks * 2);
   if (threadIdx.x < 32) ones[threadIdx.x] = 1.0f;
+  // ROWSUM (the one-row kernel, M == 1): the prologue loads the whole row and sums it itself
+  constexpr bool ROWSUM = NORM && ALGO == 2;
+  const int nch = (int)(K >> 3);  // 16-byte chunks of a row
 
-  // ---- prologue part 1 (RMSNorm): x slice and norm inputs ahead of the weight stream ----
+  // ---- prologue part 1 (RMSNorm): x slice (ROWSUM: the row) and norm inputs ahead of the weights ----
   uint4 xv[kXC], lv[kXC];
   float sv[kSC];
-  if (NORM) {
+  if (ROWSUM) {
+#pragma unroll
+    for (int c = 0; c < kXC; ++c) {
+      const int64_t e = 8 * (int64_t)min((int)threadIdx.x + c * NT, nch - 1);
+      xv[c] = ld16(x + 2 * e);
+      lv[c] = ld16(reinterpret_cast<const uint8_t*>(fa.ln) + 2 * e);
+    }
+  } else if (NORM) {
 #pragma unroll
     for (int c = 0; c < kXC; ++c) {
       const int idx = min((int)threadIdx.x + c * NT, M * cpr - 1);
@@ -107,7 +118,22 @@ __global__ __launch_bounds__(kMaxNT) void k_gemv_fused(const uint8_t* __restrict
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- prologue part 2: per-row rstd (NORM), then the (normalized) slice into LDS ----
-  if (NORM) {
+  if (ROWSUM) {  // the row's chunk sums, then the canonical sum over them
+#pragma unroll
+    for (int c = 0; c < kXC; ++c) {
+      const int i = threadIdx.x + c * NT;
+      if (i < nch) sst[i] = sumsq8(xv[c]);
+    }
+    __syncthreads();
+    row_rstd(sst, 1, nch, K, fa.eps, rstd_s);
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < kXC; ++c) {
+      const int64_t e = 8 * (int64_t)(threadIdx.x + c * NT);
+      if (e >= k0 && e < k0 + ks) *reinterpret_cast<uint4*>(hq + 2 * (e - k0)) = norm8(xv[c], lv[c], rstd_s[0]);
+    }
+    __syncthreads();
+  } else if (NORM) {
 #pragma unroll
     for (int c = 0; c < kSC; ++c) {
       const int i = threadIdx.x + c * NT;
@@ -117,7 +143,7 @@ __global__ __launch_bounds__(kMaxNT) void k_gemv_fused(const uint8_t* __restrict
     row_rstd(sst, M, T, K, fa.eps, rstd_s);
     __syncthreads();
   }
-  if (NORM) {
+  if (NORM && !ROWSUM) {
 #pragma unroll
     for (int c = 0; c < kXC; ++c) {
       const int idx = threadIdx.x + c * NT;
@@ -200,17 +226,18 @@ __global__ __launch_bounds__(kMaxNT) void k_gemv_fused(const uint8_t* __restrict
 }
 
 // RMSNorm of whole rows for shapes whose slice does not fit the GEMV's LDS staging:
-// h = bf16(bf16(x * rstd) * w_ln), rstd from the [M][K/16] sum-of-squares partials.
-template <int C>
+// h = bf16(bf16(x * rstd) * w_ln), rstd from the [M][K/16] sum-of-squares partials (ROWSUM, one
+// row: from the row itself).
+template <int C, bool ROWSUM>
 __global__ __launch_bounds__(kRowThreads) void k_rmsnorm_rows(const uint16_t* __restrict__ x,
                                                               const float* __restrict__ ss_in,
                                                               const uint16_t* __restrict__ ln, float eps, int64_t K,
                                                               uint16_t* __restrict__ h) {
-  __shared__ float sst[kRowThreads * C / 2];
+  __shared__ float sst[kRowThreads * C];
   __shared__ float rstd_sh;
   const int m = blockIdx.x;
   uint4 xv[C], lv[C];
-  const float rstd = row_prologue<C>(x, ss_in, ln, eps, K, m, sst, &rstd_sh, xv, lv);
+  const float rstd = row_prologue<C, ROWSUM>(x, ss_in, ln, eps, K, m, sst, &rstd_sh, xv, lv);
   uint8_t* hr = reinterpret_cast<uint8_t*>(h + m * K);
 #pragma unroll
   for (int c = 0; c < C; ++c) {
@@ -258,13 +285,15 @@ bool plan_fused(int64_t M, int64_t N, int64_t K, int split, int mode, bool norm,
   const int MT = M <= 16 ? 1 : 2;
   const int64_t NO = mode == KRQ_OUT_SWIGLU ? N / 2 : N;
   int nw = plan_waves((kts + 1) / 2, P, M <= 4 ? 4 : 2, NO / 16 * split);
+  // (one row: the prologue loads and sums the whole row, K / 8 chunks, instead of the partials)
   auto short_of = [&](int w) {
+    if (norm && M == 1) return (int64_t)w * 64 * kXC < K / 8;
     return norm && ((int64_t)w * 64 * kXC < M * (ks / 8) || (int64_t)w * 64 * kSC < M * (K / 16));
   };
   while (short_of(nw) && nw < kMaxNT / 64) ++nw;
   if (short_of(nw)) return false;
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) +
-                      (norm ? (size_t)M * ks * 2 + (size_t)M * (K / 16) * sizeof(float) : 0);
+                      (norm ? (size_t)M * ks * 2 + (size_t)(M == 1 ? K / 8 : M * (K / 16)) * sizeof(float) : 0);
   if (smem > kMaxSmem) return false;
   *nw_out = nw;
   *smem_out = smem;
@@ -335,8 +364,10 @@ extern "C" int krq_rmsnorm_rows(const void* x, const float* ss_in, const void* l
   KRQ_REQUIRE(M >= 1 && M <= 0x7fffffff && K > 0 && K % 16 == 0 && K <= kRowMaxK,
               "rmsnorm_rows: bad shape M=%lld K=%lld (K a multiple of 16, at most %d)", (long long)M, (long long)K,
               kRowMaxK);
-  hipLaunchKernelGGL(K <= kRowSmallK ? k_rmsnorm_rows<2> : k_rmsnorm_rows<kRowChunks>, dim3(static_cast<unsigned>(M)),
-                     dim3(kRowThreads), 0, (hipStream_t)stream,
+  // (one row: its sum of squares from the row itself, as every one-row normalizing kernel takes it)
+  auto kern = M == 1 ? (K <= kRowSmallK ? k_rmsnorm_rows<2, true> : k_rmsnorm_rows<kRowChunks, true>)
+                     : (K <= kRowSmallK ? k_rmsnorm_rows<2, false> : k_rmsnorm_rows<kRowChunks, false>);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(M)), dim3(kRowThreads), 0, (hipStream_t)stream,
                      (const uint16_t*)x, ss_in, (const uint16_t*)ln, eps, K, (uint16_t*)h);
   return krq_check_launch("rmsnorm_rows");
 }

@@ -48,6 +48,15 @@ constexpr int kOutArgmax = 3;
 // column blocks this way (k_gemv_fp8_swiglu_mixed) to even out the bytes per compute unit.
 constexpr int kOutSwiGluHalf = 5;
 
+// Internal output mode: the residual epilogue of a folded one-row block b (M = 1, split S = 4 of the
+// caller), which owns output columns 4 b .. 4 b + 3 over the whole of K. Matrix-core column c of
+// the block is output column 4 b + c % 4 over quarter c / 4 of K, and A row q < 4 holds quarter q
+// of the activation row (rows 4..15 zero), so quarter q's sum for column j lands in C[q][4 q + j].
+// With the waves and steps of the split launch, those are its S partials bit for bit; the block
+// sums them in split order and finishes the residual. 4 N / 16 blocks instead of N / 16 one-pass
+// blocks (fewer than the CUs at N = 2,560), and no cross-block reduction.
+constexpr int kOutResidualFold = 6;
+
 struct Best {
   float v;
   int i;
@@ -105,6 +114,16 @@ template <int LAYOUT>
 KRQ_DEV const uint8_t* w_addr(const uint8_t* w, int64_t rb, int64_t t, int64_t row_bytes, int lane) {
   if (LAYOUT == KRQ_W_TILED) return w + ((rb * (row_bytes >> 6) + t) * 64 + lane) * 16;
   return w + (rb * 16 + (lane & 15)) * row_bytes + t * 64 + (lane >> 4) * 16;
+}
+
+// The B-operand address of folded one-row block b (kOutResidualFold): lane column c = lane % 16
+// reads output row 4 b + c % 4 at tile t of quarter c / 4 of K (qt 64-byte tiles per quarter).
+template <int LAYOUT>
+KRQ_DEV const uint8_t* w_addr_fold(const uint8_t* w, int64_t b, int64_t K, int qt, int64_t t, int lane) {
+  const int c = lane & 15;
+  const int64_t row = 4 * b + (c & 3), tk = (int64_t)(c >> 2) * qt + t;  // the row's tile
+  if (LAYOUT == KRQ_W_TILED) return w + (((row >> 4) * (K >> 6) + tk) * 64 + (lane & 48) + (row & 15)) * 16;
+  return w + row * K + tk * 64 + (lane >> 4) * 16;
 }
 
 // The B-operand address of half-pair block b (kOutSwiGluHalf): lane column c < 8 reads gate row
@@ -446,6 +465,25 @@ KRQ_DEV uint4 norm8(uint4 xv, uint4 lv, float rstd) {
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// Sum of squares of the 8 bf16 values of a 16-byte chunk, in element order from zero: the partial
+// of chunk i (elements 8 i .. 8 i + 7) when a one-row kernel sums its row itself (see below).
+KRQ_DEV float sumsq8(uint4 v) {
+  const uint32_t a[4] = {v.x, v.y, v.z, v.w};
+  float s = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float lo = as_f32(a[q] << 16), hi = as_f32(a[q] & 0xffff0000u);
+    s = fmaf(lo, lo, s);
+    s = fmaf(hi, hi, s);
+  }
+  return s;
+}
+
+// One row (M = 1): the normalizing kernels take the row's sum of squares from the row itself, as
+// the canonical sum below over its K / 8 chunk partials sumsq8 (chunk i at lane i % 64), and read no
+// ss_in; at M > 1 they sum the [M][K/16] partials of ss_in. A one-row prologue holds the whole row
+// anyway (its per-token amax needs it), so the producer of x needs no sum of squares at M = 1 (the
+// folded residual GEMVs, kOutResidualFold, write none).
 // The canonical row sum of T sum-of-squares partials, used by every kernel that normalizes (so the
 // fused prologues, k_rmsnorm_rows and k_rmsnorm_quant_rows agree bit for bit): lane l adds
 // partials t = l, l + 64, l + 128, ... in that order, then the butterfly wave sum (every lane ends
@@ -477,7 +515,9 @@ KRQ_DEV void row_rstd(const float* sst, int M, int T, int64_t K, float eps, floa
 // Row prologue of the row kernels: loads row m's x and ln chunks (chunk c of this thread covers
 // elements 8 * (threadIdx.x + c * kRowThreads)), stages the row's T partials in sst and returns
 // rstd (every thread). Chunks past K hold a repeat of the last one.
-template <int C>
+// ROWSUM (one row): the partials are the row's own chunk sums (sumsq8), staged for the same
+// canonical sum; sst then holds K / 8 <= kRowThreads * C floats.
+template <int C, bool ROWSUM = false>
 KRQ_DEV float row_prologue(const uint16_t* __restrict__ x, const float* __restrict__ ss_in,
                            const uint16_t* __restrict__ ln, float eps, int64_t K, int m, float* sst,
                            float* rstd_sh, uint4* xv, uint4* lv) {
@@ -489,6 +529,17 @@ KRQ_DEV float row_prologue(const uint16_t* __restrict__ x, const float* __restri
     const int64_t e = min(8 * (int64_t)(threadIdx.x + c * kRowThreads), K - 8);
     xv[c] = ld16(xr + 2 * e);
     lv[c] = ld16(lr + 2 * e);
+  }
+  if constexpr (ROWSUM) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int i = threadIdx.x + c * kRowThreads;
+      if (8 * (int64_t)i < K) sst[i] = sumsq8(xv[c]);
+    }
+    __syncthreads();
+    row_rstd(sst, 1, (int)(K >> 3), K, eps, rstd_sh);
+    __syncthreads();
+    return *rstd_sh;
   }
   constexpr int kSp = C / 2;  // partials per thread: T = K / 16 <= kRowThreads * C / 2
   float sp[kSp];
@@ -563,6 +614,28 @@ KRQ_DEV void residual_epilogue(const float* red, int nw, int M, int64_t NO, int6
     if (m < M && (ln & 15) == 0) fa.ss_out[(int64_t)m * (NO >> 4) + rb] = sq;
   }
   if (S > 1 && threadIdx.x == 0) cstore(&fa.cnt[rb], 0u);
+}
+
+// Residual epilogue of folded one-row block b (kOutResidualFold; P == 1, MT == 1 accumulators in
+// red): quarter q's sum for output column 4 b + j is C[q][4 q + j], element q of lane 4 q + j.
+// Each quarter is summed over the waves and scaled as residual_epilogue scales a split's value,
+// the four are added in split order, and the residual row is finished as there. No sum of squares
+// is written (one-row consumers sum their row themselves).
+KRQ_DEV void fold_residual_epilogue(const float* red, int nw, int64_t b, const float* xs, const float* wsc,
+                                    int w_per_row, const FusedArgs& fa) {
+  if (threadIdx.x >= 4) return;
+  const int j = threadIdx.x;
+  const int64_t n = 4 * b + j;
+  const float ws = wsc[w_per_row ? n : 0];
+  float y = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float a = 0.0f;
+    for (int w2 = 0; w2 < nw; ++w2) a += red[w2 * 256 + q * 64 + 4 * q + j];
+    y += a * xs[0] * ws;
+  }
+  const float xn = round_bf16(bf16_to_f32(fa.res_in[n]) + round_bf16(y));
+  fa.res_out[n] = f32_to_bf16(xn);
 }
 
 // block of launch planning shared by the GEMV entry points

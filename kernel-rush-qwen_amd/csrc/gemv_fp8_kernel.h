@@ -52,9 +52,6 @@ constexpr int kXChunks = 8;
 constexpr int kXChunksDyn = 4;
 // 16-byte (four-partial) sum-of-squares chunks per thread in the RMSNorm prologue (staged rows)
 constexpr int kSsChunks = 4;
-// sum-of-squares partials per lane in the one-row RMSNorm prologue, where every wave sums the row
-// itself (T = K / 16 <= 64 * kSsPerLane, i.e. K <= 4096)
-constexpr int kSsPerLane = 4;
 constexpr int kMaxThreads = 512;
 // one-row activation wave: 16-byte chunks per lane (the whole row, K <= 64 * 8 * AWC)
 constexpr int kAwSmall = 8, kAwLarge = 20;
@@ -71,7 +68,8 @@ constexpr int64_t kCUs = 256;  // compute units of the MI355X
 //   KRQ_X_BF16_DYN: loads the whole row, takes its amax (ActScale arithmetic), quantizes the slice.
 //   KRQ_X_BF16_STATIC (M = 1): loads the slice and quantizes it with the given inverse scale.
 // NORM: the loaded chunks are first normalized, h = bf16(bf16(x * rstd) * w_ln), with rstd from the
-// row's sum-of-squares partials in the canonical order (K <= 4096: T = K / 16 <= 64 * kSsPerLane).
+// row's own sum of squares in the canonical order (sumsq8 of its chunks; the wave loads the whole
+// row, K <= 4096, also for a static scale, and quantizes the slice).
 // ORDER: the wave meets the weight waves at a bare s_barrier (no fence, no wait) once all of its
 // loads are issued, and the weight waves issue their ring only after it; see gemv_fp8_body.
 // CH (second stage of the chained MLP, KRQ_X_BF16_DYN): the row is written in this launch by the
@@ -86,20 +84,18 @@ KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restr
                              const float* __restrict__ xinv, int64_t K, int64_t k0, int ks, int lane,
                              uint8_t* xq, float* xs_l, const FusedArgs& fa) {
   constexpr int LC = NORM ? AWC : 1;
-  constexpr int SC = NORM ? kSsPerLane : 1;
   static_assert(!CH || (XK == KRQ_X_BF16_DYN && !NORM), "chained stage: one bf16 row scaled per token");
   bool chain_bad = false;
   if constexpr (CH) chain_bad = !chain_wait(fa);
   __builtin_amdgcn_s_setprio(3);
-  // DYN: chunk i = lane + 64 c of the row holds elements 8i .. 8i + 7 (indices past the row repeat
-  // its last chunk); STATIC: the same over the slice
+  // FULL (per-token scale, or RMSNorm): chunk i = lane + 64 c of the row holds elements 8i .. 8i + 7
+  // (indices past the row repeat its last chunk); otherwise (static scale) the same over the slice
+  constexpr bool FULL = XK == KRQ_X_BF16_DYN || NORM;
   const int lo = static_cast<int>(k0 >> 3), n = ks >> 3;
-  const int last = XK == KRQ_X_BF16_DYN ? static_cast<int>(K >> 3) - 1 : n - 1;
-  const int64_t e0 = XK == KRQ_X_BF16_DYN ? 0 : k0;  // first element of chunk 0
-  const int T = static_cast<int>(K >> 4);
+  const int last = FULL ? static_cast<int>(K >> 3) - 1 : n - 1;
+  const int64_t e0 = FULL ? 0 : k0;  // first element of chunk 0
   const uint8_t* lnb = reinterpret_cast<const uint8_t*>(fa.ln);
   uint4 v[AWC], lv[LC];
-  float sp[SC];
 #pragma unroll
   for (int c = 0; c < AWC; ++c) {
     const int64_t e = e0 + 8 * (int64_t)min(lane + 64 * c, last);
@@ -112,10 +108,6 @@ KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restr
     }
     if (NORM) lv[c] = ld16(lnb + 2 * e);
   }
-  if (NORM) {
-#pragma unroll
-    for (int c = 0; c < SC; ++c) sp[c] = fa.ss_in[min(lane + 64 * c, T - 1)];
-  }
   float inv = 0.0f;
   if (XK == KRQ_X_BF16_STATIC) {
     inv = xinv[0];
@@ -124,12 +116,12 @@ KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restr
   __builtin_amdgcn_sched_barrier(0);  // every row load in flight before the first wait
   if constexpr (ORDER) __builtin_amdgcn_s_barrier();
   if (NORM) {
-    float a = 0.0f;
+    float a = 0.0f;  // the row's canonical sum of squares: chunk i = lane + 64 c at lane i % 64
 #pragma unroll
-    for (int c = 0; c < SC; ++c)
-      if (lane + 64 * c < T) a += sp[c];
+    for (int c = 0; c < AWC; ++c)
+      if (lane + 64 * c <= last) a += sumsq8(v[c]);
     const float rstd = rstd_of(a, K, fa.eps);
-    // only chunks inside the row (slice): the clamped repeats are left raw and kept out of the amax
+    // only chunks inside the row: the clamped repeats are left raw and kept out of the amax
 #pragma unroll
     for (int c = 0; c < AWC; ++c)
       if (lane + 64 * c <= last) v[c] = norm8(v[c], lv[NORM ? c : 0], rstd);
@@ -146,7 +138,7 @@ KRQ_DEV void activation_wave(const uint8_t* __restrict__ x, const float* __restr
   }
 #pragma unroll
   for (int c = 0; c < AWC; ++c) {
-    const int i = lane + 64 * c - (XK == KRQ_X_BF16_DYN ? lo : 0);  // chunk index inside the slice
+    const int i = lane + 64 * c - (FULL ? lo : 0);  // chunk index inside the slice
     if (static_cast<unsigned>(i) < static_cast<unsigned>(n))
       *reinterpret_cast<uint2*>(xq + 8 * i) =
           XK == KRQ_X_BF16_DYN ? quant8_own_amax(v[c], inv) : quant8_clamped(v[c], inv);
@@ -183,11 +175,17 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   static_assert(!NORM || (XK != KRQ_X_FP8 && XK != KRQ_X_FP8_TILED), "the RMSNorm prologue takes bf16 activations");
   constexpr bool AW = AWC > 0;
   static_assert(!AW || (XK != KRQ_X_FP8 && XK != KRQ_X_FP8_TILED && MT == 1), "activation wave: one bf16 row");
+  static_assert(!NORM || XK != KRQ_X_BF16_DYN || AW, "one-row RMSNorm: the activation wave sums the row");
   static_assert(XK != KRQ_X_FP8_TILED || ALGO != 2, "tiled activations: matrix-core kernels");
   constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : PB;  // weight row blocks streamed per step
   constexpr bool XT = XK == KRQ_X_FP8_TILED;
   constexpr bool FUSED = XK != KRQ_X_FP8 && !XT;  // bf16 activations quantized into LDS
-  constexpr int SC = XK == KRQ_X_BF16_DYN ? kSsPerLane : kSsChunks;
+  // FOLD: folded one-row residual block (kOutResidualFold): bx owns output columns 4 bx .. 4 bx + 3,
+  // kts counts the tiles of one quarter of K, and the whole row is quantized into LDS
+  constexpr bool FOLD = MODE == kOutResidualFold;
+  static_assert(!FOLD || (MT == 1 && PB == 1 && ALGO == 1 && FUSED && !NORM && !CHAIN),
+                "folded residual: one row, bf16 activations quantized in the kernel, matrix cores");
+  constexpr int SC = kSsChunks;
   // Load order of the RMSNorm activation wave beside a single-matrix ring: the CU returns loads in
   // issue order, so the wave's row, RMSNorm-weight and partials loads, issued while the weight wave
   // issues its ring, land only after most of it. Making the weight waves issue after the activation wave's loads
@@ -203,24 +201,29 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nw = nwo > 0 ? nwo : (blockDim.x >> 6) - (AW ? 1 : 0);
   const int r = lane & 15, g = lane >> 4;
-  const int64_t rb = bx * PB, rbu = MODE == KRQ_OUT_SWIGLU ? rb + (NO >> 4) : rb + 1;
+  // FOLD: blocks b and b ^ 1 read the two halves of every weight line they touch (rows 8 h .. 8 h + 7
+  // of a tile, 64 bytes each); workgroups w and w + 8 run on one XCD, so block b = 2 (8 k + x) + h
+  // goes to workgroup w = 16 k + 8 h + x and each line is fetched into one L2 (tail: b = w).
+  // Measured in the fused FP8 layer at M = 1: O + residual 5.83 -> 5.07 us, down + residual 10.43 ->
+  // 9.15 against the identity order.
+  const int64_t bxf = FOLD && bx < (NO >> 2) / 16 * 16 ? 2 * (8 * (bx >> 4) + (bx & 7)) + ((bx >> 3) & 1) : bx;
+  const int64_t rb = bxf * PB, rbu = MODE == KRQ_OUT_SWIGLU ? rb + (NO >> 4) : rb + 1;
   const int sidx = sy >= 0 ? sy : static_cast<int>(blockIdx.y);
   const int nsteps = (kts + 1) >> 1;
   const int64_t tbase = (int64_t)sidx * kts;
   const int64_t k0 = tbase * 64;  // first K element of this split
-  const int ks = kts * 64;        // K elements of this split
+  const int ks = (FOLD ? 4 : 1) * kts * 64;  // K elements of this split (FOLD: the whole row)
   const int T = (int)(K >> 4);    // sum-of-squares partials per row
   uint8_t* xq = reinterpret_cast<uint8_t*>(red + nw * P * MT * 256);
   const int jcount = wave < nsteps ? (nsteps - wave + nw - 1) / nw : 0;
   KRQ_STAMP(0, threadIdx.x == 0);
-  const ColScales cs = load_col_scales<MODE, PB>(wsc, w_per_row, NO, rb);
+  const ColScales cs = FOLD ? ColScales{1.0f, 1.0f} : load_col_scales<MODE, PB>(wsc, w_per_row, NO, rb);
 
   // ---- fused activation prologue, part 1: activation loads ahead of the weight stream ----
   // Every load of the prologue and of the step ring is issued unconditionally, at a clamped (valid)
   // address where it is not needed: a branch around a load makes the compiler's wait counts
   // conservative (a full drain, vmcnt(0)) at the join, which serializes the weight stream.
   uint4 xv[kXChunks], lv[kXChunks], sv[SC];
-  float sp[SC];
   const uint8_t* lnb = reinterpret_cast<const uint8_t*>(fa.ln);
   if (XK == KRQ_X_BF16_DYN && !AW) {
 #pragma unroll
@@ -239,10 +242,7 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
       if (NORM) lv[c] = ld16(lnb + 2 * e);
     }
   }
-  if (NORM && XK == KRQ_X_BF16_DYN && !AW) {  // every wave reads the row's partials itself
-#pragma unroll
-    for (int c = 0; c < SC; ++c) sp[c] = fa.ss_in[min(lane + 64 * c, T - 1)];
-  } else if (NORM && !AW) {
+  if (NORM && !AW) {  // (static scale, M rows: the [M][K/16] partials, staged in LDS below)
     const int nss = M * T / 4;  // 16-byte chunks of the partials
 #pragma unroll
     for (int c = 0; c < SC; ++c)
@@ -279,6 +279,9 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
     if constexpr (MODE == kOutSwiGluHalf) {
       wl[u] = ld16nt(w_addr_hp<LAYOUT>(w8, rb, NO, t0, K, lane));
       wh[u] = ld16nt(w_addr_hp<LAYOUT>(w8, rb, NO, t1, K, lane));
+    } else if constexpr (FOLD) {
+      wl[u] = ld16nt(w_addr_fold<LAYOUT>(w8, rb, K, kts, t0, lane));
+      wh[u] = ld16nt(w_addr_fold<LAYOUT>(w8, rb, K, kts, t1, lane));
     } else {
       wl[u] = ld16nt(w_addr<LAYOUT>(w8, rb, t0, K, lane));
       wh[u] = ld16nt(w_addr<LAYOUT>(w8, rb, t1, K, lane));
@@ -306,19 +309,8 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   for (int u = 0; u < U; ++u) load_slot(u, u);
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- RMSNorm (NORM): row rstd from the partials, then normalize the loaded chunks ----
-  if (NORM && XK == KRQ_X_BF16_DYN && !AW) {
-    float a = 0.0f;
-#pragma unroll
-    for (int c = 0; c < SC; ++c)
-      if (lane + 64 * c < T) a += sp[c];
-    const float rstd = rstd_of(a, K, fa.eps);
-    // only chunks inside the row: the clamped repeats past K are left raw and kept out of the
-    // amax below (they are never quantized into the slice)
-#pragma unroll
-    for (int c = 0; c < kXChunksDyn; ++c)
-      if (8 * (int64_t)(threadIdx.x + c * blockDim.x) < K) xv[c] = norm8(xv[c], lv[c], rstd);
-  } else if (NORM && !AW) {
+  // ---- RMSNorm (NORM, static scale, M rows): rstd from the partials, then normalize the chunks ----
+  if (NORM && !AW) {
     float* sst = reinterpret_cast<float*>(xq + (size_t)M * ks);
     const int nss = M * T / 4;
 #pragma unroll
@@ -391,10 +383,16 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
       // the quantized slice ends at ks: the high tile of an odd last step is zero (not stale LDS)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const int m = ALGO == 2 ? 0 : min(mt * 16 + r, M - 1);
-        const uint8_t* xr = xq + (int64_t)m * ks + g * 16;
-        xl[u][mt] = *reinterpret_cast<const uint4*>(xr + (2 * j) * 64);
-        xh[u][mt] = sel4(2 * j + 1 < kts, *reinterpret_cast<const uint4*>(xr + min(2 * j + 1, kts - 1) * 64));
+        if constexpr (FOLD) {  // A row r < 4: quarter r of the row; rows 4..15 zero
+          const uint8_t* xr = xq + min(r, 3) * (kts * 64) + g * 16;
+          xl[u][mt] = sel4(r < 4, *reinterpret_cast<const uint4*>(xr + (2 * j) * 64));
+          xh[u][mt] = sel4(r < 4 && 2 * j + 1 < kts, *reinterpret_cast<const uint4*>(xr + min(2 * j + 1, kts - 1) * 64));
+        } else {
+          const int m = ALGO == 2 ? 0 : min(mt * 16 + r, M - 1);
+          const uint8_t* xr = xq + (int64_t)m * ks + g * 16;
+          xl[u][mt] = *reinterpret_cast<const uint4*>(xr + (2 * j) * 64);
+          xh[u][mt] = sel4(2 * j + 1 < kts, *reinterpret_cast<const uint4*>(xr + min(2 * j + 1, kts - 1) * 64));
+        }
       }
     }
     const uint4 bl = sel4(ok, wl[u]), bh = sel4(hi, wh[u]);
@@ -473,6 +471,8 @@ KRQ_DEV void gemv_fp8_body(const uint8_t* __restrict__ x, const float* __restric
   if constexpr (MODE == kOutResidual) {
     residual_epilogue<MT>(red, nw, M, NO, rb, sidx, gridDim.y, xs_l, cs.g, reinterpret_cast<float*>(out), fa,
                           &last_s);
+  } else if constexpr (FOLD) {
+    fold_residual_epilogue(red, nw, rb, xs_l, wsc, w_per_row, fa);
   } else {
     epilogue<MT, MODE, P, CHAIN>(red, 0, nw, M, NO, rb, sidx, xs_l, cs, out, aux);
     if (PB == 2) epilogue<MT, MODE, P>(red, 1, nw, M, NO, rbu, sidx, xs_l, ColScales{cs.u, 1.0f}, out, aux);

@@ -15,7 +15,10 @@ producer, summed in a fixed order by the consumer, where the reference accumulat
 with atomic adds (same-address device atomics serialize on MI355X). FusedLayerBuffers allocates ss
 in that shape; the engine only hands ss[0] / ss[1] back to these functions. Every producer
 overwrites all of its tiles, so zero_ss (the reference's reset of the next accumulator) is
-accepted and has nothing to do.
+accepted and has nothing to do. At M = 1 the normalizing kernels hold the whole row and sum its
+squares themselves, so ss is neither read there nor needed from the producer: the FP8 residual
+GEMVs at M = 1 run folded (N / 4 workgroups, each four output columns over the four quarters of K,
+the four-split sums bit for bit without a cross-workgroup reduction) and write no ss.
 
 When a block's normalized K slice does not fit the kernel's LDS staging (large M x K/split), the
 rows are normalized by krq_rmsnorm_rows first and the GEMV runs on the result: two launches, same
@@ -41,6 +44,9 @@ MAX_ROWS = 32
 # most ~0.8 us more than split 4 (O: the same), while the split-K last-arriver reduction costs
 # three memory round trips (~3 us) at the tail of the launch.
 EP_SPLIT = 1
+# FP8 weights at M = 1: the residual epilogue runs with four splits, folded into N / 4 workgroups
+# (krq_gemv_fp8_fused; no split partials, no counters); 0: EP_SPLIT as at M > 1.
+FOLD_SPLIT = 4
 
 
 class FusedLayerBuffers:
@@ -189,7 +195,8 @@ def _fp8_fused(x, q, split, mode, norm, ep, eps, a):
             return _fp8.gemv_swiglu_fp8(x, q, a)
         return _fp8.gemv_fp8(x, q, split, a)
     if mode == L.OUT_RESIDUAL:
-        part = torch.empty((split, M, N), device=x.device, dtype=torch.float32) if split > 1 else None
+        folded = M == 1 and split == 4  # (the folded launch: no split partials)
+        part = torch.empty((split, M, N), device=x.device, dtype=torch.float32) if split > 1 and not folded else None
         _launch_fp8(x, q, split, mode, norm, ep, eps, a, part)
         return None
     if mode == L.OUT_PARTIAL:
@@ -204,11 +211,15 @@ def gemv_fused(x, w, split, *, norm=None, zero_ss=None, ep=None, eps=1e-6, a=Non
     norm=(ln_w, ss_in): normalise x rows on the fly.
     zero_ss: accepted; the per-tile sums need no reset (every producer overwrites them).
     ep=(res_in, res_out, ss_out, cnt): residual epilogue; returns None. Runs with EP_SPLIT K
-    splits (default one pass) whatever `split` says: y is the full fp32 sum either way.
+    splits (default one pass) whatever `split` says, or, for FP8 weights at M = 1, FOLD_SPLIT
+    folded (ss_out then untouched: one-row consumers sum their row): y is the full fp32 sum.
     a (FP8 weights only): ActScale / SharedScale for static activation scaling; per token if None.
     Otherwise returns bf16 [M, N] (split 1) or fp32 partials [split, M, N]."""
     assert x.shape[-1] % split == 0
-    if ep is not None and EP_SPLIT is not None:
+    if (ep is not None and FOLD_SPLIT and _is_fp8(w) and x.dim() == 2 and x.shape[0] == 1
+            and x.shape[1] % (64 * FOLD_SPLIT) == 0):
+        split = FOLD_SPLIT
+    elif ep is not None and EP_SPLIT is not None:
         split = EP_SPLIT
     if _is_fp8(w):
         mode = L.OUT_RESIDUAL if ep is not None else (L.OUT_PARTIAL if split > 1 else L.OUT_BF16)

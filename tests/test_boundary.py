@@ -122,7 +122,8 @@ def test_invalid_arguments_fail_before_any_launch():
     rc = lib.krq_gemv_fp8_fused(*args, 2, 6144, 2560, 2, L.OUT_PARTIAL, p, p, 1e-6, None, None, None,
                                 None, p, _null())
     assert rc == L.KRQ_EINVAL and b"M == 1" in lib.krq_last_error()
-    rc = lib.krq_gemv_fp8_fused(*args, 1, 2560, 4096, 4, L.OUT_RESIDUAL, None, None, 1e-6, p, p, p, None,
+    # (split 2: at M = 1 the four-split residual runs folded and needs no counters)
+    rc = lib.krq_gemv_fp8_fused(*args, 1, 2560, 4096, 2, L.OUT_RESIDUAL, None, None, 1e-6, p, p, p, None,
                                 p, _null())
     assert rc == L.KRQ_EINVAL and b"cnt" in lib.krq_last_error()
     rc = lib.krq_gemv_fp8_fused(*args, 1, 2560, 4096, 4, L.OUT_RESIDUAL, p, p, 1e-6, p, p, p, p, p, _null())
