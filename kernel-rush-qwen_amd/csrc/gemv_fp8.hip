@@ -210,6 +210,197 @@ bool launch_swiglu_mixed(int awc, int u, bool rows, int M, int nfull, dim3 grid,
   return true;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Wide blocks at 16 < M <= 32 (two activation row tiles) on tiled e4m3 rows and tiled weights. At
+// M = 32 a 16-column block brings two activation bytes from L2 per weight byte. Here a workgroup
+// owns kWideRb adjacent row blocks (one per wave, 64 output columns) of one K split: its waves copy
+// the split's activation tiles (2 x kts KB) into LDS once with direct-to-LDS loads, and each wave
+// then streams only its row block's weights through a ring of U step slots, reading the A operand
+// from LDS. The sums are those of the one-row-block launch the plan would otherwise run with NS
+// waves (step j in wave j % NS, the waves' sums added in wave order): here step j goes to
+// accumulator set j % NS of the one wave, and the sets are added in the same order, so the
+// outputs are the same bit for bit. Every output is written from the wave that owns it.
+constexpr int kWideRb = 4;
+
+// 32-bit LDS address of a pointer into a __shared__ array (wave-uniform)
+KRQ_DEV uint32_t wide_lds_addr(const uint8_t* p) {
+  return __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t*)p)));
+}
+
+// global_load_lds_dwordx4: 16 bytes per lane from base + 16 lane into LDS at l + 16 lane. From inline
+// assembly, so the compiler does not count it: the kernel waits for these loads itself, and issues
+// them before every other load (vector memory loads complete in order, so the compiler's own waits
+// for later loads stay correct).
+KRQ_DEV void wide_dma(const uint8_t* base, uint32_t l, int lane) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(16u * lane), "s"(base)
+               : "memory", "m0");
+}
+
+template <int MODE, int U, int TL, int NS>
+__global__ __launch_bounds__(kWideRb * 64) void k_gemv_wide32(const uint8_t* __restrict__ x, const float* __restrict__ xsc,
+                                                              int x_per_row, const uint8_t* __restrict__ w8,
+                                                              const float* __restrict__ wsc, int w_per_row, int M,
+                                                              int64_t NO, int64_t K, int kts, void* __restrict__ out) {
+  static_assert(MODE == KRQ_OUT_PARTIAL || MODE == KRQ_OUT_BF16 || MODE == KRQ_OUT_SWIGLU, "wide block modes");
+  constexpr int P = MODE == KRQ_OUT_SWIGLU ? 2 : 1;
+  static_assert(2 * P * U < 64, "vmcnt range");
+  static_assert(U % NS == 0, "slot u feeds set u % NS");
+  __shared__ __align__(1024) uint8_t xt[TL * 1024];  // tile (mt, t) of the split at (mt kts + t) KB
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int r = lane & 15, g = lane >> 4;
+  const int sidx = blockIdx.y;
+  const int64_t rb = (int64_t)blockIdx.x * kWideRb + wave;
+  const int64_t tbase = (int64_t)sidx * kts, ktiles = K >> 6;
+  const int nsteps = (kts + 1) >> 1;
+
+  // the split's activation tiles into LDS (the oldest loads of every wave)
+  const uint32_t lx = wide_lds_addr(xt);
+  for (int i = wave; i < 2 * kts; i += kWideRb) {
+    const int mt = i >= kts ? 1 : 0, t = i - mt * kts;
+    wide_dma(x + ((int64_t)mt * ktiles + tbase + t) * 1024, lx + 1024u * static_cast<uint32_t>(i), lane);
+  }
+  // the weight ring: slot u holds step u, then u + U, ...; a slot past the last step reloads it
+  // (masked where consumed)
+  uint4 wl[P][U], wh[P][U];
+  auto load_slot = [&](int u, int cc) {
+    const int j = min(cc, nsteps - 1);
+    const int64_t t0 = tbase + 2 * j, t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int64_t rr = p == 1 ? rb + (NO >> 4) : rb;
+      wl[p][u] = ld16nt(w_addr<KRQ_W_TILED>(w8, rr, t0, K, lane));
+      wh[p][u] = ld16nt(w_addr<KRQ_W_TILED>(w8, rr, t1, K, lane));
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    load_slot(u, u);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // the tiles have landed once at most the ring's loads are outstanding; then a barrier that
+  // orders the LDS writes only (a full fence would wait for the whole ring)
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * P * U) : "memory");
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+
+  v4f acc[P][NS][2];
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int q = 0; q < NS; ++q) acc[p][q][0] = acc[p][q][1] = v4f{0.f, 0.f, 0.f, 0.f};
+  auto consume = [&](int u, int cc) {
+    const int j = min(cc, nsteps - 1);
+    const bool ok = cc < nsteps, hi = ok && (2 * j + 1 < kts);
+    v8i A[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const uint8_t* xr = xt + (mt * kts) * 1024 + lane * 16;
+      const uint4 lo = *reinterpret_cast<const uint4*>(xr + (2 * j) * 1024);
+      const uint4 hh = sel4(2 * j + 1 < kts, *reinterpret_cast<const uint4*>(xr + min(2 * j + 1, kts - 1) * 1024));
+      A[mt] = pack_v8i(lo, hh);
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const v8i B = pack_v8i(sel4(ok, wl[p][u]), sel4(hi, wh[p][u]));
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+        acc[p][u % NS][mt] =
+            __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[mt], B, acc[p][u % NS][mt], 0, 0, 0, 0, 0, 0);
+    }
+  };
+  int base = 0;
+  for (; base + U < nsteps; base += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      consume(u, base + u);
+      load_slot(u, base + u + U);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) consume(u, base + u);
+
+  // the sets in wave order (from zero, as the epilogue sums the waves; one set: as is)
+  v4f sum[P][2];
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      if constexpr (NS == 1) {
+        sum[p][mt] = acc[p][0][mt];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float a = 0.0f;
+#pragma unroll
+          for (int q = 0; q < NS; ++q) a += acc[p][q][mt][i];
+          sum[p][mt][i] = a;
+        }
+      }
+    }
+  // element i of lane l: row 16 mt + 4 (l / 16) + i, column 16 rb + l % 16
+  const int64_t n = rb * 16 + r;
+  const float wg = wsc[w_per_row ? n : 0];
+  const float wu = P == 2 ? wsc[w_per_row ? NO + n : 0] : 0.0f;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = mt * 16 + 4 * g + i;
+      if (m >= M) continue;
+      const float xs = xsc[x_per_row ? m : 0];
+      if constexpr (MODE == KRQ_OUT_PARTIAL) {
+        reinterpret_cast<float*>(out)[((int64_t)sidx * M + m) * NO + n] = sum[0][mt][i] * xs * wg;
+      } else if constexpr (MODE == KRQ_OUT_BF16) {
+        reinterpret_cast<uint16_t*>(out)[(int64_t)m * NO + n] = f32_to_bf16(sum[0][mt][i] * xs * wg);
+      } else {
+        const float gg = round_bf16(sum[0][mt][i] * xs * wg);
+        const float uu = round_bf16(sum[1][mt][i] * xs * wu);
+        const float sl = round_bf16(gg / (1.0f + expf(-gg)));
+        reinterpret_cast<uint16_t*>(out)[(int64_t)m * NO + n] = f32_to_bf16(sl * uu);
+      }
+    }
+}
+
+// The wide-block launch when it applies (16 < M <= 32, tiled e4m3 rows and tiled weights, the
+// plain output modes, one row block per block in the plan (pb 1) and ns <= 4 waves per row block,
+// row blocks a multiple of kWideRb, the split's tiles within LDS); false otherwise.
+bool launch_wide32(int M, int mode, int x_kind, int w_layout, int algo, const void* aux, int pb, int ns, int64_t NO,
+                   int split, int kts, hipStream_t s, const uint8_t* xb, const float* x_scale, int x_per_row,
+                   const uint8_t* wb, const float* w_scale, int w_per_row, int64_t K, void* out) {
+  if (M <= 16 || M > 32 || x_kind != KRQ_X_FP8_TILED || w_layout != KRQ_W_TILED || algo != 1 || pb != 1) return false;
+  // (the two-matrix SwiGLU block measured slower wide: gate_up 12.7 -> 15.1 us at 254 VGPRs)
+  if (!(mode == KRQ_OUT_PARTIAL || mode == KRQ_OUT_BF16)) return false;
+  if ((NO / 16) % kWideRb != 0 || 2 * kts > 96 || ns < 1 || ns > 4) return false;
+  const dim3 grid(static_cast<unsigned>(NO / 16 / kWideRb), static_cast<unsigned>(split)), block(kWideRb * 64);
+  const int m = M;
+  // slots: a multiple of the sets, ten at most (two-matrix blocks take 254 VGPRs with ten)
+#define KRQ_WIDE(MODE_, U_, TL_, NS_)                                                                              \
+  hipLaunchKernelGGL((k_gemv_wide32<MODE_, U_, TL_, NS_>), grid, block, 0, s, xb, x_scale, x_per_row, wb, w_scale, \
+                     w_per_row, m, NO, K, kts, out)
+#define KRQ_WIDE_TL(MODE_, U_, NS_)                  \
+  if (2 * kts <= 48) KRQ_WIDE(MODE_, U_, 48, NS_);     \
+  else KRQ_WIDE(MODE_, U_, 96, NS_);
+#define KRQ_WIDE_U(MODE_)                                 \
+  if (ns == 1) { KRQ_WIDE_TL(MODE_, 10, 1) }               \
+  else if (ns == 2) { KRQ_WIDE_TL(MODE_, 10, 2) }          \
+  else if (ns == 3) { KRQ_WIDE_TL(MODE_, 9, 3) }           \
+  else { KRQ_WIDE_TL(MODE_, 8, 4) }
+  if (mode == KRQ_OUT_PARTIAL) {
+    KRQ_WIDE_U(KRQ_OUT_PARTIAL)
+  } else if (mode == KRQ_OUT_BF16) {
+    KRQ_WIDE_U(KRQ_OUT_BF16)
+  } else {
+    KRQ_WIDE_U(KRQ_OUT_SWIGLU)
+  }
+#undef KRQ_WIDE_U
+#undef KRQ_WIDE_TL
+#undef KRQ_WIDE
+  return true;
+}
+
 // Activation-wave chunks per lane holding `span` bf16 elements (0: too long for one wave).
 int aw_chunks(int64_t span) {
   return span <= 512 * kAwRow ? kAwRow : span <= 512 * kAwSmall ? kAwSmall : span <= 512 * kAwLarge ? kAwLarge : 0;
@@ -316,6 +507,10 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
                 (long long)(xchunks * 8));
     if (awc > 0) nw = min(nw, kMaxThreads / 64 - 1);
   }
+  // 16 < M <= 32 on tiled rows: the wide-block kernel, with this plan's waves as its sets
+  if (launch_wide32(m, mode, x_kind, w_layout, algo, aux, pb, nw, NO, split, kts, s, xb, x_scale, x_per_row, wb,
+                    w_scale, w_per_row, K, out))
+    return krq_check_launch("gemv_fp8");
   // LDS: the weight waves' partial sums, then the bf16 kinds' quantized slice [M][ks]
   const size_t slice = x_kind == KRQ_X_FP8 || x_kind == KRQ_X_FP8_TILED ? 0 : (size_t)M * ks;
   const size_t smem = (size_t)nw * P * MT * 256 * sizeof(float) + slice;
