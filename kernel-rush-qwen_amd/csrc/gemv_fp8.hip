@@ -211,10 +211,10 @@ bool launch_swiglu_mixed(int awc, int u, bool rows, int M, int nfull, dim3 grid,
 }
 
 // ---------------------------------------------------------------------------------------------
-// Wide blocks at 16 < M <= 32 (two activation row tiles) on tiled e4m3 rows and tiled weights. At
+// Wide blocks at 1 < M <= 32 (MT activation row tiles) on tiled e4m3 rows and tiled weights. At
 // M = 32 a 16-column block brings two activation bytes from L2 per weight byte. Here a workgroup
 // owns kWideRb adjacent row blocks (one per wave, 64 output columns) of one K split: its waves copy
-// the split's activation tiles (2 x kts KB) into LDS once with direct-to-LDS loads, and each wave
+// the split's activation tiles (MT x kts KB) into LDS once with direct-to-LDS loads, and each wave
 // then streams only its row block's weights through a ring of U step slots, reading the A operand
 // from LDS. The sums are those of the one-row-block launch the plan would otherwise run with NS
 // waves (step j in wave j % NS, the waves' sums added in wave order): here step j goes to
@@ -237,7 +237,7 @@ KRQ_DEV void wide_dma(const uint8_t* base, uint32_t l, int lane) {
                : "memory", "m0");
 }
 
-template <int MODE, int U, int TL, int NS>
+template <int MODE, int U, int TL, int NS, int MT>
 __global__ __launch_bounds__(kWideRb * 64) void k_gemv_wide32(const uint8_t* __restrict__ x, const float* __restrict__ xsc,
                                                               int x_per_row, const uint8_t* __restrict__ w8,
                                                               const float* __restrict__ wsc, int w_per_row, int M,
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(kWideRb * 64) void k_gemv_wide32(const uint8_t* __r
 
   // the split's activation tiles into LDS (the oldest loads of every wave)
   const uint32_t lx = wide_lds_addr(xt);
-  for (int i = wave; i < 2 * kts; i += kWideRb) {
+  for (int i = wave; i < MT * kts; i += kWideRb) {
     const int mt = i >= kts ? 1 : 0, t = i - mt * kts;
     wide_dma(x + ((int64_t)mt * ktiles + tbase + t) * 1024, lx + 1024u * static_cast<uint32_t>(i), lane);
   }
@@ -285,17 +285,19 @@ __global__ __launch_bounds__(kWideRb * 64) void k_gemv_wide32(const uint8_t* __r
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 
-  v4f acc[P][NS][2];
+  v4f acc[P][NS][MT];
 #pragma unroll
   for (int p = 0; p < P; ++p)
 #pragma unroll
-    for (int q = 0; q < NS; ++q) acc[p][q][0] = acc[p][q][1] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < NS; ++q)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[p][q][mt] = v4f{0.f, 0.f, 0.f, 0.f};
   auto consume = [&](int u, int cc) {
     const int j = min(cc, nsteps - 1);
     const bool ok = cc < nsteps, hi = ok && (2 * j + 1 < kts);
-    v8i A[2];
+    v8i A[MT];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
       const uint8_t* xr = xt + (mt * kts) * 1024 + lane * 16;
       const uint4 lo = *reinterpret_cast<const uint4*>(xr + (2 * j) * 1024);
       const uint4 hh = sel4(2 * j + 1 < kts, *reinterpret_cast<const uint4*>(xr + min(2 * j + 1, kts - 1) * 1024));
@@ -305,7 +307,7 @@ __global__ __launch_bounds__(kWideRb * 64) void k_gemv_wide32(const uint8_t* __r
     for (int p = 0; p < P; ++p) {
       const v8i B = pack_v8i(sel4(ok, wl[p][u]), sel4(hi, wh[p][u]));
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
         acc[p][u % NS][mt] =
             __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[mt], B, acc[p][u % NS][mt], 0, 0, 0, 0, 0, 0);
     }
@@ -323,11 +325,11 @@ __global__ __launch_bounds__(kWideRb * 64) void k_gemv_wide32(const uint8_t* __r
   for (int u = 0; u < U; ++u) consume(u, base + u);
 
   // the sets in wave order (from zero, as the epilogue sums the waves; one set: as is)
-  v4f sum[P][2];
+  v4f sum[P][MT];
 #pragma unroll
   for (int p = 0; p < P; ++p)
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
       if constexpr (NS == 1) {
         sum[p][mt] = acc[p][0][mt];
       } else {
@@ -345,7 +347,7 @@ __global__ __launch_bounds__(kWideRb * 64) void k_gemv_wide32(const uint8_t* __r
   const float wg = wsc[w_per_row ? n : 0];
   const float wu = P == 2 ? wsc[w_per_row ? NO + n : 0] : 0.0f;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = mt * 16 + 4 * g + i;
@@ -370,18 +372,26 @@ __global__ __launch_bounds__(kWideRb * 64) void k_gemv_wide32(const uint8_t* __r
 bool launch_wide32(int M, int mode, int x_kind, int w_layout, int algo, const void* aux, int pb, int ns, int64_t NO,
                    int split, int kts, hipStream_t s, const uint8_t* xb, const float* x_scale, int x_per_row,
                    const uint8_t* wb, const float* w_scale, int w_per_row, int64_t K, void* out) {
-  if (M <= 16 || M > 32 || x_kind != KRQ_X_FP8_TILED || w_layout != KRQ_W_TILED || algo != 1 || pb != 1) return false;
+  // (at M <= 16 one activation row tile: wide only where the plan has several waves per row block,
+  // measured at M = 16: down 7.48 -> 7.03 us, QKV even, O 4.49 -> 4.85 with one wave)
+  if (M <= 16 && ns < 2) return false;
+  if (M < 2 || M > 32 || x_kind != KRQ_X_FP8_TILED || w_layout != KRQ_W_TILED || algo != 1 || pb != 1) return false;
   // (the two-matrix SwiGLU block measured slower wide: gate_up 12.7 -> 15.1 us at 254 VGPRs)
   if (!(mode == KRQ_OUT_PARTIAL || mode == KRQ_OUT_BF16)) return false;
-  if ((NO / 16) % kWideRb != 0 || 2 * kts > 96 || ns < 1 || ns > 4) return false;
+  const int mt = M > 16 ? 2 : 1;  // activation row tiles
+  if ((NO / 16) % kWideRb != 0 || mt * kts > 96 || ns < 1 || ns > 4) return false;
   const dim3 grid(static_cast<unsigned>(NO / 16 / kWideRb), static_cast<unsigned>(split)), block(kWideRb * 64);
   const int m = M;
   // slots: a multiple of the sets, ten at most (two-matrix blocks take 254 VGPRs with ten)
 #define KRQ_WIDE(MODE_, U_, TL_, NS_)                                                                              \
-  hipLaunchKernelGGL((k_gemv_wide32<MODE_, U_, TL_, NS_>), grid, block, 0, s, xb, x_scale, x_per_row, wb, w_scale, \
-                     w_per_row, m, NO, K, kts, out)
+  if (M > 16)                                                                                                   \
+    hipLaunchKernelGGL((k_gemv_wide32<MODE_, U_, TL_, NS_, 2>), grid, block, 0, s, xb, x_scale, x_per_row, wb,      \
+                       w_scale, w_per_row, m, NO, K, kts, out);                                                     \
+  else                                                                                                            \
+    hipLaunchKernelGGL((k_gemv_wide32<MODE_, U_, TL_, NS_, 1>), grid, block, 0, s, xb, x_scale, x_per_row, wb,      \
+                       w_scale, w_per_row, m, NO, K, kts, out)
 #define KRQ_WIDE_TL(MODE_, U_, NS_)                  \
-  if (2 * kts <= 48) KRQ_WIDE(MODE_, U_, 48, NS_);     \
+  if (mt * kts <= 48) KRQ_WIDE(MODE_, U_, 48, NS_);    \
   else KRQ_WIDE(MODE_, U_, 96, NS_);
 #define KRQ_WIDE_U(MODE_)                                 \
   if (ns == 1) { KRQ_WIDE_TL(MODE_, 10, 1) }               \
@@ -507,7 +517,7 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
                 (long long)(xchunks * 8));
     if (awc > 0) nw = min(nw, kMaxThreads / 64 - 1);
   }
-  // 16 < M <= 32 on tiled rows: the wide-block kernel, with this plan's waves as its sets
+  // 1 < M <= 32 on tiled rows: the wide-block kernel, with this plan's waves as its sets
   if (launch_wide32(m, mode, x_kind, w_layout, algo, aux, pb, nw, NO, split, kts, s, xb, x_scale, x_per_row, wb,
                     w_scale, w_per_row, K, out))
     return krq_check_launch("gemv_fp8");
