@@ -253,6 +253,7 @@ __global__ __launch_bounds__(kWideRb * 64) void k_gemv_wide32(const uint8_t* __r
   const int64_t rb = (int64_t)blockIdx.x * kWideRb + wave;
   const int64_t tbase = (int64_t)sidx * kts, ktiles = K >> 6;
   const int nsteps = (kts + 1) >> 1;
+  KRQ_STAMP(0, threadIdx.x == 0);
 
   // the split's activation tiles into LDS (the oldest loads of every wave)
   const uint32_t lx = wide_lds_addr(xt);
@@ -260,6 +261,16 @@ __global__ __launch_bounds__(kWideRb * 64) void k_gemv_wide32(const uint8_t* __r
     const int mt = i >= kts ? 1 : 0, t = i - mt * kts;
     wide_dma(x + ((int64_t)mt * ktiles + tbase + t) * 1024, lx + 1024u * static_cast<uint32_t>(i), lane);
   }
+  // the epilogue's weight and row scales, loaded now (behind the tiles, ahead of the ring: the
+  // tiles' wait below covers them) so their latency is not paid after the loop
+  const int64_t n = rb * 16 + r;
+  const float wg = wsc[w_per_row ? n : 0];
+  const float wu = P == 2 ? wsc[w_per_row ? NO + n : 0] : 0.0f;
+  float xs[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xs[mt][i] = xsc[x_per_row ? min(mt * 16 + 4 * g + i, M - 1) : 0];
   // the weight ring: slot u holds step u, then u + U, ...; a slot past the last step reloads it
   // (masked where consumed)
   uint4 wl[P][U], wh[P][U];
@@ -284,6 +295,7 @@ __global__ __launch_bounds__(kWideRb * 64) void k_gemv_wide32(const uint8_t* __r
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  KRQ_STAMP(1, threadIdx.x == 0);
 
   v4f acc[P][NS][MT];
 #pragma unroll
@@ -323,6 +335,7 @@ __global__ __launch_bounds__(kWideRb * 64) void k_gemv_wide32(const uint8_t* __r
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) consume(u, base + u);
+  KRQ_STAMP(2, threadIdx.x == 0);
 
   // the sets in wave order (from zero, as the epilogue sums the waves; one set: as is)
   v4f sum[P][MT];
@@ -343,27 +356,24 @@ __global__ __launch_bounds__(kWideRb * 64) void k_gemv_wide32(const uint8_t* __r
       }
     }
   // element i of lane l: row 16 mt + 4 (l / 16) + i, column 16 rb + l % 16
-  const int64_t n = rb * 16 + r;
-  const float wg = wsc[w_per_row ? n : 0];
-  const float wu = P == 2 ? wsc[w_per_row ? NO + n : 0] : 0.0f;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = mt * 16 + 4 * g + i;
       if (m >= M) continue;
-      const float xs = xsc[x_per_row ? m : 0];
       if constexpr (MODE == KRQ_OUT_PARTIAL) {
-        reinterpret_cast<float*>(out)[((int64_t)sidx * M + m) * NO + n] = sum[0][mt][i] * xs * wg;
+        reinterpret_cast<float*>(out)[((int64_t)sidx * M + m) * NO + n] = sum[0][mt][i] * xs[mt][i] * wg;
       } else if constexpr (MODE == KRQ_OUT_BF16) {
-        reinterpret_cast<uint16_t*>(out)[(int64_t)m * NO + n] = f32_to_bf16(sum[0][mt][i] * xs * wg);
+        reinterpret_cast<uint16_t*>(out)[(int64_t)m * NO + n] = f32_to_bf16(sum[0][mt][i] * xs[mt][i] * wg);
       } else {
-        const float gg = round_bf16(sum[0][mt][i] * xs * wg);
-        const float uu = round_bf16(sum[1][mt][i] * xs * wu);
+        const float gg = round_bf16(sum[0][mt][i] * xs[mt][i] * wg);
+        const float uu = round_bf16(sum[1][mt][i] * xs[mt][i] * wu);
         const float sl = round_bf16(gg / (1.0f + expf(-gg)));
         reinterpret_cast<uint16_t*>(out)[(int64_t)m * NO + n] = f32_to_bf16(sl * uu);
       }
     }
+  KRQ_STAMP(3, threadIdx.x == 0);
 }
 
 // The wide-block launch when it applies (16 < M <= 32, tiled e4m3 rows and tiled weights, the

@@ -1,4 +1,5 @@
-"""Per-block timeline of the decode step's FP8 GEMV launches (M = 1 and M = 16), read from the
+"""Per-block timeline of the decode step's FP8 GEMV launches (M = 1 and M = 16 by default, any of 1,
+16 and 32 with --m), read from the
 timeline build of the library, whose GEMV kernel stamps the wall clock (100 MHz) per block at
   t0  entry,
   t1  activation slice ready (bf16 kinds: the activation wave's, or the whole block's, prologue
@@ -8,7 +9,7 @@ timeline build of the library, whose GEMV kernel stamps the wall clock (100 MHz)
 and the compute unit each block ran on (__smid: XCD, shader engine, CU).
 
     python kernel-rush-qwen_amd/build_lib.py --timeline     # on the build host: libkrq_timeline.so
-    python kernel-rush-qwen_amd/timeline.py [--json PATH]    # on the GPU
+    python kernel-rush-qwen_amd/timeline.py [--m 1,16,32] [--json PATH]    # on the GPU
 
 Each projection runs the way bench.py's kernel table runs it (a graph of 72 launches cycling 36
 layers' weights, hipEvents around each replay); the stamps are those of the graph's last launch.
@@ -39,7 +40,12 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--json", default=None, help="also write the summary here")
     ap.add_argument("--reps", type=int, default=72, help="launches per graph")
+    ap.add_argument("--m", default="1,16", help="comma-separated rows per launch, each 1, 16 or 32 "
+                    "(above one row: per-token tiled e4m3 rows, as bench.py's kernel table)")
     args = ap.parse_args()
+    ms = [int(v) for v in args.m.split(",")]
+    if not ms or any(v not in (1, 16, 32) for v in ms):
+        sys.exit("timeline.py: --m takes 1, 16 and 32")
     if not os.path.exists(LIB):
         sys.exit(f"timeline.py: {LIB} is missing; build it first: python kernel-rush-qwen_amd/build_lib.py "
                  "--timeline")
@@ -77,7 +83,7 @@ def main():
           f"stamps (us from the first block's entry) p50/p90/max over blocks", flush=True)
     print(f"  {'launch':<12} {'blocks':>6} {'us/launch':>9} {'span':>6} {'outside':>7} | {'t0 (entry)':>17} | "
           f"{'t1 (act ready)':>17} | {'t2 (loop done)':>17} | {'t3 (outputs)':>17}", flush=True)
-    for M in (1, 16):
+    for M in ms:
         xs = bench.make_inputs(torch, dev, M)
         for name, N, K, split, mode in bench.PROJ:
             x, m = xs[name], modes[mode]
