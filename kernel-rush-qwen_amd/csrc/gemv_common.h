@@ -554,15 +554,37 @@ KRQ_DEV float row_prologue(const uint16_t* __restrict__ x, const float* __restri
   return *rstd_sh;
 }
 
+// Residual values a thread of row block rb's residual epilogue adds, res_in at the rows and
+// columns it finishes (clamped to row M - 1), loaded at kernel start so their latency hides under
+// the weight stream.
+template <int MT>
+struct ResidualPre {
+  uint16_t v[MT * 4];
+};
+template <int MT>
+KRQ_DEV ResidualPre<MT> load_residual(const FusedArgs& fa, int M, int64_t NO, int64_t rb) {
+  constexpr int NV = MT * 256;
+  ResidualPre<MT> p;
+  const int NT = blockDim.x;
+#pragma unroll
+  for (int q = 0; q < MT * 4; ++q) {
+    const int v = min((int)threadIdx.x + q * NT, NV - 1);
+    const int ln = v & 63, m = (v >> 8) * 16 + 4 * (ln >> 4) + ((v >> 6) & 3);
+    p.v[q] = fa.res_in[(int64_t)min(m, M - 1) * NO + rb * 16 + (ln & 15)];
+  }
+  return p;
+}
+
 // Residual epilogue of one row block rb (P == 1 accumulators in red). One split's value is
 // (sum over waves) * xs[m] * wsc, as the partials epilogue writes it. With S > 1 splits each split
 // writes its partial tile to part [S][M][NO] with write-through stores, waits for them, and bumps
 // cnt[rb]; the split that brings the count to S sums the S partials in split order, finishes the
-// tile and zeroes the counter. last_s: a shared word. Called by every thread of the block.
+// tile and zeroes the counter. last_s: a shared word. rp: this thread's residual values
+// (load_residual), or null to read them here. Called by every thread of the block.
 template <int MT>
 KRQ_DEV void residual_epilogue(const float* red, int nw, int M, int64_t NO, int64_t rb, int sidx, int S,
                                const float* xs, float wsc, float* part, const FusedArgs& fa,
-                               uint32_t* last_s) {
+                               uint32_t* last_s, const ResidualPre<MT>* rp = nullptr) {
   constexpr int NV = MT * 256;
   constexpr int VPT = NV / 64;  // values per thread at most (blockDim.x >= 64)
   const int NT = blockDim.x;
@@ -606,7 +628,8 @@ KRQ_DEV void residual_epilogue(const float* red, int nw, int M, int64_t NO, int6
       for (int s2 = 0; s2 < S; ++s2)
         y += s2 == sidx ? av[q] : as_f32(cload(reinterpret_cast<const uint32_t*>(part + ((int64_t)s2 * M + mm) * NO + n)));
     }
-    const float xn = round_bf16(bf16_to_f32(fa.res_in[(int64_t)mm * NO + n]) + round_bf16(y));
+    const uint16_t rv = rp ? rp->v[q] : fa.res_in[(int64_t)mm * NO + n];
+    const float xn = round_bf16(bf16_to_f32(rv) + round_bf16(y));
     if (m < M) fa.res_out[(int64_t)m * NO + n] = f32_to_bf16(xn);
     float sq = xn * xn;  // the 16 lanes sharing (mt, i, g) hold the 16 columns of one row
 #pragma unroll
