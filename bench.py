@@ -431,7 +431,7 @@ def summarize_trace(csv_path):
 STEP_KERNELS = {
     1: {"qkv": "k_gemv_fp8<1, 1, 1, 1, 1, 10, 1, 5>", "o": "k_gemv_fp8<1, 1, 1, 1, 1, 8, 1, 8>",
         "gate_up": "k_gemv_fp8_swiglu_mixed<1, 1, 1, 5, 5, 1>", "down": "k_gemv_fp8<1, 1, 1, 1, 1, 20, 1, 20>"},
-    16: {"qkv": "k_gemv_fp8<1, 1, 1, 3, 1, 10, 1, 0>", "o": "k_gemv_fp8<1, 1, 1, 3, 1, 8, 1, 0>",
+    16: {"qkv": "k_gemv_wide32<1, 10, 48, 1, 1>", "o": "k_gemv_wide32<1, 8, 48, 1, 1>",
          "gate_up": "k_gemv_fp8_swiglu_mixed<1, 3, 1, 5, 0, 1>", "down": "k_gemv_wide32<1, 8, 48, 4, 1>"},
 }
 PMC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --output-format csv -d <out> -o pmc -- python3 bench.py "

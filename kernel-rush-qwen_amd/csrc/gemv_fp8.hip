@@ -376,15 +376,14 @@ __global__ __launch_bounds__(kWideRb * 64) void k_gemv_wide32(const uint8_t* __r
   KRQ_STAMP(3, threadIdx.x == 0);
 }
 
-// The wide-block launch when it applies (16 < M <= 32, tiled e4m3 rows and tiled weights, the
+// The wide-block launch when it applies (1 < M <= 32, tiled e4m3 rows and tiled weights, the
 // plain output modes, one row block per block in the plan (pb 1) and ns <= 4 waves per row block,
 // row blocks a multiple of kWideRb, the split's tiles within LDS); false otherwise.
 bool launch_wide32(int M, int mode, int x_kind, int w_layout, int algo, const void* aux, int pb, int ns, int64_t NO,
                    int split, int kts, hipStream_t s, const uint8_t* xb, const float* x_scale, int x_per_row,
                    const uint8_t* wb, const float* w_scale, int w_per_row, int64_t K, void* out) {
-  // (at M <= 16 one activation row tile: wide only where the plan has several waves per row block,
-  // measured at M = 16: down 7.48 -> 7.03 us, QKV even, O 4.49 -> 4.85 with one wave)
-  if (M <= 16 && ns < 2) return false;
+  // (at M = 16, graph-timed: down 7.48 -> 7.03 us, QKV 4.87 -> 4.66, O 4.52 -> 4.20 with eight
+  // slots for its eight steps; ten, two of them masked, measured 4.57)
   if (M < 2 || M > 32 || x_kind != KRQ_X_FP8_TILED || w_layout != KRQ_W_TILED || algo != 1 || pb != 1) return false;
   // (the two-matrix SwiGLU block measured slower wide: gate_up 12.7 -> 15.1 us at 254 VGPRs)
   if (!(mode == KRQ_OUT_PARTIAL || mode == KRQ_OUT_BF16)) return false;
@@ -392,7 +391,8 @@ bool launch_wide32(int M, int mode, int x_kind, int w_layout, int algo, const vo
   if ((NO / 16) % kWideRb != 0 || mt * kts > 96 || ns < 1 || ns > 4) return false;
   const dim3 grid(static_cast<unsigned>(NO / 16 / kWideRb), static_cast<unsigned>(split)), block(kWideRb * 64);
   const int m = M;
-  // slots: a multiple of the sets, ten at most (two-matrix blocks take 254 VGPRs with ten)
+  // slots: a multiple of the sets, ten at most (two-matrix blocks take 254 VGPRs with ten); one
+  // set over at most eight steps: eight
 #define KRQ_WIDE(MODE_, U_, TL_, NS_)                                                                              \
   if (M > 16)                                                                                                   \
     hipLaunchKernelGGL((k_gemv_wide32<MODE_, U_, TL_, NS_, 2>), grid, block, 0, s, xb, x_scale, x_per_row, wb,      \
@@ -404,16 +404,15 @@ bool launch_wide32(int M, int mode, int x_kind, int w_layout, int algo, const vo
   if (mt * kts <= 48) KRQ_WIDE(MODE_, U_, 48, NS_);    \
   else KRQ_WIDE(MODE_, U_, 96, NS_);
 #define KRQ_WIDE_U(MODE_)                                 \
-  if (ns == 1) { KRQ_WIDE_TL(MODE_, 10, 1) }               \
+  if (ns == 1 && kts <= 16) { KRQ_WIDE_TL(MODE_, 8, 1) }   \
+  else if (ns == 1) { KRQ_WIDE_TL(MODE_, 10, 1) }          \
   else if (ns == 2) { KRQ_WIDE_TL(MODE_, 10, 2) }          \
   else if (ns == 3) { KRQ_WIDE_TL(MODE_, 9, 3) }           \
   else { KRQ_WIDE_TL(MODE_, 8, 4) }
   if (mode == KRQ_OUT_PARTIAL) {
     KRQ_WIDE_U(KRQ_OUT_PARTIAL)
-  } else if (mode == KRQ_OUT_BF16) {
-    KRQ_WIDE_U(KRQ_OUT_BF16)
   } else {
-    KRQ_WIDE_U(KRQ_OUT_SWIGLU)
+    KRQ_WIDE_U(KRQ_OUT_BF16)
   }
 #undef KRQ_WIDE_U
 #undef KRQ_WIDE_TL
