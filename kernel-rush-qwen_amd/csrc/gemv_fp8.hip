@@ -420,6 +420,140 @@ bool launch_wide32(int M, int mode, int x_kind, int w_layout, int algo, const vo
   return true;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Wide one-row blocks (M = 1, bf16 activations scaled in the kernel, tiled weights): a workgroup
+// owns RB adjacent row blocks of one K split, one weight wave each holding every step of its row
+// block in a ring of U slots, and one activation wave that scales and quantizes the split's slice
+// into LDS once for all of them (the one-row launch's activation wave does it once per row block:
+// at K = 9,728 that is the whole bf16 row read per 16 output columns). Each row block's products,
+// their order and the output arithmetic are those of the one-row launch with one weight wave per
+// row block, so the outputs are the same bit for bit.
+template <int MODE, int XK, int U, int AWC, int RB>
+__global__ __launch_bounds__((RB + 1) * 64) void k_gemv_wide1(const uint8_t* __restrict__ x,
+                                                             const float* __restrict__ xsc,
+                                                             const float* __restrict__ xinv,
+                                                             const uint8_t* __restrict__ w8,
+                                                             const float* __restrict__ wsc, int w_per_row,
+                                                             int64_t NO, int64_t K, int kts, void* __restrict__ out) {
+  static_assert(MODE == KRQ_OUT_PARTIAL || MODE == KRQ_OUT_BF16, "wide one-row modes");
+  static_assert(XK == KRQ_X_BF16_DYN || XK == KRQ_X_BF16_STATIC, "bf16 activations scaled in the kernel");
+  static_assert(2 * U < 64, "vmcnt range");
+  extern __shared__ __align__(16) uint8_t xq[];  // the split's e4m3 slice (ks bytes), then its scale
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int sidx = blockIdx.y;
+  const int ks = kts * 64;
+  const int64_t k0 = (int64_t)sidx * ks, tbase = (int64_t)sidx * kts;
+  const int nsteps = (kts + 1) >> 1;
+  float* xs_l = reinterpret_cast<float*>(xq + ks);
+  KRQ_STAMP(0, threadIdx.x == 0);
+  if (wave == RB) {
+    activation_wave<XK, AWC, false, false>(x, xsc, xinv, K, k0, ks, lane, xq, xs_l, FusedArgs{});
+    KRQ_STAMP(1, lane == 0);
+    // the slice and its scale are in LDS (a barrier that orders LDS only: the weight waves' rings
+    // stay in flight)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    return;
+  }
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t rb = (int64_t)blockIdx.x * RB + wave;
+  const float ws = wsc[w_per_row ? rb * 16 + r : 0];  // (read now, not after the loop)
+  // the weight ring: slot u holds step u, then u + U, ...; a slot past the last step reloads it
+  // (masked where consumed)
+  uint4 wl[U], wh[U];
+  auto load_slot = [&](int u, int cc) {
+    const int j = min(cc, nsteps - 1);
+    const int64_t t0 = tbase + 2 * j, t1 = (2 * j + 1 < kts) ? t0 + 1 : t0;
+    wl[u] = ld16nt(w_addr<KRQ_W_TILED>(w8, rb, t0, K, lane));
+    wh[u] = ld16nt(w_addr<KRQ_W_TILED>(w8, rb, t1, K, lane));
+  };
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    load_slot(u, u);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+  // A: every row is the one activation row (lane 16 g + r: bytes 16 g .. 16 g + 15 of the step's
+  // 64-byte chunks), as in the one-row launch
+  auto consume = [&](int u, int cc) {
+    const int j = min(cc, nsteps - 1);
+    const bool ok = cc < nsteps, hi = ok && (2 * j + 1 < kts);
+    const uint8_t* xr = xq + g * 16;
+    const uint4 lo = *reinterpret_cast<const uint4*>(xr + (2 * j) * 64);
+    const uint4 hh = sel4(2 * j + 1 < kts, *reinterpret_cast<const uint4*>(xr + min(2 * j + 1, kts - 1) * 64));
+    const v8i B = pack_v8i(sel4(ok, wl[u]), sel4(hi, wh[u]));
+    acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(pack_v8i(lo, hh), B, acc, 0, 0, 0, 0, 0, 0);
+  };
+  int base = 0;
+  for (; base + U < nsteps; base += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      consume(u, base + u);
+      load_slot(u, base + u + U);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) consume(u, base + u);
+  KRQ_STAMP(2, threadIdx.x == 0);
+  // row 0 of the product: element 0 of lanes 0-15, column 16 rb + lane
+  if (g == 0) {
+    const int64_t n = rb * 16 + r;
+    const float y = acc[0] * xs_l[0] * ws;
+    if constexpr (MODE == KRQ_OUT_BF16)
+      reinterpret_cast<uint16_t*>(out)[n] = f32_to_bf16(y);
+    else
+      reinterpret_cast<float*>(out)[(int64_t)sidx * NO + n] = y;
+  }
+  KRQ_STAMP(3, threadIdx.x == 0);
+}
+
+constexpr int kWide1Rb = 4;
+
+// The wide one-row launch when it applies (M = 1, bf16 activations with the plan's activation
+// wave, tiled weights, the plain output modes, a plan of one weight wave per row block holding
+// all of its steps, row blocks a multiple of kWide1Rb); false otherwise.
+bool launch_wide1(int M, int mode, int x_kind, int w_layout, int algo, int pb, int nw, int awc, int u, int64_t NO,
+                  int split, int kts, hipStream_t s, const uint8_t* xb, const float* x_scale, const float* x_inv,
+                  const uint8_t* wb, const float* w_scale, int w_per_row, int64_t K, void* out) {
+  if (M != 1 || awc <= 0 || algo != 1 || w_layout != KRQ_W_TILED || pb != 1 || nw != 1) return false;
+  if (!(mode == KRQ_OUT_PARTIAL || mode == KRQ_OUT_BF16)) return false;
+  if (!(x_kind == KRQ_X_BF16_DYN || x_kind == KRQ_X_BF16_STATIC)) return false;
+  if ((NO / 16) % kWide1Rb != 0 || !(u == kMidU || u == kDeepU || u == kBigU)) return false;
+  // at most 96 KB of weights per workgroup: the wide launch uses one workgroup per CU on fewer CUs,
+  // so a CU streams more bytes than in the one-row launch. Measured (graph of 72 launches, same box,
+  // alternating): QKV 4.53 -> 4.27 us (80 KB), O 3.99 -> 3.85 (64 KB), down 6.34 -> 6.83 (152 KB).
+  if ((int64_t)kWide1Rb * 16 * kts * 64 > 96 * 1024) return false;
+  if (!(awc == kAwRow || awc == kAwSmall || awc == kAwLarge)) return false;
+  const dim3 grid(static_cast<unsigned>(NO / 16 / kWide1Rb), static_cast<unsigned>(split)), block((kWide1Rb + 1) * 64);
+  const size_t smem = (size_t)kts * 64 + 16;
+#define KRQ_W1(MODE_, XK_, U_, AWC_)                                                                        \
+  hipLaunchKernelGGL((k_gemv_wide1<MODE_, XK_, U_, AWC_, kWide1Rb>), grid, block, smem, s, xb, x_scale, x_inv, \
+                     wb, w_scale, w_per_row, NO, K, kts, out)
+#define KRQ_W1_AWC(MODE_, XK_, U_)                      \
+  if (awc == kAwRow) { KRQ_W1(MODE_, XK_, U_, kAwRow); }     \
+  else if (awc == kAwSmall) { KRQ_W1(MODE_, XK_, U_, kAwSmall); } \
+  else { KRQ_W1(MODE_, XK_, U_, kAwLarge); }
+#define KRQ_W1_U(MODE_, XK_)                              \
+  if (u == kMidU) { KRQ_W1_AWC(MODE_, XK_, kMidU) }         \
+  else if (u == kDeepU) { KRQ_W1_AWC(MODE_, XK_, kDeepU) }  \
+  else { KRQ_W1_AWC(MODE_, XK_, kBigU) }
+  if (x_kind == KRQ_X_BF16_DYN) {
+    if (mode == KRQ_OUT_PARTIAL) { KRQ_W1_U(KRQ_OUT_PARTIAL, KRQ_X_BF16_DYN) }
+    else { KRQ_W1_U(KRQ_OUT_BF16, KRQ_X_BF16_DYN) }
+  } else {
+    if (mode == KRQ_OUT_PARTIAL) { KRQ_W1_U(KRQ_OUT_PARTIAL, KRQ_X_BF16_STATIC) }
+    else { KRQ_W1_U(KRQ_OUT_BF16, KRQ_X_BF16_STATIC) }
+  }
+#undef KRQ_W1_U
+#undef KRQ_W1_AWC
+#undef KRQ_W1
+  return true;
+}
+
 // Activation-wave chunks per lane holding `span` bf16 elements (0: too long for one wave).
 int aw_chunks(int64_t span) {
   return span <= 512 * kAwRow ? kAwRow : span <= 512 * kAwSmall ? kAwSmall : span <= 512 * kAwLarge ? kAwLarge : 0;
@@ -526,6 +660,10 @@ int krq::gemv_fp8_run(const void* x, int x_kind, const float* x_scale, const flo
                 (long long)(xchunks * 8));
     if (awc > 0) nw = min(nw, kMaxThreads / 64 - 1);
   }
+  // one row with the activation wave: four row blocks per workgroup share its slice
+  if (launch_wide1(m, mode, x_kind, w_layout, algo, pb, nw, awc, u, NO, split, kts, s, xb, x_scale, x_inv, wb,
+                   w_scale, w_per_row, K, out))
+    return krq_check_launch("gemv_fp8");
   // 1 < M <= 32 on tiled rows: the wide-block kernel, with this plan's waves as its sets
   if (launch_wide32(m, mode, x_kind, w_layout, algo, aux, pb, nw, NO, split, kts, s, xb, x_scale, x_per_row, wb,
                     w_scale, w_per_row, K, out))
