@@ -429,7 +429,7 @@ def summarize_trace(csv_path):
 # The kernel template each step projection runs (tiled weights), per M: the keys of the counter
 # summaries profiles/traffic_c2.json / traffic_c3.json that --summarize-pmc writes.
 STEP_KERNELS = {
-    1: {"qkv": "k_gemv_wide1<1, 1, 10, 5, 4>", "o": "k_gemv_wide1<1, 1, 8, 8, 4>",
+    1: {"qkv": "k_gemv_wide1<1, 1, 10, 5, 4>", "o": "k_gemv_fp8<1, 1, 1, 1, 1, 8, 1, 8>",
         "gate_up": "k_gemv_fp8_swiglu_mixed<1, 1, 1, 5, 5, 1>", "down": "k_gemv_fp8<1, 1, 1, 1, 1, 20, 1, 20>"},
     16: {"qkv": "k_gemv_wide32<1, 10, 48, 1, 1>", "o": "k_gemv_wide32<1, 8, 48, 1, 1>",
          "gate_up": "k_gemv_fp8_swiglu_mixed<1, 3, 1, 5, 0, 1>", "down": "k_gemv_wide32<1, 8, 48, 4, 1>"},

@@ -527,6 +527,11 @@ bool launch_wide1(int M, int mode, int x_kind, int w_layout, int algo, int pb, i
   // so a CU streams more bytes than in the one-row launch. Measured (graph of 72 launches, same box,
   // alternating): QKV 4.53 -> 4.27 us (80 KB), O 3.99 -> 3.85 (64 KB), down 6.34 -> 6.83 (152 KB).
   if ((int64_t)kWide1Rb * 16 * kts * 64 > 96 * 1024) return false;
+  // and splits of more than 16 tiles (QKV, not O): alone each gains, but in the decode step O right
+  // after QKV on the wide blocks costs more than both gain (C5 at M = 1, same box, alternating:
+  // 1,038.5 us per step with neither, 1,038.3 with QKV, 1,035.8 with O, 1,059.7 with both; the
+  // kernel trace shows an extra ~3.7 us gap before O when both run wide)
+  if (kts <= 16) return false;
   if (!(awc == kAwRow || awc == kAwSmall || awc == kAwLarge)) return false;
   const dim3 grid(static_cast<unsigned>(NO / 16 / kWide1Rb), static_cast<unsigned>(split)), block((kWide1Rb + 1) * 64);
   const size_t smem = (size_t)kts * 64 + 16;
