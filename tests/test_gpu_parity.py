@@ -178,7 +178,7 @@ def _fp8_case(N, K, M, seed):
 
 
 SHAPES = {"qkv": QKV, "o": O_PROJ, "down": DOWN, "small": (64, 384)}
-SEEDS = {"qkv": 0, "o": 1, "down": 3, "small": 5}
+SEEDS = {"qkv": 0, "o": 1, "down": 3, "small": 5, "odd": 6}
 
 
 @pytest.mark.parametrize("name", list(SHAPES))
@@ -616,7 +616,9 @@ def test_static_scale_multi_row_routes(dev, M):
     assert torch.equal(fp8.gemv_swiglu_fp8(xd, q, a), direct(xd, q, 1, L.OUT_SWIGLU))
 
 
-TILED_SHAPES = {"qkv": (QKV, (1, 2)), "o": (O_PROJ, (4,)), "down": (DOWN, (4,)), "small": ((64, 384), (1, 2))}
+# ("odd": five row blocks, not a multiple of the wide blocks' four, so the 16-column plan runs)
+TILED_SHAPES = {"qkv": (QKV, (1, 2)), "o": (O_PROJ, (4,)), "down": (DOWN, (4,)), "small": ((64, 384), (1, 2)),
+                "odd": ((80, 640), (1, 5))}
 
 
 @pytest.mark.parametrize("name", list(TILED_SHAPES))
