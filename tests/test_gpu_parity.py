@@ -650,6 +650,25 @@ def test_gemv_on_tiled_activations(dev, name, M):
     assert torch.equal(sw, fp8.gemv_fp8_launch(x8, xs, qs, 1, L.OUT_SWIGLU)), (name, M)
 
 
+@pytest.mark.parametrize("static", [False, True])
+def test_wide_one_row_blocks_match_one_row_launch(dev, static):
+    """QKV at M = 1 runs the wide one-row blocks (four row blocks per workgroup share one activation
+    wave). The same weight's first 6,128 rows (383 row blocks, not a multiple of four) run the
+    one-row launch with the same plan (one weight wave holding all ten steps beside the activation
+    wave); per-channel quantization gives those rows the same bytes and scales, so the shared
+    output columns must be equal bit for bit, for per-token and static activation scales."""
+    N, K = QKV
+    w, x = _fp8_case(N, K, 1, 95)
+    wd, xd = w.to(dev), x.to(dev)
+    q, q_cut = fp8.quantize(wd), fp8.quantize(wd[:N - 16].contiguous())
+    assert torch.equal(q_cut[0], q[0][:N - 16]) and torch.equal(q_cut[1], q[1][:N - 16])
+    a = fp8.ActScale(xd) if static else None
+    for split in (1, 2):
+        y = fp8.gemv_fp8(xd, q, split, a)
+        y_cut = fp8.gemv_fp8(xd, q_cut, split, a)
+        assert torch.equal(y[..., :N - 16], y_cut), (static, split)
+
+
 @pytest.mark.parametrize("M", [1, 4, 16])
 def test_fused_static_quant_matches_cast_path(dev, M):
     N, K = O_PROJ
