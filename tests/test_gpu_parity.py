@@ -650,6 +650,37 @@ def test_gemv_on_tiled_activations(dev, name, M):
     assert torch.equal(sw, fp8.gemv_fp8_launch(x8, xs, qs, 1, L.OUT_SWIGLU)), (name, M)
 
 
+@pytest.mark.parametrize("M", [17, 32])
+@pytest.mark.parametrize("scales", ["channel", "tensor", "static"])
+def test_gate_up_tiled_rows_match_row_major(dev, M, scales):
+    """gate_up at 16 < M <= 32 at its real shape (608 column blocks: the mixed launch of two-matrix
+    and half-pair blocks): bf16 rows through the tiled e4m3 operand (quant_rows_tiled or
+    cast_tiled) give the act of the row-major e4m3 rows bit for bit, with per-channel, per-tensor
+    and static scales, and meet the oracle's bar."""
+    N, K = GATE_UP
+    w, x = _fp8_case(N, K, M, 96)
+    wd, xd = w.to(dev), x.to(dev)
+    q = fp8.quantize_weight(wd) if scales == "tensor" else fp8.quantize(wd)
+    if scales == "static":
+        a = fp8.ActScale(xd)
+        y = fp8.gemv_swiglu_fp8(xd, q, a)
+        x8, xs = fp8._cast(xd, a), a.scale.reshape(1)
+    else:
+        y = fp8.gemv_swiglu_fp8(xd, q)
+        x8, xs = fp8.quant_rows(xd)
+    assert torch.equal(y, fp8.gemv_fp8_launch(x8, xs, q, 1, L.OUT_SWIGLU)), (M, scales)
+    I = N // 2
+    r8, rs = O.quantize_weight(u16(w)) if scales == "tensor" else O.quantize(u16(w))
+    if scales == "static":
+        am, inv, sc = O.act_scale(u16(x))
+        x8r, xsr = O.cast(u16(x), inv), sc
+    else:
+        x8r, xsr = O.quant_rows(u16(x))
+    _, full = O.fp8_matmul(x8r, xsr, r8, rs)
+    ref = O.bf16_to_f32(O.swiglu(full[:, :I].astype(np.float32), full[:, I:].astype(np.float32)))
+    assert rel_err(y.float().cpu().numpy(), ref) <= TOL, (M, scales)
+
+
 @pytest.mark.parametrize("static", [False, True])
 def test_wide_one_row_blocks_match_one_row_launch(dev, static):
     """QKV at M = 1 runs the wide one-row blocks (four row blocks per workgroup share one activation
