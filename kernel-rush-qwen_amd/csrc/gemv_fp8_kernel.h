@@ -500,22 +500,25 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8(KRQ_FP8_KERNEL_PARAMS)
                                                                K, kts, out, aux, FusedArgs{}, blockIdx.x);
 }
 
-// The SwiGLU launch (MT 16-row tiles) with its last column blocks split in half: workgroups
-// below nfull are the two-matrix blocks of output columns 16 i .. 16 i + 15; workgroup nfull + j
-// is half-pair block 2 nfull + j (columns 8 (2 nfull + j) ..), which streams half the bytes with
-// the same steps per wave. Workgroup i runs on compute unit i mod 256, so nfull = 512 puts two
-// full blocks on every CU and at most one half block more, instead of a third full block on some
-// CUs.
+// The SwiGLU launch (MT 16-row tiles) with its last column blocks split in half: nfull two-matrix
+// blocks (output columns 16 i .. 16 i + 15) and nh = gridDim.x - nfull half-pair blocks 2 nfull + j
+// (columns 8 (2 nfull + j) ..), which stream half the bytes with the same steps per wave.
+// Workgroup i runs on compute unit i mod 256, so nfull = 512 puts two full blocks on every CU and
+// at most one half block more, instead of a third full block on some CUs. hfirst = 0: workgroups
+// below nfull are the full blocks; hfirst = 1: the half blocks come first, so their loads lead
+// their CUs' queues (at M = 16 they otherwise issue behind two full blocks' rings and end the
+// launch: gate_up 10.65 -> 10.52 us; at M = 1 they end with the full blocks either way).
 template <int LAYOUT, int XK, int ALGO, int U, int AWC, int MT = 1>
-__global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8_swiglu_mixed(KRQ_FP8_KERNEL_PARAMS, int nfull) {
-  if (static_cast<int>(blockIdx.x) < nfull)
+__global__ __launch_bounds__(kMaxThreads) void k_gemv_fp8_swiglu_mixed(KRQ_FP8_KERNEL_PARAMS, int nfull, int hfirst) {
+  const int nh = static_cast<int>(gridDim.x) - nfull, w = static_cast<int>(blockIdx.x);
+  const int f = hfirst ? w - nh : w;  // full block index (< 0 or >= nfull: a half block)
+  if (f >= 0 && f < nfull)
     gemv_fp8_body<MT, KRQ_OUT_SWIGLU, LAYOUT, XK, ALGO, U, 1, false, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row,
-                                                                         M, NO, K, kts, out, aux, FusedArgs{},
-                                                                         blockIdx.x);
+                                                                         M, NO, K, kts, out, aux, FusedArgs{}, f);
   else
     gemv_fp8_body<MT, kOutSwiGluHalf, LAYOUT, XK, ALGO, U, 1, false, AWC>(x, xsc, xinv, x_per_row, w8, wsc, w_per_row,
                                                                          M, NO, K, kts, out, aux, FusedArgs{},
-                                                                         (int64_t)blockIdx.x + nfull);
+                                                                         2 * (int64_t)nfull + (hfirst ? w : w - nfull));
 }
 
 // The chained FP8 MLP at M = 1 (krq_mlp_chain_fp8): act = SwiGLU(x . Wgu^T) and the split-K
