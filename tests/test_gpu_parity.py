@@ -253,7 +253,9 @@ def test_gemv_fp8_layouts_and_algos(dev, layout, algo):
         assert rel_err(y, yref) <= TOL
 
 
-@pytest.mark.parametrize("M", [1, 16, 23, 32])
+# (5 and 12: row-major e4m3 rows; 16, 23, 32: tiled; all but 1 the multi-row mixed launch, its
+# half-pair blocks first)
+@pytest.mark.parametrize("M", [1, 5, 12, 16, 23, 32])
 def test_gemv_swiglu_fp8(dev, M):
     N, K = GATE_UP
     I = N // 2
