@@ -327,51 +327,54 @@ __global__ __launch_bounds__(NT) void k_act_rows_fast(const uint16_t* __restrict
   }
 }
 
-// quant_rows_tiled by single-wave workgroups: workgroup (s, r) reads row r whole (16-element pieces
-// p = lane + 64 c, two 16-byte loads each, every load in flight; lanes past the row repeat its last
-// piece), takes the row's amax with DPP steps (no LDS, no barrier), and quantizes and writes only
-// its pieces c in [s sp, (s + 1) sp) into the tiled layout; pad rows r >= M get zeros. The same
-// arithmetic as k_act_rows_fast (quant_rows: the row's fp32 magnitude bits, the ActScale inverse,
-// the hardware convert), so the same bytes and scales, permuted. Single-wave workgroups with one
-// piece per lane each (ch workgroups per row) measured fastest at M = 16, K = 2,560 / 4,096 /
-// 9,728 (graph of 72 launches): 2.36 / 2.39 / 2.87 us, against 2.47 / 2.54 / 3.09 for one
-// 512-thread block per row (the row-major kernel above with a tiled store), 2.65 / 2.80 / 3.28
-// with two pieces per lane and 3.21 / 3.69 / 6.60 with one workgroup per row.
-template <int CH>
-__global__ __launch_bounds__(64) void k_act_rows_wave(const uint16_t* __restrict__ x, int64_t M, int64_t K, int sp,
-                                                      float* __restrict__ scale, uint8_t* __restrict__ x8) {
-  const int lane = threadIdx.x, s = blockIdx.y;
+// quant_rows_tiled by four-wave workgroups: workgroup (r, g) reads row r whole, wave w taking the
+// pieces of slices w + 4 c (c < CW; piece p = lane + 64 (w + 4 c), two 16-byte loads each, every
+// load in flight; pieces past the row repeat its last piece), so each lane loads 2 CW chunks instead
+// of the whole row's 2 ch. The waves' maxima (DPP within a wave) meet in LDS at one barrier; then
+// wave w quantizes slice w + 4 g, which it holds as its chunk c = g, into the tiled layout. Pad rows
+// r >= M get zeros. The same arithmetic as k_act_rows_fast (quant_rows: the row's fp32 magnitude
+// bits, the ActScale inverse, the hardware convert), so the same bytes and scales, permuted.
+// Measured at M = 16 (graph of 72 launches), K = 2,560 / 4,096 / 9,728: 2.40 / 2.46 / 2.67 us,
+// against 2.38 / 2.49 / 2.89 for single-wave workgroups that each read the whole row (one
+// workgroup per slice), 2.47 / 2.54 / 3.09 for one 512-thread block per row, and 3.21 / 3.69 /
+// 6.60 for one single-wave workgroup per row.
+template <int CW>
+__global__ __launch_bounds__(256) void k_act_rows_wg(const uint16_t* __restrict__ x, int64_t M, int64_t K,
+                                                     float* __restrict__ scale, uint8_t* __restrict__ x8) {
+  __shared__ uint32_t wmax[4];
+  const int lane = threadIdx.x & 63, w = static_cast<int>(threadIdx.x >> 6), gi = static_cast<int>(blockIdx.y);
   const int64_t r = blockIdx.x;
-  const int np = static_cast<int>(K >> 4), c0 = s * sp;
-  if (r >= M) {
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      const int p = lane + 64 * c;
-      if (c >= c0 && c < c0 + sp && p < np) *reinterpret_cast<uint4*>(x8 + tiled_offset(r, 16 * (int64_t)p, K)) = zero4();
-    }
+  const int np = static_cast<int>(K >> 4);
+  const int ps = lane + 64 * (w + 4 * gi);  // the piece this lane stores
+  if (r >= M) {  // (uniform per workgroup: no barrier below is skipped by part of it)
+    if (ps < np) *reinterpret_cast<uint4*>(x8 + tiled_offset(r, 16 * (int64_t)ps, K)) = zero4();
     return;
   }
   const uint8_t* row = reinterpret_cast<const uint8_t*>(x + r * K);
-  uint4 v[CH][2];
+  uint4 v[CW][2];
   uint32_t mb = 0;
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int p = min(lane + 64 * c, np - 1);
+  for (int c = 0; c < CW; ++c) {
+    const int p = min(lane + 64 * (w + 4 * c), np - 1);
     v[c][0] = ld16(row + 32 * (int64_t)p);
     v[c][1] = ld16(row + 32 * (int64_t)p + 16);
   }
 #pragma unroll
-  for (int c = 0; c < CH; ++c) mb = absmax8(v[c][1], absmax8(v[c][0], mb));
-  const float a = clamp_min_nan(as_f32(wave_max_u32_dpp(mb)), 1e-6f);
+  for (int c = 0; c < CW; ++c) mb = absmax8(v[c][1], absmax8(v[c][0], mb));
+  mb = wave_max_u32_dpp(mb);
+  if (lane == 0) wmax[w] = mb;
+  __syncthreads();
+  mb = umax32(umax32(wmax[0], wmax[1]), umax32(wmax[2], wmax[3]));
+  const float a = clamp_min_nan(as_f32(mb), 1e-6f);
   const float iv = inv_from_amax(a);
-  if (s == 0 && lane == 0) scale[r] = scale_from_amax(a);
+  if (gi == 0 && threadIdx.x == 0) scale[r] = scale_from_amax(a);
+  if (ps < np) {
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int p = lane + 64 * c;
-    if (c >= c0 && c < c0 + sp && p < np) {
-      const uint2 lo = quant8(v[c][0], iv), hi = quant8(v[c][1], iv);
-      *reinterpret_cast<uint4*>(x8 + tiled_offset(r, 16 * (int64_t)p, K)) = make_uint4(lo.x, lo.y, hi.x, hi.y);
-    }
+    for (int c = 0; c < CW; ++c)
+      if (c == gi) {
+        const uint2 lo = quant8(v[c][0], iv), hi = quant8(v[c][1], iv);
+        *reinterpret_cast<uint4*>(x8 + tiled_offset(r, 16 * (int64_t)ps, K)) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      }
   }
 }
 
@@ -589,17 +592,16 @@ extern "C" int krq_quant_rows_tiled(const void* x_bf16, int64_t M, int64_t K, vo
               "quant_rows_tiled: x and x8_tiled must be 16-byte aligned and K at most %lld", (long long)kVecMaxK);
   const int64_t mp = (M + 15) / 16 * 16;  // rows padded to whole 16-row tiles
   const int np = static_cast<int>(K / 16), ch = (np + 63) / 64;  // pieces per lane of a whole row (<= 16)
-  const int sp = 1;                                               // pieces each workgroup stores per lane
-  const dim3 grid(static_cast<unsigned>(mp), static_cast<unsigned>((ch + sp - 1) / sp));
-#define KRQ_ROWS_WAVE(CH)                                                                                         \
-  hipLaunchKernelGGL((k_act_rows_wave<CH>), grid, dim3(64), 0, (hipStream_t)stream, (const uint16_t*)x_bf16, M, K, \
-                     sp, xs, (uint8_t*)x8_tiled)
-  if (ch <= 3) KRQ_ROWS_WAVE(3);
-  else if (ch <= 4) KRQ_ROWS_WAVE(4);
-  else if (ch <= 8) KRQ_ROWS_WAVE(8);
-  else if (ch <= 10) KRQ_ROWS_WAVE(10);
-  else KRQ_ROWS_WAVE(16);
-#undef KRQ_ROWS_WAVE
+  const int cw = (ch + 3) / 4;                                     // chunks per lane of a four-wave workgroup
+  const dim3 grid(static_cast<unsigned>(mp), static_cast<unsigned>(cw));
+#define KRQ_ROWS_WG(CW)                                                                                        \
+  hipLaunchKernelGGL((k_act_rows_wg<CW>), grid, dim3(256), 0, (hipStream_t)stream, (const uint16_t*)x_bf16, M, K, \
+                     xs, (uint8_t*)x8_tiled)
+  if (cw <= 1) KRQ_ROWS_WG(1);
+  else if (cw <= 2) KRQ_ROWS_WG(2);
+  else if (cw <= 3) KRQ_ROWS_WG(3);
+  else KRQ_ROWS_WG(4);
+#undef KRQ_ROWS_WG
   return krq_check_launch("quant_rows_tiled");
 }
 
