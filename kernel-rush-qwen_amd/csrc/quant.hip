@@ -337,7 +337,8 @@ __global__ __launch_bounds__(NT) void k_act_rows_fast(const uint16_t* __restrict
 // Measured at M = 16 (graph of 72 launches), K = 2,560 / 4,096 / 9,728: 2.40 / 2.46 / 2.67 us,
 // against 2.38 / 2.49 / 2.89 for single-wave workgroups that each read the whole row (one
 // workgroup per slice), 2.47 / 2.54 / 3.09 for one 512-thread block per row, and 3.21 / 3.69 /
-// 6.60 for one single-wave workgroup per row.
+// 6.60 for one single-wave workgroup per row; eight-wave workgroups (two chunks per lane at
+// K = 9,728) measured 2.95 there.
 template <int CW>
 __global__ __launch_bounds__(256) void k_act_rows_wg(const uint16_t* __restrict__ x, int64_t M, int64_t K,
                                                      float* __restrict__ scale, uint8_t* __restrict__ x8) {
