@@ -432,7 +432,7 @@ STEP_KERNELS = {
     1: {"qkv": "k_gemv_wide1<1, 1, 10, 5, 4>", "o": "k_gemv_fp8<1, 1, 1, 1, 1, 8, 1, 8>",
         "gate_up": "k_gemv_fp8_swiglu_mixed<1, 1, 1, 5, 5, 1>", "down": "k_gemv_fp8<1, 1, 1, 1, 1, 20, 1, 20>"},
     16: {"qkv": "k_gemv_wide32<1, 10, 48, 1, 1>", "o": "k_gemv_wide32<1, 8, 48, 1, 1>",
-         "gate_up": "k_gemv_fp8_swiglu_mixed<1, 3, 1, 5, 0, 1>", "down": "k_gemv_wide32<1, 8, 48, 4, 1>"},
+         "gate_up": "k_gemv_fp8_swiglu_mixed<1, 3, 1, 5, 0, 1>", "down": "k_gemv_wide32<1, 4, 48, 4, 1>"},
 }
 PMC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --output-format csv -d <out> -o pmc -- python3 bench.py "
               "--no-cpu --no-prefill --no-extra --steps 36 --warmup 2 --reps 36 --replays 1 --calibrate-copy; "
