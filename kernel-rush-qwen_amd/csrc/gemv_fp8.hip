@@ -396,7 +396,8 @@ bool launch_wide32(int M, int mode, int x_kind, int w_layout, int algo, const vo
   // slots: a multiple of the sets, ten at most (two-matrix blocks take 254 VGPRs with ten); one
   // set over at most eight steps: eight. Four sets (down, 19 steps per split): four slots, one per
   // set (graph-timed, same box, alternating: down at M = 16 6.80 -> 6.33 us, at M = 32 8.21 ->
-  // 7.44; rings of 12 and 20 at M = 16 measured 7.1 and 7.2)
+  // 7.44; rings of 12 and 20 at M = 16 measured 7.1 and 7.2). Two sets (QKV at M = 32): four
+  // slots, 5.84 -> 5.63 us (two slots 6.33)
 #define KRQ_WIDE(MODE_, U_, TL_, NS_)                                                                              \
   if (M > 16)                                                                                                   \
     hipLaunchKernelGGL((k_gemv_wide32<MODE_, U_, TL_, NS_, 2>), grid, block, 0, s, xb, x_scale, x_per_row, wb,      \
@@ -410,7 +411,7 @@ bool launch_wide32(int M, int mode, int x_kind, int w_layout, int algo, const vo
 #define KRQ_WIDE_U(MODE_)                                 \
   if (ns == 1 && kts <= 16) { KRQ_WIDE_TL(MODE_, 8, 1) }   \
   else if (ns == 1) { KRQ_WIDE_TL(MODE_, 10, 1) }          \
-  else if (ns == 2) { KRQ_WIDE_TL(MODE_, 10, 2) }          \
+  else if (ns == 2) { KRQ_WIDE_TL(MODE_, 4, 2) }          \
   else if (ns == 3) { KRQ_WIDE_TL(MODE_, 9, 3) }           \
   else { KRQ_WIDE_TL(MODE_, 4, 4) }
   if (mode == KRQ_OUT_PARTIAL) {
